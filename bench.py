@@ -1,0 +1,262 @@
+"""W8A8 linear engine benchmark on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
+
+A step is one E2B-class decoder layer's prefill linears on one 512-row micro-batch, bf16 in
+-> bf16 out, each with its fused quant prologue and dequant epilogue:
+  qkv     K=1536 N=2560            (dequant)
+  o       K=2048 N=1536            (dequant)
+  gate_up K=1536 N=2x6144          (dequant + gelu_tanh(gate) * up)
+  down    K=6144 N=1536            (dequant + residual add)
+`value` is int8 TOP/s over the step's 2*M*N*K ops with inputs resident in HBM.  The JSON line
+also carries the roofline of the dominant kernel (the gate_up GEMM, timed live with HIP
+events on the launch stream), the host CPU's torch._int_mm on the same GEMMs (the
+reference's --backend cpu-int8 path, pipeline.py:237), and `extra`: the full-prefill GEMM
+sweep at M=3658 / 4096, the M=16384 stress GEMMs, and the decode GEMV bandwidth.
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "gemma-npu_amd"))
+sys.path.insert(0, ROOT)
+
+PEAK_INT8_TOPS = 5000.0   # MI355X dense int8 MFMA, published
+PEAK_HBM_GBS = 8000.0     # MI355X HBM3E, published
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "gemm_gate_up_m512_traffic.json")
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def event_time_ms(fn, reps, warmup):
+    import torch
+    for _ in range(warmup):
+        fn()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s.record()
+    for _ in range(reps):
+        fn()
+    e.record()
+    e.synchronize()
+    return s.elapsed_time(e) / reps
+
+
+def build_layer(M, dev, seed0=0):
+    import torch
+    from w8a8 import ops, workloads
+    groups = []
+    for gi, (name, (K, N, epi)) in enumerate(workloads.LAYER_GROUPS.items()):
+        x = workloads.activations(M, K, seed=seed0 + 10 * gi).to(dev)
+        w, sw = workloads.weights(N, K, seed=seed0 + 10 * gi + 1)
+        pw = ops.pack_weight(w.to(dev), "nk", N // 2 if epi == "gelu" else 0, sw=sw.to(dev))
+        ncols = N // 2 if epi == "gelu" else N
+        out = torch.empty((M, ncols), dtype=torch.bfloat16, device=dev)
+        res = workloads.activations(M, N, seed=seed0 + 10 * gi + 2, outliers=False).to(dev) if epi == "residual" else None
+        ws = torch.empty(ops.linear_workspace_bytes(M, K), dtype=torch.uint8, device=dev)
+        q, sx = ops.quant_rows(x)
+        groups.append(dict(name=name, K=K, N=N, epi=epi, x=x, w=w, pw=pw, out=out, res=res, ws=ws, q=q, sx=sx))
+    return groups
+
+
+def layer_step(groups):
+    from w8a8 import ops
+    for g in groups:
+        ops.linear_bf16(g["x"], g["pw"], epilogue=g["epi"], residual=g["res"], out=g["out"], workspace=g["ws"])
+
+
+def cpu_int_mm_ms(shapes, M, warm=3, reps=5):
+    """Median ms of torch._int_mm (host CPU) per (K, N) shape."""
+    import torch
+    out = {}
+    g = torch.Generator().manual_seed(0)
+    for K, N in shapes:
+        a = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
+        w = torch.randint(-127, 128, (K, N), generator=g, dtype=torch.int8)
+        for _ in range(warm):
+            torch._int_mm(a, w)
+        ts = []
+        for _ in range(reps):
+            t = time.perf_counter()
+            torch._int_mm(a, w)
+            ts.append(time.perf_counter() - t)
+        out[(K, N)] = statistics.median(ts) * 1e3
+    return out
+
+
+def sweep(M, dev, reps):
+    """All prefill GEMMs of one prompt: 35 layers x 4 groups + the PLE projection, int8 A ->
+    int32 C (the reference's NPU launches, gemma_npu.py:99-115), distinct weights per layer."""
+    import torch
+    from w8a8 import ops, workloads
+    shapes = workloads.sweep_shapes()
+    A = {}
+    packed = []
+    for name, layer, gi, K, N in shapes:
+        if K not in A:
+            A[K] = ops.quant_rows(workloads.activations(M, K, seed=K).to(dev))[0]
+        g = torch.Generator(device=dev).manual_seed(workloads.layer_seed(layer, gi))
+        w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8, device=dev)
+        packed.append((K, N, ops.pack_weight(w, "nk")))
+        del w
+    C = {N: torch.empty((M, N), dtype=torch.int32, device=dev) for _, _, _, _, N in shapes}
+
+    def run():
+        for K, N, pw in packed:
+            ops.gemm_i32(A[K], pw, C[N])
+
+    ms = event_time_ms(run, reps, 2)
+    total_ops = sum(workloads.gemm_ops(M, N, K) for _, _, _, K, N in shapes)
+    wbytes = sum(K * N for _, _, _, K, N in shapes)
+    return ms, total_ops, wbytes, [(K, N) for _, _, _, K, N in shapes]
+
+
+def gemv_bench(M, K, N, dev, reps, seed=5):
+    import torch
+    from w8a8 import ops, workloads
+    x = workloads.activations(M, K, seed=seed, outliers=False).to(dev)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8, device=dev)
+    s = (torch.rand(N, generator=g, device=dev) * 0.015 + 0.005).to(torch.bfloat16)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    ms = event_time_ms(lambda: ops.gemv_bf16(x, w, s, y), reps, 3)
+    nbytes = K * N + 2 * N + 2 * M * K + 2 * M * N
+    return ms, nbytes
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the host CPU baseline")
+    ap.add_argument("--no-extra", action="store_true", help="skip the sweep / stress / GEMV sub-results")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the W8A8 path runs "
+              "per GPU with no cross-GPU exchange)", file=sys.stderr)
+        return 2
+
+    import torch
+    from w8a8 import ops, workloads
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    M = 512
+    log(f"bench: building one E2B layer at M={M}")
+    groups = build_layer(M, dev)
+    step_ops = sum(workloads.gemm_ops(M, g["N"], g["K"]) for g in groups)
+
+    # ---- timed region: K steps bracketed by synchronisation ------------------------------
+    for _ in range(args.warmup):
+        layer_step(groups)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    s.record()
+    for _ in range(args.steps):
+        layer_step(groups)
+    e.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = s.elapsed_time(e) / args.steps
+    value = step_ops / (ms_step * 1e-3) / 1e12
+    log(f"bench: layer step {ms_step * 1e3:.1f} us = {value:.1f} TOP/s (wall {wall:.3f} s)")
+
+    # ---- dominant kernel: the gate_up GEMM with fused GELU epilogue ----------------------
+    gu = next(g for g in groups if g["name"] == "gate_up")
+    per_ms = {}
+    for g in groups:
+        per_ms[g["name"]] = event_time_ms(
+            lambda g=g: ops.gemm_bf16(g["q"], g["sx"], g["pw"], epilogue=g["epi"], residual=g["res"],
+                                      out=g["out"]), 200, 20)
+    gu_ops = workloads.gemm_ops(M, gu["N"], gu["K"])
+    gu_ms = per_ms["gate_up"]
+    achieved = gu_ops / (gu_ms * 1e-3) / 1e12
+    traffic = None
+    if os.path.exists(PMC_SUMMARY):
+        with open(PMC_SUMMARY) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+    roofline = {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": traffic,
+                "kernel": "gemm_kernel<EPI_GELU> gate_up M=512 K=1536 N=12288",
+                "avg_launch_us": round(gu_ms * 1e3, 2)}
+    log(f"bench: per-GEMM us: " + ", ".join(f"{k} {v * 1e3:.1f}" for k, v in per_ms.items()))
+
+    # ---- host CPU baseline: torch._int_mm on the same four GEMMs -------------------------
+    cpu = None
+    if not args.no_cpu:
+        torch.set_num_threads(os.cpu_count() or 1)
+        cm = cpu_int_mm_ms([(g["K"], g["N"]) for g in groups], M)
+        cpu_ms = sum(cm.values())
+        cpu = {"value": round(step_ops / (cpu_ms * 1e-3) / 1e12, 3), "unit": "TOP/s",
+               "cores": torch.get_num_threads(), "kind": "reference",
+               "sample": f"torch._int_mm (pipeline.py:237, --backend cpu-int8) on the layer's 4 GEMMs at M={M}: "
+                         f"3 warm-up + median of 5 per GEMM, {cpu_ms:.1f} ms per layer"}
+        log(f"bench: cpu _int_mm layer {cpu_ms:.1f} ms")
+
+    extra = {}
+    if not args.no_extra:
+        for Ms in (3658, 4096):
+            ms, tops_ops, wbytes, shp = sweep(Ms, dev, reps=5)
+            entry = {"ms": round(ms, 3), "gemms": len(shp), "tops": round(tops_ops / (ms * 1e-3) / 1e12, 1),
+                     "frac_mfma": round(tops_ops / (ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4)}
+            if not args.no_cpu and Ms == 3658:
+                uniq = sorted(set(shp))
+                cm = cpu_int_mm_ms(uniq, Ms, warm=2, reps=3)
+                cpu_total = sum(cm[s] for s in shp)
+                entry["cpu_int_mm_ms"] = round(cpu_total, 1)
+                entry["speedup_vs_cpu"] = round(cpu_total / ms, 1)
+            extra[f"prefill_sweep_m{Ms}"] = entry
+            log(f"bench: sweep M={Ms}: {entry}")
+            torch.cuda.empty_cache()
+        # M=16384 stress: gate_up with fused GELU, down with residual
+        for name in ("gate_up", "down"):
+            K, N, epi = workloads.LAYER_GROUPS[name]
+            Ms = 16384
+            x = workloads.activations(Ms, K, seed=9, row_spread=True).to(dev)
+            q, sx = ops.quant_rows(x)
+            gw = torch.Generator(device=dev).manual_seed(10)
+            w = torch.randint(-127, 128, (N, K), generator=gw, dtype=torch.int8, device=dev)
+            sw = torch.rand(N, generator=gw, device=dev) * 0.015 + 0.005
+            pw = ops.pack_weight(w, "nk", N // 2 if epi == "gelu" else 0, sw=sw)
+            res = torch.randn((Ms, N), device=dev).to(torch.bfloat16) if epi == "residual" else None
+            out = torch.empty((Ms, N // 2 if epi == "gelu" else N), dtype=torch.bfloat16, device=dev)
+            ms = event_time_ms(lambda: ops.gemm_bf16(q, sx, pw, epilogue=epi, residual=res, out=out), 20, 3)
+            t = workloads.gemm_ops(Ms, N, K) / (ms * 1e-3) / 1e12
+            extra[f"stress_m16384_{name}"] = {"us": round(ms * 1e3, 1), "tops": round(t, 1),
+                                              "frac_mfma": round(t / PEAK_INT8_TOPS, 4)}
+            log(f"bench: stress {name}: {extra[f'stress_m16384_{name}']}")
+            del x, q, w, pw, res, out
+        for Mg in (1, 4, 16):
+            K, N = workloads.LM_HEAD
+            ms, nbytes = gemv_bench(Mg, K, N, dev, reps=50)
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            extra[f"gemv_lm_head_m{Mg}"] = {"us": round(ms * 1e3, 1), "gbs": round(gbs, 1),
+                                            "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
+            log(f"bench: gemv lm head M={Mg}: {extra[f'gemv_lm_head_m{Mg}']}")
+        torch.cuda.empty_cache()
+
+    line = {
+        "metric": "W8A8 GEMM int8 TOPS (% of MFMA peak) at M=512/3658; GEMV HBM GB/s",
+        "value": round(value, 2), "unit": "TOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8", "data": "synthetic (seeded N(0,1) bf16 activations with 0.1% x20 outliers, "
+                                 "int8 U[-127,127] weights)",
+        "config": {"workload": "one E2B-class decoder layer's prefill linears, M=512 micro-batch, bf16 in -> bf16 "
+                               "out with fused per-token quant and dequant/GELU/residual epilogues",
+                   "M": M, "groups": {g["name"]: [g["K"], g["N"], g["epi"]] for g in groups}},
+        "roofline": roofline, "cpu_baseline": cpu, "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,205 @@
+// Per-row int8 quantisation and weight packing.
+//
+// quant_rows: one wave per row.  s = max(amax(|x|), 1e-8) / 127 and
+// q = clamp(rint(x / s), -127, 127) with an IEEE (correctly rounded) fp32 divide and
+// round-half-even, the arithmetic of pipeline.py:49-52 / gemma_npu.py:37-42 and, applied to
+// weight rows, of the per-output-channel weight quant at gemma_npu.py:68-69.
+//
+// pack_weight: rewrites an int8 weight into the GEMM's resident layout of 1 KiB MFMA
+// fragments.  Fragment (t, j) holds output channels [16t, 16t+16) x inputs [64j, 64j+64);
+// byte 16*l + b of it is channel 16t + l%16, input 64j + 16*(l/16) + b, i.e. exactly the
+// 16 bytes lane l feeds to v_mfma_i32_16x16x64_i8.  Fragments are stored n-tile major
+// ((t * KT + j) * 1024).  With `interleave` = I > 0 the n-tiles alternate gate / up:
+// tile 2u is channels [16u, 16u+16) and tile 2u+1 is channels [I+16u, I+16u+16), so a
+// lane holds matching gate and up accumulators for the fused GELU epilogue.
+#include "w8a8_common.h"
+
+namespace w8a8 {
+
+template <typename T>
+__device__ __forceinline__ void load8(const T* p, float (&v)[8]);
+
+template <>
+__device__ __forceinline__ void load8<uint16_t>(const uint16_t* p, float (&v)[8]) {
+  v4u d = *reinterpret_cast<const v4u*>(p);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = __uint_as_float(d[i] << 16);
+    v[2 * i + 1] = __uint_as_float(d[i] & 0xffff0000u);
+  }
+}
+
+template <>
+__device__ __forceinline__ void load8<float>(const float* p, float (&v)[8]) {
+  v4f a = *reinterpret_cast<const v4f*>(p);
+  v4f b = *reinterpret_cast<const v4f*>(p + 4);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[i] = a[i];
+    v[4 + i] = b[i];
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ float load1(const T* p);
+template <>
+__device__ __forceinline__ float load1<uint16_t>(const uint16_t* p) { return bf16_to_f32(*p); }
+template <>
+__device__ __forceinline__ float load1<float>(const float* p) { return *p; }
+
+__device__ __forceinline__ int8_t quant1(float v, float s) {
+  float r = __builtin_rintf(v / s);
+  r = fminf(fmaxf(r, -127.0f), 127.0f);
+  return int8_t(int(r));
+}
+
+// VEC: rows are 16-byte aligned and K % 8 == 0, so 8 elements move per access.
+template <typename T, bool VEC>
+__global__ __launch_bounds__(256) void quant_rows_kernel(const T* __restrict__ x, int64_t ldx, int M, int K,
+                                                         int8_t* __restrict__ q, int64_t ldq,
+                                                         float* __restrict__ scale) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const T* xr = x + int64_t(row) * ldx;
+  int8_t* qr = q + int64_t(row) * ldq;
+  float amax = 0.0f;
+  if (VEC) {
+    for (int k = lane * 8; k < K; k += 512) {
+      float v[8];
+      load8<T>(xr + k, v);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    }
+  } else {
+    for (int k = lane; k < K; k += 64) amax = fmaxf(amax, fabsf(load1<T>(xr + k)));
+  }
+  amax = wave_max(amax);
+  const float s = fmaxf(amax, 1e-8f) / 127.0f;
+  if (lane == 0) scale[row] = s;
+  if (VEC) {
+    for (int k = lane * 8; k < K; k += 512) {
+      float v[8];
+      load8<T>(xr + k, v);
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        lo |= uint32_t(uint8_t(quant1(v[i], s))) << (8 * i);
+        hi |= uint32_t(uint8_t(quant1(v[4 + i], s))) << (8 * i);
+      }
+      *reinterpret_cast<v2u*>(qr + k) = v2u{lo, hi};
+    }
+  } else {
+    for (int k = lane; k < K; k += 64) qr[k] = quant1(load1<T>(xr + k), s);
+  }
+}
+
+// One thread per 16-byte chunk of the packed output.  src_kn: the source is [K, N] (ld = ldw,
+// the reference's B layout, npu_kernels.py:46); otherwise it is [N, K] (gemma_npu.py:69).
+__global__ __launch_bounds__(256) void pack_weight_kernel(const int8_t* __restrict__ w, int64_t ldw, int N, int K,
+                                                          int src_kn, int interleave, int KT, int64_t nchunks,
+                                                          int8_t* __restrict__ out) {
+  const int64_t c = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (c >= nchunks) return;
+  const int lane = int(c & 63);
+  const int64_t f = c >> 6;
+  const int t = int(f / KT);
+  const int j = int(f % KT);
+  int n;
+  int limit;
+  if (interleave > 0) {
+    const int u = t >> 1;
+    n = (t & 1 ? interleave : 0) + 16 * u + (lane & 15);
+    limit = (t & 1 ? N : interleave);
+    if (16 * u + (lane & 15) >= interleave) n = -1;
+  } else {
+    n = 16 * t + (lane & 15);
+    limit = N;
+  }
+  const int k0 = 64 * j + 16 * (lane >> 4);
+  uint32_t word[4] = {0, 0, 0, 0};
+  if (n >= 0 && n < limit) {
+#pragma unroll
+    for (int b = 0; b < 16; ++b) {
+      const int k = k0 + b;
+      if (k < K) {
+        const int8_t v = src_kn ? w[int64_t(k) * ldw + n] : w[int64_t(n) * ldw + k];
+        word[b >> 2] |= uint32_t(uint8_t(v)) << (8 * (b & 3));
+      }
+    }
+  }
+  *reinterpret_cast<v4u*>(out + c * 16) = v4u{word[0], word[1], word[2], word[3]};
+}
+
+}  // namespace w8a8
+
+using namespace w8a8;
+
+extern "C" {
+
+int w8a8_quant_rows_bf16(const uint16_t* x, int64_t ldx, int64_t M, int64_t K, int8_t* q, int64_t ldq,
+                         float* scale, hipStream_t stream) {
+  if (M < 0 || K <= 0 || ldx < K || ldq < K) return fail(W8A8_EINVAL, "quant_rows: bad shape M=%lld K=%lld ldx=%lld ldq=%lld",
+                                                         (long long)M, (long long)K, (long long)ldx, (long long)ldq);
+  if (!x || !q || !scale) return fail(W8A8_EINVAL, "quant_rows: null pointer");
+  if (M == 0) return W8A8_OK;
+  if (M > INT32_MAX / 4 || K > INT32_MAX) return fail(W8A8_ENOTSUP, "quant_rows: too large");
+  const bool vec = (K % 8 == 0) && (ldx % 8 == 0) && (ldq % 8 == 0) && ((uintptr_t)x % 16 == 0) &&
+                   ((uintptr_t)q % 8 == 0);
+  dim3 grid((unsigned)((M + 3) / 4));
+  if (vec)
+    quant_rows_kernel<uint16_t, true><<<grid, 256, 0, stream>>>(x, ldx, (int)M, (int)K, q, ldq, scale);
+  else
+    quant_rows_kernel<uint16_t, false><<<grid, 256, 0, stream>>>(x, ldx, (int)M, (int)K, q, ldq, scale);
+  return check_launch("quant_rows_bf16");
+}
+
+int w8a8_quant_rows_f32(const float* x, int64_t ldx, int64_t M, int64_t K, int8_t* q, int64_t ldq, float* scale,
+                        hipStream_t stream) {
+  if (M < 0 || K <= 0 || ldx < K || ldq < K) return fail(W8A8_EINVAL, "quant_rows_f32: bad shape");
+  if (!x || !q || !scale) return fail(W8A8_EINVAL, "quant_rows_f32: null pointer");
+  if (M == 0) return W8A8_OK;
+  if (M > INT32_MAX / 4 || K > INT32_MAX) return fail(W8A8_ENOTSUP, "quant_rows_f32: too large");
+  const bool vec = (K % 8 == 0) && (ldx % 8 == 0) && (ldq % 8 == 0) && ((uintptr_t)x % 16 == 0) &&
+                   ((uintptr_t)q % 8 == 0);
+  dim3 grid((unsigned)((M + 3) / 4));
+  if (vec)
+    quant_rows_kernel<float, true><<<grid, 256, 0, stream>>>(x, ldx, (int)M, (int)K, q, ldq, scale);
+  else
+    quant_rows_kernel<float, false><<<grid, 256, 0, stream>>>(x, ldx, (int)M, (int)K, q, ldq, scale);
+  return check_launch("quant_rows_f32");
+}
+
+int64_t w8a8_packed_weight_bytes(int64_t N, int64_t K, int64_t interleave) {
+  return w8a8_packed_weight_bytes_internal(N, K, interleave);
+}
+
+static int pack_common(const int8_t* w, int64_t ldw, int64_t N, int64_t K, int src_kn, int64_t interleave,
+                       int8_t* packed, hipStream_t stream) {
+  if (!w || !packed) return fail(W8A8_EINVAL, "pack_weight: null pointer");
+  if (N <= 0 || K <= 0) return fail(W8A8_EINVAL, "pack_weight: bad shape N=%lld K=%lld", (long long)N, (long long)K);
+  if (src_kn ? ldw < N : ldw < K) return fail(W8A8_EINVAL, "pack_weight: leading dimension %lld too small", (long long)ldw);
+  if (interleave > 0 && (interleave % 16 != 0 || N != 2 * interleave))
+    return fail(W8A8_EINVAL, "pack_weight: interleave %lld needs N == 2*I and I %% 16 == 0 (N=%lld)",
+                (long long)interleave, (long long)N);
+  if ((uintptr_t)packed % 16 != 0) return fail(W8A8_EALIGN, "pack_weight: packed buffer not 16-byte aligned");
+  const int64_t bytes = w8a8_packed_weight_bytes_internal(N, K, interleave);
+  if (bytes > INT32_MAX) return fail(W8A8_ENOTSUP, "pack_weight: packed weight of %lld bytes exceeds 2 GiB", (long long)bytes);
+  const int KT = int((K + 63) / 64);
+  const int64_t nchunks = bytes / 16;
+  dim3 grid((unsigned)((nchunks + 255) / 256));
+  pack_weight_kernel<<<grid, 256, 0, stream>>>(w, ldw, (int)N, (int)K, src_kn, (int)interleave, KT, nchunks, packed);
+  return check_launch("pack_weight");
+}
+
+int w8a8_pack_weight_nk(const int8_t* w_nk, int64_t ldw, int64_t N, int64_t K, int64_t interleave, int8_t* packed,
+                        hipStream_t stream) {
+  return pack_common(w_nk, ldw, N, K, 0, interleave, packed, stream);
+}
+
+int w8a8_pack_weight_kn(const int8_t* b_kn, int64_t ldb, int64_t K, int64_t N, int64_t interleave, int8_t* packed,
+                        hipStream_t stream) {
+  return pack_common(b_kn, ldb, N, K, 1, interleave, packed, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,102 @@
+"""Drop-in for the reference's `npu_kernels` module (npu_kernels.py:1-64), on MI355X.
+
+Same names and call signature:
+
+    mm_i8(a, b, c) -> c        a [M, K] int8, b [K, N] int8, c [M, N] int32; C = A @ B exactly
+    use_npu()                  select this process's GPU for the calling thread
+    BLOCK_M, BLOCK_N, BLOCK_K  the padding granules the reference's callers read
+                               (gemma_npu.py:65, 67, 129); the HIP GEMM itself needs none
+
+`b` is normally the PackedWeight returned by `resident.to_npu(w, static=True)` (the weight
+stays resident in HBM in the MFMA layout); a plain int8 [K, N] tensor also works and is
+packed on every call.  `a` and `c` may be host tensors (the reference's host-visible
+resident buffers): rows are copied to the GPU, multiplied, and copied back before
+mm_i8 returns, matching the reference's synchronous launch.  With GPU tensors the call is
+ordered on torch's current stream instead.
+
+Importing this module also makes `from triton.backends.amd_triton_npu import resident`
+resolve to `w8a8.resident`, so gemma_npu.py's NPUGemm runs on it unchanged.
+"""
+import importlib.util
+import os
+import sys
+import types
+
+import torch
+
+from w8a8 import ops, resident
+from w8a8.ops import PackedWeight
+
+BLOCK_M = BLOCK_N = 512
+BLOCK_K = 128
+
+_DEVICE_INDEX = int(os.environ.get("W8A8_DEVICE", "0"))
+
+
+def use_npu():
+    """HIP device selection is per host thread, like the reference's per-thread driver
+    (npu_kernels.py:20-26): call this first on a thread that launches GEMMs."""
+    torch.cuda.set_device(_DEVICE_INDEX)
+
+
+def _device():
+    return torch.device("cuda", _DEVICE_INDEX)
+
+
+def mm_i8(a, b, c):
+    """c[M, N] = a[M, K] @ b[K, N] (int8 x int8 -> int32, exact).  Returns c.
+
+    Unlike the reference (npu_kernels.py:59-64), any M and N work, and a shape mismatch
+    raises instead of truncating to multiples of 512.
+    """
+    if a.dtype != torch.int8 or a.dim() != 2:
+        raise TypeError(f"mm_i8: a must be int8 [M, K], got {a.dtype} {tuple(a.shape)}")
+    if c.dtype != torch.int32 or c.dim() != 2:
+        raise TypeError(f"mm_i8: c must be int32 [M, N], got {c.dtype} {tuple(c.shape)}")
+    M, K = a.shape
+    if isinstance(b, PackedWeight):
+        Kb, N = b.K, b.N
+        dev = b.device
+    else:
+        if b.dtype != torch.int8 or b.dim() != 2:
+            raise TypeError(f"mm_i8: b must be int8 [K, N], got {b.dtype} {tuple(b.shape)}")
+        Kb, N = b.shape
+        dev = b.device if b.is_cuda else (a.device if a.is_cuda else (c.device if c.is_cuda else _device()))
+    if Kb != K:
+        raise ValueError(f"mm_i8: a is [{M}, {K}] but b is [{Kb}, {N}]")
+    if tuple(c.shape) != (M, N):
+        raise ValueError(f"mm_i8: c is {tuple(c.shape)}, expected ({M}, {N})")
+    if M == 0:
+        return c
+    w = b if isinstance(b, PackedWeight) else ops.pack_weight(b.to(dev), layout="kn")
+    a_d = a if a.is_cuda else a.to(dev, non_blocking=a.is_pinned())
+    if a_d.stride(1) != 1 or a_d.stride(0) % 16 or a_d.data_ptr() % 16:
+        a_d = a_d.contiguous()
+    if c.is_cuda and c.stride(1) == 1 and c.stride(0) % 4 == 0 and c.data_ptr() % 16 == 0:
+        ops.gemm_i32(a_d, w, c)
+        return c
+    c_d = torch.empty((M, N), dtype=torch.int32, device=dev)
+    ops.gemm_i32(a_d, w, c_d)
+    c.copy_(c_d)  # blocking for host c: the result is there when mm_i8 returns
+    return c
+
+
+def _install_resident_alias():
+    """Register w8a8.resident as triton.backends.amd_triton_npu.resident (gemma_npu.py:60, 88)."""
+    name = "triton.backends.amd_triton_npu"
+    if name in sys.modules:
+        return
+    if importlib.util.find_spec("triton") is None:
+        for parent in ("triton", "triton.backends"):
+            if parent not in sys.modules:
+                m = types.ModuleType(parent)
+                m.__path__ = []
+                sys.modules[parent] = m
+    mod = types.ModuleType(name)
+    mod.__path__ = []
+    mod.resident = resident
+    sys.modules[name] = mod
+    sys.modules[name + ".resident"] = resident
+
+
+_install_resident_alias()

@@ -1,0 +1,10 @@
+"""W8A8 linear engine for MI355X (gfx950): HIP kernels behind the C ABI in include/w8a8.h.
+
+    from w8a8 import ops          # torch-facing entry points (GEMM, quant, GEMV, linear)
+    import npu_kernels            # drop-in for the reference's npu_kernels.mm_i8
+"""
+from ._lib import LIB_PATH, W8A8Error, lib  # noqa: F401
+from .ops import (  # noqa: F401
+    PackedWeight, dequant_bf16, gemm_bf16, gemm_i32, gemv_bf16, linear_bf16, pack_weight, packed_weight_bytes,
+    quant_rows, quant_weight, rms_residual,
+)

@@ -1,0 +1,288 @@
+"""torch-facing wrappers of the libw8a8 C ABI.
+
+Every function takes device tensors on a ROCm GPU, checks dtype / layout on the host, and
+launches on torch's current stream for that device.  Results are stream-ordered: they are
+ready for any later work on the same stream.  There is no CPU fallback.
+"""
+import torch
+
+from ._lib import call, lib
+
+EPILOGUES = {"none": 0, "gelu": 1, "residual": 2, "residual_rms": 3}
+
+
+def _stream(t):
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _check(t, name, dtype, ndim=2):
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name}: expected a tensor, got {type(t).__name__}")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name}: expected a GPU tensor, got device {t.device}")
+    if t.dtype != dtype:
+        raise TypeError(f"{name}: expected {dtype}, got {t.dtype}")
+    if t.dim() != ndim:
+        raise ValueError(f"{name}: expected {ndim}-D, got shape {tuple(t.shape)}")
+    if ndim == 2 and t.shape[1] > 1 and t.stride(1) != 1:
+        raise ValueError(f"{name}: rows must be contiguous (stride(1) == 1), got strides {t.stride()}")
+    if ndim == 1 and t.shape[0] > 1 and t.stride(0) != 1:
+        raise ValueError(f"{name}: must be contiguous")
+
+
+def _ld(t):
+    return t.stride(0) if t.shape[0] > 1 else max(t.shape[1], 1)
+
+
+def _same_device(*ts):
+    devs = {t.device for t in ts if t is not None}
+    if len(devs) > 1:
+        raise ValueError(f"tensors on different devices: {sorted(map(str, devs))}")
+
+
+class PackedWeight:
+    """An int8 weight resident on the GPU in the GEMM's MFMA-fragment layout.
+
+    N output channels x K inputs; `interleave` = I > 0 marks a [gate; up] pair (N = 2I)
+    packed for the fused GELU epilogue.  `sw` (fp32 [N]) optionally carries the
+    per-channel scales that belong to it.
+    """
+
+    __slots__ = ("data", "N", "K", "interleave", "sw")
+
+    def __init__(self, data, N, K, interleave=0, sw=None):
+        self.data, self.N, self.K, self.interleave, self.sw = data, int(N), int(K), int(interleave), sw
+
+    @property
+    def device(self):
+        return self.data.device
+
+    @property
+    def shape(self):
+        """(K, N), the shape of the reference's B operand (npu_kernels.py:46)."""
+        return (self.K, self.N)
+
+    def __repr__(self):
+        return f"PackedWeight(N={self.N}, K={self.K}, interleave={self.interleave}, device={self.device})"
+
+
+def packed_weight_bytes(N, K, interleave=0):
+    n = lib().w8a8_packed_weight_bytes(N, K, interleave)
+    if n < 0:
+        raise ValueError(f"invalid packed weight shape N={N} K={K} interleave={interleave}")
+    return n
+
+
+def pack_weight(w, layout="nk", interleave=0, sw=None):
+    """int8 weight -> PackedWeight.  layout "nk": w is [N, K] (gemma_npu.py:69);
+    "kn": w is [K, N], the reference GEMM's B operand (npu_kernels.py:46)."""
+    _check(w, "w", torch.int8)
+    if layout == "nk":
+        N, K = w.shape
+        fn = "w8a8_pack_weight_nk"
+    elif layout == "kn":
+        K, N = w.shape
+        fn = "w8a8_pack_weight_kn"
+    else:
+        raise ValueError(f"layout must be 'nk' or 'kn', got {layout!r}")
+    nbytes = packed_weight_bytes(N, K, interleave)
+    data = torch.empty(nbytes, dtype=torch.int8, device=w.device)
+    ld = w.stride(0) if w.shape[0] > 1 else w.shape[1]
+    call(fn, w.data_ptr(), ld, *((N, K) if layout == "nk" else (K, N)), interleave, data.data_ptr(), _stream(w))
+    return PackedWeight(data, N, K, interleave, sw)
+
+
+def quant_rows(x, q=None, scale=None):
+    """Per-row int8 quant of bf16 or fp32 rows (pipeline.py:49-52) -> (q int8 [M,K], scale fp32 [M])."""
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"quant_rows: x must be bf16 or fp32, got {x.dtype}")
+    _check(x, "x", x.dtype)
+    M, K = x.shape
+    if q is None:
+        q = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    if scale is None:
+        scale = torch.empty((M,), dtype=torch.float32, device=x.device)
+    _check(q, "q", torch.int8)
+    _check(scale, "scale", torch.float32, 1)
+    if tuple(q.shape) != (M, K) or scale.shape[0] != M:
+        raise ValueError("quant_rows: output shapes do not match x")
+    _same_device(x, q, scale)
+    fn = "w8a8_quant_rows_bf16" if x.dtype == torch.bfloat16 else "w8a8_quant_rows_f32"
+    call(fn, x.data_ptr(), _ld(x), M, K, q.data_ptr(), _ld(q), scale.data_ptr(), _stream(x))
+    return q, scale
+
+
+def quant_weight(w, layout="nk", interleave=0):
+    """Float weight [N, K] -> PackedWeight with per-output-channel fp32 scales
+    (absmax/127 per channel, gemma_npu.py:68-69)."""
+    if layout != "nk":
+        raise ValueError("quant_weight takes a float [N, K] weight")
+    q, sw = quant_rows(w.contiguous())
+    return pack_weight(q, "nk", interleave, sw=sw)
+
+
+def _packed(w):
+    if not isinstance(w, PackedWeight):
+        raise TypeError(f"expected a PackedWeight, got {type(w).__name__}")
+    return w
+
+
+def gemm_i32(a, w, c=None, tile_cfg=-1):
+    """C[M,N] int32 = A[M,K] int8 @ W (exact; npu_kernels.py:40-56)."""
+    w = _packed(w)
+    _check(a, "a", torch.int8)
+    M, K = a.shape
+    if K != w.K:
+        raise ValueError(f"gemm_i32: A has K={K}, weight has K={w.K}")
+    if w.interleave:
+        raise ValueError("gemm_i32: a gate/up-interleaved weight has no plain int32 column order")
+    if c is None:
+        c = torch.empty((M, w.N), dtype=torch.int32, device=a.device)
+    _check(c, "c", torch.int32)
+    if tuple(c.shape) != (M, w.N):
+        raise ValueError(f"gemm_i32: C has shape {tuple(c.shape)}, expected {(M, w.N)}")
+    _same_device(a, w.data, c)
+    call("w8a8_gemm_i32_cfg", a.data_ptr(), _ld(a), w.data.data_ptr(), M, w.N, K, c.data_ptr(), _ld(c),
+         tile_cfg, _stream(a))
+    return c
+
+
+def gemm_bf16(a, sx, w, sw=None, epilogue="none", residual=None, out=None, tile_cfg=-1):
+    """GEMM + dequant epilogue -> bf16 (pipeline.py:55-57, 102-107)."""
+    w = _packed(w)
+    sw = w.sw if sw is None else sw
+    if sw is None:
+        raise ValueError("gemm_bf16: no per-channel scales")
+    _check(a, "a", torch.int8)
+    _check(sx, "sx", torch.float32, 1)
+    _check(sw, "sw", torch.float32, 1)
+    M, K = a.shape
+    if K != w.K or sx.shape[0] != M or sw.shape[0] != w.N:
+        raise ValueError("gemm_bf16: operand shapes do not match")
+    epi = EPILOGUES[epilogue]
+    if epi == 3:
+        raise ValueError("gemm_bf16: use linear_bf16 or rms_residual for the RMSNorm residual")
+    ncols = w.interleave if epi == 1 else w.N
+    if out is None:
+        out = torch.empty((M, ncols), dtype=torch.bfloat16, device=a.device)
+    _check(out, "out", torch.bfloat16)
+    if tuple(out.shape) != (M, ncols):
+        raise ValueError(f"gemm_bf16: out has shape {tuple(out.shape)}, expected {(M, ncols)}")
+    rp, ldr = None, 0
+    if epi == 2:
+        if residual is None:
+            raise ValueError("gemm_bf16: residual epilogue without a residual")
+        _check(residual, "residual", torch.bfloat16)
+        if tuple(residual.shape) != (M, w.N):
+            raise ValueError("gemm_bf16: residual shape does not match")
+        rp, ldr = residual.data_ptr(), _ld(residual)
+    _same_device(a, sx, sw, w.data, out, residual)
+    call("w8a8_gemm_bf16_cfg", a.data_ptr(), _ld(a), sx.data_ptr(), w.data.data_ptr(), sw.data_ptr(), M, w.N, K,
+         epi, w.interleave, rp, ldr, out.data_ptr(), _ld(out), tile_cfg, _stream(a))
+    return out
+
+
+def dequant_bf16(acc, sx, sw, out=None):
+    """bf16((acc * sx[:,None]) * sw[None,:]) (pipeline.py:55-57)."""
+    _check(acc, "acc", torch.int32)
+    _check(sx, "sx", torch.float32, 1)
+    _check(sw, "sw", torch.float32, 1)
+    M, N = acc.shape
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=acc.device)
+    _check(out, "out", torch.bfloat16)
+    _same_device(acc, sx, sw, out)
+    call("w8a8_dequant_bf16", acc.data_ptr(), _ld(acc), sx.data_ptr(), sw.data_ptr(), M, N, out.data_ptr(),
+         _ld(out), _stream(acc))
+    return out
+
+
+def rms_residual(y, res, w, eps, out=None, quant=False):
+    """h = res + bf16(rms(y) * w)  (k_post_ff, pipeline.py:110-114); with quant=True also
+    returns the int8 rows and scales of h."""
+    _check(y, "y", torch.bfloat16)
+    _check(res, "res", torch.bfloat16)
+    M, N = y.shape
+    if tuple(res.shape) != (M, N):
+        raise ValueError("rms_residual: shapes differ")
+    wp = None
+    if w is not None:
+        _check(w, "w", torch.bfloat16, 1)
+        wp = w.data_ptr()
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=y.device)
+    _check(out, "out", torch.bfloat16)
+    q = sq = None
+    if quant:
+        q = torch.empty((M, N), dtype=torch.int8, device=y.device)
+        sq = torch.empty((M,), dtype=torch.float32, device=y.device)
+    _same_device(y, res, w, out)
+    call("w8a8_rms_residual_bf16", y.data_ptr(), _ld(y), res.data_ptr(), _ld(res), wp, float(eps), M, N,
+         out.data_ptr(), _ld(out), q.data_ptr() if quant else None, N if quant else 0,
+         sq.data_ptr() if quant else None, _stream(y))
+    return (out, q, sq) if quant else out
+
+
+def linear_workspace_bytes(M, K):
+    return lib().w8a8_linear_workspace_bytes(M, K)
+
+
+def linear_bf16(x, w, sw=None, epilogue="none", residual=None, rms_w=None, eps=1e-6, out=None, workspace=None):
+    """bf16 x -> per-token quant -> W8A8 GEMM -> dequant epilogue -> bf16 (gemma_npu.py:117-152)."""
+    w = _packed(w)
+    sw = w.sw if sw is None else sw
+    if sw is None:
+        raise ValueError("linear_bf16: no per-channel scales")
+    _check(x, "x", torch.bfloat16)
+    _check(sw, "sw", torch.float32, 1)
+    M, K = x.shape
+    if K != w.K or sw.shape[0] != w.N:
+        raise ValueError("linear_bf16: operand shapes do not match")
+    epi = EPILOGUES[epilogue]
+    ncols = w.interleave if epi == 1 else w.N
+    if out is None:
+        out = torch.empty((M, ncols), dtype=torch.bfloat16, device=x.device)
+    _check(out, "out", torch.bfloat16)
+    if tuple(out.shape) != (M, ncols):
+        raise ValueError(f"linear_bf16: out has shape {tuple(out.shape)}, expected {(M, ncols)}")
+    rp, ldr = None, 0
+    if epi in (2, 3):
+        if residual is None:
+            raise ValueError("linear_bf16: residual epilogue without a residual")
+        _check(residual, "residual", torch.bfloat16)
+        if tuple(residual.shape) != (M, w.N):
+            raise ValueError("linear_bf16: residual shape does not match")
+        rp, ldr = residual.data_ptr(), _ld(residual)
+    rwp = None
+    if rms_w is not None:
+        _check(rms_w, "rms_w", torch.bfloat16, 1)
+        rwp = rms_w.data_ptr()
+    need = linear_workspace_bytes(M, K)
+    if workspace is None:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
+    _same_device(x, sw, w.data, out, residual, rms_w, workspace)
+    call("w8a8_linear_bf16", x.data_ptr(), _ld(x), w.data.data_ptr(), sw.data_ptr(), M, w.N, K, epi,
+         w.interleave, rp, ldr, rwp, float(eps), out.data_ptr(), _ld(out), workspace.data_ptr(),
+         workspace.numel(), _stream(x))
+    return out
+
+
+def gemv_bf16(x, w, s, out=None):
+    """y = bf16((x @ w^T) * s): torch._weight_int8pack_mm semantics (gemma_npu.py:155-156).
+    x bf16 [M<=16, K]; w int8 [N, K]; s bf16 or fp32 [N]."""
+    _check(x, "x", torch.bfloat16)
+    _check(w, "w", torch.int8)
+    if s.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"gemv_bf16: scales must be bf16 or fp32, got {s.dtype}")
+    _check(s, "s", s.dtype, 1)
+    M, K = x.shape
+    N = w.shape[0]
+    if w.shape[1] != K or s.shape[0] != N:
+        raise ValueError("gemv_bf16: operand shapes do not match")
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    _check(out, "out", torch.bfloat16)
+    _same_device(x, w, s, out)
+    call("w8a8_gemv_bf16", x.data_ptr(), _ld(x), M, w.data_ptr(), _ld(w), N, K, s.data_ptr(),
+         1 if s.dtype == torch.float32 else 0, out.data_ptr(), _ld(out), _stream(x))
+    return out

@@ -1,0 +1,143 @@
+/*
+ * libw8a8 -- W8A8 linear engine for MI355X (gfx950): the C ABI.
+ *
+ * Every entry point takes plain device pointers, element counts / leading dimensions (in
+ * elements) and a hipStream_t, enqueues its kernels on that stream and returns a status:
+ * 0 (W8A8_OK) or one of W8A8_E*.  On failure nothing was launched and w8a8_last_error()
+ * (thread-local) describes why.  The library never allocates device memory, never frees
+ * caller memory and never synchronises; results are ready when the stream reaches them.
+ * Matrices are row-major.  bf16 data is passed as uint16_t bit patterns.
+ *
+ * Reference interfaces replaced (AyaSakura-comp/gemma-npu, file:line):
+ *   npu_kernels.mm_i8 / matmul_i8_k ........ npu_kernels.py:40-64      -> w8a8_gemm_i32
+ *   resident.to_npu(w, static=True) ........ gemma_npu.py:70-75        -> w8a8_pack_weight_kn / _nk
+ *   _quant / _quant_rows ................... pipeline.py:49-52, gemma_npu.py:37-42 -> w8a8_quant_rows_*
+ *   per-channel weight quant ............... gemma_npu.py:68-69        -> w8a8_quant_rows_f32 / _bf16 on W[N,K]
+ *   _deq / _dequant ........................ pipeline.py:55-57, gemma_npu.py:45-47 -> w8a8_dequant_bf16,
+ *                                                                         w8a8_gemm_bf16 (epilogue 0)
+ *   k_gelu ................................. pipeline.py:102-107       -> w8a8_gemm_bf16 (epilogue 1)
+ *   k_post_ff / _rms ....................... pipeline.py:43-46,110-114 -> w8a8_rms_residual_bf16
+ *   NPUGemm.matmul (quant->GEMM->dequant) .. gemma_npu.py:117-152      -> w8a8_linear_bf16
+ *   cpu_int8_linear / Int8Head ............. gemma_npu.py:155-172      -> w8a8_gemv_bf16
+ *     (torch._weight_int8pack_mm semantics)
+ */
+#ifndef W8A8_H
+#define W8A8_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define W8A8_OK 0
+#define W8A8_EINVAL 1  /* bad shape, pointer, leading dimension or option */
+#define W8A8_EALIGN 2  /* pointer or leading dimension not aligned as required */
+#define W8A8_EHIP 3    /* a HIP launch failed */
+#define W8A8_ENOTSUP 4 /* valid but unsupported (K % 16 != 0, offsets beyond 32 bits, ...) */
+
+/* Message for the last failing call on this thread ("" if none). */
+const char *w8a8_last_error(void);
+
+/* ABI revision of this header (1). */
+int w8a8_abi_version(void);
+
+/* ---- resident weights ------------------------------------------------------------------ */
+
+/* Bytes of the packed (MFMA-fragment) weight for N output channels x K inputs.  With
+ * interleave = I > 0 the weight is a [gate; up] pair (N == 2*I, I % 16 == 0) whose channels
+ * are interleaved in 16-channel tiles for the fused GELU epilogue.  -1 if invalid.
+ * Replaces the zero-padded [K, N_pad] resident copy of gemma_npu.py:67-75. */
+int64_t w8a8_packed_weight_bytes(int64_t N, int64_t K, int64_t interleave);
+
+/* Pack an int8 weight given in the reference GEMM's B layout, b_kn[K, N] (ld = ldb)
+ * (npu_kernels.py:46 B[K,N]; gemma_npu.py:70-71 wt[K, N_pad]).  `packed` is 16-byte aligned,
+ * w8a8_packed_weight_bytes(N, K, interleave) long. */
+int w8a8_pack_weight_kn(const int8_t *b_kn, int64_t ldb, int64_t K, int64_t N, int64_t interleave,
+                        int8_t *packed, hipStream_t stream);
+
+/* Same, from the [N, K] layout (gemma_npu.py:69 q, :81 w_cpu). */
+int w8a8_pack_weight_nk(const int8_t *w_nk, int64_t ldw, int64_t N, int64_t K, int64_t interleave,
+                        int8_t *packed, hipStream_t stream);
+
+/* ---- prologue: per-row int8 quantisation (pipeline.py:49-52) ---------------------------- */
+
+/* scale[m] = max(amax_k |x[m,k]|, 1e-8) / 127;  q[m,k] = clamp(rint(x[m,k] / scale[m]), +-127)
+ * with IEEE fp32 division and round-half-even.  x bf16 [M, K]. */
+int w8a8_quant_rows_bf16(const uint16_t *x, int64_t ldx, int64_t M, int64_t K, int8_t *q, int64_t ldq,
+                         float *scale, hipStream_t stream);
+
+/* Same for fp32 rows; applied to a weight W[N, K] it is the per-output-channel weight quant
+ * of gemma_npu.py:68-69. */
+int w8a8_quant_rows_f32(const float *x, int64_t ldx, int64_t M, int64_t K, int8_t *q, int64_t ldq,
+                        float *scale, hipStream_t stream);
+
+/* ---- GEMM (npu_kernels.py:40-64) --------------------------------------------------------- */
+
+/* C[M, N] int32 = A[M, K] int8 @ W, W packed by w8a8_pack_weight_* (interleave 0).
+ * Exact integer arithmetic.  K % 16 == 0; A rows 16-byte aligned (lda % 16 == 0); C rows
+ * 16-byte aligned (ldc % 4 == 0).  Any M >= 0 and N >= 1: no padding to 512 is needed
+ * (the reference's mm_i8 floors M and N to multiples of 512, npu_kernels.py:63). */
+int w8a8_gemm_i32(const int8_t *a, int64_t lda, const int8_t *w_packed, int64_t M, int64_t N, int64_t K,
+                  int32_t *c, int64_t ldc, hipStream_t stream);
+
+/* As w8a8_gemm_i32 with an explicit tile configuration (0 .. count-1, -1 = automatic);
+ * for tuning and tests. */
+int w8a8_gemm_i32_cfg(const int8_t *a, int64_t lda, const int8_t *w_packed, int64_t M, int64_t N, int64_t K,
+                      int32_t *c, int64_t ldc, int tile_cfg, hipStream_t stream);
+
+/* GEMM with the dequantising epilogue, bf16 out:
+ *   y[m, n] = bf16((float(acc[m, n]) * sx[m]) * sw[n])                 (pipeline.py:55-57)
+ * epilogue 0: out = y                                                  [M, N]
+ *          1: out = bf16(bf16(gelu_tanh(y[:, :I])) * y[:, I:])          [M, I] (pipeline.py:106);
+ *             needs the weight packed with interleave = I = N / 2
+ *          2: out = bf16(res + y)                                      [M, N]
+ * sx fp32 [M] (per token), sw fp32 [N] (per channel, [gate; up] order for epilogue 1). */
+int w8a8_gemm_bf16(const int8_t *a, int64_t lda, const float *sx, const int8_t *w_packed, const float *sw,
+                   int64_t M, int64_t N, int64_t K, int epilogue, int64_t interleave, const uint16_t *res,
+                   int64_t ldr, uint16_t *out, int64_t ldo, hipStream_t stream);
+
+int w8a8_gemm_bf16_cfg(const int8_t *a, int64_t lda, const float *sx, const int8_t *w_packed, const float *sw,
+                       int64_t M, int64_t N, int64_t K, int epilogue, int64_t interleave, const uint16_t *res,
+                       int64_t ldr, uint16_t *out, int64_t ldo, int tile_cfg, hipStream_t stream);
+
+/* ---- element-wise neighbours ------------------------------------------------------------- */
+
+/* out = bf16((float(acc) * sx[m]) * sw[n])  (pipeline.py:55-57 on an int32 result). */
+int w8a8_dequant_bf16(const int32_t *acc, int64_t ldacc, const float *sx, const float *sw, int64_t M, int64_t N,
+                      uint16_t *out, int64_t ldo, hipStream_t stream);
+
+/* h = bf16(res + bf16(y * (mean(y^2) + eps)^-0.5 * w))  (k_post_ff, pipeline.py:110-114); w may be
+ * NULL (no weight, pipeline.py:46).  If q / sq are given, also the int8 rows and scales of h
+ * (the `_quant(h)` of k_post_ff).  h may alias y. */
+int w8a8_rms_residual_bf16(const uint16_t *y, int64_t ldy, const uint16_t *res, int64_t ldr, const uint16_t *w,
+                           float eps, int64_t M, int64_t N, uint16_t *h, int64_t ldh, int8_t *q, int64_t ldq,
+                           float *sq, hipStream_t stream);
+
+/* ---- whole linear: bf16 in -> bf16 out (NPUGemm.matmul, gemma_npu.py:117-152) ------------ */
+
+/* Workspace for w8a8_linear_bf16: int8 rows + per-row scales. */
+int64_t w8a8_linear_workspace_bytes(int64_t M, int64_t K);
+
+/* quant_rows(x) -> GEMM -> epilogue.  epilogue 0-2 as w8a8_gemm_bf16; 3: residual with RMSNorm,
+ * out = bf16(res + bf16(rms(y) * rms_w)) (pipeline.py:113).  workspace: 256-byte aligned,
+ * w8a8_linear_workspace_bytes(M, K) long. */
+int w8a8_linear_bf16(const uint16_t *x, int64_t ldx, const int8_t *w_packed, const float *sw, int64_t M, int64_t N,
+                     int64_t K, int epilogue, int64_t interleave, const uint16_t *res, int64_t ldr,
+                     const uint16_t *rms_w, float eps, uint16_t *out, int64_t ldo, void *workspace,
+                     int64_t workspace_bytes, hipStream_t stream);
+
+/* ---- decode GEMV (gemma_npu.py:155-172, torch._weight_int8pack_mm) ---------------------- */
+
+/* y[m, n] = bf16((sum_k x[m, k] * w[n, k]) * s[n]),  x bf16 [M, K] with 1 <= M <= 16,
+ * w int8 [N, K] (ld = ldw), s bf16 (scale_is_f32 = 0, as gemma_npu.py:82) or fp32 [N].
+ * K % 16 == 0; x and w rows 16-byte aligned.  fp32 accumulation; deterministic. */
+int w8a8_gemv_bf16(const uint16_t *x, int64_t ldx, int64_t M, const int8_t *w, int64_t ldw, int64_t N, int64_t K,
+                   const void *scales, int scale_is_f32, uint16_t *y, int64_t ldy, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* W8A8_H */

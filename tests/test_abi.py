@@ -1,0 +1,93 @@
+"""The C-ABI library: it loads, exports every symbol include/w8a8.h declares, and rejects bad
+arguments with a status code and a message before launching anything (no GPU needed)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from w8a8 import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "w8a8.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(w8a8_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_abi():
+    names = declared_functions()
+    assert "w8a8_gemm_i32" in names and "w8a8_gemv_bf16" in names
+    assert set(names) == set(_lib.SIGNATURES), "ctypes signature table and header disagree"
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    missing = [n for n in declared_functions() if not hasattr(L, n)]
+    assert not missing, f"not exported: {missing}"
+    assert L.w8a8_abi_version() == 1
+
+
+def test_packed_weight_bytes():
+    L = _lib.lib()
+    assert L.w8a8_packed_weight_bytes(6144, 1536, 0) == 6144 // 16 * 1536 // 64 * 1024
+    assert L.w8a8_packed_weight_bytes(2560, 1536, 0) == 2560 * 1536
+    assert L.w8a8_packed_weight_bytes(17, 70, 0) == 2 * 2 * 1024  # padded to 16 x 64 tiles
+    assert L.w8a8_packed_weight_bytes(12288, 1536, 6144) == 12288 * 1536
+    assert L.w8a8_packed_weight_bytes(12288, 1536, 6000) == -1   # I must be a multiple of 16
+    assert L.w8a8_packed_weight_bytes(12288, 1536, 4096) == -1   # N must be 2 I
+    assert L.w8a8_packed_weight_bytes(0, 64, 0) == -1
+
+
+def test_linear_workspace_bytes():
+    L = _lib.lib()
+    assert L.w8a8_linear_workspace_bytes(512, 1536) == 512 * 1536 + 512 * 4
+    assert L.w8a8_linear_workspace_bytes(3, 40) == 256 + 12
+
+
+def _status(name, *args):
+    L = _lib.lib()
+    rc = getattr(L, name)(*args)
+    return rc, L.w8a8_last_error().decode()
+
+
+def test_errors_are_reported_without_launching():
+    fake = ctypes.c_void_p(0x100000)  # never dereferenced: validation fails first
+    rc, msg = _status("w8a8_gemm_i32", None, 64, fake, 4, 8, 64, fake, 8, None)
+    assert rc == _lib.W8A8_EINVAL and "null" in msg
+    rc, msg = _status("w8a8_gemm_i32", fake, 64, fake, 4, 8, 60, fake, 8, None)
+    assert rc == _lib.W8A8_ENOTSUP and "multiple of 16" in msg
+    rc, msg = _status("w8a8_gemm_i32", fake, 32, fake, 4, 8, 64, fake, 8, None)
+    assert rc == _lib.W8A8_EINVAL and "lda" in msg
+    rc, msg = _status("w8a8_gemm_i32", ctypes.c_void_p(0x100001), 64, fake, 4, 8, 64, fake, 8, None)
+    assert rc == _lib.W8A8_EALIGN
+    rc, msg = _status("w8a8_gemm_i32", fake, 64, fake, 4, 8, 64, fake, 6, None)
+    assert rc == _lib.W8A8_EINVAL and "ldc" in msg
+    rc, msg = _status("w8a8_gemm_i32_cfg", fake, 64, fake, 4, 8, 64, fake, 8, 99, None)
+    assert rc == _lib.W8A8_EINVAL and "config" in msg
+    rc, msg = _status("w8a8_gemm_bf16", fake, 64, fake, fake, fake, 4, 16, 64, 1, 0, None, 0, fake, 16, None)
+    assert rc == _lib.W8A8_EINVAL and "interleave" in msg
+    rc, msg = _status("w8a8_gemm_bf16", fake, 64, fake, fake, fake, 4, 16, 64, 2, 0, None, 0, fake, 16, None)
+    assert rc == _lib.W8A8_EINVAL and "residual" in msg
+    rc, msg = _status("w8a8_gemv_bf16", fake, 64, 17, fake, 64, 8, 64, fake, 0, fake, 8, None)
+    assert rc == _lib.W8A8_EINVAL and "1..16" in msg
+    rc, msg = _status("w8a8_gemv_bf16", fake, 64, 1, fake, 64, 8, 40, fake, 0, fake, 8, None)
+    assert rc == _lib.W8A8_ENOTSUP
+    rc, msg = _status("w8a8_quant_rows_bf16", fake, 8, 4, 16, fake, 16, fake, None)
+    assert rc == _lib.W8A8_EINVAL
+    rc, msg = _status("w8a8_pack_weight_nk", fake, 64, 32, 64, 24, fake, None)
+    assert rc == _lib.W8A8_EINVAL and "interleave" in msg
+    rc, msg = _status("w8a8_rms_residual_bf16", fake, 8, fake, 8, None, 1e-6, 2, 8, fake, 8, fake, 8, None, None)
+    assert rc == _lib.W8A8_EINVAL
+
+
+def test_python_layer_raises():
+    import torch
+    from w8a8 import ops
+    with pytest.raises(ValueError, match="GPU tensor"):
+        ops.quant_rows(torch.zeros(2, 16, dtype=torch.bfloat16))
+    with pytest.raises(TypeError):
+        ops.gemm_i32(torch.zeros(2, 16, dtype=torch.int8), object())

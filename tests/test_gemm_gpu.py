@@ -1,0 +1,172 @@
+"""GPU parity of the int8 GEMM (npu_kernels.py:40-56) and its fused epilogues, through the
+C ABI.  int32 results must be bit-exact against the oracle / torch._int_mm; bf16 epilogues
+bit-exact where the arithmetic is exact (dequant, residual add) and within
+max(1e-2 |ref|, 2 ulp) where it involves tanh."""
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_bf16_close, f32, to_bits
+
+import oracle.oracle as orc
+from w8a8 import ops, workloads
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def rand_i8(shape, seed, lo=-128, hi=128):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(lo, hi, shape, generator=g, dtype=torch.int8)
+
+
+def packed_from_nk(w_nk, interleave=0):
+    return ops.pack_weight(w_nk.to(DEV), "nk", interleave)
+
+
+@pytest.mark.parametrize("cfg", [0, 1, 2])
+@pytest.mark.parametrize("M,N,K", [(1, 16, 64), (37, 72, 128), (130, 200, 192), (300, 520, 320),
+                                   (64, 48, 80), (257, 33, 1536)])
+def test_gemm_i32_vs_oracle(cfg, M, N, K):
+    a = rand_i8((M, K), seed=M * 7 + K)
+    w = rand_i8((N, K), seed=N * 13 + K)
+    ref = orc.int_mm_nk(a.numpy(), w.numpy())
+    c = ops.gemm_i32(a.to(DEV), packed_from_nk(w), tile_cfg=cfg)
+    got = c.cpu().numpy()
+    assert np.array_equal(got, ref), f"mismatches: {(got != ref).sum()}"
+
+
+def test_gemm_i32_from_kn_layout():
+    """The reference's B is [K, N] (npu_kernels.py:46); packing from it gives the same product."""
+    a = rand_i8((96, 256), 1)
+    b = rand_i8((256, 144), 2)
+    w = ops.pack_weight(b.to(DEV), "kn")
+    c = ops.gemm_i32(a.to(DEV), w)
+    assert torch.equal(c.cpu(), torch._int_mm(a, b))
+
+
+def test_gemm_i32_extremes():
+    K = 12288  # the largest K in the model's double-wide layers: |acc| = 128*128*K < 2^31
+    a = torch.full((40, K), -128, dtype=torch.int8)
+    w = torch.full((24, K), -128, dtype=torch.int8)
+    c = ops.gemm_i32(a.to(DEV), packed_from_nk(w))
+    assert (c == 128 * 128 * K).all()
+    w[3] = 127
+    c = ops.gemm_i32(a.to(DEV), packed_from_nk(w)).cpu()
+    assert (c[:, 3] == -128 * 127 * K).all() and (c[:, 0] == 128 * 128 * K).all()
+
+
+def test_gemm_i32_one_hot_rows_select_weights():
+    K, N = 128, 80
+    w = rand_i8((N, K), 5)
+    a = torch.zeros((K, K), dtype=torch.int8)
+    a[torch.arange(K), torch.arange(K)] = 1
+    c = ops.gemm_i32(a.to(DEV), packed_from_nk(w)).cpu()
+    assert torch.equal(c, w.t().int())
+
+
+def test_gemm_i32_empty_m():
+    w = packed_from_nk(rand_i8((32, 64), 1))
+    c = ops.gemm_i32(torch.empty((0, 64), dtype=torch.int8, device=DEV), w)
+    assert c.shape == (0, 32)
+
+
+def test_gemm_i32_strided_views():
+    """Row-strided A and C views, as the reference's slot buffers are (gemma_npu.py:104-115)."""
+    M, K, N = 50, 128, 96
+    a_big = rand_i8((M, K + 64), 3)
+    w = rand_i8((N, K), 4)
+    c_big = torch.full((M, N + 32), -7, dtype=torch.int32, device=DEV)
+    a_view = a_big.to(DEV)[:, :K]
+    c_view = c_big[:, :N]
+    ops.gemm_i32(a_view, packed_from_nk(w), c_view)
+    ref = torch._int_mm(a_big[:, :K].contiguous(), w.t().contiguous())
+    assert torch.equal(c_view.cpu(), ref)
+    assert (c_big[:, N:] == -7).all(), "wrote past N"
+
+
+def test_gemm_i32_single_prefill_microbatch():
+    """One prefill micro-batch GEMM, M=512 K=1536 N=6144, seed 0: bit-exact vs torch._int_mm."""
+    M, K, N = 512, 1536, 6144
+    x = workloads.activations(M, K, seed=0)
+    a, _ = ops.quant_rows(x.to(DEV))
+    w, _ = workloads.weights(N, K, seed=1)
+    c = ops.gemm_i32(a, packed_from_nk(w))
+    ref = torch._int_mm(a.cpu(), w.t().contiguous())
+    assert torch.equal(c.cpu(), ref)
+
+
+@pytest.mark.parametrize("M", [3658, 4096])
+def test_gemm_i32_prefill_m_unpadded_and_padded(M):
+    """M=3658 runs unpadded (no 512-row micro-batching); the rows of M=4096 agree."""
+    K, N = 2048, 1536
+    x = workloads.activations(M, K, seed=11)
+    a, _ = ops.quant_rows(x.to(DEV))
+    w, _ = workloads.weights(N, K, seed=12)
+    c = ops.gemm_i32(a, packed_from_nk(w))
+    ref = torch._int_mm(a.cpu(), w.t().contiguous())
+    assert torch.equal(c.cpu(), ref)
+
+
+# ---- bf16 epilogues -------------------------------------------------------------------------
+
+def _inputs(M, K, N, seed):
+    x = workloads.activations(M, K, seed)
+    w, sw = workloads.weights(N, K, seed + 1)
+    q, sx = orc.quant_rows(to_bits(x), "bf16")
+    return x, w, sw, q, sx
+
+
+@pytest.mark.parametrize("cfg", [0, 1, 2])
+def test_gemm_dequant_epilogue_exact(cfg):
+    M, K, N = 200, 256, 320
+    x, w, sw, q, sx = _inputs(M, K, N, 21)
+    ref = orc.dequant(orc.int_mm_nk(q, w.numpy()), sx, sw.numpy())
+    out = ops.gemm_bf16(torch.from_numpy(q).to(DEV), torch.from_numpy(sx).to(DEV), packed_from_nk(w),
+                        sw.to(DEV), tile_cfg=cfg)
+    assert np.array_equal(to_bits(out), ref)
+
+
+@pytest.mark.parametrize("cfg", [0, 1, 2])
+def test_gemm_residual_epilogue_exact(cfg):
+    M, K, N = 130, 192, 256
+    x, w, sw, q, sx = _inputs(M, K, N, 31)
+    res = workloads.activations(M, N, 32, outliers=False)
+    y = orc.dequant(orc.int_mm_nk(q, w.numpy()), sx, sw.numpy())
+    ref = orc.add_residual(y, to_bits(res))
+    out = ops.gemm_bf16(torch.from_numpy(q).to(DEV), torch.from_numpy(sx).to(DEV), packed_from_nk(w),
+                        sw.to(DEV), epilogue="residual", residual=res.to(DEV), tile_cfg=cfg)
+    assert np.array_equal(to_bits(out), ref)
+
+
+@pytest.mark.parametrize("cfg", [0, 1, 2])
+def test_gemm_gelu_epilogue(cfg):
+    M, K, I = 150, 256, 192
+    x, w, sw, q, sx = _inputs(M, K, 2 * I, 41)
+    y = orc.dequant(orc.int_mm_nk(q, w.numpy()), sx, sw.numpy())
+    ref = orc.gelu_mul(y)
+    out = ops.gemm_bf16(torch.from_numpy(q).to(DEV), torch.from_numpy(sx).to(DEV),
+                        packed_from_nk(w, interleave=I), sw.to(DEV), epilogue="gelu", tile_cfg=cfg)
+    got = to_bits(out)
+    assert_bf16_close(f32(got), f32(ref), what="gelu epilogue")
+    assert (got == ref).mean() > 0.99
+
+
+def test_gemm_gelu_ragged_tiles():
+    """I not a multiple of the 128/256-column block: gate/up tiles straddle the block edge."""
+    M, K, I = 70, 128, 80
+    x, w, sw, q, sx = _inputs(M, K, 2 * I, 43)
+    ref = orc.gelu_mul(orc.dequant(orc.int_mm_nk(q, w.numpy()), sx, sw.numpy()))
+    out = ops.gemm_bf16(torch.from_numpy(q).to(DEV), torch.from_numpy(sx).to(DEV),
+                        packed_from_nk(w, interleave=I), sw.to(DEV), epilogue="gelu")
+    assert_bf16_close(f32(to_bits(out)), f32(ref), what="gelu ragged")
+
+
+def test_standalone_dequant_exact():
+    M, N = 77, 300
+    g = torch.Generator().manual_seed(3)
+    acc = torch.randint(-(2 ** 30), 2 ** 30, (M, N), generator=g, dtype=torch.int32)
+    sx = torch.rand(M, generator=g) * 1e-3
+    sw = torch.rand(N, generator=g) * 0.02
+    out = ops.dequant_bf16(acc.to(DEV), sx.to(DEV), sw.to(DEV))
+    assert np.array_equal(to_bits(out), orc.dequant(acc.numpy(), sx.numpy(), sw.numpy()))

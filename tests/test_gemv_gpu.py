@@ -1,0 +1,73 @@
+"""GPU parity of the decode GEMV (torch._weight_int8pack_mm semantics, gemma_npu.py:155-172).
+
+bf16 results agree with the oracle and with torch's CPU op within max(1e-2 |ref|, 2 ulp);
+with integer-valued activations every partial sum is exact, so the result must be
+bf16(int32 product * s) bit for bit."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_bf16_close, f32, from_bits, to_bits
+
+import oracle.oracle as orc
+from w8a8 import ops, workloads
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "w8a8_golden.npz")
+
+
+@pytest.mark.parametrize("name", ["gemv_a", "gemv_b", "gemv_c"])
+def test_gemv_golden(name):
+    d = np.load(GOLDEN)
+    x = from_bits(d[f"{name}_x"]).to(DEV)
+    w = torch.from_numpy(d[f"{name}_w"]).to(DEV)
+    yb = ops.gemv_bf16(x, w, from_bits(d[f"{name}_sb"]).to(DEV))
+    assert_bf16_close(f32(to_bits(yb)), f32(d[f"{name}_yb"]), what=f"{name} bf16 scales vs torch")
+    yf = ops.gemv_bf16(x, w, torch.from_numpy(d[f"{name}_sf"]).to(DEV))
+    assert_bf16_close(f32(to_bits(yf)), f32(d[f"{name}_yf"]), what=f"{name} fp32 scales vs torch")
+
+
+@pytest.mark.parametrize("M", [1, 4, 16])
+@pytest.mark.parametrize("K,N", [(1536, 2560), (2048, 1536), (1536, 12288), (6144, 1536), (80, 40)])
+def test_gemv_layer_shapes(M, K, N):
+    x = workloads.activations(M, K, seed=M * 31 + K, outliers=False)
+    w, sw = workloads.weights(N, K, seed=N + 1)
+    s = sw.to(torch.bfloat16)
+    y = ops.gemv_bf16(x.to(DEV), w.to(DEV), s.to(DEV))
+    ref = orc.gemv(to_bits(x), w.numpy(), to_bits(s), "bf16")
+    assert_bf16_close(f32(to_bits(y)), f32(ref), what=f"gemv M{M} K{K} N{N} vs oracle")
+    ref_t = torch._weight_int8pack_mm(x, w, s)
+    assert_bf16_close(f32(to_bits(y)), f32(to_bits(ref_t)), what=f"gemv M{M} K{K} N{N} vs torch")
+
+
+def test_gemv_exact_on_integer_activations():
+    g = torch.Generator().manual_seed(3)
+    xi = torch.randint(-8, 9, (5, 1536), generator=g)
+    w = torch.randint(-128, 128, (1000, 1536), generator=g, dtype=torch.int8)
+    s = torch.rand(1000, generator=g) * 0.01 + 0.005
+    y = ops.gemv_bf16(xi.to(torch.bfloat16).to(DEV), w.to(DEV), s.to(DEV))
+    acc = (xi.long() @ w.t().long()).float()  # |acc| < 2^24: exact in fp32
+    assert torch.equal(y.cpu(), (acc * s[None, :]).to(torch.bfloat16))
+
+
+def test_gemv_lm_head_m1():
+    """The LM head at decode (K=1536, N=262144, M=1) against torch's CPU op."""
+    K, N = workloads.LM_HEAD
+    x = workloads.activations(1, K, seed=77, outliers=False)
+    w, sw = workloads.weights(N, K, seed=78)
+    s = sw.to(torch.bfloat16)
+    y = ops.gemv_bf16(x.to(DEV), w.to(DEV), s.to(DEV))
+    ref = torch._weight_int8pack_mm(x, w, s)
+    assert_bf16_close(f32(to_bits(y)), f32(to_bits(ref)), what="lm head")
+
+
+def test_gemv_deterministic():
+    x = workloads.activations(4, 6144, seed=1, outliers=False).to(DEV)
+    w, sw = workloads.weights(1536, 6144, seed=2)
+    w, s = w.to(DEV), sw.to(DEV)
+    y0 = ops.gemv_bf16(x, w, s)
+    for _ in range(3):
+        assert torch.equal(ops.gemv_bf16(x, w, s), y0)
