@@ -30,7 +30,7 @@ int check_launch(const char* what) {
 // Shared validation of the int8 A operand and packed weight for every GEMM entry point.
 static int check_gemm_operands(const char* fn, const int8_t* a, int64_t lda, const int8_t* wp, int64_t M, int64_t N,
                                int64_t K, int64_t interleave, GemmParams& p) {
-  if (!a || !wp) return fail(W8A8_EINVAL, "%s: null pointer", fn);
+  if ((M > 0 && !a) || !wp) return fail(W8A8_EINVAL, "%s: null pointer", fn);
   if (M < 0 || N <= 0 || K <= 0) return fail(W8A8_EINVAL, "%s: bad shape M=%lld N=%lld K=%lld", fn, (long long)M,
                                            (long long)N, (long long)K);
   if (K % 16 != 0) return fail(W8A8_ENOTSUP, "%s: K=%lld must be a multiple of 16", fn, (long long)K);
@@ -88,13 +88,14 @@ int w8a8_gemm_i32_cfg(const int8_t* a, int64_t lda, const int8_t* w_packed, int6
   GemmParams p;
   int rc = check_gemm_operands("gemm_i32", a, lda, w_packed, M, N, K, 0, p);
   if (rc) return rc;
-  if (!c) return fail(W8A8_EINVAL, "gemm_i32: null C");
+  if (!c && M > 0) return fail(W8A8_EINVAL, "gemm_i32: null C");
   if (ldc < N) return fail(W8A8_EINVAL, "gemm_i32: ldc=%lld < N=%lld", (long long)ldc, (long long)N);
-  if (ldc % 4 != 0 || (uintptr_t)c % 16 != 0) return fail(W8A8_EALIGN, "gemm_i32: C rows must be 16-byte aligned");
+  if ((uintptr_t)c % 4 != 0) return fail(W8A8_EALIGN, "gemm_i32: C must be 4-byte aligned");
   if (tile_cfg >= gemm_config_count()) return fail(W8A8_EINVAL, "gemm_i32: tile config %d out of range", tile_cfg);
   if (M == 0) return W8A8_OK;
   p.c = c;
   p.ldc = ldc;
+  p.vec_store = (ldc % 4 == 0) && ((uintptr_t)c % 16 == 0);
   return gemm_launch(p, EPI_I32, tile_cfg, stream);
 }
 
@@ -109,7 +110,8 @@ int w8a8_gemm_bf16_cfg(const int8_t* a, int64_t lda, const float* sx, const int8
   GemmParams p;
   int rc = check_gemm_operands("gemm_bf16", a, lda, w_packed, M, N, K, interleave, p);
   if (rc) return rc;
-  if (!sx || !sw || !out) return fail(W8A8_EINVAL, "gemm_bf16: null scale or output pointer");
+  if (M > 0 && (!sx || !out)) return fail(W8A8_EINVAL, "gemm_bf16: null scale or output pointer");
+  if (!sw) return fail(W8A8_EINVAL, "gemm_bf16: null per-channel scales");
   int epi;
   int64_t out_cols = N;
   switch (epilogue) {
@@ -130,13 +132,14 @@ int w8a8_gemm_bf16_cfg(const int8_t* a, int64_t lda, const float* sx, const int8
   if (epi != EPI_GELU && interleave > 0)
     return fail(W8A8_EINVAL, "gemm_bf16: a gate/up-interleaved weight only goes with the GELU epilogue");
   if (ldo < out_cols) return fail(W8A8_EINVAL, "gemm_bf16: ldo=%lld too small", (long long)ldo);
-  if (ldo % 4 != 0 || (uintptr_t)out % 8 != 0) return fail(W8A8_EALIGN, "gemm_bf16: output rows must be 8-byte aligned");
+  if ((uintptr_t)out % 2 != 0) return fail(W8A8_EALIGN, "gemm_bf16: output must be 2-byte aligned");
   if (tile_cfg >= gemm_config_count()) return fail(W8A8_EINVAL, "gemm_bf16: tile config %d out of range", tile_cfg);
   if (M == 0) return W8A8_OK;
   p.sx = sx;
   p.sw = sw;
   p.out = out;
   p.ldo = ldo;
+  p.vec_store = (ldo % 4 == 0) && ((uintptr_t)out % 8 == 0);
   p.res = res;
   p.ldr = ldr;
   return gemm_launch(p, epi, tile_cfg, stream);

@@ -15,6 +15,7 @@ struct GemmParams {
   int64_t lda;
   int M, N, KT, NT;     // N: logical output columns (EPI_GELU: 2*I); KT = ceil(K/64); NT packed n-tiles
   int I;                // EPI_GELU: width of the gate (and up) half
+  int vec_store;        // output rows allow 4-wide vector stores (alignment checked on the host)
   int32_t* c; int64_t ldc;          // EPI_I32
   const float* sx; const float* sw; // per-row / per-channel scales
   uint16_t* out; int64_t ldo;       // bf16 epilogues

@@ -151,7 +151,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmParams p) {
       for (int j = 0; j < WTN; ++j) {
         const int n = (t0 + wn * WTN + j) * 16 + lcol;
         int32_t* dst = p.c + int64_t(m) * p.ldc + n;
-        if (n + 3 < p.N) {
+        if (p.vec_store && n + 3 < p.N) {
           *reinterpret_cast<v4i*>(dst) = acc[i][j];
         } else {
 #pragma unroll
@@ -177,7 +177,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmParams p) {
             if (n + r < p.N) y[r] = y[r] + bf16_to_f32(rs[r]);
         }
         uint16_t* dst = p.out + int64_t(m) * p.ldo + n;
-        if (n + 3 < p.N) {
+        if (p.vec_store && n + 3 < p.N) {
           *reinterpret_cast<v2u*>(dst) = v2u{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
         } else {
 #pragma unroll
@@ -203,7 +203,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmParams p) {
           o[r] = ge * up;
         }
         uint16_t* dst = p.out + int64_t(m) * p.ldo + g;
-        if (g + 3 < p.I) {
+        if (p.vec_store && g + 3 < p.I) {
           *reinterpret_cast<v2u*>(dst) = v2u{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
         } else {
 #pragma unroll

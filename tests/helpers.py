@@ -14,16 +14,35 @@ def ulp_bf16(v):
     return (2.0 ** (e - 7)).astype(np.float32)
 
 
-def bf16_close(y, ref, rel=REL, ulps=ULPS):
-    """Boolean mask of elements within tolerance; y, ref as fp32 arrays."""
+def bf16_close(y, ref, rel=REL, ulps=ULPS, ulp_at=None, extra=None):
+    """Boolean mask of elements within tolerance; y, ref as fp32 arrays.
+
+    ulp_at: magnitudes at which to take the ulp instead of |ref| (for a sum a + b the rounding
+            error of each addend is an ulp of that addend, not of the sum: pass max(|a|, |b|)).
+    extra:  an additional absolute allowance per element (e.g. the fp32 dot-product error
+            bound of a long accumulation, see dot_error_bound).
+    """
     y = np.asarray(y, dtype=np.float32)
     ref = np.asarray(ref, dtype=np.float32)
-    tol = np.maximum(rel * np.abs(ref), ulps * ulp_bf16(ref))
+    mag = np.abs(ref) if ulp_at is None else np.maximum(np.abs(ref), np.abs(np.asarray(ulp_at, np.float32)))
+    tol = np.maximum(rel * np.abs(ref), ulps * ulp_bf16(mag))
+    if extra is not None:
+        tol = np.maximum(tol, np.asarray(extra, dtype=np.float32))
     return np.abs(y - ref) <= tol
 
 
-def assert_bf16_close(y, ref, rel=REL, ulps=ULPS, what=""):
-    ok = bf16_close(y, ref, rel, ulps)
+def dot_error_bound(x, w, s):
+    """Absolute error allowance of y = (sum_k x[m,k] w[n,k]) * s[n] accumulated in fp32 in any
+    order: 4 * 2^-24 * sum_k |x w| * |s|.  Two fp32 accumulations of the same products (the
+    oracle's sequential sum, torch's vectorised one, the MFMA's) may each be off by rounding
+    of the running sum, which matters only where the sum cancels to near zero."""
+    xa = torch.as_tensor(np.abs(np.asarray(x, np.float32)))
+    wa = torch.as_tensor(np.abs(np.asarray(w, np.float32)))
+    return (4.0 * 2.0 ** -24) * (xa @ wa.T).numpy() * np.abs(np.asarray(s, np.float32))[None, :]
+
+
+def assert_bf16_close(y, ref, rel=REL, ulps=ULPS, what="", ulp_at=None, extra=None):
+    ok = bf16_close(y, ref, rel, ulps, ulp_at, extra)
     if not ok.all():
         bad = np.argwhere(~ok)
         i = tuple(bad[0])

@@ -1,7 +1,10 @@
 """GPU parity of the decode GEMV (torch._weight_int8pack_mm semantics, gemma_npu.py:155-172).
 
-bf16 results agree with the oracle and with torch's CPU op within max(1e-2 |ref|, 2 ulp);
-with integer-valued activations every partial sum is exact, so the result must be
+bf16 results agree with the oracle and with torch's CPU op within
+max(1e-2 |ref|, 2 ulp, 4 * 2^-24 * sum_k |x w| * |s|): the last term is the fp32 accumulation
+error bound, which only matters where the K-long sum cancels to near zero (there the oracle's
+sequential sum and torch's own vectorised sum disagree with each other by the same amount).
+With integer-valued activations every partial sum is exact, so the result must be
 bf16(int32 product * s) bit for bit."""
 import os
 
@@ -9,7 +12,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import assert_bf16_close, f32, from_bits, to_bits
+from helpers import assert_bf16_close, dot_error_bound, f32, from_bits, to_bits
 
 import oracle.oracle as orc
 from w8a8 import ops, workloads
@@ -24,10 +27,11 @@ def test_gemv_golden(name):
     d = np.load(GOLDEN)
     x = from_bits(d[f"{name}_x"]).to(DEV)
     w = torch.from_numpy(d[f"{name}_w"]).to(DEV)
+    extra = dot_error_bound(f32(d[f"{name}_x"]), d[f"{name}_w"], d[f"{name}_sf"])
     yb = ops.gemv_bf16(x, w, from_bits(d[f"{name}_sb"]).to(DEV))
-    assert_bf16_close(f32(to_bits(yb)), f32(d[f"{name}_yb"]), what=f"{name} bf16 scales vs torch")
+    assert_bf16_close(f32(to_bits(yb)), f32(d[f"{name}_yb"]), what=f"{name} bf16 scales vs torch", extra=extra)
     yf = ops.gemv_bf16(x, w, torch.from_numpy(d[f"{name}_sf"]).to(DEV))
-    assert_bf16_close(f32(to_bits(yf)), f32(d[f"{name}_yf"]), what=f"{name} fp32 scales vs torch")
+    assert_bf16_close(f32(to_bits(yf)), f32(d[f"{name}_yf"]), what=f"{name} fp32 scales vs torch", extra=extra)
 
 
 @pytest.mark.parametrize("M", [1, 4, 16])
@@ -37,10 +41,14 @@ def test_gemv_layer_shapes(M, K, N):
     w, sw = workloads.weights(N, K, seed=N + 1)
     s = sw.to(torch.bfloat16)
     y = ops.gemv_bf16(x.to(DEV), w.to(DEV), s.to(DEV))
+    extra = dot_error_bound(x.float().numpy(), w.numpy(), s.float().numpy())
     ref = orc.gemv(to_bits(x), w.numpy(), to_bits(s), "bf16")
-    assert_bf16_close(f32(to_bits(y)), f32(ref), what=f"gemv M{M} K{K} N{N} vs oracle")
+    got = f32(to_bits(y))
+    assert_bf16_close(got, f32(ref), what=f"gemv M{M} K{K} N{N} vs oracle", extra=extra)
     ref_t = torch._weight_int8pack_mm(x, w, s)
-    assert_bf16_close(f32(to_bits(y)), f32(to_bits(ref_t)), what=f"gemv M{M} K{K} N{N} vs torch")
+    assert_bf16_close(got, f32(to_bits(ref_t)), what=f"gemv M{M} K{K} N{N} vs torch", extra=extra)
+    # outside the cancellation zone the plain bf16 bar holds for almost every element
+    assert (got == f32(ref)).mean() > 0.97
 
 
 def test_gemv_exact_on_integer_activations():
@@ -61,7 +69,8 @@ def test_gemv_lm_head_m1():
     s = sw.to(torch.bfloat16)
     y = ops.gemv_bf16(x.to(DEV), w.to(DEV), s.to(DEV))
     ref = torch._weight_int8pack_mm(x, w, s)
-    assert_bf16_close(f32(to_bits(y)), f32(to_bits(ref)), what="lm head")
+    extra = dot_error_bound(x.float().numpy(), w.numpy(), s.float().numpy())
+    assert_bf16_close(f32(to_bits(y)), f32(to_bits(ref)), what="lm head", extra=extra)
 
 
 def test_gemv_deterministic():

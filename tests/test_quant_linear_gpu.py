@@ -76,7 +76,11 @@ def test_rms_residual(with_w):
     ref = orc.rms_residual(to_bits(y), to_bits(res), to_bits(w) if with_w else None, 1e-6)
     h, q, sq = ops.rms_residual(y.to(DEV), res.to(DEV), w.to(DEV) if with_w else None, 1e-6, quant=True)
     got = to_bits(h)
-    assert_bf16_close(f32(got), f32(ref), what="rms_residual")
+    # h = res + n: the rounding of n (one bf16 ulp of |n|, from fp32 reduction-order
+    # differences in mean(y^2)) carries into h even where res cancels n, so the ulp is taken
+    # at max(|h|, |res|, |n|)
+    addends = np.maximum(np.abs(f32(to_bits(res))), np.abs(f32(ref) - f32(to_bits(res))))
+    assert_bf16_close(f32(got), f32(ref), what="rms_residual", ulp_at=addends)
     assert (got == ref).mean() > 0.99
     # the fused quant of h is the prologue's quant of the h it wrote
     q_ref, s_ref = orc.quant_rows(got, "bf16")
@@ -117,7 +121,9 @@ def test_linear_bf16_residual_rms():
     out = ops.linear_bf16(x.to(DEV), pw, epilogue="residual_rms", residual=res.to(DEV), rms_w=rw.to(DEV), eps=1e-6)
     ref, _, _ = orc.linear_bf16(to_bits(x), w.numpy(), sw.numpy(), "residual_rms", to_bits(res), to_bits(rw), 1e-6)
     got = to_bits(out)
-    assert_bf16_close(f32(got), f32(ref), what="residual_rms")
+    addends = np.maximum(np.abs(f32(to_bits(res))), np.abs(f32(ref) - f32(to_bits(res))))
+    assert_bf16_close(f32(got), f32(ref), what="residual_rms", ulp_at=addends)
+    assert (got == ref).mean() > 0.99
 
 
 def test_quant_weight_roundtrip():
