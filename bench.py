@@ -8,11 +8,14 @@ A step is one E2B-class decoder layer's prefill linears on one 512-row micro-bat
   o       K=2048 N=1536            (dequant)
   gate_up K=1536 N=2x6144          (dequant + gelu_tanh(gate) * up)
   down    K=6144 N=1536            (dequant + residual add)
-`value` is int8 TOP/s over the step's 2*M*N*K ops with inputs resident in HBM.  The JSON line
-also carries the roofline of the dominant kernel (the gate_up GEMM, timed live with HIP
-events on the launch stream), the host CPU's torch._int_mm on the same GEMMs (the
-reference's --backend cpu-int8 path, pipeline.py:237), and `extra`: the full-prefill GEMM
-sweep at M=3658 / 4096, the M=16384 stress GEMMs, and the decode GEMV bandwidth.
+The step's 8 launches (quant-to-packed + GEMM per linear) are captured once in a HIP graph
+and replayed, the way a serving loop runs them; the replayed outputs are checked bit for bit
+against an eager run before timing.  `value` is int8 TOP/s over the step's 2*M*N*K ops with
+inputs resident in HBM.  The JSON line also carries the roofline of the dominant kernel (the
+gate_up GEMM, timed live with HIP events on the launch stream), the host CPU's torch._int_mm
+on the same GEMMs (the reference's --backend cpu-int8 path, pipeline.py:237), and `extra`:
+the eager (uncaptured) step, the full-prefill GEMM sweep at M=3658 / 4096, the M=16384
+stress GEMMs, and the decode GEMV bandwidth.
 """
 import argparse
 import json
@@ -59,16 +62,51 @@ def build_layer(M, dev, seed0=0):
         ncols = N // 2 if epi == "gelu" else N
         out = torch.empty((M, ncols), dtype=torch.bfloat16, device=dev)
         res = workloads.activations(M, N, seed=seed0 + 10 * gi + 2, outliers=False).to(dev) if epi == "residual" else None
-        ws = torch.empty(ops.linear_workspace_bytes(M, K), dtype=torch.uint8, device=dev)
-        q, sx = ops.quant_rows(x)
-        groups.append(dict(name=name, K=K, N=N, epi=epi, x=x, w=w, pw=pw, out=out, res=res, ws=ws, q=q, sx=sx))
+        q, sx = ops.quant_rows_packed(x)
+        groups.append(dict(name=name, K=K, N=N, epi=epi, x=x, w=w, pw=pw, out=out, res=res, q=q, sx=sx))
     return groups
 
 
-def layer_step(groups):
+def layer_step(groups, ws=None):
     from w8a8 import ops
     for g in groups:
-        ops.linear_bf16(g["x"], g["pw"], epilogue=g["epi"], residual=g["res"], out=g["out"], workspace=g["ws"])
+        ops.linear_bf16(g["x"], g["pw"], epilogue=g["epi"], residual=g["res"], out=g["out"], ws_arg=ws)
+
+
+def capture(fn, dev):
+    """fn's launches captured in one HIP graph (after one warm run on the capture stream)."""
+    import torch
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn()
+    torch.cuda.synchronize(dev)
+    return graph
+
+
+def graph_time_ms(fn, dev, launches=50, reps=10):
+    """Average duration of fn's launch sequence: `launches` copies captured in one graph,
+    replayed `reps` times between HIP events on the current stream."""
+    import torch
+
+    def many():
+        for _ in range(launches):
+            fn()
+    graph = capture(many, dev)
+    graph.replay()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize(dev)
+    s.record()
+    for _ in range(reps):
+        graph.replay()
+    e.record()
+    e.synchronize()
+    return s.elapsed_time(e) / (reps * launches)
 
 
 def cpu_int_mm_ms(shapes, M, warm=3, reps=5):
@@ -100,7 +138,7 @@ def sweep(M, dev, reps):
     packed = []
     for name, layer, gi, K, N in shapes:
         if K not in A:
-            A[K] = ops.quant_rows(workloads.activations(M, K, seed=K).to(dev))[0]
+            A[K] = ops.quant_rows_packed(workloads.activations(M, K, seed=K).to(dev))[0]
         g = torch.Generator(device=dev).manual_seed(workloads.layer_seed(layer, gi))
         w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8, device=dev)
         packed.append((K, N, ops.pack_weight(w, "nk")))
@@ -130,6 +168,26 @@ def gemv_bench(M, K, N, dev, reps, seed=5):
     return ms, nbytes
 
 
+COPY_BYTES = 64 << 20
+
+
+def profile_kernel(groups, dev, launches):
+    """The dominant kernel alone, plus one plain copy of COPY_BYTES (read COPY_BYTES, write
+    COPY_BYTES) whose FETCH_SIZE / WRITE_SIZE readings give the counters' byte scale."""
+    import torch
+    from w8a8 import ops
+    gu = next(g for g in groups if g["name"] == "gate_up")
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    for _ in range(launches):
+        ops.gemm_bf16(gu["q"], gu["sx"], gu["pw"], epilogue="gelu", out=gu["out"])
+    torch.cuda.synchronize()
+    log(f"bench: profiled {launches} gate_up launches and one {COPY_BYTES >> 20} MiB copy")
+    return 0
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -137,6 +195,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the host CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip the sweep / stress / GEMV sub-results")
+    ap.add_argument("--profile-kernel", action="store_true",
+                    help="for counter collection: launch only the dominant GEMM (eager, --steps times) and a "
+                         "64 MiB device copy that calibrates the byte counters, then exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the W8A8 path runs "
@@ -151,31 +212,49 @@ def main():
     M = 512
     log(f"bench: building one E2B layer at M={M}")
     groups = build_layer(M, dev)
+    if args.profile_kernel:
+        return profile_kernel(groups, dev, args.steps)
     step_ops = sum(workloads.gemm_ops(M, g["N"], g["K"]) for g in groups)
+    ws = torch.zeros(max(ops.linear_workspace_bytes(M, g["N"], g["K"]) for g in groups), dtype=torch.uint8,
+                     device=dev)
+
+    # eager reference outputs, then the captured step must reproduce them bit for bit
+    layer_step(groups, ws)
+    eager_out = [g["out"].clone() for g in groups]
+    graph = capture(lambda: layer_step(groups, ws), dev)
+    for g in groups:
+        g["out"].zero_()
+    graph.replay()
+    torch.cuda.synchronize()
+    for g, ref in zip(groups, eager_out):
+        if not torch.equal(g["out"], ref):
+            raise RuntimeError(f"captured layer step differs from eager for {g['name']}")
 
     # ---- timed region: K steps bracketed by synchronisation ------------------------------
     for _ in range(args.warmup):
-        layer_step(groups)
+        graph.replay()
     torch.cuda.synchronize()
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     s.record()
     for _ in range(args.steps):
-        layer_step(groups)
+        graph.replay()
     e.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_step = s.elapsed_time(e) / args.steps
     value = step_ops / (ms_step * 1e-3) / 1e12
     log(f"bench: layer step {ms_step * 1e3:.1f} us = {value:.1f} TOP/s (wall {wall:.3f} s)")
+    eager_ms = event_time_ms(lambda: layer_step(groups, ws), args.steps, args.warmup)
+    log(f"bench: eager layer step {eager_ms * 1e3:.1f} us")
 
     # ---- dominant kernel: the gate_up GEMM with fused GELU epilogue ----------------------
     gu = next(g for g in groups if g["name"] == "gate_up")
     per_ms = {}
     for g in groups:
-        per_ms[g["name"]] = event_time_ms(
+        per_ms[g["name"]] = graph_time_ms(
             lambda g=g: ops.gemm_bf16(g["q"], g["sx"], g["pw"], epilogue=g["epi"], residual=g["res"],
-                                      out=g["out"]), 200, 20)
+                                      out=g["out"]), dev)
     gu_ops = workloads.gemm_ops(M, gu["N"], gu["K"])
     gu_ms = per_ms["gate_up"]
     achieved = gu_ops / (gu_ms * 1e-3) / 1e12
@@ -185,7 +264,7 @@ def main():
             traffic = json.load(f).get("hbm_bytes_per_launch")
     roofline = {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": traffic,
-                "kernel": "gemm_kernel<EPI_GELU> gate_up M=512 K=1536 N=12288",
+                "kernel": "gemm_kernel<EPI_GELU> gate_up M=512 K=1536 N=12288, packed A",
                 "avg_launch_us": round(gu_ms * 1e3, 2)}
     log(f"bench: per-GEMM us: " + ", ".join(f"{k} {v * 1e3:.1f}" for k, v in per_ms.items()))
 
@@ -201,7 +280,8 @@ def main():
                          f"3 warm-up + median of 5 per GEMM, {cpu_ms:.1f} ms per layer"}
         log(f"bench: cpu _int_mm layer {cpu_ms:.1f} ms")
 
-    extra = {}
+    extra = {"eager_layer_step_us": round(eager_ms * 1e3, 1),
+             "gemm_us_m512": {k: round(v * 1e3, 2) for k, v in per_ms.items()}}
     if not args.no_extra:
         for Ms in (3658, 4096):
             ms, tops_ops, wbytes, shp = sweep(Ms, dev, reps=5)

@@ -8,14 +8,22 @@ namespace w8a8 {
 enum { EPI_I32 = 0, EPI_BF16 = 1, EPI_GELU = 2, EPI_RESID = 3 };
 
 struct GemmParams {
-  const int8_t* a;      // activations [M, K] row-major, leading dimension lda (bytes)
+  const int8_t* a;      // activations: [M, K] row-major (leading dimension lda) or packed
+                        // 32-row MFMA fragments (pack_act / quant_rows_packed)
   const int8_t* wp;     // packed weight fragments (pack_weight)
   uint32_t a_bytes;     // (M-1)*lda + K: loads at or past this offset read zero
-  uint32_t w_bytes;     // NT * KT * 1024
+  uint32_t w_bytes;     // NT * KF * 1024
   int64_t lda;
-  int M, N, KT, NT;     // N: logical output columns (EPI_GELU: 2*I); KT = ceil(K/64); NT packed n-tiles
+  int M, N, KF, NT;     // N: logical output columns (EPI_GELU: 2*I); KF = 32-wide k fragments per
+                        // 32-channel tile (K padded to 64); NT = packed 32-channel tiles
   int I;                // EPI_GELU: width of the gate (and up) half
   int vec_store;        // output rows allow 4-wide vector stores (alignment checked on the host)
+  int gm;               // row tiles per group in the block -> tile order (set by the launcher)
+  int split_req;        // requested split-K: 0 = automatic, n = at most n splits
+  int splits;           // blocks per output tile along K (1 = no split)
+  int kt_per_split;     // k-tiles of 64 per split
+  int32_t* ws;          // split-K partial sums (splits > 1)
+  int* counters;        // split-K arrival counters, one per output tile, zero between calls
   int32_t* c; int64_t ldc;          // EPI_I32
   const float* sx; const float* sw; // per-row / per-channel scales
   uint16_t* out; int64_t ldo;       // bf16 epilogues
@@ -24,6 +32,9 @@ struct GemmParams {
 
 int gemm_config_count();
 int gemm_pick_config(int M, int NP, int K);
-int gemm_launch(const GemmParams& p, int epi, int cfg, hipStream_t stream);
+// ws: split-K workspace (zero-filled before first use; the kernels leave it zeroed), may be null.
+int gemm_launch(const GemmParams& p, int epi, int cfg, bool a_packed, void* ws, int64_t ws_bytes,
+                hipStream_t stream);
+int64_t gemm_workspace_bytes(int M, int NP, int KF, int cfg, int split_k);
 
 }  // namespace w8a8

@@ -6,12 +6,13 @@
 // weight rows, of the per-output-channel weight quant at gemma_npu.py:68-69.
 //
 // pack_weight: rewrites an int8 weight into the GEMM's resident layout of 1 KiB MFMA
-// fragments.  Fragment (t, j) holds output channels [16t, 16t+16) x inputs [64j, 64j+64);
-// byte 16*l + b of it is channel 16t + l%16, input 64j + 16*(l/16) + b, i.e. exactly the
-// 16 bytes lane l feeds to v_mfma_i32_16x16x64_i8.  Fragments are stored n-tile major
-// ((t * KT + j) * 1024).  With `interleave` = I > 0 the n-tiles alternate gate / up:
-// tile 2u is channels [16u, 16u+16) and tile 2u+1 is channels [I+16u, I+16u+16), so a
-// lane holds matching gate and up accumulators for the fused GELU epilogue.
+// fragments.  Fragment (t, j) holds output channels [32t, 32t+32) x inputs [32j, 32j+32);
+// byte 16*l + b of it is channel 32t + l%32, input 32j + 16*(l/32) + b, i.e. exactly the
+// 16 bytes lane l feeds to v_mfma_i32_32x32x32_i8.  Fragments are stored tile-major
+// ((t * KF + j) * 1024) with K zero-padded to a multiple of 64 (KF = 2 * ceil(K/64)) and N to
+// a multiple of 32.  With `interleave` = I > 0 the tiles alternate gate / up: tile 2u is
+// channels [32u, 32u+32) and tile 2u+1 is channels [I+32u, I+32u+32), so a lane holds
+// matching gate and up accumulators for the fused GELU epilogue.
 #include "w8a8_common.h"
 
 namespace w8a8 {
@@ -97,28 +98,27 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const T* __restrict__ x
 // One thread per 16-byte chunk of the packed output.  src_kn: the source is [K, N] (ld = ldw,
 // the reference's B layout, npu_kernels.py:46); otherwise it is [N, K] (gemma_npu.py:69).
 __global__ __launch_bounds__(256) void pack_weight_kernel(const int8_t* __restrict__ w, int64_t ldw, int N, int K,
-                                                          int src_kn, int interleave, int KT, int64_t nchunks,
+                                                          int src_kn, int interleave, int KF, int64_t nchunks,
                                                           int8_t* __restrict__ out) {
   const int64_t c = int64_t(blockIdx.x) * 256 + threadIdx.x;
   if (c >= nchunks) return;
   const int lane = int(c & 63);
   const int64_t f = c >> 6;
-  const int t = int(f / KT);
-  const int j = int(f % KT);
+  const int t = int(f / KF);
+  const int j = int(f % KF);
   int n;
   int limit;
   if (interleave > 0) {
     const int u = t >> 1;
-    n = (t & 1 ? interleave : 0) + 16 * u + (lane & 15);
+    n = (t & 1 ? interleave : 0) + 32 * u + (lane & 31);
     limit = (t & 1 ? N : interleave);
-    if (16 * u + (lane & 15) >= interleave) n = -1;
   } else {
-    n = 16 * t + (lane & 15);
+    n = 32 * t + (lane & 31);
     limit = N;
   }
-  const int k0 = 64 * j + 16 * (lane >> 4);
+  const int k0 = 32 * j + 16 * (lane >> 5);
   uint32_t word[4] = {0, 0, 0, 0};
-  if (n >= 0 && n < limit) {
+  if (n < limit) {
 #pragma unroll
     for (int b = 0; b < 16; ++b) {
       const int k = k0 + b;
@@ -129,6 +129,82 @@ __global__ __launch_bounds__(256) void pack_weight_kernel(const int8_t* __restri
     }
   }
   *reinterpret_cast<v4u*>(out + c * 16) = v4u{word[0], word[1], word[2], word[3]};
+}
+
+// ---- packed activations ----------------------------------------------------------------------
+// The GEMM reads A fastest when it is laid out like the packed weight: 1 KiB fragments of 32
+// rows x 32 k, fragment (mt, j) at (mt * KF + j) * 1024 with KF = 2 * ceil(K/64), byte 16*l + b
+// of it = row 32*mt + l%32, k 32*j + 16*(l/32) + b.  Rows up to the next multiple of 32 and k up
+// to the next multiple of 64 are zero.
+
+__device__ __forceinline__ uint32_t packed_act_offset(int row, int k, int KF) {
+  const int lane = (row & 31) + 32 * ((k >> 4) & 1);
+  return (uint32_t(row >> 5) * uint32_t(KF) + uint32_t(k >> 5)) * 1024u + uint32_t(lane) * 16u;
+}
+
+// One wave per row (padding rows included): absmax, then 16-element chunks quantised and
+// stored as 16-byte vectors at their packed position.
+template <bool VEC>
+__global__ __launch_bounds__(256) void quant_rows_packed_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M,
+                                                                int Mp, int K, int KF, int8_t* __restrict__ q,
+                                                                float* __restrict__ scale) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= Mp) return;
+  const int KP = KF * 32;
+  if (row >= M) {
+    for (int k = lane * 16; k < KP; k += 1024)
+      *reinterpret_cast<v4u*>(q + packed_act_offset(row, k, KF)) = v4u{0, 0, 0, 0};
+    return;
+  }
+  const uint16_t* xr = x + int64_t(row) * ldx;
+  float amax = 0.0f;
+  for (int k = lane * 16; k < K; k += 1024) {
+    float v[16];
+    if (VEC) {
+      load8<uint16_t>(xr + k, *reinterpret_cast<float(*)[8]>(&v[0]));
+      load8<uint16_t>(xr + k + 8, *reinterpret_cast<float(*)[8]>(&v[8]));
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) v[i] = bf16_to_f32(xr[k + i]);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  }
+  amax = wave_max(amax);
+  const float s = fmaxf(amax, 1e-8f) / 127.0f;
+  if (lane == 0) scale[row] = s;
+  for (int k = lane * 16; k < KP; k += 1024) {
+    uint32_t w[4] = {0, 0, 0, 0};
+    if (k < K) {
+      float v[16];
+      if (VEC) {
+        load8<uint16_t>(xr + k, *reinterpret_cast<float(*)[8]>(&v[0]));
+        load8<uint16_t>(xr + k + 8, *reinterpret_cast<float(*)[8]>(&v[8]));
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = bf16_to_f32(xr[k + i]);
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) w[i >> 2] |= uint32_t(uint8_t(quant1(v[i], s))) << (8 * (i & 3));
+    }
+    *reinterpret_cast<v4u*>(q + packed_act_offset(row, k, KF)) = v4u{w[0], w[1], w[2], w[3]};
+  }
+}
+
+// Row-major int8 A -> packed activations; one thread per 16-byte chunk of the output.
+__global__ __launch_bounds__(256) void pack_act_kernel(const int8_t* __restrict__ a, int64_t lda, int M, int K, int KF,
+                                                       int64_t nchunks, int8_t* __restrict__ out) {
+  const int64_t c = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (c >= nchunks) return;
+  const int l = int(c & 63);
+  const int64_t f = c >> 6;
+  const int mt = int(f / KF), j = int(f % KF);
+  const int row = 32 * mt + (l & 31);
+  const int k = 32 * j + 16 * (l >> 5);
+  v4u v = {0, 0, 0, 0};
+  if (row < M && k < K) v = *reinterpret_cast<const v4u*>(a + int64_t(row) * lda + k);
+  *reinterpret_cast<v4u*>(out + c * 16) = v;
 }
 
 }  // namespace w8a8
@@ -179,16 +255,16 @@ static int pack_common(const int8_t* w, int64_t ldw, int64_t N, int64_t K, int s
   if (!w || !packed) return fail(W8A8_EINVAL, "pack_weight: null pointer");
   if (N <= 0 || K <= 0) return fail(W8A8_EINVAL, "pack_weight: bad shape N=%lld K=%lld", (long long)N, (long long)K);
   if (src_kn ? ldw < N : ldw < K) return fail(W8A8_EINVAL, "pack_weight: leading dimension %lld too small", (long long)ldw);
-  if (interleave > 0 && (interleave % 16 != 0 || N != 2 * interleave))
-    return fail(W8A8_EINVAL, "pack_weight: interleave %lld needs N == 2*I and I %% 16 == 0 (N=%lld)",
+  if (interleave > 0 && (interleave % 32 != 0 || N != 2 * interleave))
+    return fail(W8A8_EINVAL, "pack_weight: interleave %lld needs N == 2*I and I %% 32 == 0 (N=%lld)",
                 (long long)interleave, (long long)N);
   if ((uintptr_t)packed % 16 != 0) return fail(W8A8_EALIGN, "pack_weight: packed buffer not 16-byte aligned");
   const int64_t bytes = w8a8_packed_weight_bytes_internal(N, K, interleave);
   if (bytes > INT32_MAX) return fail(W8A8_ENOTSUP, "pack_weight: packed weight of %lld bytes exceeds 2 GiB", (long long)bytes);
-  const int KT = int((K + 63) / 64);
+  const int KF = int(2 * ((K + 63) / 64));
   const int64_t nchunks = bytes / 16;
   dim3 grid((unsigned)((nchunks + 255) / 256));
-  pack_weight_kernel<<<grid, 256, 0, stream>>>(w, ldw, (int)N, (int)K, src_kn, (int)interleave, KT, nchunks, packed);
+  pack_weight_kernel<<<grid, 256, 0, stream>>>(w, ldw, (int)N, (int)K, src_kn, (int)interleave, KF, nchunks, packed);
   return check_launch("pack_weight");
 }
 
@@ -200,6 +276,48 @@ int w8a8_pack_weight_nk(const int8_t* w_nk, int64_t ldw, int64_t N, int64_t K, i
 int w8a8_pack_weight_kn(const int8_t* b_kn, int64_t ldb, int64_t K, int64_t N, int64_t interleave, int8_t* packed,
                         hipStream_t stream) {
   return pack_common(b_kn, ldb, N, K, 1, interleave, packed, stream);
+}
+
+int64_t w8a8_packed_act_bytes(int64_t M, int64_t K) {
+  if (M < 0 || K <= 0) return -1;
+  return (M + 31) / 32 * 2 * ((K + 63) / 64) * 1024;
+}
+
+int w8a8_pack_act(const int8_t* a, int64_t lda, int64_t M, int64_t K, int8_t* packed, hipStream_t stream) {
+  if (M < 0 || K <= 0 || lda < K) return fail(W8A8_EINVAL, "pack_act: bad shape M=%lld K=%lld lda=%lld", (long long)M,
+                                               (long long)K, (long long)lda);
+  if (M == 0) return W8A8_OK;
+  if (!a || !packed) return fail(W8A8_EINVAL, "pack_act: null pointer");
+  if (K % 16 != 0) return fail(W8A8_ENOTSUP, "pack_act: K=%lld must be a multiple of 16", (long long)K);
+  if (lda % 16 != 0 || (uintptr_t)a % 16 != 0 || (uintptr_t)packed % 16 != 0)
+    return fail(W8A8_EALIGN, "pack_act: rows and the packed buffer must be 16-byte aligned");
+  const int64_t bytes = w8a8_packed_act_bytes(M, K);
+  if (bytes > INT32_MAX || M > INT32_MAX) return fail(W8A8_ENOTSUP, "pack_act: too large");
+  const int KF = int(2 * ((K + 63) / 64));
+  const int64_t nchunks = bytes / 16;
+  pack_act_kernel<<<unsigned((nchunks + 255) / 256), 256, 0, stream>>>(a, lda, int(M), int(K), KF, nchunks, packed);
+  return check_launch("pack_act");
+}
+
+int w8a8_quant_rows_packed_bf16(const uint16_t* x, int64_t ldx, int64_t M, int64_t K, int8_t* packed, float* scale,
+                                hipStream_t stream) {
+  if (M < 0 || K <= 0 || ldx < K) return fail(W8A8_EINVAL, "quant_rows_packed: bad shape M=%lld K=%lld ldx=%lld",
+                                               (long long)M, (long long)K, (long long)ldx);
+  if (M == 0) return W8A8_OK;
+  if (!x || !packed || !scale) return fail(W8A8_EINVAL, "quant_rows_packed: null pointer");
+  if (K % 16 != 0) return fail(W8A8_ENOTSUP, "quant_rows_packed: K=%lld must be a multiple of 16", (long long)K);
+  if ((uintptr_t)packed % 16 != 0) return fail(W8A8_EALIGN, "quant_rows_packed: packed buffer not 16-byte aligned");
+  const int64_t bytes = w8a8_packed_act_bytes(M, K);
+  if (bytes > INT32_MAX || M > INT32_MAX / 4) return fail(W8A8_ENOTSUP, "quant_rows_packed: too large");
+  const int KF = int(2 * ((K + 63) / 64));
+  const int Mp = int((M + 31) / 32 * 32);
+  const bool vec = (ldx % 8 == 0) && ((uintptr_t)x % 16 == 0);
+  dim3 grid(unsigned((Mp + 3) / 4));
+  if (vec)
+    quant_rows_packed_kernel<true><<<grid, 256, 0, stream>>>(x, ldx, int(M), Mp, int(K), KF, packed, scale);
+  else
+    quant_rows_packed_kernel<false><<<grid, 256, 0, stream>>>(x, ldx, int(M), Mp, int(K), KF, packed, scale);
+  return check_launch("quant_rows_packed_bf16");
 }
 
 }  // extern "C"

@@ -28,13 +28,17 @@ SIGNATURES = {
     "w8a8_quant_rows_bf16": (_i32, [_p, _i64, _i64, _i64, _p, _i64, _p, _p]),
     "w8a8_quant_rows_f32": (_i32, [_p, _i64, _i64, _i64, _p, _i64, _p, _p]),
     "w8a8_gemm_i32": (_i32, [_p, _i64, _p, _i64, _i64, _i64, _p, _i64, _p]),
-    "w8a8_gemm_i32_cfg": (_i32, [_p, _i64, _p, _i64, _i64, _i64, _p, _i64, _i32, _p]),
+    "w8a8_gemm_workspace_bytes": (_i64, [_i64, _i64, _i64, _i32, _i32]),
+    "w8a8_gemm_i32_ex": (_i32, [_p, _i64, _i32, _p, _i64, _i64, _i64, _p, _i64, _i32, _i32, _p, _i64, _p]),
+    "w8a8_packed_act_bytes": (_i64, [_i64, _i64]),
+    "w8a8_pack_act": (_i32, [_p, _i64, _i64, _i64, _p, _p]),
+    "w8a8_quant_rows_packed_bf16": (_i32, [_p, _i64, _i64, _i64, _p, _p, _p]),
     "w8a8_gemm_bf16": (_i32, [_p, _i64, _p, _p, _p, _i64, _i64, _i64, _i32, _i64, _p, _i64, _p, _i64, _p]),
-    "w8a8_gemm_bf16_cfg": (_i32, [_p, _i64, _p, _p, _p, _i64, _i64, _i64, _i32, _i64, _p, _i64, _p, _i64, _i32,
-                                  _p]),
+    "w8a8_gemm_bf16_ex": (_i32, [_p, _i64, _i32, _p, _p, _p, _i64, _i64, _i64, _i32, _i64, _p, _i64, _p, _i64,
+                                 _i32, _i32, _p, _i64, _p]),
     "w8a8_dequant_bf16": (_i32, [_p, _i64, _p, _p, _i64, _i64, _p, _i64, _p]),
     "w8a8_rms_residual_bf16": (_i32, [_p, _i64, _p, _i64, _p, _f32, _i64, _i64, _p, _i64, _p, _i64, _p, _p]),
-    "w8a8_linear_workspace_bytes": (_i64, [_i64, _i64]),
+    "w8a8_linear_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "w8a8_linear_bf16": (_i32, [_p, _i64, _p, _p, _i64, _i64, _i64, _i32, _i64, _p, _i64, _p, _f32, _p, _i64, _p,
                                 _i64, _p]),
     "w8a8_gemv_bf16": (_i32, [_p, _i64, _i64, _p, _i64, _i64, _i64, _p, _i32, _p, _i64, _p]),

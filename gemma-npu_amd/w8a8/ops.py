@@ -34,6 +34,22 @@ def _ld(t):
     return t.stride(0) if t.shape[0] > 1 else max(t.shape[1], 1)
 
 
+_WORKSPACES = {}
+
+
+def workspace(device, nbytes):
+    """The zero-initialised split-K / linear workspace of (device, current stream), grown to at
+    least nbytes.  Calls on one stream are ordered, so they can share it; its first 4 KiB of
+    counters are zero between calls by the kernels' own contract."""
+    device = torch.device(device)
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(int(nbytes), 1 << 20), dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws
+
+
 def _same_device(*ts):
     devs = {t.device for t in ts if t is not None}
     if len(devs) > 1:
@@ -127,36 +143,96 @@ def _packed(w):
     return w
 
 
-def gemm_i32(a, w, c=None, tile_cfg=-1):
-    """C[M,N] int32 = A[M,K] int8 @ W (exact; npu_kernels.py:40-56)."""
-    w = _packed(w)
+class PackedActivation:
+    """int8 activations [M, K] in the GEMM's packed fragment layout (w8a8_packed_act_bytes),
+    the fastest form of the A operand."""
+
+    __slots__ = ("data", "M", "K")
+
+    def __init__(self, data, M, K):
+        self.data, self.M, self.K = data, int(M), int(K)
+
+    @property
+    def device(self):
+        return self.data.device
+
+    @property
+    def shape(self):
+        return (self.M, self.K)
+
+
+def packed_act_bytes(M, K):
+    n = lib().w8a8_packed_act_bytes(M, K)
+    if n < 0:
+        raise ValueError(f"invalid activation shape M={M} K={K}")
+    return n
+
+
+def pack_act(a, out=None):
+    """Row-major int8 A [M, K] -> PackedActivation."""
     _check(a, "a", torch.int8)
     M, K = a.shape
+    n = packed_act_bytes(M, K)
+    if out is None:
+        out = torch.empty(max(n, 1), dtype=torch.int8, device=a.device)
+    call("w8a8_pack_act", a.data_ptr(), _ld(a), M, K, out.data_ptr(), _stream(a))
+    return PackedActivation(out, M, K)
+
+
+def quant_rows_packed(x, out=None, scale=None):
+    """Per-row int8 quant of bf16 rows straight into the packed layout -> (PackedActivation, scale)."""
+    _check(x, "x", torch.bfloat16)
+    M, K = x.shape
+    n = packed_act_bytes(M, K)
+    if out is None:
+        out = torch.empty(max(n, 1), dtype=torch.int8, device=x.device)
+    if scale is None:
+        scale = torch.empty((M,), dtype=torch.float32, device=x.device)
+    _same_device(x, out, scale)
+    call("w8a8_quant_rows_packed_bf16", x.data_ptr(), _ld(x), M, K, out.data_ptr(), scale.data_ptr(), _stream(x))
+    return PackedActivation(out, M, K), scale
+
+
+def _a_operand(a):
+    """(pointer, lda, a_packed, M, K, tensor) of a row-major int8 tensor or a PackedActivation."""
+    if isinstance(a, PackedActivation):
+        return a.data.data_ptr(), 0, 1, a.M, a.K, a.data
+    _check(a, "a", torch.int8)
+    return a.data_ptr(), _ld(a), 0, a.shape[0], a.shape[1], a
+
+
+def gemm_i32(a, w, c=None, tile_cfg=-1, split_k=0):
+    """C[M,N] int32 = A[M,K] int8 @ W (exact; npu_kernels.py:40-56).  A is a row-major int8
+    tensor or a PackedActivation."""
+    w = _packed(w)
+    ap, lda, a_packed, M, K, at = _a_operand(a)
     if K != w.K:
         raise ValueError(f"gemm_i32: A has K={K}, weight has K={w.K}")
     if w.interleave:
         raise ValueError("gemm_i32: a gate/up-interleaved weight has no plain int32 column order")
     if c is None:
-        c = torch.empty((M, w.N), dtype=torch.int32, device=a.device)
+        c = torch.empty((M, w.N), dtype=torch.int32, device=at.device)
     _check(c, "c", torch.int32)
     if tuple(c.shape) != (M, w.N):
         raise ValueError(f"gemm_i32: C has shape {tuple(c.shape)}, expected {(M, w.N)}")
-    _same_device(a, w.data, c)
-    call("w8a8_gemm_i32_cfg", a.data_ptr(), _ld(a), w.data.data_ptr(), M, w.N, K, c.data_ptr(), _ld(c),
-         tile_cfg, _stream(a))
+    _same_device(at, w.data, c)
+    need = lib().w8a8_gemm_workspace_bytes(M, w.N, K, tile_cfg, split_k) if M else 0
+    ws = workspace(at.device, need) if need > 0 else None
+    call("w8a8_gemm_i32_ex", ap, lda, a_packed, w.data.data_ptr(), M, w.N, K, c.data_ptr(), _ld(c), tile_cfg,
+         split_k, ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0, _stream(at))
     return c
 
 
-def gemm_bf16(a, sx, w, sw=None, epilogue="none", residual=None, out=None, tile_cfg=-1):
-    """GEMM + dequant epilogue -> bf16 (pipeline.py:55-57, 102-107)."""
+def gemm_bf16(a, sx, w, sw=None, epilogue="none", residual=None, out=None, tile_cfg=-1, split_k=0):
+    """GEMM + dequant epilogue -> bf16 (pipeline.py:55-57, 102-107).  A is a row-major int8
+    tensor or a PackedActivation."""
     w = _packed(w)
     sw = w.sw if sw is None else sw
     if sw is None:
         raise ValueError("gemm_bf16: no per-channel scales")
-    _check(a, "a", torch.int8)
+    ap, lda, a_packed, M, K, at = _a_operand(a)
     _check(sx, "sx", torch.float32, 1)
     _check(sw, "sw", torch.float32, 1)
-    M, K = a.shape
     if K != w.K or sx.shape[0] != M or sw.shape[0] != w.N:
         raise ValueError("gemm_bf16: operand shapes do not match")
     epi = EPILOGUES[epilogue]
@@ -164,7 +240,7 @@ def gemm_bf16(a, sx, w, sw=None, epilogue="none", residual=None, out=None, tile_
         raise ValueError("gemm_bf16: use linear_bf16 or rms_residual for the RMSNorm residual")
     ncols = w.interleave if epi == 1 else w.N
     if out is None:
-        out = torch.empty((M, ncols), dtype=torch.bfloat16, device=a.device)
+        out = torch.empty((M, ncols), dtype=torch.bfloat16, device=at.device)
     _check(out, "out", torch.bfloat16)
     if tuple(out.shape) != (M, ncols):
         raise ValueError(f"gemm_bf16: out has shape {tuple(out.shape)}, expected {(M, ncols)}")
@@ -176,9 +252,12 @@ def gemm_bf16(a, sx, w, sw=None, epilogue="none", residual=None, out=None, tile_
         if tuple(residual.shape) != (M, w.N):
             raise ValueError("gemm_bf16: residual shape does not match")
         rp, ldr = residual.data_ptr(), _ld(residual)
-    _same_device(a, sx, sw, w.data, out, residual)
-    call("w8a8_gemm_bf16_cfg", a.data_ptr(), _ld(a), sx.data_ptr(), w.data.data_ptr(), sw.data_ptr(), M, w.N, K,
-         epi, w.interleave, rp, ldr, out.data_ptr(), _ld(out), tile_cfg, _stream(a))
+    _same_device(at, sx, sw, w.data, out, residual)
+    need = lib().w8a8_gemm_workspace_bytes(M, w.N, K, tile_cfg, split_k) if M else 0
+    ws = workspace(at.device, need) if need > 0 else None
+    call("w8a8_gemm_bf16_ex", ap, lda, a_packed, sx.data_ptr(), w.data.data_ptr(), sw.data_ptr(), M, w.N, K,
+         epi, w.interleave, rp, ldr, out.data_ptr(), _ld(out), tile_cfg, split_k,
+         ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0, _stream(at))
     return out
 
 
@@ -223,12 +302,13 @@ def rms_residual(y, res, w, eps, out=None, quant=False):
     return (out, q, sq) if quant else out
 
 
-def linear_workspace_bytes(M, K):
-    return lib().w8a8_linear_workspace_bytes(M, K)
+def linear_workspace_bytes(M, N, K):
+    return lib().w8a8_linear_workspace_bytes(M, N, K)
 
 
-def linear_bf16(x, w, sw=None, epilogue="none", residual=None, rms_w=None, eps=1e-6, out=None, workspace=None):
-    """bf16 x -> per-token quant -> W8A8 GEMM -> dequant epilogue -> bf16 (gemma_npu.py:117-152)."""
+def linear_bf16(x, w, sw=None, epilogue="none", residual=None, rms_w=None, eps=1e-6, out=None, ws_arg=None):
+    """bf16 x -> per-token quant -> W8A8 GEMM -> dequant epilogue -> bf16 (gemma_npu.py:117-152).
+    ws_arg: a zero-initialised uint8 workspace to use instead of the per-stream one."""
     w = _packed(w)
     sw = w.sw if sw is None else sw
     if sw is None:
@@ -257,13 +337,11 @@ def linear_bf16(x, w, sw=None, epilogue="none", residual=None, rms_w=None, eps=1
     if rms_w is not None:
         _check(rms_w, "rms_w", torch.bfloat16, 1)
         rwp = rms_w.data_ptr()
-    need = linear_workspace_bytes(M, K)
-    if workspace is None:
-        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
-    _same_device(x, sw, w.data, out, residual, rms_w, workspace)
+    need = linear_workspace_bytes(M, w.N, K)
+    ws = workspace(x.device, need) if ws_arg is None else ws_arg
+    _same_device(x, sw, w.data, out, residual, rms_w, ws)
     call("w8a8_linear_bf16", x.data_ptr(), _ld(x), w.data.data_ptr(), sw.data_ptr(), M, w.N, K, epi,
-         w.interleave, rp, ldr, rwp, float(eps), out.data_ptr(), _ld(out), workspace.data_ptr(),
-         workspace.numel(), _stream(x))
+         w.interleave, rp, ldr, rwp, float(eps), out.data_ptr(), _ld(out), ws.data_ptr(), ws.numel(), _stream(x))
     return out
 
 

@@ -46,8 +46,8 @@ int w8a8_abi_version(void);
 /* ---- resident weights ------------------------------------------------------------------ */
 
 /* Bytes of the packed (MFMA-fragment) weight for N output channels x K inputs.  With
- * interleave = I > 0 the weight is a [gate; up] pair (N == 2*I, I % 16 == 0) whose channels
- * are interleaved in 16-channel tiles for the fused GELU epilogue.  -1 if invalid.
+ * interleave = I > 0 the weight is a [gate; up] pair (N == 2*I, I % 32 == 0) whose channels
+ * are interleaved in 32-channel tiles for the fused GELU epilogue.  -1 if invalid.
  * Replaces the zero-padded [K, N_pad] resident copy of gemma_npu.py:67-75. */
 int64_t w8a8_packed_weight_bytes(int64_t N, int64_t K, int64_t interleave);
 
@@ -76,16 +76,44 @@ int w8a8_quant_rows_f32(const float *x, int64_t ldx, int64_t M, int64_t K, int8_
 /* ---- GEMM (npu_kernels.py:40-64) --------------------------------------------------------- */
 
 /* C[M, N] int32 = A[M, K] int8 @ W, W packed by w8a8_pack_weight_* (interleave 0).
- * Exact integer arithmetic.  K % 16 == 0; A rows 16-byte aligned (lda % 16 == 0); C rows
- * 16-byte aligned (ldc % 4 == 0).  Any M >= 0 and N >= 1: no padding to 512 is needed
+ * Exact integer arithmetic.  K % 16 == 0; A rows 16-byte aligned (lda % 16 == 0); C 4-byte
+ * aligned (rows 16-byte aligned use vector stores).  Any M >= 0 and N >= 1: no padding to 512 is needed
  * (the reference's mm_i8 floors M and N to multiples of 512, npu_kernels.py:63). */
 int w8a8_gemm_i32(const int8_t *a, int64_t lda, const int8_t *w_packed, int64_t M, int64_t N, int64_t K,
                   int32_t *c, int64_t ldc, hipStream_t stream);
 
-/* As w8a8_gemm_i32 with an explicit tile configuration (0 .. count-1, -1 = automatic);
- * for tuning and tests. */
-int w8a8_gemm_i32_cfg(const int8_t *a, int64_t lda, const int8_t *w_packed, int64_t M, int64_t N, int64_t K,
-                      int32_t *c, int64_t ldc, int tile_cfg, hipStream_t stream);
+/* ---- packed activations ----------------------------------------------------------------- */
+
+/* The GEMM streams A fastest when it is laid out like the packed weight: 1 KiB fragments of
+ * 32 rows x 32 k (fragment (mt, j) at (mt * KF + j) * 1024, KF = 2 * ceil(K/64); byte 16*l + b
+ * = row 32*mt + l%32, k 32*j + 16*(l/32) + b), zero past M (to a multiple of 32) and past K (to
+ * a multiple of 64).  Bytes of that layout for M rows of K; -1 if invalid. */
+int64_t w8a8_packed_act_bytes(int64_t M, int64_t K);
+
+/* Row-major int8 A[M, K] (lda % 16 == 0) -> packed activations. */
+int w8a8_pack_act(const int8_t *a, int64_t lda, int64_t M, int64_t K, int8_t *packed, hipStream_t stream);
+
+/* Per-row quantisation of bf16 rows (as w8a8_quant_rows_bf16) written straight into the packed
+ * activation layout; scale[m] fp32 per row. */
+int w8a8_quant_rows_packed_bf16(const uint16_t *x, int64_t ldx, int64_t M, int64_t K, int8_t *packed, float *scale,
+                                hipStream_t stream);
+
+/* Split-K workspace the _ex GEMMs use for [M, N, K] with tile_cfg (-1 = automatic) and split_k
+ * (0 = automatic, which currently never splits; n >= 1 = at most n blocks per output tile
+ * along K, used only when there are few output tiles): 0 when no split will happen.  Its first 4 KiB
+ * hold arrival counters that must be zero before a call and are zero again after it (zero-fill
+ * a new workspace once); the rest is scratch, so one workspace serves any shapes.  Calls that
+ * overlap in time need separate workspaces. */
+int64_t w8a8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int tile_cfg, int split_k);
+
+/* As w8a8_gemm_i32 with A given either row-major (a_packed = 0, lda used) or packed
+ * (a_packed = 1, lda ignored), an explicit tile configuration (0 .. 7, -1 = automatic), a split-K
+ * request (as w8a8_gemm_workspace_bytes) and its workspace (NULL or too small: no split;
+ * 256-byte aligned).  Split-K keeps the result bit-exact: int32 partial sums are added in a
+ * fixed order by the last block of each output tile. */
+int w8a8_gemm_i32_ex(const int8_t *a, int64_t lda, int a_packed, const int8_t *w_packed, int64_t M, int64_t N,
+                     int64_t K, int32_t *c, int64_t ldc, int tile_cfg, int split_k, void *workspace,
+                     int64_t workspace_bytes, hipStream_t stream);
 
 /* GEMM with the dequantising epilogue, bf16 out:
  *   y[m, n] = bf16((float(acc[m, n]) * sx[m]) * sw[n])                 (pipeline.py:55-57)
@@ -98,9 +126,12 @@ int w8a8_gemm_bf16(const int8_t *a, int64_t lda, const float *sx, const int8_t *
                    int64_t M, int64_t N, int64_t K, int epilogue, int64_t interleave, const uint16_t *res,
                    int64_t ldr, uint16_t *out, int64_t ldo, hipStream_t stream);
 
-int w8a8_gemm_bf16_cfg(const int8_t *a, int64_t lda, const float *sx, const int8_t *w_packed, const float *sw,
-                       int64_t M, int64_t N, int64_t K, int epilogue, int64_t interleave, const uint16_t *res,
-                       int64_t ldr, uint16_t *out, int64_t ldo, int tile_cfg, hipStream_t stream);
+/* As w8a8_gemm_bf16 with packed or row-major A, an explicit tile configuration and an
+ * optional split-K workspace (as w8a8_gemm_i32_ex). */
+int w8a8_gemm_bf16_ex(const int8_t *a, int64_t lda, int a_packed, const float *sx, const int8_t *w_packed,
+                      const float *sw, int64_t M, int64_t N, int64_t K, int epilogue, int64_t interleave,
+                      const uint16_t *res, int64_t ldr, uint16_t *out, int64_t ldo, int tile_cfg, int split_k,
+                      void *workspace, int64_t workspace_bytes, hipStream_t stream);
 
 /* ---- element-wise neighbours ------------------------------------------------------------- */
 
@@ -117,12 +148,14 @@ int w8a8_rms_residual_bf16(const uint16_t *y, int64_t ldy, const uint16_t *res, 
 
 /* ---- whole linear: bf16 in -> bf16 out (NPUGemm.matmul, gemma_npu.py:117-152) ------------ */
 
-/* Workspace for w8a8_linear_bf16: int8 rows + per-row scales. */
-int64_t w8a8_linear_workspace_bytes(int64_t M, int64_t K);
+/* Workspace for w8a8_linear_bf16: the GEMM's split-K workspace (counters first, as
+ * w8a8_gemm_workspace_bytes), packed int8 rows and per-row scales.  Same rules: zero-fill it
+ * once; calls that overlap in time need separate workspaces. */
+int64_t w8a8_linear_workspace_bytes(int64_t M, int64_t N, int64_t K);
 
 /* quant_rows(x) -> GEMM -> epilogue.  epilogue 0-2 as w8a8_gemm_bf16; 3: residual with RMSNorm,
  * out = bf16(res + bf16(rms(y) * rms_w)) (pipeline.py:113).  workspace: 256-byte aligned,
- * w8a8_linear_workspace_bytes(M, K) long. */
+ * w8a8_linear_workspace_bytes(M, N, K) long. */
 int w8a8_linear_bf16(const uint16_t *x, int64_t ldx, const int8_t *w_packed, const float *sw, int64_t M, int64_t N,
                      int64_t K, int epilogue, int64_t interleave, const uint16_t *res, int64_t ldr,
                      const uint16_t *rms_w, float eps, uint16_t *out, int64_t ldo, void *workspace,

@@ -33,19 +33,27 @@ def test_library_exports_every_declared_symbol():
 
 def test_packed_weight_bytes():
     L = _lib.lib()
-    assert L.w8a8_packed_weight_bytes(6144, 1536, 0) == 6144 // 16 * 1536 // 64 * 1024
+    assert L.w8a8_packed_weight_bytes(6144, 1536, 0) == 6144 * 1536
     assert L.w8a8_packed_weight_bytes(2560, 1536, 0) == 2560 * 1536
-    assert L.w8a8_packed_weight_bytes(17, 70, 0) == 2 * 2 * 1024  # padded to 16 x 64 tiles
+    assert L.w8a8_packed_weight_bytes(17, 70, 0) == 32 * 128       # padded to 32 channels x 64 k
+    assert L.w8a8_packed_weight_bytes(33, 64, 0) == 64 * 64
     assert L.w8a8_packed_weight_bytes(12288, 1536, 6144) == 12288 * 1536
-    assert L.w8a8_packed_weight_bytes(12288, 1536, 6000) == -1   # I must be a multiple of 16
+    assert L.w8a8_packed_weight_bytes(12288, 1536, 6000) == -1   # I must be a multiple of 32
     assert L.w8a8_packed_weight_bytes(12288, 1536, 4096) == -1   # N must be 2 I
     assert L.w8a8_packed_weight_bytes(0, 64, 0) == -1
 
 
 def test_linear_workspace_bytes():
     L = _lib.lib()
-    assert L.w8a8_linear_workspace_bytes(512, 1536) == 512 * 1536 + 512 * 4
-    assert L.w8a8_linear_workspace_bytes(3, 40) == 256 + 12
+    assert L.w8a8_packed_act_bytes(512, 1536) == 512 * 1536
+    assert L.w8a8_packed_act_bytes(33, 40) == 64 * 64       # rows to 32, k to 64
+    assert L.w8a8_packed_act_bytes(0, 64) == 0
+    assert L.w8a8_gemm_workspace_bytes(16384, 12288, 1536, -1, 8) == 0       # enough tiles: no split
+    assert L.w8a8_gemm_workspace_bytes(512, 1536, 6144, 4, 0) == 0           # automatic: K kept whole
+    g = L.w8a8_gemm_workspace_bytes(512, 1536, 6144, 4, 8)                   # 48 tiles, asked to split
+    assert g == 4096 + 48 * 5 * 128 * 128 * 4
+    assert L.w8a8_linear_workspace_bytes(512, 1536, 6144) == 4096 + 512 * 6144 + 512 * 4
+    assert L.w8a8_linear_workspace_bytes(3, 64, 64) == 4096 + 32 * 64 + 256  # counters kept; rows to 32
 
 
 def _status(name, *args):
@@ -66,7 +74,7 @@ def test_errors_are_reported_without_launching():
     assert rc == _lib.W8A8_EALIGN
     rc, msg = _status("w8a8_gemm_i32", fake, 64, fake, 4, 8, 64, fake, 6, None)
     assert rc == _lib.W8A8_EINVAL and "ldc" in msg
-    rc, msg = _status("w8a8_gemm_i32_cfg", fake, 64, fake, 4, 8, 64, fake, 8, 99, None)
+    rc, msg = _status("w8a8_gemm_i32_ex", fake, 64, 0, fake, 4, 8, 64, fake, 8, 99, 0, None, 0, None)
     assert rc == _lib.W8A8_EINVAL and "config" in msg
     rc, msg = _status("w8a8_gemm_bf16", fake, 64, fake, fake, fake, 4, 16, 64, 1, 0, None, 0, fake, 16, None)
     assert rc == _lib.W8A8_EINVAL and "interleave" in msg
@@ -78,7 +86,7 @@ def test_errors_are_reported_without_launching():
     assert rc == _lib.W8A8_ENOTSUP
     rc, msg = _status("w8a8_quant_rows_bf16", fake, 8, 4, 16, fake, 16, fake, None)
     assert rc == _lib.W8A8_EINVAL
-    rc, msg = _status("w8a8_pack_weight_nk", fake, 64, 32, 64, 24, fake, None)
+    rc, msg = _status("w8a8_pack_weight_nk", fake, 64, 96, 64, 48, fake, None)
     assert rc == _lib.W8A8_EINVAL and "interleave" in msg
     rc, msg = _status("w8a8_rms_residual_bf16", fake, 8, fake, 8, None, 1e-6, 2, 8, fake, 8, fake, 8, None, None)
     assert rc == _lib.W8A8_EINVAL

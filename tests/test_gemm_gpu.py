@@ -24,7 +24,7 @@ def packed_from_nk(w_nk, interleave=0):
     return ops.pack_weight(w_nk.to(DEV), "nk", interleave)
 
 
-@pytest.mark.parametrize("cfg", [0, 1, 2])
+@pytest.mark.parametrize("cfg", list(range(8)))
 @pytest.mark.parametrize("M,N,K", [(1, 16, 64), (37, 72, 128), (130, 200, 192), (300, 520, 320),
                                    (64, 48, 80), (257, 33, 1536)])
 def test_gemm_i32_vs_oracle(cfg, M, N, K):
@@ -117,7 +117,7 @@ def _inputs(M, K, N, seed):
     return x, w, sw, q, sx
 
 
-@pytest.mark.parametrize("cfg", [0, 1, 2])
+@pytest.mark.parametrize("cfg", list(range(8)))
 def test_gemm_dequant_epilogue_exact(cfg):
     M, K, N = 200, 256, 320
     x, w, sw, q, sx = _inputs(M, K, N, 21)
@@ -127,7 +127,7 @@ def test_gemm_dequant_epilogue_exact(cfg):
     assert np.array_equal(to_bits(out), ref)
 
 
-@pytest.mark.parametrize("cfg", [0, 1, 2])
+@pytest.mark.parametrize("cfg", list(range(8)))
 def test_gemm_residual_epilogue_exact(cfg):
     M, K, N = 130, 192, 256
     x, w, sw, q, sx = _inputs(M, K, N, 31)
@@ -139,7 +139,7 @@ def test_gemm_residual_epilogue_exact(cfg):
     assert np.array_equal(to_bits(out), ref)
 
 
-@pytest.mark.parametrize("cfg", [0, 1, 2])
+@pytest.mark.parametrize("cfg", list(range(8)))
 def test_gemm_gelu_epilogue(cfg):
     M, K, I = 150, 256, 192
     x, w, sw, q, sx = _inputs(M, K, 2 * I, 41)
@@ -154,7 +154,7 @@ def test_gemm_gelu_epilogue(cfg):
 
 def test_gemm_gelu_ragged_tiles():
     """I not a multiple of the 128/256-column block: gate/up tiles straddle the block edge."""
-    M, K, I = 70, 128, 80
+    M, K, I = 70, 128, 96
     x, w, sw, q, sx = _inputs(M, K, 2 * I, 43)
     ref = orc.gelu_mul(orc.dequant(orc.int_mm_nk(q, w.numpy()), sx, sw.numpy()))
     out = ops.gemm_bf16(torch.from_numpy(q).to(DEV), torch.from_numpy(sx).to(DEV),
@@ -170,3 +170,126 @@ def test_standalone_dequant_exact():
     sw = torch.rand(N, generator=g) * 0.02
     out = ops.dequant_bf16(acc.to(DEV), sx.to(DEV), sw.to(DEV))
     assert np.array_equal(to_bits(out), orc.dequant(acc.numpy(), sx.numpy(), sw.numpy()))
+
+
+# ---- packed activations ---------------------------------------------------------------------
+
+def unpack_act(packed, M, K):
+    """Inverse of the packed activation layout (fragment (mt, j), byte 16*l + b = row
+    32*mt + l%32, k 32*j + 16*(l/32) + b), written out independently of the kernels."""
+    KF = 2 * ((K + 63) // 64)
+    MT = (M + 31) // 32
+    arr = packed.reshape(MT, KF, 2, 32, 16)            # [mt][j][h][r][b]
+    full = arr.transpose(0, 3, 1, 2, 4).reshape(MT * 32, KF * 32)
+    return full
+
+
+@pytest.mark.parametrize("M,K", [(1, 64), (33, 80), (512, 1536), (100, 2048)])
+def test_pack_act_layout(M, K):
+    a = rand_i8((M, K), seed=M + K)
+    pa = ops.pack_act(a.to(DEV))
+    full = unpack_act(pa.data.cpu().numpy(), M, K)
+    assert np.array_equal(full[:M, :K], a.numpy())
+    assert not full[M:].any() and not full[:, K:].any(), "padding must be zero"
+
+
+@pytest.mark.parametrize("M,K", [(5, 16), (64, 1536), (77, 6144), (300, 2048)])
+def test_quant_rows_packed_vs_oracle(M, K):
+    x = workloads.activations(M, K, seed=M * K, row_spread=True)
+    q_ref, s_ref = orc.quant_rows(to_bits(x), "bf16")
+    pa, s = ops.quant_rows_packed(x.to(DEV))
+    full = unpack_act(pa.data.cpu().numpy(), M, K)
+    assert np.array_equal(s.cpu().numpy(), s_ref)
+    assert np.array_equal(full[:M, :K], q_ref)
+    assert not full[M:].any() and not full[:, K:].any()
+
+
+@pytest.mark.parametrize("cfg", list(range(8)))
+@pytest.mark.parametrize("M,N,K", [(1, 16, 64), (37, 72, 128), (300, 520, 320), (257, 33, 1536)])
+def test_gemm_i32_packed_a(cfg, M, N, K):
+    a = rand_i8((M, K), seed=M * 3 + K)
+    w = rand_i8((N, K), seed=N * 5 + K)
+    ref = orc.int_mm_nk(a.numpy(), w.numpy())
+    c = ops.gemm_i32(ops.pack_act(a.to(DEV)), packed_from_nk(w), tile_cfg=cfg)
+    assert np.array_equal(c.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("cfg", list(range(8)))
+def test_gemm_bf16_packed_a_epilogues(cfg):
+    M, K, I = 150, 256, 192
+    x, w, sw, q, sx = _inputs(M, K, 2 * I, 51)
+    pa, sx_d = ops.quant_rows_packed(x.to(DEV))
+    assert np.array_equal(sx_d.cpu().numpy(), sx)
+    y = orc.dequant(orc.int_mm_nk(q, w.numpy()), sx, sw.numpy())
+    out = ops.gemm_bf16(pa, sx_d, packed_from_nk(w), sw.to(DEV), tile_cfg=cfg)
+    assert np.array_equal(to_bits(out), y)
+    g = ops.gemm_bf16(pa, sx_d, packed_from_nk(w, interleave=I), sw.to(DEV), epilogue="gelu", tile_cfg=cfg)
+    assert_bf16_close(f32(to_bits(g)), f32(orc.gelu_mul(y)), what="gelu packed A")
+
+
+# ---- split-K ----------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("packed_a", [False, True])
+@pytest.mark.parametrize("M,N,K", [(64, 256, 6144), (512, 1536, 6144), (512, 2560, 1536), (100, 96, 2048)])
+def test_gemm_i32_split_k(packed_a, M, N, K):
+    """Few output tiles: the GEMM splits K over blocks and the last block adds the int32
+    partials, so the result stays bit-exact.  Run twice (the arrival counters must reset)."""
+    from w8a8 import lib
+    assert lib().w8a8_gemm_workspace_bytes(M, N, K, 4, 8) > 0, "shape should split K"
+    a = rand_i8((M, K), seed=M + 7 * N)
+    w = rand_i8((N, K), seed=K + 3 * N)
+    ref = torch._int_mm(a, w.t().contiguous()) if M > 16 else torch.from_numpy(orc.int_mm_nk(a.numpy(), w.numpy()))
+    pw = packed_from_nk(w)
+    A = ops.pack_act(a.to(DEV)) if packed_a else a.to(DEV)
+    for _ in range(2):
+        c = ops.gemm_i32(A, pw, tile_cfg=4, split_k=8)
+        assert torch.equal(c.cpu(), ref)
+
+
+def test_split_k_epilogues_and_workspace_reuse():
+    M, K, I = 256, 4096, 256
+    x, w, sw, q, sx = _inputs(M, K, 2 * I, 61)
+    pa, sx_d = ops.quant_rows_packed(x.to(DEV))
+    y = orc.dequant(orc.int_mm_nk(q, w.numpy()), sx, sw.numpy())
+    kw = dict(tile_cfg=4, split_k=8)
+    out = ops.gemm_bf16(pa, sx_d, packed_from_nk(w), sw.to(DEV), **kw)
+    assert np.array_equal(to_bits(out), y)
+    g = ops.gemm_bf16(pa, sx_d, packed_from_nk(w, interleave=I), sw.to(DEV), epilogue="gelu", **kw)
+    assert_bf16_close(f32(to_bits(g)), f32(orc.gelu_mul(y)), what="split-K gelu")
+    res = workloads.activations(M, 2 * I, 62, outliers=False)
+    r = ops.gemm_bf16(pa, sx_d, packed_from_nk(w), sw.to(DEV), epilogue="residual", residual=res.to(DEV), **kw)
+    assert np.array_equal(to_bits(r), orc.add_residual(y, to_bits(res)))
+    # a different shape on the same per-stream workspace, then the first again
+    a2 = rand_i8((40, 2048), 63)
+    w2 = rand_i8((128, 2048), 64)
+    c2 = ops.gemm_i32(a2.to(DEV), packed_from_nk(w2), **kw)
+    assert np.array_equal(c2.cpu().numpy(), orc.int_mm_nk(a2.numpy(), w2.numpy()))
+    out2 = ops.gemm_bf16(pa, sx_d, packed_from_nk(w), sw.to(DEV), **kw)
+    assert np.array_equal(to_bits(out2), y)
+
+
+def test_linear_split_k_layer_shapes():
+    """The M=512 micro-batch groups that split K (o: K=2048 N=1536; down: K=6144 N=1536)."""
+    for K, N in ((2048, 1536), (6144, 1536)):
+        x = workloads.activations(512, K, seed=K)
+        w, sw = workloads.weights(N, K, seed=N + K)
+        pw = ops.pack_weight(w.to(DEV), "nk", sw=sw.to(DEV))
+        out = ops.linear_bf16(x.to(DEV), pw)
+        ref, _, _ = orc.linear_bf16(to_bits(x), w.numpy(), sw.numpy())
+        assert np.array_equal(to_bits(out), ref)
+
+
+def test_split_k_repeated_launches_fresh_inputs():
+    """Back-to-back split-K launches with different A each time: a stale partial or a counter
+    left non-zero by an earlier launch would show up as a wrong product."""
+    M, N, K = 512, 1536, 6144
+    w = rand_i8((N, K), 71)
+    pw = packed_from_nk(w)
+    wt = w.t().contiguous()
+    outs, refs = [], []
+    for it in range(12):
+        a = rand_i8((M, K), 100 + it)
+        outs.append(ops.gemm_i32(ops.pack_act(a.to(DEV)), pw, tile_cfg=4, split_k=8))
+        refs.append(torch._int_mm(a, wt))
+    for it, (c, r) in enumerate(zip(outs, refs)):
+        assert torch.equal(c.cpu(), r), f"launch {it}"
