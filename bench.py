@@ -301,7 +301,7 @@ def main():
             K, N, epi = workloads.LAYER_GROUPS[name]
             Ms = 16384
             x = workloads.activations(Ms, K, seed=9, row_spread=True).to(dev)
-            q, sx = ops.quant_rows(x)
+            q, sx = ops.quant_rows_packed(x)
             gw = torch.Generator(device=dev).manual_seed(10)
             w = torch.randint(-127, 128, (N, K), generator=gw, dtype=torch.int8, device=dev)
             sw = torch.rand(N, generator=gw, device=dev) * 0.015 + 0.005

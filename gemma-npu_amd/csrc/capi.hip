@@ -89,6 +89,8 @@ const char* w8a8_last_error(void) { return g_err; }
 
 int w8a8_abi_version(void) { return 1; }
 
+int w8a8_gemm_tile_configs(void) { return gemm_config_count(); }
+
 int64_t w8a8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int tile_cfg, int split_k) {
   if (M <= 0 || N <= 0 || K <= 0 || M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) return 0;
   if (tile_cfg >= gemm_config_count()) return -1;
@@ -160,6 +162,7 @@ int w8a8_gemm_bf16_ex(const int8_t* a, int64_t lda, int a_packed, const float* s
   p.vec_store = (ldo % 4 == 0) && ((uintptr_t)out % 8 == 0);
   p.res = res;
   p.ldr = ldr;
+  p.res_vec = res && (ldr % 4 == 0) && ((uintptr_t)res % 8 == 0);
   p.split_req = split_k < 0 ? 0 : split_k;
   if (workspace && (uintptr_t)workspace % 256 != 0) return fail(W8A8_EALIGN, "gemm_bf16: workspace not 256-byte aligned");
   return gemm_launch(p, epi, tile_cfg, a_packed != 0, workspace, workspace_bytes, stream);

@@ -18,6 +18,7 @@ struct GemmParams {
                         // 32-channel tile (K padded to 64); NT = packed 32-channel tiles
   int I;                // EPI_GELU: width of the gate (and up) half
   int vec_store;        // output rows allow 4-wide vector stores (alignment checked on the host)
+  int res_vec;          // residual rows allow 4-wide (8-byte) vector loads
   int gm;               // row tiles per group in the block -> tile order (set by the launcher)
   int split_req;        // requested split-K: 0 = automatic, n = at most n splits
   int splits;           // blocks per output tile along K (1 = no split)

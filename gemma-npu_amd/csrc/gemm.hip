@@ -29,12 +29,27 @@ namespace w8a8 {
 
 typedef int v16i __attribute__((ext_vector_type(16)));
 
+// tanh(u) in fp32 as 1 - 2 / (1 + e^(2|u|)) with the sign of u.  What matters downstream is
+// 1 + tanh(u) (gelu below): for u << 0 that is the cancellation 1 - fl(1 - d), d = 2 / (1 + e^(2|u|)),
+// which lands on the fp32 grid just below 1 exactly where a correctly rounded tanhf does, as long as
+// d carries a small *relative* error.  Here d has ~1e-6 relative error (hardware exp2 / rcp), so
+// 1 + tanh(u) matches the correctly rounded form except within ~1e-6 of a rounding tie; for
+// |u| > 9.01 fl(1 - d) is exactly 1 and tanh saturates to +-1 as tanhf does.
+__device__ __forceinline__ float tanh_f32(float u) {
+  const float a = fabsf(u);
+  const float e = __builtin_amdgcn_exp2f(a * 2.8853900817779268f);  // e^(2a) = 2^(2a log2 e)
+  const float d = 2.0f * __builtin_amdgcn_rcpf(1.0f + e);
+  return copysignf(1.0f - d, u);
+}
+
+// GELU, tanh form: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), evaluated in the operation
+// order of torch's gelu(approximate="tanh") on float: x^3 = (x * x) * x, inner = beta * (x +
+// kappa * x^3), result = (0.5 * x) * (1 + tanh(inner)).
 __device__ __forceinline__ float gelu_tanh_f32(float x) {
-  // 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), the approximate="tanh" form.
   const float kBeta = 0.7978845608028654f;
   const float kKappa = 0.044715f;
-  const float inner = kBeta * (x + kKappa * x * x * x);
-  return 0.5f * x * (1.0f + tanhf(inner));
+  const float inner = kBeta * (x + kKappa * (x * x * x));
+  return 0.5f * x * (1.0f + tanh_f32(inner));
 }
 
 // s_waitcnt with only the vector-memory counter constrained (gfx9 encoding: vmcnt in bits
@@ -61,10 +76,12 @@ __device__ __forceinline__ int xcd_remap(int b, int nblocks) {
 }
 
 // Epilogue for one 32x32 accumulator tile.  Lane l holds row m and, for register group
-// g = 0..3, packed columns t*32 + 8g + lcol + r (r = 0..3, lcol = 4*(l/32)).
+// g = 0..3, packed columns t*32 + 8g + lcol + r (r = 0..3, lcol = 4*(l/32)).  sxm is the row's
+// scale; swt points at the LDS copy of the per-channel scales of this tile's packed columns
+// (swt[8g + r] belongs to packed column t*32 + 8g + lcol + r; for GELU, swt + 32 is the up tile).
 template <int EPI>
 __device__ __forceinline__ void store_tile(const GemmParams& p, const v16i& acc, const v16i* acc_up, int m, int t,
-                                           int lcol) {
+                                           int lcol, float sxm, const float* swt) {
   if constexpr (EPI == EPI_I32) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
@@ -80,21 +97,36 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, const v16i& acc,
       }
     }
   } else if constexpr (EPI == EPI_BF16 || EPI == EPI_RESID) {
-    const float sxm = p.sx[m];
+    // The residual may alias the output: every residual value this lane needs is loaded before
+    // any of its stores, and each element is read and written by this lane only.
+    v2u rv[4];
+    if constexpr (EPI == EPI_RESID) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int n = t * 32 + 8 * g + lcol;
+        const uint16_t* rs = p.res + int64_t(m) * p.ldr + n;
+        if (p.res_vec && n + 3 < p.N) {
+          rv[g] = *reinterpret_cast<const v2u*>(rs);
+        } else {
+          uint32_t h[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) h[r] = n + r < p.N ? rs[r] : 0u;
+          rv[g] = v2u{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+        }
+      }
+    }
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int n = t * 32 + 8 * g + lcol;
+      const v4f sw = *reinterpret_cast<const v4f*>(swt + 8 * g);
       float y[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float swn = (n + r < p.N) ? p.sw[n + r] : 0.0f;
-        y[r] = bf16_to_f32(f32_to_bf16((float(acc[4 * g + r]) * sxm) * swn));
-      }
+      for (int r = 0; r < 4; ++r) y[r] = bf16_to_f32(f32_to_bf16((float(acc[4 * g + r]) * sxm) * sw[r]));
       if constexpr (EPI == EPI_RESID) {
-        const uint16_t* rs = p.res + int64_t(m) * p.ldr + n;
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (n + r < p.N) y[r] = y[r] + bf16_to_f32(rs[r]);
+        y[0] += bf16_to_f32(uint16_t(rv[g][0]));
+        y[1] += bf16_to_f32(uint16_t(rv[g][0] >> 16));
+        y[2] += bf16_to_f32(uint16_t(rv[g][1]));
+        y[3] += bf16_to_f32(uint16_t(rv[g][1] >> 16));
       }
       uint16_t* dst = p.out + int64_t(m) * p.ldo + n;
       if (p.vec_store && n + 3 < p.N) {
@@ -107,18 +139,16 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, const v16i& acc,
     }
   } else if constexpr (EPI == EPI_GELU) {
     // t is an even (gate) tile u = t/2; acc_up is the matching up tile t+1.
-    const float sxm = p.sx[m];
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int c = (t >> 1) * 32 + 8 * g + lcol;  // logical gate column
+      const v4f swg = *reinterpret_cast<const v4f*>(swt + 8 * g);
+      const v4f swu = *reinterpret_cast<const v4f*>(swt + 32 + 8 * g);
       float o[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const bool ok = c + r < p.I;
-        const float swg = ok ? p.sw[c + r] : 0.0f;
-        const float swu = ok ? p.sw[p.I + c + r] : 0.0f;
-        const float gate = bf16_to_f32(f32_to_bf16((float(acc[4 * g + r]) * sxm) * swg));
-        const float up = bf16_to_f32(f32_to_bf16((float((*acc_up)[4 * g + r]) * sxm) * swu));
+        const float gate = bf16_to_f32(f32_to_bf16((float(acc[4 * g + r]) * sxm) * swg[r]));
+        const float up = bf16_to_f32(f32_to_bf16((float((*acc_up)[4 * g + r]) * sxm) * swu[r]));
         const float ge = bf16_to_f32(f32_to_bf16(gelu_tanh_f32(gate)));
         o[r] = ge * up;
       }
@@ -147,25 +177,33 @@ __device__ __forceinline__ void tile_coords(int t, int ntm, int ntn, int gm, int
   tn = r / gsz;
 }
 
-template <int BM, int BN, int WGM, int WGN, int NS, int EPI, bool A_PACKED, bool SPLIT, int MINB>
+template <int BM, int BN, int WGM, int WGN, int KS, int NS, int EPI, bool A_PACKED, bool SPLIT, int MINB>
 __global__ __launch_bounds__(WGM * WGN * 64, MINB) void gemm_kernel(GemmParams p) {
   constexpr int NW = WGM * WGN;
   constexpr int MT = BM / 32;         // A row-tiles per block
   constexpr int NTB = BN / 32;        // W column-tiles per block
-  constexpr int F = 2 * (MT + NTB);   // fragments per k-tile of 64 (one ring slot)
-  static_assert((2 * MT) % NW == 0 && (2 * NTB) % NW == 0, "each wave moves whole A and W fragments");
-  constexpr int FA = 2 * MT / NW, FB = 2 * NTB / NW;  // fragments per wave per k-tile
+  constexpr int F = KS * (MT + NTB);  // fragments per k-tile (one ring slot)
+  static_assert((KS * MT) % NW == 0 && (KS * NTB) % NW == 0, "each wave moves whole A and W fragments");
+  constexpr int FA = KS * MT / NW, FB = KS * NTB / NW;  // fragments per wave per k-tile
+  constexpr int FW = FA + FB;
   constexpr int WTM = MT / WGM;       // 32-row tiles per wave
   constexpr int WTN = NTB / WGN;      // 32-column tiles per wave
   static_assert(WTM * WGM == MT && WTN * WGN == NTB, "wave grid must divide the block tile");
   static_assert(EPI != EPI_GELU || (WTN % 2 == 0), "GELU pairs need an even tile count per wave");
-  static_assert(NS >= 3, "the ring needs three slots: one read, one landing, one in flight");
+  static_assert(KS % 2 == 0, "k-steps alternate between two register sets");
+  static_assert(NS >= 2, "the ring needs one slot being read and one landing");
+  static_assert(FW * (NS - 1) < 64, "outstanding loads must fit the 6-bit vmcnt");
   constexpr int NQ = WTM * WTN;                   // MFMAs per k-step
   constexpr int EARLY = NQ >= 8 ? NQ / 4 : 1;     // MFMAs issued before the next fragment reads
 
   // Slot layout: A fragments (s, mt) at (s*MT + mt) KiB, then W fragments (s, nt) at
-  // (2*MT + s*NTB + nt) KiB, s = 0, 1 the two 32-wide k-steps of the k-tile.
+  // (KS*MT + s*NTB + nt) KiB, s = 0 .. KS-1 the 32-wide k-steps of the k-tile.
   __shared__ __attribute__((aligned(1024))) char lds[NS][F * 1024];
+  // The tile's per-row scales sx (first BM) and per-packed-column scales sw (next BN), parked in
+  // LDS so the epilogue never waits on memory for them.
+  constexpr int NSCALE = EPI == EPI_I32 ? 4 : BM + BN;
+  constexpr int SCALE_PER_THREAD = (NSCALE + NW * 64 - 1) / (NW * 64);
+  __shared__ __attribute__((aligned(16))) float s_scale[NSCALE];
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -182,11 +220,37 @@ __global__ __launch_bounds__(WGM * WGN * 64, MINB) void gemm_kernel(GemmParams p
   tile_coords(tile, ntm, ntn, p.gm, tm, tn);
   const int m0 = tm * BM;
   const int t0 = tn * NTB;
+  const int KTT = (p.KF + KS - 1) / KS;  // k-tiles over the whole K
   const int k_lo = split * p.kt_per_split;
-  const int k_hi = min(p.KF >> 1, k_lo + p.kt_per_split);
+  const int k_hi = min(KTT, k_lo + p.kt_per_split);
+  // k-steps (of 32) in this block's last k-tile: K is padded to 64, not to 32 * KS.
+  const int last_steps = min(p.KF, k_hi * KS) - (k_hi - 1) * KS;
 
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a, p.a_bytes);
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.wp, p.w_bytes);
+
+  // Scales are fetched before the operand DMA starts and written to LDS once the prologue's
+  // loads have landed, so their latency hides under the first k-tiles.
+  float scale_v[SCALE_PER_THREAD];
+#pragma unroll
+  for (int u = 0; u < SCALE_PER_THREAD; ++u) {
+    scale_v[u] = 0.0f;
+    if constexpr (EPI != EPI_I32) {
+      const int i = int(threadIdx.x) + u * NW * 64;
+      if (i < BM) {
+        if (m0 + i < p.M) scale_v[u] = p.sx[m0 + i];
+      } else if (i < BM + BN) {
+        const int pc = i - BM, tt = t0 + pc / 32;
+        if constexpr (EPI == EPI_GELU) {
+          const int c = (tt >> 1) * 32 + pc % 32;  // gate / up channel of interleaved tile tt
+          if (c < p.I) scale_v[u] = p.sw[(tt & 1 ? p.I : 0) + c];
+        } else {
+          const int n = tt * 32 + pc % 32;
+          if (n < p.N) scale_v[u] = p.sw[n];
+        }
+      }
+    }
+  }
 
   // This lane's byte offsets for k-tile 0 of each fragment it moves; fragment f = (s, mt) of
   // A is rows m0 + 32*mt + l%32, k 32*s + 16*(l/32) (row-major A: at row*lda + k; packed A: in
@@ -207,21 +271,24 @@ __global__ __launch_bounds__(WGM * WGN * 64, MINB) void gemm_kernel(GemmParams p
     const int s = f / NTB, nt = f % NTB;
     offb[i] = (uint32_t(t0 + nt) * uint32_t(p.KF) + uint32_t(s)) * 1024u + uint32_t(lane) * 16u;
   }
-  constexpr uint32_t A_STEP = A_PACKED ? 2048u : 64u;  // bytes per k-tile
+  constexpr uint32_t A_STEP = A_PACKED ? KS * 1024u : KS * 32u;  // bytes per k-tile
+  constexpr uint32_t W_STEP = KS * 1024u;
 
+  // Fragments past K (a partial last k-tile) are loaded but never multiplied; loads past the
+  // end of A or W read zero.
   auto issue = [&](int kt) {
     char* slot = lds[kt % NS];
 #pragma unroll
     for (int i = 0; i < FA; ++i) dma16(ra, slot + (i * NW + wave) * 1024, offa[i] + uint32_t(kt) * A_STEP);
 #pragma unroll
-    for (int i = 0; i < FB; ++i) dma16(rw, slot + (2 * MT + i * NW + wave) * 1024, offb[i] + uint32_t(kt) * 2048u);
+    for (int i = 0; i < FB; ++i) dma16(rw, slot + (KS * MT + i * NW + wave) * 1024, offb[i] + uint32_t(kt) * W_STEP);
   };
   // This wave's operand fragments of k-step s of k-tile kt.
   auto read = [&](int kt, int s, v4i (&a)[WTM], v4i (&b)[WTN]) {
     const char* slot = lds[kt % NS];
 #pragma unroll
     for (int j = 0; j < WTN; ++j)
-      b[j] = *reinterpret_cast<const v4i*>(slot + (2 * MT + s * NTB + wn * WTN + j) * 1024 + lane * 16);
+      b[j] = *reinterpret_cast<const v4i*>(slot + (KS * MT + s * NTB + wn * WTN + j) * 1024 + lane * 16);
 #pragma unroll
     for (int i = 0; i < WTM; ++i)
       a[i] = *reinterpret_cast<const v4i*>(slot + (s * MT + wm * WTM + i) * 1024 + lane * 16);
@@ -241,47 +308,61 @@ __global__ __launch_bounds__(WGM * WGN * 64, MINB) void gemm_kernel(GemmParams p
       acc[q / WTN][q % WTN] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b[q % WTN], a[q / WTN], acc[q / WTN][q % WTN], 0, 0, 0);
   };
 
-  // Pipeline.  DMA runs NS-1 k-tiles ahead of the multiply.  Fragments are read from LDS one
-  // k-step ahead of their MFMAs, and the reads that refill a register set are issued only
-  // after EARLY MFMAs of the other set, so they never wait on MFMAs still reading the set
-  // they overwrite; sched_barrier keeps the compiler from reordering the phases.  The barrier
-  // that publishes the next k-tile sits in the middle of the current one.
-  const int KT = k_hi - k_lo;  // k-tiles of 64 this block multiplies
-  auto issue_local = [&](int t) { issue(k_lo + t); };
-  auto read_local = [&](int t, int s, v4i (&a)[WTM], v4i (&b)[WTN]) { read(k_lo + t, s, a, b); };
+  // Pipeline.  All NS slots are filled up front; k-tile kt+NS is issued into k-tile kt's slot
+  // as soon as every wave has finished reading it, so NS-1 k-tiles are in flight while one is
+  // multiplied.  Fragments are read from LDS one k-step ahead of their MFMAs, and the reads
+  // that refill a register set are issued only after EARLY MFMAs of the other set, so they never
+  // wait on MFMAs still reading the set they overwrite; sched_barrier keeps the compiler from
+  // reordering the phases.  One barrier per k-tile publishes the next k-tile and frees the
+  // current slot.
+  const int KT = k_hi - k_lo;  // k-tiles this block multiplies
 #pragma unroll
-  for (int s = 0; s < NS - 1; ++s)
-    if (s < KT) issue_local(s);
-  if (NS - 2 < KT)
-    wait_vmcnt<(FA + FB) * (NS - 2)>();
+  for (int s = 0; s < NS; ++s)
+    if (s < KT) issue(k_lo + s);
+  if (NS <= KT)
+    wait_vmcnt<FW * (NS - 1)>();
   else
     wait_vmcnt<0>();
   __builtin_amdgcn_s_barrier();
+  if constexpr (EPI != EPI_I32) {
+#pragma unroll
+    for (int u = 0; u < SCALE_PER_THREAD; ++u) {
+      const int i = int(threadIdx.x) + u * NW * 64;
+      if (i < NSCALE) s_scale[i] = scale_v[u];
+    }
+  }
 
   v4i a0[WTM], b0[WTN], a1[WTM], b1[WTN];
-  if (KT > 0) read_local(0, 0, a0, b0);
+  if (KT > 0) read(k_lo, 0, a0, b0);
   for (int kt = 0; kt < KT; ++kt) {
-    mma(a0, b0, 0, EARLY);
-    __builtin_amdgcn_sched_barrier(0);
-    read_local(kt, 1, a1, b1);
-    __builtin_amdgcn_sched_barrier(0);
-    mma(a0, b0, EARLY, NQ);
-    mma(a1, b1, 0, EARLY);
-    __builtin_amdgcn_sched_barrier(0);
-    if (kt + 1 < KT) {
-      // k-tile kt+1 has landed once at most the NS-3 k-tiles issued after it are in flight.
-      if (kt + NS - 2 < KT)
-        wait_vmcnt<(FA + FB) * (NS - 3)>();
-      else
-        wait_vmcnt<0>();
-      __builtin_amdgcn_s_barrier();
-      // Every wave has consumed k-tile kt-1 (its MFMAs waited on those reads), so its slot,
-      // (kt-1) % NS = (kt+NS-1) % NS, can be refilled.
-      if (kt + NS - 1 < KT) issue_local(kt + NS - 1);
-      read_local(kt + 1, 0, a0, b0);
+    const bool more = kt + 1 < KT;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      v4i(&ca)[WTM] = (s % 2 == 0) ? a0 : a1;
+      v4i(&cb)[WTN] = (s % 2 == 0) ? b0 : b1;
+      v4i(&na)[WTM] = (s % 2 == 0) ? a1 : a0;
+      v4i(&nb)[WTN] = (s % 2 == 0) ? b1 : b0;
+      const bool live = more || s < last_steps;  // k-step inside K
+      if (live) mma(ca, cb, 0, EARLY);
+      __builtin_amdgcn_sched_barrier(0);
+      if (s + 1 < KS) {
+        read(k_lo + kt, s + 1, na, nb);
+      } else if (more) {
+        // Every read of this k-tile has completed (lgkmcnt 0) and, after the barrier, on every
+        // wave: its slot takes k-tile kt+NS.  k-tile kt+1 has landed once at most the NS-2
+        // k-tiles issued after it are in flight.
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+        if (kt + NS - 1 < KT)
+          wait_vmcnt<FW * (NS - 2)>();
+        else
+          wait_vmcnt<0>();
+        __builtin_amdgcn_s_barrier();
+        if (kt + NS < KT) issue(k_lo + kt + NS);
+        read(k_lo + kt + 1, 0, na, nb);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (live) mma(ca, cb, EARLY, NQ);
     }
-    __builtin_amdgcn_sched_barrier(0);
-    mma(a1, b1, EARLY, NQ);
   }
 
   // ---- split-K: park partial sums; the last block of the tile adds them up -------------------
@@ -333,40 +414,64 @@ __global__ __launch_bounds__(WGM * WGN * 64, MINB) void gemm_kernel(GemmParams p
   }
 
   // ---- epilogue ---------------------------------------------------------------------------
+  if constexpr (EPI != EPI_I32) __syncthreads();  // s_scale is visible to every wave
   const int lrow = lane & 31;
   const int lcol = 4 * (lane >> 5);
 #pragma unroll
   for (int i = 0; i < WTM; ++i) {
-    const int m = m0 + (wm * WTM + i) * 32 + lrow;
+    const int ml = (wm * WTM + i) * 32 + lrow;  // row within the tile
+    const int m = m0 + ml;
     if (m >= p.M) continue;
+    const float sxm = EPI == EPI_I32 ? 0.0f : s_scale[ml];
+    const float* swt = s_scale + (EPI == EPI_I32 ? 0 : BM) + wn * WTN * 32 + lcol;
     if constexpr (EPI == EPI_GELU) {
 #pragma unroll
-      for (int j = 0; j < WTN; j += 2) store_tile<EPI>(p, acc[i][j], &acc[i][j + 1], m, t0 + wn * WTN + j, lcol);
+      for (int j = 0; j < WTN; j += 2)
+        store_tile<EPI>(p, acc[i][j], &acc[i][j + 1], m, t0 + wn * WTN + j, lcol, sxm, swt + j * 32);
     } else {
 #pragma unroll
-      for (int j = 0; j < WTN; ++j) store_tile<EPI>(p, acc[i][j], nullptr, m, t0 + wn * WTN + j, lcol);
+      for (int j = 0; j < WTN; ++j)
+        store_tile<EPI>(p, acc[i][j], nullptr, m, t0 + wn * WTN + j, lcol, sxm, swt + j * 32);
     }
   }
 }
 
 // ---- host-side launch ----------------------------------------------------------------------
 
-static const int kBM[8] = {256, 256, 128, 256, 128, 128, 256, 128};
+// Tile configurations: block tile BM x BN, waves (WGM x WGN, one wave per 32-multiple sub-tile),
+// k-tile depth 32*KS, LDS ring of NS k-tiles.
+struct TileCfg {
+  int bm, bn, waves, ks, ns;
+};
+static constexpr TileCfg kCfg[] = {
+    {256, 256, 8, 2, 4},  // 0: 32 KiB slots, 128 KiB ring
+    {256, 256, 8, 4, 2},  // 1: 64 KiB slots, 128 KiB ring
+    {128, 256, 8, 4, 3},  // 2: 48 KiB slots, 144 KiB ring
+    {256, 128, 8, 4, 3},  // 3: 48 KiB slots, 144 KiB ring
+    {128, 256, 8, 2, 4},  // 4: 24 KiB slots, 96 KiB ring
+    {256, 128, 8, 2, 4},  // 5: 24 KiB slots, 96 KiB ring
+    {128, 128, 4, 4, 4},  // 6: 32 KiB slots, 128 KiB ring
+    {128, 128, 4, 4, 2},  // 7: 32 KiB slots, 64 KiB ring (two blocks per CU)
+    {128, 128, 4, 2, 4},  // 8: 16 KiB slots, 64 KiB ring (two blocks per CU)
+    {128, 256, 4, 2, 3},  // 9: 24 KiB slots, 72 KiB ring (two blocks per CU)
+};
+static constexpr int kNumCfg = int(sizeof(kCfg) / sizeof(kCfg[0]));
 static constexpr int64_t kCounterBytes = 4096;
-static const int kBN[8] = {256, 256, 256, 128, 128, 128, 128, 256};
 
-// Split-K: blocks per output tile so the grid covers the 256 CUs when there are few tiles.
-// Every split keeps at least 4 k-tiles of 64; `kps` is the number of k-tiles per split.
-// Measured on MI355X the partial-sum exchange costs more than the extra CUs gain on the E2B
-// shapes, so automatic selection keeps K whole (kAutoSplit = false); the machinery stays
-// available behind the workspace argument.
-static constexpr bool kAutoSplit = false;
-// req: 0 = automatic, n >= 1 = at most n splits.
-static int pick_splits(int tiles, int KT, int req, int& kps) {
+int gemm_config_count() { return kNumCfg; }
+
+// Split-K: blocks per output tile along K.  Explicit requests (req = n >= 1) split into at most
+// n parts, only when there are few output tiles.  Automatic selection (req = 0) splits the
+// few-tile, long-K shapes (the down projection at one 512-row micro-batch: 48 tiles of
+// 128x128 over K = 6144), where measured on MI355X two halves of K beat one block per tile;
+// shorter K loses more to the partial-sum exchange than it gains.  Every split keeps at least
+// 256 of K; `kps` is the number of k-tiles per split.
+static int pick_splits(int tiles, int KT, int ks, int req, int& kps) {
   int s = 1;
-  if (tiles < 200 && (req > 1 || (req == 0 && kAutoSplit))) s = 256 / tiles;  // and so tiles < kCounterBytes / 4
-  if (req > 0) s = min(s, req);
-  s = max(1, min(s, min(8, KT / 4)));
+  if (req > 1 && tiles < 200) s = min(req, 256 / tiles);  // and so tiles < kCounterBytes / 4
+  if (req == 0 && tiles <= 64 && KT * ks * 32 >= 4096) s = 2;
+  const int min_kt = max(1, 8 / ks);
+  s = max(1, min(s, min(8, KT / min_kt)));
   kps = (KT + s - 1) / s;
   return (KT + kps - 1) / kps;
 }
@@ -374,43 +479,41 @@ static int pick_splits(int tiles, int KT, int req, int& kps) {
 // Split-K workspace: kCounterBytes of arrival counters (one int per output tile; zero before
 // and after every call) followed by the partial sums (scratch).
 int64_t gemm_workspace_bytes(int M, int NP, int KF, int cfg, int split_k) {
-  if (cfg <= 1) return 0;  // the 256x256 tiles run without split-K
-  const int ntm = (M + kBM[cfg] - 1) / kBM[cfg], ntn = (NP + kBN[cfg] - 1) / kBN[cfg];
+  const TileCfg& c = kCfg[cfg];
+  const int ntm = (M + c.bm - 1) / c.bm, ntn = (NP + c.bn - 1) / c.bn;
   int kps;
-  const int s = pick_splits(ntm * ntn, KF / 2, split_k, kps);
+  const int s = pick_splits(ntm * ntn, (KF + c.ks - 1) / c.ks, c.ks, split_k, kps);
   if (s <= 1) return 0;
-  return kCounterBytes + int64_t(ntm) * ntn * s * kBM[cfg] * kBN[cfg] * 4;
+  return kCounterBytes + int64_t(ntm) * ntn * s * c.bm * c.bn * 4;
 }
 
 // Blocks per CU the tile is built for: two when two rings fit in the 160 KiB of LDS.
-template <int BM, int BN, int NS>
-constexpr int blocks_per_cu() { return 2 * NS * 2 * (BM / 32 + BN / 32) * 1024 <= 160 * 1024 ? 2 : 1; }
+template <int BM, int BN, int KS, int NS>
+constexpr int blocks_per_cu() { return 2 * NS * KS * (BM / 32 + BN / 32) * 1024 <= 160 * 1024 ? 2 : 1; }
 
-template <int BM, int BN, int WGM, int WGN, int NS, bool AP, bool SPLIT>
+template <int BM, int BN, int WGM, int WGN, int KS, int NS, bool AP, bool SPLIT>
 static void launch_kernel(const GemmParams& p, int epi, dim3 grid, hipStream_t stream) {
   const int threads = WGM * WGN * 64;
-  constexpr int B = blocks_per_cu<BM, BN, NS>();
+  constexpr int B = blocks_per_cu<BM, BN, KS, NS>();
   switch (epi) {
-    case EPI_I32: gemm_kernel<BM, BN, WGM, WGN, NS, EPI_I32, AP, SPLIT, B><<<grid, threads, 0, stream>>>(p); break;
-    case EPI_BF16: gemm_kernel<BM, BN, WGM, WGN, NS, EPI_BF16, AP, SPLIT, B><<<grid, threads, 0, stream>>>(p); break;
-    case EPI_GELU: gemm_kernel<BM, BN, WGM, WGN, NS, EPI_GELU, AP, SPLIT, B><<<grid, threads, 0, stream>>>(p); break;
-    case EPI_RESID: gemm_kernel<BM, BN, WGM, WGN, NS, EPI_RESID, AP, SPLIT, B><<<grid, threads, 0, stream>>>(p); break;
+    case EPI_I32: gemm_kernel<BM, BN, WGM, WGN, KS, NS, EPI_I32, AP, SPLIT, B><<<grid, threads, 0, stream>>>(p); break;
+    case EPI_BF16: gemm_kernel<BM, BN, WGM, WGN, KS, NS, EPI_BF16, AP, SPLIT, B><<<grid, threads, 0, stream>>>(p); break;
+    case EPI_GELU: gemm_kernel<BM, BN, WGM, WGN, KS, NS, EPI_GELU, AP, SPLIT, B><<<grid, threads, 0, stream>>>(p); break;
+    case EPI_RESID: gemm_kernel<BM, BN, WGM, WGN, KS, NS, EPI_RESID, AP, SPLIT, B><<<grid, threads, 0, stream>>>(p); break;
   }
 }
 
-// CAN_SPLIT: this tile shape has a split-K instantiation (the 256x256 tiles, used only when
-// there are enough tiles to fill the GPU, do not).
-template <int BM, int BN, int WGM, int WGN, int NS, bool AP, bool CAN_SPLIT>
+template <int BM, int BN, int WGM, int WGN, int KS, int NS, bool AP>
 static void launch_epi(GemmParams p, int epi, void* ws, int64_t ws_bytes, hipStream_t stream) {
   const int ntm = (p.M + BM - 1) / BM;
   const int ntn = (p.NT * 32 + BN - 1) / BN;
   p.gm = min(ntm, BM >= BN ? 4 : 8);
-  const int KT = p.KF / 2;
+  const int KT = (p.KF + KS - 1) / KS;
   p.splits = 1;
   p.kt_per_split = KT;
-  if (CAN_SPLIT && ws) {
+  if (ws) {
     int kps;
-    const int s = pick_splits(ntm * ntn, KT, p.split_req, kps);
+    const int s = pick_splits(ntm * ntn, KT, KS, p.split_req, kps);
     const int64_t need = kCounterBytes + int64_t(ntm) * ntn * s * BM * BN * 4;
     if (s > 1 && ws_bytes >= need && ntm * ntn * 4 <= kCounterBytes) {
       p.splits = s;
@@ -420,55 +523,47 @@ static void launch_epi(GemmParams p, int epi, void* ws, int64_t ws_bytes, hipStr
     }
   }
   dim3 grid(unsigned(ntm * ntn * p.splits));
-  if (CAN_SPLIT && p.splits > 1)
-    launch_kernel<BM, BN, WGM, WGN, NS, AP, CAN_SPLIT>(p, epi, grid, stream);
+  if (p.splits > 1)
+    launch_kernel<BM, BN, WGM, WGN, KS, NS, AP, true>(p, epi, grid, stream);
   else
-    launch_kernel<BM, BN, WGM, WGN, NS, AP, false>(p, epi, grid, stream);
+    launch_kernel<BM, BN, WGM, WGN, KS, NS, AP, false>(p, epi, grid, stream);
 }
 
-template <int BM, int BN, int WGM, int WGN, int NS, bool CAN_SPLIT>
+template <int CFG>
 static void launch(const GemmParams& p, int epi, bool a_packed, void* ws, int64_t ws_bytes, hipStream_t stream) {
+  constexpr TileCfg c = kCfg[CFG];
+  // waves laid out along the longer side of the block tile: 8 waves as 4x2 (BM >= BN) or 2x4
+  constexpr int WGM = c.waves == 4 ? 2 : (c.bm >= c.bn ? 4 : 2);
+  constexpr int WGN = c.waves / WGM;
   if (a_packed)
-    launch_epi<BM, BN, WGM, WGN, NS, true, CAN_SPLIT>(p, epi, ws, ws_bytes, stream);
+    launch_epi<c.bm, c.bn, WGM, WGN, c.ks, c.ns, true>(p, epi, ws, ws_bytes, stream);
   else
-    launch_epi<BM, BN, WGM, WGN, NS, false, CAN_SPLIT>(p, epi, ws, ws_bytes, stream);
+    launch_epi<c.bm, c.bn, WGM, WGN, c.ks, c.ns, false>(p, epi, ws, ws_bytes, stream);
 }
 
-// Tile configurations (block tile, 4 waves in 2 x 2, LDS ring depth):
-//   0: 256x256, waves of 128x128, 4 slots (128 KiB)
-//   1: 256x256, waves of 128x128, 5 slots (160 KiB)
-//   2: 128x256, waves of 64x128,  6 slots (144 KiB)
-//   3: 256x128, waves of 128x64,  6 slots (144 KiB)
-//   4: 128x128, waves of 64x64,   8 slots (128 KiB)
-//   5: 128x128, waves of 64x64,   4 slots (64 KiB, two blocks per CU)
-//   6: 256x128, waves of 128x64,  3 slots (72 KiB, two blocks per CU)
-//   7: 128x256, waves of 64x128,  3 slots (72 KiB, two blocks per CU)
-int gemm_config_count() { return 8; }
-
-// Tile choice, from timing every configuration on the E2B prefill shapes (M = 512, 3658,
-// 16384): 256x256 when there are enough of them (>= 4 waves of blocks), else the two-blocks-
-// per-CU tiles, 256 wide along the longer of M and N when that still gives >= 384 tiles.
+// Tile choice, from timing every configuration with the bf16 epilogues on the E2B prefill
+// shapes (M = 512, 3658, 16384): the 128x128 tile two blocks per CU (7) everywhere, except the
+// wide gate/up projection at long M, where the 128x256 tile two blocks per CU (9) wins.
 int gemm_pick_config(int M, int NP, int K) {
   (void)K;
-  auto tiles = [&](int c) { return long((M + kBM[c] - 1) / kBM[c]) * ((NP + kBN[c] - 1) / kBN[c]); };
-  if (tiles(0) >= 1024) return 0;
-  const int wide = M >= NP ? 6 : 7;
-  if (tiles(wide) >= 384) return wide;
-  return 5;
+  if (M >= 2048 && NP >= 8192) return 9;
+  return 7;
 }
 
 int gemm_launch(const GemmParams& p, int epi, int cfg, bool a_packed, void* ws, int64_t ws_bytes,
                 hipStream_t stream) {
   if (cfg < 0) cfg = gemm_pick_config(p.M, p.NT * 32, p.KF * 32);
   switch (cfg) {
-    case 0: launch<256, 256, 2, 2, 4, false>(p, epi, a_packed, ws, ws_bytes, stream); break;
-    case 1: launch<256, 256, 2, 2, 5, false>(p, epi, a_packed, ws, ws_bytes, stream); break;
-    case 2: launch<128, 256, 2, 2, 6, true>(p, epi, a_packed, ws, ws_bytes, stream); break;
-    case 3: launch<256, 128, 2, 2, 6, true>(p, epi, a_packed, ws, ws_bytes, stream); break;
-    case 4: launch<128, 128, 2, 2, 8, true>(p, epi, a_packed, ws, ws_bytes, stream); break;
-    case 5: launch<128, 128, 2, 2, 4, true>(p, epi, a_packed, ws, ws_bytes, stream); break;
-    case 6: launch<256, 128, 2, 2, 3, true>(p, epi, a_packed, ws, ws_bytes, stream); break;
-    case 7: launch<128, 256, 2, 2, 3, true>(p, epi, a_packed, ws, ws_bytes, stream); break;
+    case 0: launch<0>(p, epi, a_packed, ws, ws_bytes, stream); break;
+    case 1: launch<1>(p, epi, a_packed, ws, ws_bytes, stream); break;
+    case 2: launch<2>(p, epi, a_packed, ws, ws_bytes, stream); break;
+    case 3: launch<3>(p, epi, a_packed, ws, ws_bytes, stream); break;
+    case 4: launch<4>(p, epi, a_packed, ws, ws_bytes, stream); break;
+    case 5: launch<5>(p, epi, a_packed, ws, ws_bytes, stream); break;
+    case 6: launch<6>(p, epi, a_packed, ws, ws_bytes, stream); break;
+    case 7: launch<7>(p, epi, a_packed, ws, ws_bytes, stream); break;
+    case 8: launch<8>(p, epi, a_packed, ws, ws_bytes, stream); break;
+    case 9: launch<9>(p, epi, a_packed, ws, ws_bytes, stream); break;
     default: return fail(W8A8_EINVAL, "gemm: unknown tile config %d", cfg);
   }
   return check_launch("gemm");

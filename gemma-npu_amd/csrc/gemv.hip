@@ -4,12 +4,12 @@
 // s bf16 or fp32 [N]: the contract of torch._weight_int8pack_mm as the reference calls it
 // (gemma_npu.py:155-156, decode linears gemma_npu.py:120-121, Int8Head gemma_npu.py:159-172).
 //
-// The weight is streamed once from HBM with 16-byte loads; each byte is widened to bf16
-// (exact: |w| <= 128) and multiplied on the bf16 MFMA (v_mfma_f32_16x16x32_bf16, fp32
-// accumulate), with the M <= 16 activation rows as the MFMA's other operand.  A wave covers
-// one 16-row n-tile; SPLIT waves of a workgroup share one n-tile's K range (k-blocks of 64
-// dealt round-robin) and their partial sums are added in LDS in fixed wave order, so the
-// result is deterministic.
+// The weight is streamed once from HBM with 16-byte loads; each byte is widened to bf16 (exact:
+// |w| <= 128) and multiplied on the bf16 MFMA (v_mfma_f32_16x16x32_bf16, fp32 accumulate), with
+// the M <= 16 activation rows as the MFMA's other operand.  A wave covers TPW 16-row n-tiles, so each activation fragment it loads serves
+// TPW weight fragments; for shapes with few n-tiles, `split` waves of a workgroup share one
+// n-tile's K range (k-blocks of 64 dealt round-robin) and their partial sums are added in LDS in
+// fixed wave order, so the result is deterministic.
 #include "w8a8_common.h"
 
 namespace w8a8 {
@@ -21,7 +21,7 @@ struct GemvParams {
   uint16_t* y; int64_t ldy;        // bf16 [M, N]
   uint32_t x_bytes, w_bytes;
   int M, N, K, KB;                 // KB = ceil(K / 64)
-  int split;                       // waves per n-tile
+  int split;                       // waves per group of n-tiles, each taking every split-th k-block
 };
 
 // Widen 8 signed bytes (two dwords) to 8 bf16 values, exactly.
@@ -40,85 +40,104 @@ __device__ __forceinline__ v8bf widen8(uint32_t lo, uint32_t hi) {
   return __builtin_bit_cast(v8bf, r);
 }
 
-template <int U>
-__global__ __launch_bounds__(1024) void gemv_kernel(GemvParams p) {
-  __shared__ v4f red[16][64];
+// A wave multiplies TPW n-tiles of 16 weight rows against the M <= 16 activation rows: per k-block
+// of 64 it loads the activation fragment once and TPW weight fragments, and issues 2*TPW MFMAs.
+// With split > 1 the waves of a group take interleaved k-blocks and their partial sums are added
+// in LDS in wave order (deterministic).
+template <int TPW, int U>
+__global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
+  __shared__ v4f red[4][TPW][64];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int tile_in_block = wave / p.split;
+  const int group_in_block = wave / p.split;
   const int ks = wave % p.split;
-  const int tiles_per_block = (blockDim.x >> 6) / p.split;
-  const int tile = blockIdx.x * tiles_per_block + tile_in_block;
+  const int groups_per_block = 4 / p.split;
+  const int group = blockIdx.x * groups_per_block + group_in_block;
+  const int tile0 = group * TPW;
   const int ntiles = (p.N + 15) >> 4;
-  const bool active = tile < ntiles;
+  const bool active = tile0 < ntiles;
 
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.w, p.w_bytes);
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.x, p.x_bytes);
-  const int n = tile * 16 + (lane & 15);     // weight row this lane streams
-  const int kc = (lane >> 4) * 16;           // its 16-byte chunk inside each 64-wide k-block
+  const int kc = (lane >> 4) * 16;           // this lane's 16-byte chunk inside each 64-wide k-block
   const int mrow = lane & 15;                // activation row this lane supplies
-  // Rows past N / M start at or past the buffer ends and read as zero.
-  const uint32_t wbase = uint32_t(n) * uint32_t(p.ldw) + uint32_t(kc);
+  // Weight rows past N and activation rows past M start at or past the buffer ends and read 0.
+  uint32_t wbase[TPW];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) wbase[t] = uint32_t((tile0 + t) * 16 + (lane & 15)) * uint32_t(p.ldw) + uint32_t(kc);
   const uint32_t xbase = (uint32_t(mrow) * uint32_t(p.ldx) + uint32_t(kc)) * 2u;
 
-  v4f acc = {0.f, 0.f, 0.f, 0.f};
+  v4f acc[TPW];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
   if (active) {
     const int stride = p.split * U;
     for (int kb0 = ks; kb0 < p.KB; kb0 += stride) {
-      v4i wv[U], xa[U], xb[U];
+      v4i wv[U][TPW], xa[U], xb[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int kb = kb0 + u * p.split;
-        const bool ok = kb < p.KB && kb * 64 + kc < p.K;
-        if (ok) {
-          wv[u] = buf_load16(rw, wbase + uint32_t(kb) * 64u);
+        if (kb < p.KB && kb * 64 + kc < p.K) {
           xa[u] = buf_load16(rx, xbase + uint32_t(kb) * 128u);
           xb[u] = buf_load16(rx, xbase + uint32_t(kb) * 128u + 16u);
+#pragma unroll
+          for (int t = 0; t < TPW; ++t) wv[u][t] = buf_load16(rw, wbase[t] + uint32_t(kb) * 64u);
         } else {
-          wv[u] = v4i{0, 0, 0, 0};
           xa[u] = v4i{0, 0, 0, 0};
           xb[u] = v4i{0, 0, 0, 0};
+#pragma unroll
+          for (int t = 0; t < TPW; ++t) wv[u][t] = v4i{0, 0, 0, 0};
         }
       }
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const v8bf w0 = widen8(uint32_t(wv[u][0]), uint32_t(wv[u][1]));
-        const v8bf w1 = widen8(uint32_t(wv[u][2]), uint32_t(wv[u][3]));
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0, __builtin_bit_cast(v8bf, xa[u]), acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1, __builtin_bit_cast(v8bf, xb[u]), acc, 0, 0, 0);
-      }
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int t = 0; t < TPW; ++t) {
+          const v8bf w0 = widen8(uint32_t(wv[u][t][0]), uint32_t(wv[u][t][1]));
+          const v8bf w1 = widen8(uint32_t(wv[u][t][2]), uint32_t(wv[u][t][3]));
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0, __builtin_bit_cast(v8bf, xa[u]), acc[t], 0, 0, 0);
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1, __builtin_bit_cast(v8bf, xb[u]), acc[t], 0, 0, 0);
+        }
     }
   }
 
   if (p.split > 1) {
-    red[wave][lane] = acc;
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) red[wave][t][lane] = acc[t];
     __syncthreads();
     if (ks != 0) return;
-    acc = red[wave][lane];
-    for (int q = 1; q < p.split; ++q) acc += red[wave + q][lane];
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      acc[t] = red[wave][t][lane];
+      for (int q = 1; q < p.split; ++q) acc[t] += red[wave + q][t][lane];
+    }
   }
   if (!active) return;
 
-  // acc lane l: row m = l % 16, columns n0 .. n0+3 with n0 = tile*16 + 4*(l/16).
+  // acc[t] lane l: row m = l % 16, columns n0 .. n0+3 with n0 = (tile0 + t)*16 + 4*(l/16).
   const int m = lane & 15;
   if (m >= p.M) return;
-  const int n0 = tile * 16 + 4 * (lane >> 4);
-  float o[4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int nn = n0 + r;
-    float sc = 0.0f;
-    if (nn < p.N) sc = p.s_f32 ? reinterpret_cast<const float*>(p.s)[nn]
-                               : bf16_to_f32(reinterpret_cast<const uint16_t*>(p.s)[nn]);
-    o[r] = acc[r] * sc;
-  }
-  uint16_t* dst = p.y + int64_t(m) * p.ldy + n0;
-  if (n0 + 3 < p.N && ((reinterpret_cast<uintptr_t>(dst) & 7) == 0)) {
-    *reinterpret_cast<v2u*>(dst) = v2u{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
-  } else {
+  for (int t = 0; t < TPW; ++t) {
+    const int n0 = (tile0 + t) * 16 + 4 * (lane >> 4);
+    if (n0 >= p.N) continue;
+    float o[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      if (n0 + r < p.N) dst[r] = f32_to_bf16(o[r]);
+    for (int r = 0; r < 4; ++r) {
+      const int nn = n0 + r;
+      float sc = 0.0f;
+      if (nn < p.N) sc = p.s_f32 ? reinterpret_cast<const float*>(p.s)[nn]
+                                 : bf16_to_f32(reinterpret_cast<const uint16_t*>(p.s)[nn]);
+      o[r] = acc[t][r] * sc;
+    }
+    uint16_t* dst = p.y + int64_t(m) * p.ldy + n0;
+    if (n0 + 3 < p.N && ((reinterpret_cast<uintptr_t>(dst) & 7) == 0)) {
+      *reinterpret_cast<v2u*>(dst) = v2u{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (n0 + r < p.N) dst[r] = f32_to_bf16(o[r]);
+    }
   }
 }
 
@@ -144,13 +163,25 @@ extern "C" int w8a8_gemv_bf16(const uint16_t* x, int64_t ldx, int64_t M, const i
   p.y = y; p.ldy = ldy; p.x_bytes = uint32_t(xb); p.w_bytes = uint32_t(wb);
   p.M = int(M); p.N = int(N); p.K = int(K); p.KB = int((K + 63) / 64);
   const int64_t ntiles = (N + 15) / 16;
-  // Aim for ~16 waves per CU over 256 CUs; split K only when there are too few n-tiles.
-  int split = 1;
-  while (split < 16 && ntiles * split < 4096 && split * 2 <= p.KB) split *= 2;
-  p.split = split;
-  const int tpb = split >= 4 ? 1 : 4 / split;
-  const int threads = 64 * split * tpb;
-  dim3 grid(unsigned((ntiles + tpb - 1) / tpb));
-  gemv_kernel<4><<<grid, threads, 0, stream>>>(p);
+  if (ntiles >= 4096) {
+    // Many n-tiles (the LM head): each activation fragment serves two (M <= 8) or four
+    // weight tiles per wave.
+    p.split = 1;
+    if (M <= 8) {
+      const int64_t groups = (ntiles + 1) / 2;
+      gemv_kernel<2, 4><<<unsigned((groups + 3) / 4), 256, 0, stream>>>(p);
+    } else {
+      const int64_t groups = (ntiles + 3) / 4;
+      gemv_kernel<4, 2><<<unsigned((groups + 3) / 4), 256, 0, stream>>>(p);
+    }
+  } else {
+    // Few n-tiles (per-layer decode shapes): one tile per wave and K split over up to four
+    // waves, aiming for ~16 waves per CU over 256 CUs.
+    int split = 1;
+    while (split < 4 && ntiles * split < 4096 && split * 2 <= p.KB) split *= 2;
+    p.split = split;
+    const int gpb = 4 / split;
+    gemv_kernel<1, 4><<<unsigned((ntiles + gpb - 1) / gpb), 256, 0, stream>>>(p);
+  }
   return check_launch("gemv_bf16");
 }

@@ -192,6 +192,88 @@ __global__ __launch_bounds__(256) void quant_rows_packed_kernel(const uint16_t* 
   }
 }
 
+// Single-pass quantisation of bf16 rows held in registers: one 256-thread block per row; thread
+// t holds chunks c = 0 .. CH-1 of 8 consecutive elements at k = 8 * (256c + t), all loaded in one
+// burst, so the row costs one memory round trip and its divisions are spread over four waves.
+// The absmax is a DPP wave reduction plus one LDS exchange between the waves.  The int8 bytes
+// leave as 8-byte stores, row-major or into the packed fragment layout (half of the 16-byte
+// piece holding k: fragment (row/32, k/32), lane slot row%32 + 32 * ((k/16) % 2), byte k % 16).
+// PACKED also zero-fills rows M .. Mp-1 and k K .. 32*KF-1.
+template <int CH, bool PACKED>
+__global__ __launch_bounds__(256) void quant_rows_blk_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M,
+                                                             int K, int KF, int8_t* __restrict__ q, int64_t ldq,
+                                                             float* __restrict__ scale) {
+  __shared__ float wave_amax[4];
+  const int t = threadIdx.x;
+  const int row = blockIdx.x;
+  const int KP = PACKED ? KF * 32 : K;
+  auto dst = [&](int k) -> int8_t* {
+    if constexpr (PACKED)
+      return q + packed_act_offset(row, k & ~15, KF) + (k & 15);
+    else
+      return q + int64_t(row) * ldq + k;
+  };
+  if (row >= M) {  // PACKED only: padding rows are zero
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int k = 8 * (256 * c + t);
+      if (k < KP) *reinterpret_cast<v2u*>(dst(k)) = v2u{0u, 0u};
+    }
+    return;
+  }
+  const uint16_t* xr = x + int64_t(row) * ldx;
+  v4u v[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int k = 8 * (256 * c + t);
+    v[c] = k < K ? *reinterpret_cast<const v4u*>(xr + k) : v4u{0u, 0u, 0u, 0u};
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      amax = fmaxf(amax, fmaxf(fabsf(__uint_as_float(v[c][i] << 16)), fabsf(__uint_as_float(v[c][i] & 0xffff0000u))));
+  amax = wave_max_dpp(amax);
+  if ((t & 63) == 0) wave_amax[t >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(wave_amax[0], wave_amax[1]), fmaxf(wave_amax[2], wave_amax[3]));
+  const float s = fmaxf(amax, 1e-8f) / 127.0f;
+  if (t == 0) scale[row] = s;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int k = 8 * (256 * c + t);
+    if (k >= KP) continue;
+    uint32_t w[2] = {0u, 0u};
+    if (k < K) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t lo = uint8_t(quant1(__uint_as_float(v[c][i] << 16), s));
+        const uint32_t hi = uint8_t(quant1(__uint_as_float(v[c][i] & 0xffff0000u), s));
+        w[i >> 1] |= (lo | (hi << 8)) << (16 * (i & 1));
+      }
+    }
+    *reinterpret_cast<v2u*>(dst(k)) = v2u{w[0], w[1]};
+  }
+}
+
+// Launch the block-per-row kernel for K <= 8 * 256 * 6 = 12288; false if K is beyond it.
+template <bool PACKED>
+static bool launch_quant_reg(const uint16_t* x, int64_t ldx, int M, int Mp, int K, int KF, int8_t* q, int64_t ldq,
+                             float* scale, hipStream_t stream) {
+  const int ch = (K + 2047) / 2048;
+  const dim3 grid{static_cast<unsigned>(Mp)};
+#define W8A8_QBLK(N) quant_rows_blk_kernel<N, PACKED><<<grid, 256, 0, stream>>>(x, ldx, M, K, KF, q, ldq, scale)
+  if (ch <= 1) W8A8_QBLK(1);
+  else if (ch <= 2) W8A8_QBLK(2);
+  else if (ch <= 3) W8A8_QBLK(3);
+  else if (ch <= 4) W8A8_QBLK(4);
+  else if (ch <= 6) W8A8_QBLK(6);
+  else return false;
+#undef W8A8_QBLK
+  return true;
+}
+
 // Row-major int8 A -> packed activations; one thread per 16-byte chunk of the output.
 __global__ __launch_bounds__(256) void pack_act_kernel(const int8_t* __restrict__ a, int64_t lda, int M, int K, int KF,
                                                        int64_t nchunks, int8_t* __restrict__ out) {
@@ -222,6 +304,8 @@ int w8a8_quant_rows_bf16(const uint16_t* x, int64_t ldx, int64_t M, int64_t K, i
   if (M > INT32_MAX / 4 || K > INT32_MAX) return fail(W8A8_ENOTSUP, "quant_rows: too large");
   const bool vec = (K % 8 == 0) && (ldx % 8 == 0) && (ldq % 8 == 0) && ((uintptr_t)x % 16 == 0) &&
                    ((uintptr_t)q % 8 == 0);
+  if (vec && launch_quant_reg<false>(x, ldx, int(M), int(M), int(K), 0, q, ldq, scale, stream))
+    return check_launch("quant_rows_bf16");
   dim3 grid((unsigned)((M + 3) / 4));
   if (vec)
     quant_rows_kernel<uint16_t, true><<<grid, 256, 0, stream>>>(x, ldx, (int)M, (int)K, q, ldq, scale);
@@ -312,6 +396,8 @@ int w8a8_quant_rows_packed_bf16(const uint16_t* x, int64_t ldx, int64_t M, int64
   const int KF = int(2 * ((K + 63) / 64));
   const int Mp = int((M + 31) / 32 * 32);
   const bool vec = (ldx % 8 == 0) && ((uintptr_t)x % 16 == 0);
+  if (vec && launch_quant_reg<true>(x, ldx, int(M), Mp, int(K), KF, packed, 0, scale, stream))
+    return check_launch("quant_rows_packed_bf16");
   dim3 grid(unsigned((Mp + 3) / 4));
   if (vec)
     quant_rows_packed_kernel<true><<<grid, 256, 0, stream>>>(x, ldx, int(M), Mp, int(K), KF, packed, scale);

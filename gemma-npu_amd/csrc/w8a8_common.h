@@ -12,17 +12,18 @@ typedef unsigned v2u __attribute__((ext_vector_type(2)));
 // ---- bf16 <-> fp32 --------------------------------------------------------------------------
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float(uint32_t(h) << 16); }
 
-// Round to nearest even; NaN stays a quiet NaN (torch's .to(torch.bfloat16)).
-__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return uint16_t(u >> 16);
-}
+// Round to nearest even; NaN stays NaN (torch's .to(torch.bfloat16)).  One v_cvt_pk_bf16_f32 on
+// gfx950; checked against the bit-level round-half-even form over all 2^32 fp32 inputs.
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return uint32_t(f32_to_bf16(lo)) | (uint32_t(f32_to_bf16(hi)) << 16);
+  const v2bf v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
 }
+
+// bf16(x) as fp32: the value x rounds to.
+__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
 // ---- raw buffer loads -----------------------------------------------------------------------
 // A raw buffer resource over [base, base + bytes).  Loads whose byte offset is at or past
@@ -42,6 +43,31 @@ __device__ __forceinline__ float wave_max(float v) {
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
   return v;
 }
+// Wave maximum of v broadcast to every lane, through DPP lane moves (no LDS round trips):
+// butterflies inside each row of 16 lanes, then row_bcast:15 / row_bcast:31 carry the row maxima
+// up to lane 63, which is read back as a scalar.
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  auto dpp = [](float x, int ctrl, int row_mask) {
+    const int xi = __builtin_bit_cast(int, x);
+    switch (ctrl) {
+      case 0xB1: return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(xi, xi, 0xB1, 0xF, 0xF, false));
+      case 0x4E: return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(xi, xi, 0x4E, 0xF, 0xF, false));
+      case 0x141: return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(xi, xi, 0x141, 0xF, 0xF, false));
+      case 0x140: return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(xi, xi, 0x140, 0xF, 0xF, false));
+      case 0x142: return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(xi, xi, 0x142, 0xA, 0xF, false));
+      default: return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(xi, xi, 0x143, 0xC, 0xF, false));
+    }
+    (void)row_mask;
+  };
+  v = fmaxf(v, dpp(v, 0xB1, 0xF));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp(v, 0x4E, 0xF));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp(v, 0x141, 0xF));  // row_half_mirror: 8 lanes
+  v = fmaxf(v, dpp(v, 0x140, 0xF));  // row_mirror: 16 lanes
+  v = fmaxf(v, dpp(v, 0x142, 0xA));  // row_bcast:15 into rows 1, 3
+  v = fmaxf(v, dpp(v, 0x143, 0xC));  // row_bcast:31 into rows 2, 3
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);

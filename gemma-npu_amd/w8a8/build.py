@@ -20,6 +20,8 @@ ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 CFLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",
+    # Evaluate a * b + c as the two roundings the reference performs, never as one fused op.
+    "-ffp-contract=off",
     # Keep hipcc from forming packed fp32 (v_pk_*_f32) instructions.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{CSRC}",

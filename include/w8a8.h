@@ -98,6 +98,9 @@ int w8a8_pack_act(const int8_t *a, int64_t lda, int64_t M, int64_t K, int8_t *pa
 int w8a8_quant_rows_packed_bf16(const uint16_t *x, int64_t ldx, int64_t M, int64_t K, int8_t *packed, float *scale,
                                 hipStream_t stream);
 
+/* Number of explicit tile configurations the _ex GEMMs accept (tile_cfg 0 .. n-1). */
+int w8a8_gemm_tile_configs(void);
+
 /* Split-K workspace the _ex GEMMs use for [M, N, K] with tile_cfg (-1 = automatic) and split_k
  * (0 = automatic, which currently never splits; n >= 1 = at most n blocks per output tile
  * along K, used only when there are few output tiles): 0 when no split will happen.  Its first 4 KiB
@@ -107,7 +110,7 @@ int w8a8_quant_rows_packed_bf16(const uint16_t *x, int64_t ldx, int64_t M, int64
 int64_t w8a8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int tile_cfg, int split_k);
 
 /* As w8a8_gemm_i32 with A given either row-major (a_packed = 0, lda used) or packed
- * (a_packed = 1, lda ignored), an explicit tile configuration (0 .. 7, -1 = automatic), a split-K
+ * (a_packed = 1, lda ignored), an explicit tile configuration (0 .. w8a8_gemm_tile_configs()-1, -1 = automatic), a split-K
  * request (as w8a8_gemm_workspace_bytes) and its workspace (NULL or too small: no split;
  * 256-byte aligned).  Split-K keeps the result bit-exact: int32 partial sums are added in a
  * fixed order by the last block of each output tile. */

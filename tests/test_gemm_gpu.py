@@ -9,10 +9,11 @@ import torch
 from helpers import assert_bf16_close, f32, to_bits
 
 import oracle.oracle as orc
-from w8a8 import ops, workloads
+from w8a8 import lib, ops, workloads
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
+CONFIGS = list(range(lib().w8a8_gemm_tile_configs()))
 
 
 def rand_i8(shape, seed, lo=-128, hi=128):
@@ -24,7 +25,7 @@ def packed_from_nk(w_nk, interleave=0):
     return ops.pack_weight(w_nk.to(DEV), "nk", interleave)
 
 
-@pytest.mark.parametrize("cfg", list(range(8)))
+@pytest.mark.parametrize("cfg", CONFIGS)
 @pytest.mark.parametrize("M,N,K", [(1, 16, 64), (37, 72, 128), (130, 200, 192), (300, 520, 320),
                                    (64, 48, 80), (257, 33, 1536)])
 def test_gemm_i32_vs_oracle(cfg, M, N, K):
@@ -117,7 +118,7 @@ def _inputs(M, K, N, seed):
     return x, w, sw, q, sx
 
 
-@pytest.mark.parametrize("cfg", list(range(8)))
+@pytest.mark.parametrize("cfg", CONFIGS)
 def test_gemm_dequant_epilogue_exact(cfg):
     M, K, N = 200, 256, 320
     x, w, sw, q, sx = _inputs(M, K, N, 21)
@@ -127,7 +128,7 @@ def test_gemm_dequant_epilogue_exact(cfg):
     assert np.array_equal(to_bits(out), ref)
 
 
-@pytest.mark.parametrize("cfg", list(range(8)))
+@pytest.mark.parametrize("cfg", CONFIGS)
 def test_gemm_residual_epilogue_exact(cfg):
     M, K, N = 130, 192, 256
     x, w, sw, q, sx = _inputs(M, K, N, 31)
@@ -139,7 +140,7 @@ def test_gemm_residual_epilogue_exact(cfg):
     assert np.array_equal(to_bits(out), ref)
 
 
-@pytest.mark.parametrize("cfg", list(range(8)))
+@pytest.mark.parametrize("cfg", CONFIGS)
 def test_gemm_gelu_epilogue(cfg):
     M, K, I = 150, 256, 192
     x, w, sw, q, sx = _inputs(M, K, 2 * I, 41)
@@ -204,7 +205,7 @@ def test_quant_rows_packed_vs_oracle(M, K):
     assert not full[M:].any() and not full[:, K:].any()
 
 
-@pytest.mark.parametrize("cfg", list(range(8)))
+@pytest.mark.parametrize("cfg", CONFIGS)
 @pytest.mark.parametrize("M,N,K", [(1, 16, 64), (37, 72, 128), (300, 520, 320), (257, 33, 1536)])
 def test_gemm_i32_packed_a(cfg, M, N, K):
     a = rand_i8((M, K), seed=M * 3 + K)
@@ -214,7 +215,7 @@ def test_gemm_i32_packed_a(cfg, M, N, K):
     assert np.array_equal(c.cpu().numpy(), ref)
 
 
-@pytest.mark.parametrize("cfg", list(range(8)))
+@pytest.mark.parametrize("cfg", CONFIGS)
 def test_gemm_bf16_packed_a_epilogues(cfg):
     M, K, I = 150, 256, 192
     x, w, sw, q, sx = _inputs(M, K, 2 * I, 51)
@@ -229,20 +230,22 @@ def test_gemm_bf16_packed_a_epilogues(cfg):
 
 # ---- split-K ----------------------------------------------------------------------------------
 
+@pytest.mark.parametrize("cfg", [8, 6, 2])
 @pytest.mark.parametrize("packed_a", [False, True])
-@pytest.mark.parametrize("M,N,K", [(64, 256, 6144), (512, 1536, 6144), (512, 2560, 1536), (100, 96, 2048)])
-def test_gemm_i32_split_k(packed_a, M, N, K):
+@pytest.mark.parametrize("M,N,K", [(64, 256, 6144), (512, 1536, 6144), (512, 2560, 1536), (100, 96, 2048),
+                                   (96, 128, 2112)])
+def test_gemm_i32_split_k(cfg, packed_a, M, N, K):
     """Few output tiles: the GEMM splits K over blocks and the last block adds the int32
     partials, so the result stays bit-exact.  Run twice (the arrival counters must reset)."""
     from w8a8 import lib
-    assert lib().w8a8_gemm_workspace_bytes(M, N, K, 4, 8) > 0, "shape should split K"
+    assert lib().w8a8_gemm_workspace_bytes(M, N, K, cfg, 8) > 0, "shape should split K"
     a = rand_i8((M, K), seed=M + 7 * N)
     w = rand_i8((N, K), seed=K + 3 * N)
     ref = torch._int_mm(a, w.t().contiguous()) if M > 16 else torch.from_numpy(orc.int_mm_nk(a.numpy(), w.numpy()))
     pw = packed_from_nk(w)
     A = ops.pack_act(a.to(DEV)) if packed_a else a.to(DEV)
     for _ in range(2):
-        c = ops.gemm_i32(A, pw, tile_cfg=4, split_k=8)
+        c = ops.gemm_i32(A, pw, tile_cfg=cfg, split_k=8)
         assert torch.equal(c.cpu(), ref)
 
 
@@ -251,7 +254,7 @@ def test_split_k_epilogues_and_workspace_reuse():
     x, w, sw, q, sx = _inputs(M, K, 2 * I, 61)
     pa, sx_d = ops.quant_rows_packed(x.to(DEV))
     y = orc.dequant(orc.int_mm_nk(q, w.numpy()), sx, sw.numpy())
-    kw = dict(tile_cfg=4, split_k=8)
+    kw = dict(tile_cfg=8, split_k=8)
     out = ops.gemm_bf16(pa, sx_d, packed_from_nk(w), sw.to(DEV), **kw)
     assert np.array_equal(to_bits(out), y)
     g = ops.gemm_bf16(pa, sx_d, packed_from_nk(w, interleave=I), sw.to(DEV), epilogue="gelu", **kw)
@@ -289,7 +292,7 @@ def test_split_k_repeated_launches_fresh_inputs():
     outs, refs = [], []
     for it in range(12):
         a = rand_i8((M, K), 100 + it)
-        outs.append(ops.gemm_i32(ops.pack_act(a.to(DEV)), pw, tile_cfg=4, split_k=8))
+        outs.append(ops.gemm_i32(ops.pack_act(a.to(DEV)), pw, tile_cfg=8, split_k=8))
         refs.append(torch._int_mm(a, wt))
     for it, (c, r) in enumerate(zip(outs, refs)):
         assert torch.equal(c.cpu(), r), f"launch {it}"
