@@ -30,7 +30,7 @@ sys.path.insert(0, ROOT)
 
 PEAK_INT8_TOPS = 5000.0   # MI355X dense int8 MFMA, published
 PEAK_HBM_GBS = 8000.0     # MI355X HBM3E, published
-PMC_SUMMARY = os.path.join(ROOT, "profiles", "gemm_gate_up_m512_traffic.json")
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "gemm_gate_up_m512_traffic.md")
 
 
 def log(msg):
@@ -109,23 +109,46 @@ def graph_time_ms(fn, dev, launches=50, reps=10):
     return s.elapsed_time(e) / (reps * launches)
 
 
-def cpu_int_mm_ms(shapes, M, warm=3, reps=5):
-    """Median ms of torch._int_mm (host CPU) per (K, N) shape."""
+def read_traffic():
+    """HBM bytes per launch of the dominant kernel, from the committed rocprofv3 counter summary
+    (FETCH_SIZE + WRITE_SIZE, each calibrated on a 64 MiB copy); None if it is absent."""
+    try:
+        with open(PMC_SUMMARY) as f:
+            for line in f:
+                if line.startswith("hbm_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
+def cpu_int_mm_ms(shapes, M, warm=3, reps=5, budget_s=None):
+    """Median ms of torch._int_mm (host CPU) per (K, N) shape: `warm` untimed calls, then `reps`
+    timed ones, or as many rounds over all shapes as fit in `budget_s` seconds."""
     import torch
-    out = {}
     g = torch.Generator().manual_seed(0)
+    ops = {}
     for K, N in shapes:
         a = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
         w = torch.randint(-127, 128, (K, N), generator=g, dtype=torch.int8)
         for _ in range(warm):
             torch._int_mm(a, w)
-        ts = []
-        for _ in range(reps):
+        ops[(K, N)] = (a, w)
+    ts = {s: [] for s in ops}
+    t_start = time.perf_counter()
+    rounds = 0
+    while True:
+        for s, (a, w) in ops.items():
             t = time.perf_counter()
             torch._int_mm(a, w)
-            ts.append(time.perf_counter() - t)
-        out[(K, N)] = statistics.median(ts) * 1e3
-    return out
+            ts[s].append(time.perf_counter() - t)
+        rounds += 1
+        if budget_s is None:
+            if rounds >= reps:
+                break
+        elif time.perf_counter() - t_start >= budget_s and rounds >= 3:
+            break
+    return {s: statistics.median(v) * 1e3 for s, v in ts.items()}, rounds
 
 
 def sweep(M, dev, reps):
@@ -258,10 +281,7 @@ def main():
     gu_ops = workloads.gemm_ops(M, gu["N"], gu["K"])
     gu_ms = per_ms["gate_up"]
     achieved = gu_ops / (gu_ms * 1e-3) / 1e12
-    traffic = None
-    if os.path.exists(PMC_SUMMARY):
-        with open(PMC_SUMMARY) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+    traffic = read_traffic()
     roofline = {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": traffic,
                 "kernel": "gemm_kernel<EPI_GELU> gate_up M=512 K=1536 N=12288, packed A",
@@ -272,12 +292,13 @@ def main():
     cpu = None
     if not args.no_cpu:
         torch.set_num_threads(os.cpu_count() or 1)
-        cm = cpu_int_mm_ms([(g["K"], g["N"]) for g in groups], M)
+        cm, rounds = cpu_int_mm_ms([(g["K"], g["N"]) for g in groups], M, budget_s=10.0)
         cpu_ms = sum(cm.values())
         cpu = {"value": round(step_ops / (cpu_ms * 1e-3) / 1e12, 3), "unit": "TOP/s",
                "cores": torch.get_num_threads(), "kind": "reference",
-               "sample": f"torch._int_mm (pipeline.py:237, --backend cpu-int8) on the layer's 4 GEMMs at M={M}: "
-                         f"3 warm-up + median of 5 per GEMM, {cpu_ms:.1f} ms per layer"}
+               "sample": f"torch._int_mm (the reference's --backend cpu-int8 GEMM, pipeline.py:237) on the same "
+                         f"layer's 4 GEMMs at M={M} (int8 in, int32 out): 3 warm-up calls each, then {rounds} "
+                         f"rounds over the 4 (~10 s), median per GEMM summed: {cpu_ms:.1f} ms per layer"}
         log(f"bench: cpu _int_mm layer {cpu_ms:.1f} ms")
 
     extra = {"eager_layer_step_us": round(eager_ms * 1e3, 1),
@@ -289,7 +310,7 @@ def main():
                      "frac_mfma": round(tops_ops / (ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4)}
             if not args.no_cpu and Ms == 3658:
                 uniq = sorted(set(shp))
-                cm = cpu_int_mm_ms(uniq, Ms, warm=2, reps=3)
+                cm, _ = cpu_int_mm_ms(uniq, Ms, warm=2, reps=3)
                 cpu_total = sum(cm[s] for s in shp)
                 entry["cpu_int_mm_ms"] = round(cpu_total, 1)
                 entry["speedup_vs_cpu"] = round(cpu_total / ms, 1)
