@@ -454,6 +454,10 @@ static constexpr TileCfg kCfg[] = {
     {128, 128, 4, 4, 2},  // 7: 32 KiB slots, 64 KiB ring (two blocks per CU)
     {128, 128, 4, 2, 4},  // 8: 16 KiB slots, 64 KiB ring (two blocks per CU)
     {128, 256, 4, 2, 3},  // 9: 24 KiB slots, 72 KiB ring (two blocks per CU)
+    {64, 128, 4, 4, 2},   // 10: 24 KiB slots, 48 KiB ring (three blocks per CU)
+    {64, 128, 4, 4, 3},   // 11: 24 KiB slots, 72 KiB ring (two blocks per CU)
+    {64, 64, 2, 4, 2},    // 12: 16 KiB slots, 32 KiB ring, 2 waves (four blocks per CU)
+    {64, 128, 4, 2, 4},   // 13: 12 KiB slots, 48 KiB ring (three blocks per CU)
 };
 static constexpr int kNumCfg = int(sizeof(kCfg) / sizeof(kCfg[0]));
 static constexpr int64_t kCounterBytes = 4096;
@@ -462,14 +466,14 @@ int gemm_config_count() { return kNumCfg; }
 
 // Split-K: blocks per output tile along K.  Explicit requests (req = n >= 1) split into at most
 // n parts, only when there are few output tiles.  Automatic selection (req = 0) splits the
-// few-tile, long-K shapes (the down projection at one 512-row micro-batch: 48 tiles of
-// 128x128 over K = 6144), where measured on MI355X two halves of K beat one block per tile;
+// few-tile, long-K shapes (the down projection at one 512-row micro-batch: 96 tiles of
+// 64x128 over K = 6144), where measured on MI355X two halves of K beat one block per tile;
 // shorter K loses more to the partial-sum exchange than it gains.  Every split keeps at least
 // 256 of K; `kps` is the number of k-tiles per split.
 static int pick_splits(int tiles, int KT, int ks, int req, int& kps) {
   int s = 1;
   if (req > 1 && tiles < 200) s = min(req, 256 / tiles);  // and so tiles < kCounterBytes / 4
-  if (req == 0 && tiles <= 64 && KT * ks * 32 >= 4096) s = 2;
+  if (req == 0 && tiles <= 128 && KT * ks * 32 >= 4096) s = 2;
   const int min_kt = max(1, 8 / ks);
   s = max(1, min(s, min(8, KT / min_kt)));
   kps = (KT + s - 1) / s;
@@ -487,9 +491,12 @@ int64_t gemm_workspace_bytes(int M, int NP, int KF, int cfg, int split_k) {
   return kCounterBytes + int64_t(ntm) * ntn * s * c.bm * c.bn * 4;
 }
 
-// Blocks per CU the tile is built for: two when two rings fit in the 160 KiB of LDS.
+// Blocks per CU the tile is built for: as many rings as fit in the 160 KiB of LDS, at most four.
 template <int BM, int BN, int KS, int NS>
-constexpr int blocks_per_cu() { return 2 * NS * KS * (BM / 32 + BN / 32) * 1024 <= 160 * 1024 ? 2 : 1; }
+constexpr int blocks_per_cu() {
+  constexpr int ring = NS * KS * (BM / 32 + BN / 32) * 1024 + 2048;
+  return 4 * ring <= 160 * 1024 ? 4 : (3 * ring <= 160 * 1024 ? 3 : (2 * ring <= 160 * 1024 ? 2 : 1));
+}
 
 template <int BM, int BN, int WGM, int WGN, int KS, int NS, bool AP, bool SPLIT>
 static void launch_kernel(const GemmParams& p, int epi, dim3 grid, hipStream_t stream) {
@@ -532,8 +539,9 @@ static void launch_epi(GemmParams p, int epi, void* ws, int64_t ws_bytes, hipStr
 template <int CFG>
 static void launch(const GemmParams& p, int epi, bool a_packed, void* ws, int64_t ws_bytes, hipStream_t stream) {
   constexpr TileCfg c = kCfg[CFG];
-  // waves laid out along the longer side of the block tile: 8 waves as 4x2 (BM >= BN) or 2x4
-  constexpr int WGM = c.waves == 4 ? 2 : (c.bm >= c.bn ? 4 : 2);
+  // waves laid out along the longer side of the block tile: 8 waves as 4x2 (BM >= BN) or 2x4,
+  // 4 waves as 2x2, 2 waves as 2x1
+  constexpr int WGM = c.waves == 2 ? 2 : (c.waves == 4 ? 2 : (c.bm >= c.bn ? 4 : 2));
   constexpr int WGN = c.waves / WGM;
   if (a_packed)
     launch_epi<c.bm, c.bn, WGM, WGN, c.ks, c.ns, true>(p, epi, ws, ws_bytes, stream);
@@ -542,10 +550,13 @@ static void launch(const GemmParams& p, int epi, bool a_packed, void* ws, int64_
 }
 
 // Tile choice, from timing every configuration with the bf16 epilogues on the E2B prefill
-// shapes (M = 512, 3658, 16384): the 128x128 tile two blocks per CU (7) everywhere, except the
-// wide gate/up projection at long M, where the 128x256 tile two blocks per CU (9) wins.
+// shapes (M = 512, 3658, 16384).  At one 512-row micro-batch the GEMMs are bound by how fast
+// each CU streams its operands, so small tiles that spread the work over more CUs win: 64x64
+// (12) for the narrow, short-K output projection, 64x128 three blocks per CU (10) otherwise.
+// At long M: 128x128 two blocks per CU (7), and 128x256 two blocks per CU (9) for the wide
+// gate/up projection.
 int gemm_pick_config(int M, int NP, int K) {
-  (void)K;
+  if (M <= 1024) return (NP <= 2048 && K < 4096) ? 12 : 10;
   if (M >= 2048 && NP >= 8192) return 9;
   return 7;
 }
@@ -564,6 +575,10 @@ int gemm_launch(const GemmParams& p, int epi, int cfg, bool a_packed, void* ws, 
     case 7: launch<7>(p, epi, a_packed, ws, ws_bytes, stream); break;
     case 8: launch<8>(p, epi, a_packed, ws, ws_bytes, stream); break;
     case 9: launch<9>(p, epi, a_packed, ws, ws_bytes, stream); break;
+    case 10: launch<10>(p, epi, a_packed, ws, ws_bytes, stream); break;
+    case 11: launch<11>(p, epi, a_packed, ws, ws_bytes, stream); break;
+    case 12: launch<12>(p, epi, a_packed, ws, ws_bytes, stream); break;
+    case 13: launch<13>(p, epi, a_packed, ws, ws_bytes, stream); break;
     default: return fail(W8A8_EINVAL, "gemm: unknown tile config %d", cfg);
   }
   return check_launch("gemm");
