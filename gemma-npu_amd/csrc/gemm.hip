@@ -444,20 +444,21 @@ struct TileCfg {
   int bm, bn, waves, ks, ns;
 };
 static constexpr TileCfg kCfg[] = {
-    {256, 256, 8, 2, 4},  // 0: 32 KiB slots, 128 KiB ring
-    {256, 256, 8, 4, 2},  // 1: 64 KiB slots, 128 KiB ring
-    {128, 256, 8, 4, 3},  // 2: 48 KiB slots, 144 KiB ring
-    {256, 128, 8, 4, 3},  // 3: 48 KiB slots, 144 KiB ring
-    {128, 256, 8, 2, 4},  // 4: 24 KiB slots, 96 KiB ring
-    {256, 128, 8, 2, 4},  // 5: 24 KiB slots, 96 KiB ring
-    {128, 128, 4, 4, 4},  // 6: 32 KiB slots, 128 KiB ring
-    {128, 128, 4, 4, 2},  // 7: 32 KiB slots, 64 KiB ring (two blocks per CU)
-    {128, 128, 4, 2, 4},  // 8: 16 KiB slots, 64 KiB ring (two blocks per CU)
-    {128, 256, 4, 2, 3},  // 9: 24 KiB slots, 72 KiB ring (two blocks per CU)
-    {64, 128, 4, 4, 2},   // 10: 24 KiB slots, 48 KiB ring (three blocks per CU)
-    {64, 128, 4, 4, 3},   // 11: 24 KiB slots, 72 KiB ring (two blocks per CU)
-    {64, 64, 2, 4, 2},    // 12: 16 KiB slots, 32 KiB ring, 2 waves (four blocks per CU)
-    {64, 128, 4, 2, 4},   // 13: 12 KiB slots, 48 KiB ring (three blocks per CU)
+    {256, 256, 8, 4, 2},  // 0: 64 KiB slots, 128 KiB ring
+    {128, 256, 8, 4, 3},  // 1: 48 KiB slots, 144 KiB ring
+    {256, 128, 8, 4, 3},  // 2: 48 KiB slots, 144 KiB ring
+    {128, 256, 8, 2, 4},  // 3: 24 KiB slots, 96 KiB ring
+    {256, 128, 8, 2, 4},  // 4: 24 KiB slots, 96 KiB ring
+    {128, 256, 8, 2, 3},  // 5: 24 KiB slots, 72 KiB ring (two blocks per CU, 16 waves)
+    {256, 128, 8, 2, 3},  // 6: 24 KiB slots, 72 KiB ring (two blocks per CU, 16 waves)
+    {128, 128, 8, 4, 2},  // 7: 32 KiB slots, 64 KiB ring (two blocks per CU, 16 waves)
+    {128, 128, 4, 4, 4},  // 8: 32 KiB slots, 128 KiB ring
+    {128, 128, 4, 4, 2},  // 9: 32 KiB slots, 64 KiB ring (two blocks per CU)
+    {128, 128, 4, 2, 4},  // 10: 16 KiB slots, 64 KiB ring (two blocks per CU)
+    {128, 256, 4, 2, 3},  // 11: 24 KiB slots, 72 KiB ring (two blocks per CU)
+    {64, 128, 4, 4, 2},   // 12: 24 KiB slots, 48 KiB ring (three blocks per CU)
+    {64, 128, 4, 4, 3},   // 13: 24 KiB slots, 72 KiB ring (two blocks per CU)
+    {64, 64, 2, 4, 2},    // 14: 16 KiB slots, 32 KiB ring, 2 waves (four blocks per CU)
 };
 static constexpr int kNumCfg = int(sizeof(kCfg) / sizeof(kCfg[0]));
 static constexpr int64_t kCounterBytes = 4096;
@@ -552,13 +553,12 @@ static void launch(const GemmParams& p, int epi, bool a_packed, void* ws, int64_
 // Tile choice, from timing every configuration with the bf16 epilogues on the E2B prefill
 // shapes (M = 512, 3658, 16384).  At one 512-row micro-batch the GEMMs are bound by how fast
 // each CU streams its operands, so small tiles that spread the work over more CUs win: 64x64
-// (12) for the narrow, short-K output projection, 64x128 three blocks per CU (10) otherwise.
-// At long M: 128x128 two blocks per CU (7), and 128x256 two blocks per CU (9) for the wide
-// gate/up projection.
+// (14) for the narrow, short-K output projection, 64x128 three blocks per CU (12) otherwise.
+// At long M, 16 waves per CU (two 8-wave blocks) hide each block's barrier stalls behind the
+// other's MFMAs: 128x128 (7), and 128x256 (5) for the wide gate/up projection.
 int gemm_pick_config(int M, int NP, int K) {
-  if (M <= 1024) return (NP <= 2048 && K < 4096) ? 12 : 10;
-  if (M >= 2048 && NP >= 8192) return 9;
-  return 7;
+  if (M <= 1024) return (NP <= 2048 && K < 4096) ? 14 : 12;
+  return NP >= 8192 ? 5 : 7;
 }
 
 int gemm_launch(const GemmParams& p, int epi, int cfg, bool a_packed, void* ws, int64_t ws_bytes,
@@ -579,6 +579,7 @@ int gemm_launch(const GemmParams& p, int epi, int cfg, bool a_packed, void* ws, 
     case 11: launch<11>(p, epi, a_packed, ws, ws_bytes, stream); break;
     case 12: launch<12>(p, epi, a_packed, ws, ws_bytes, stream); break;
     case 13: launch<13>(p, epi, a_packed, ws, ws_bytes, stream); break;
+    case 14: launch<14>(p, epi, a_packed, ws, ws_bytes, stream); break;
     default: return fail(W8A8_EINVAL, "gemm: unknown tile config %d", cfg);
   }
   return check_launch("gemm");

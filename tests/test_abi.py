@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
     missing = [n for n in declared_functions() if not hasattr(L, n)]
     assert not missing, f"not exported: {missing}"
     assert L.w8a8_abi_version() == 1
-    assert L.w8a8_gemm_tile_configs() == 14
+    assert L.w8a8_gemm_tile_configs() == 15
 
 
 def test_packed_weight_bytes():
@@ -50,10 +50,10 @@ def test_linear_workspace_bytes():
     assert L.w8a8_packed_act_bytes(33, 40) == 64 * 64       # rows to 32, k to 64
     assert L.w8a8_packed_act_bytes(0, 64) == 0
     assert L.w8a8_gemm_workspace_bytes(16384, 12288, 1536, -1, 8) == 0       # enough tiles: no split
-    assert L.w8a8_gemm_workspace_bytes(512, 1536, 2048, 8, 0) == 0           # automatic: short K kept whole
-    auto = L.w8a8_gemm_workspace_bytes(512, 1536, 6144, 8, 0)              # automatic: few tiles, long K
+    assert L.w8a8_gemm_workspace_bytes(512, 1536, 2048, 10, 0) == 0           # automatic: short K kept whole
+    auto = L.w8a8_gemm_workspace_bytes(512, 1536, 6144, 10, 0)             # automatic: few tiles, long K
     assert auto == 4096 + 48 * 2 * 128 * 128 * 4
-    g = L.w8a8_gemm_workspace_bytes(512, 1536, 6144, 8, 8)                   # 48 tiles, asked to split
+    g = L.w8a8_gemm_workspace_bytes(512, 1536, 6144, 10, 8)                  # 48 tiles, asked to split
     assert g == 4096 + 48 * 5 * 128 * 128 * 4
     g7 = L.w8a8_gemm_workspace_bytes(512, 1536, 6144, -1, 0)
     assert g7 == 4096 + 48 * 2 * 128 * 128 * 4
