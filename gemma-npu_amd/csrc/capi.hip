@@ -202,6 +202,14 @@ int w8a8_linear_bf16(const uint16_t* x, int64_t ldx, const int8_t* w_packed, con
   if (M == 0) return W8A8_OK;
   if (!workspace || workspace_bytes < need || (uintptr_t)workspace % 256 != 0)
     return fail(W8A8_EINVAL, "linear_bf16: workspace needs %lld bytes, 256-byte aligned", (long long)need);
+  if (epilogue == 3) {
+    if (!res) return fail(W8A8_EINVAL, "linear_bf16: residual_rms epilogue without a residual");
+    if (N % 8 != 0 || N > 12288)
+      return fail(W8A8_ENOTSUP, "linear_bf16: the RMSNorm residual needs N %% 8 == 0 and N <= 12288 (N=%lld)",
+                  (long long)N);
+    if ((uintptr_t)out % 16 || ldo % 8 || (uintptr_t)res % 16 || ldr % 8 || (uintptr_t)rms_w % 16)
+      return fail(W8A8_EALIGN, "linear_bf16: the RMSNorm residual needs 16-byte aligned out / res rows and rms_w");
+  }
   char* base = static_cast<char*>(workspace);
   const int64_t gbytes = linear_gemm_part(w8a8_gemm_workspace_bytes(M, N, K, -1, 0));
   void* gws = base;
@@ -211,7 +219,6 @@ int w8a8_linear_bf16(const uint16_t* x, int64_t ldx, const int8_t* w_packed, con
   if (rc) return rc;
   if (epilogue == 3) {
     // Reference order (pipeline.py:113): y = dequant (bf16) first, then res + rms(y) * w.
-    if (!res) return fail(W8A8_EINVAL, "linear_bf16: residual_rms epilogue without a residual");
     rc = w8a8_gemm_bf16_ex(q, 0, 1, sx, w_packed, sw, M, N, K, 0, 0, nullptr, 0, out, ldo, -1, 0, gws, gbytes,
                            stream);
     if (rc) return rc;

@@ -29,29 +29,6 @@ namespace w8a8 {
 
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-// tanh(u) in fp32 as 1 - 2 / (1 + e^(2|u|)) with the sign of u.  What matters downstream is
-// 1 + tanh(u) (gelu below): for u << 0 that is the cancellation 1 - fl(1 - d), d = 2 / (1 + e^(2|u|)),
-// which lands on the fp32 grid just below 1 exactly where a correctly rounded tanhf does, as long as
-// d carries a small *relative* error.  Here d has ~1e-6 relative error (hardware exp2 / rcp), so
-// 1 + tanh(u) matches the correctly rounded form except within ~1e-6 of a rounding tie; for
-// |u| > 9.01 fl(1 - d) is exactly 1 and tanh saturates to +-1 as tanhf does.
-__device__ __forceinline__ float tanh_f32(float u) {
-  const float a = fabsf(u);
-  const float e = __builtin_amdgcn_exp2f(a * 2.8853900817779268f);  // e^(2a) = 2^(2a log2 e)
-  const float d = 2.0f * __builtin_amdgcn_rcpf(1.0f + e);
-  return copysignf(1.0f - d, u);
-}
-
-// GELU, tanh form: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), evaluated in the operation
-// order of torch's gelu(approximate="tanh") on float: x^3 = (x * x) * x, inner = beta * (x +
-// kappa * x^3), result = (0.5 * x) * (1 + tanh(inner)).
-__device__ __forceinline__ float gelu_tanh_f32(float x) {
-  const float kBeta = 0.7978845608028654f;
-  const float kKappa = 0.044715f;
-  const float inner = kBeta * (x + kKappa * (x * x * x));
-  return 0.5f * x * (1.0f + tanh_f32(inner));
-}
-
 // s_waitcnt with only the vector-memory counter constrained (gfx9 encoding: vmcnt in bits
 // [3:0] and [15:14], expcnt [6:4] and lgkmcnt [11:8] left at their maxima).
 template <int N>

@@ -48,12 +48,6 @@ __device__ __forceinline__ float load1<uint16_t>(const uint16_t* p) { return bf1
 template <>
 __device__ __forceinline__ float load1<float>(const float* p) { return *p; }
 
-__device__ __forceinline__ int8_t quant1(float v, float s) {
-  float r = __builtin_rintf(v / s);
-  r = fminf(fmaxf(r, -127.0f), 127.0f);
-  return int8_t(int(r));
-}
-
 // VEC: rows are 16-byte aligned and K % 8 == 0, so 8 elements move per access.
 template <typename T, bool VEC>
 __global__ __launch_bounds__(256) void quant_rows_kernel(const T* __restrict__ x, int64_t ldx, int M, int K,
@@ -129,17 +123,6 @@ __global__ __launch_bounds__(256) void pack_weight_kernel(const int8_t* __restri
     }
   }
   *reinterpret_cast<v4u*>(out + c * 16) = v4u{word[0], word[1], word[2], word[3]};
-}
-
-// ---- packed activations ----------------------------------------------------------------------
-// The GEMM reads A fastest when it is laid out like the packed weight: 1 KiB fragments of 32
-// rows x 32 k, fragment (mt, j) at (mt * KF + j) * 1024 with KF = 2 * ceil(K/64), byte 16*l + b
-// of it = row 32*mt + l%32, k 32*j + 16*(l/32) + b.  Rows up to the next multiple of 32 and k up
-// to the next multiple of 64 are zero.
-
-__device__ __forceinline__ uint32_t packed_act_offset(int row, int k, int KF) {
-  const int lane = (row & 31) + 32 * ((k >> 4) & 1);
-  return (uint32_t(row >> 5) * uint32_t(KF) + uint32_t(k >> 5)) * 1024u + uint32_t(lane) * 16u;
 }
 
 // One wave per row (padding rows included): absmax, then 16-element chunks quantised and

@@ -74,6 +74,49 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// ---- per-row int8 quantisation step (pipeline.py:51) -----------------------------------------
+// q = clamp(rint(v / s), +-127): IEEE fp32 division, round half to even.
+__device__ __forceinline__ int8_t quant1(float v, float s) {
+  float r = __builtin_rintf(v / s);
+  r = fminf(fmaxf(r, -127.0f), 127.0f);
+  return int8_t(int(r));
+}
+
+// ---- packed activations ----------------------------------------------------------------------
+// The GEMM reads A fastest when it is laid out like the packed weight: 1 KiB fragments of 32
+// rows x 32 k, fragment (mt, j) at (mt * KF + j) * 1024 with KF = 2 * ceil(K/64), byte 16*l + b
+// of it = row 32*mt + l%32, k 32*j + 16*(l/32) + b.  Rows up to the next multiple of 32 and k up
+// to the next multiple of 64 are zero.
+
+__device__ __forceinline__ uint32_t packed_act_offset(int row, int k, int KF) {
+  const int lane = (row & 31) + 32 * ((k >> 4) & 1);
+  return (uint32_t(row >> 5) * uint32_t(KF) + uint32_t(k >> 5)) * 1024u + uint32_t(lane) * 16u;
+}
+
+// ---- GELU ------------------------------------------------------------------------------------
+// tanh(u) in fp32 as 1 - 2 / (1 + e^(2|u|)) with the sign of u.  What matters downstream is
+// 1 + tanh(u) (gelu below): for u << 0 that is the cancellation 1 - fl(1 - d), d = 2 / (1 + e^(2|u|)),
+// which lands on the fp32 grid just below 1 exactly where a correctly rounded tanhf does, as long as
+// d carries a small *relative* error.  Here d has ~1e-6 relative error (hardware exp2 / rcp), so
+// 1 + tanh(u) matches the correctly rounded form except within ~1e-6 of a rounding tie; for
+// |u| > 9.01 fl(1 - d) is exactly 1 and tanh saturates to +-1 as tanhf does.
+__device__ __forceinline__ float tanh_f32(float u) {
+  const float a = fabsf(u);
+  const float e = __builtin_amdgcn_exp2f(a * 2.8853900817779268f);  // e^(2a) = 2^(2a log2 e)
+  const float d = 2.0f * __builtin_amdgcn_rcpf(1.0f + e);
+  return copysignf(1.0f - d, u);
+}
+
+// GELU, tanh form: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), evaluated in the operation
+// order of torch's gelu(approximate="tanh") on float: x^3 = (x * x) * x, inner = beta * (x +
+// kappa * x^3), result = (0.5 * x) * (1 + tanh(inner)).
+__device__ __forceinline__ float gelu_tanh_f32(float x) {
+  const float kBeta = 0.7978845608028654f;
+  const float kKappa = 0.044715f;
+  const float inner = kBeta * (x + kKappa * (x * x * x));
+  return 0.5f * x * (1.0f + tanh_f32(inner));
+}
+
 // Status codes and the extern "C" declarations every source implements.
 #include "w8a8.h"
 

@@ -39,6 +39,16 @@ SIGNATURES = {
                                  _i32, _i32, _p, _i64, _p]),
     "w8a8_dequant_bf16": (_i32, [_p, _i64, _p, _p, _i64, _i64, _p, _i64, _p]),
     "w8a8_rms_residual_bf16": (_i32, [_p, _i64, _p, _i64, _p, _f32, _i64, _i64, _p, _i64, _p, _i64, _p, _p]),
+    "w8a8_k_in": (_i32, [_p, _i64, _p, _f32, _i64, _i64, _p, _i64, _i32, _p, _p]),
+    "w8a8_k_qkv": (_i32, [_p, _i64, _p, _p, _p, _p, _i64, _p, _p, _f32, _i64, _i64, _i64, _i64, _i32, _p, _p, _p,
+                          _p]),
+    "w8a8_k_attn_out": (_i32, [_p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i32, _p, _p]),
+    "w8a8_k_post_attn": (_i32, [_p, _i64, _p, _p, _p, _i64, _p, _p, _f32, _i64, _i64, _p, _i64, _p, _i64, _i32, _p,
+                                _p]),
+    "w8a8_k_gelu": (_i32, [_p, _i64, _p, _p, _i64, _i64, _p, _i64, _i32, _p, _p]),
+    "w8a8_k_post_ff": (_i32, [_p, _i64, _p, _p, _p, _i64, _p, _f32, _i64, _i64, _p, _i64, _p, _i64, _i32, _p, _p]),
+    "w8a8_k_ple_gate": (_i32, [_p, _i64, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _i32, _p, _p]),
+    "w8a8_k_ple_out": (_i32, [_p, _i64, _p, _p, _p, _i64, _p, _p, _f32, _i64, _i64, _p, _i64, _p]),
     "w8a8_linear_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "w8a8_linear_bf16": (_i32, [_p, _i64, _p, _p, _i64, _i64, _i64, _i32, _i64, _p, _i64, _p, _f32, _p, _i64, _p,
                                 _i64, _p]),

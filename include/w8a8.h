@@ -16,7 +16,13 @@
  *   _deq / _dequant ........................ pipeline.py:55-57, gemma_npu.py:45-47 -> w8a8_dequant_bf16,
  *                                                                         w8a8_gemm_bf16 (epilogue 0)
  *   k_gelu ................................. pipeline.py:102-107       -> w8a8_gemm_bf16 (epilogue 1)
- *   k_post_ff / _rms ....................... pipeline.py:43-46,110-114 -> w8a8_rms_residual_bf16
+ *   k_post_ff / _rms ....................... pipeline.py:43-46,110-114 -> w8a8_rms_residual_bf16, w8a8_k_post_ff
+ *   k_in ................................... pipeline.py:66-69         -> w8a8_k_in
+ *   k_qkv (+ _rope) ........................ pipeline.py:60-63, 72-85  -> w8a8_k_qkv
+ *   k_attn_out ............................. pipeline.py:88-92         -> w8a8_k_attn_out
+ *   k_post_attn ............................ pipeline.py:95-99         -> w8a8_k_post_attn
+ *   k_gelu on an int32 result .............. pipeline.py:102-107       -> w8a8_k_gelu
+ *   k_ple_gate / k_ple_out ................. pipeline.py:117-127       -> w8a8_k_ple_gate / w8a8_k_ple_out
  *   NPUGemm.matmul (quant->GEMM->dequant) .. gemma_npu.py:117-152      -> w8a8_linear_bf16
  *   cpu_int8_linear / Int8Head ............. gemma_npu.py:155-172      -> w8a8_gemv_bf16
  *     (torch._weight_int8pack_mm semantics)
@@ -142,12 +148,77 @@ int w8a8_gemm_bf16_ex(const int8_t *a, int64_t lda, int a_packed, const float *s
 int w8a8_dequant_bf16(const int32_t *acc, int64_t ldacc, const float *sx, const float *sw, int64_t M, int64_t N,
                       uint16_t *out, int64_t ldo, hipStream_t stream);
 
-/* h = bf16(res + bf16(y * (mean(y^2) + eps)^-0.5 * w))  (k_post_ff, pipeline.py:110-114); w may be
- * NULL (no weight, pipeline.py:46).  If q / sq are given, also the int8 rows and scales of h
- * (the `_quant(h)` of k_post_ff).  h may alias y. */
+/* h = bf16(res + bf16(y * (mean(y^2) + eps)^-0.5 * w))  (k_post_ff, pipeline.py:110-114) on a
+ * bf16 y; w may be NULL (no weight, pipeline.py:46).  If q / sq are given, also the int8 rows
+ * (row-major, ld = ldq) and scales of h (the `_quant(h)` of k_post_ff).  h may alias y or res.
+ * N % 8 == 0, N <= 12288, 16-byte aligned rows and w. */
 int w8a8_rms_residual_bf16(const uint16_t *y, int64_t ldy, const uint16_t *res, int64_t ldr, const uint16_t *w,
                            float eps, int64_t M, int64_t N, uint16_t *h, int64_t ldh, int8_t *q, int64_t ldq,
                            float *sq, hipStream_t stream);
+
+/* ---- the fused kernels between the GEMMs (pipeline.py:66-127) ---------------------------------
+ *
+ * Each takes the int32 GEMM result acc [M, N] (ld = ldacc) with its per-token scales sx fp32 [M]
+ * and per-channel scales sw fp32 [N], exactly as the reference's k_* functions do, and applies
+ *   y = bf16((float(acc) * sx[m]) * sw[n])                              (_deq, pipeline.py:55-57)
+ *   rms(x, w) = x * (mean(x^2) + eps)^-0.5 * w in fp32, w NULL: no weight (_rms, pipeline.py:43-46)
+ *   quant(x): s = max(amax|x|, 1e-8) / 127, q = clamp(rint(x / s), +-127)  (_quant, pipeline.py:49-52)
+ * with every bf16 rounding the eager torch expressions perform.  Where an int8 output q is
+ * produced, q_packed = 0 writes it row-major (ld = ldq, 8-byte aligned rows) and q_packed = 1 in
+ * the packed activation layout (w8a8_packed_act_bytes(M, N) bytes, 16-byte aligned; ldq ignored),
+ * ready as the next GEMM's A operand; sq fp32 [M] receives the scales.  Row lengths N are
+ * multiples of 8 up to 12288; bf16 / int32 rows and the sw / weight vectors are 16-byte aligned
+ * (ld % 8 == 0 for bf16, ldacc % 4 == 0).  Outputs may alias the residual they replace. */
+
+/* k_in (pipeline.py:66-69): q, sq = quant(bf16(rms(x, w))), x bf16 [M, N]. */
+int w8a8_k_in(const uint16_t *x, int64_t ldx, const uint16_t *w, float eps, int64_t M, int64_t N, int8_t *q,
+              int64_t ldq, int q_packed, float *sq, hipStream_t stream);
+
+/* k_qkv (pipeline.py:72-85): y = dequant(acc) [T, slots * D] with columns [q heads; k heads; v heads];
+ * per token and head: q = rope(bf16(rms(q_h, qw))), k = rope(bf16(rms(k_h, kw))),
+ * v = bf16(rms(v_h, NULL)), rope(x) = bf16(bf16(x * cos) + bf16(cat(-x[D/2:], x[:D/2]) * sin))
+ * (pipeline.py:60-63) with cos / sin bf16 [T, D] (ld = ldcs).  Outputs are head-major and
+ * contiguous: q [H, T, D], k and v [KV, T, D] (the reference's .transpose(0, 1) views, stored).
+ * shared != 0 (a KV-shared layer): only the H query heads exist; k, v, kw are not used.
+ * D in {128, 256, 512}. */
+int w8a8_k_qkv(const int32_t *acc, int64_t ldacc, const float *sx, const float *sw, const uint16_t *cos_,
+               const uint16_t *sin_, int64_t ldcs, const uint16_t *qw, const uint16_t *kw, float eps, int64_t T,
+               int64_t H, int64_t KV, int64_t D, int shared, uint16_t *q, uint16_t *k, uint16_t *v,
+               hipStream_t stream);
+
+/* k_attn_out (pipeline.py:88-92): the attention output o [H, T, D] bf16, element (h, t, d) at
+ * o + h * head_stride + t * row_stride + d, read as rows [T, H * D] and quantised. */
+int w8a8_k_attn_out(const uint16_t *o, int64_t head_stride, int64_t row_stride, int64_t H, int64_t T, int64_t D,
+                    int8_t *q, int64_t ldq, int q_packed, float *sq, hipStream_t stream);
+
+/* k_post_attn (pipeline.py:95-99): h = bf16(res + bf16(rms(y, w_post)));
+ * q, sq = quant(bf16(rms(h, w_pre_ff))). */
+int w8a8_k_post_attn(const int32_t *acc, int64_t ldacc, const float *sx, const float *sw, const uint16_t *res,
+                     int64_t ldr, const uint16_t *w_post, const uint16_t *w_pre_ff, float eps, int64_t M, int64_t N,
+                     uint16_t *h, int64_t ldh, int8_t *q, int64_t ldq, int q_packed, float *sq, hipStream_t stream);
+
+/* k_gelu (pipeline.py:102-107) on an int32 result acc [M, 2I] in [gate; up] column order:
+ * q, sq = quant(bf16(bf16(gelu_tanh(y[:, :I])) * y[:, I:])).  (The fused GEMM epilogue 1 computes
+ * the same activation without the int32 round trip.) */
+int w8a8_k_gelu(const int32_t *acc, int64_t ldacc, const float *sx, const float *sw, int64_t M, int64_t I, int8_t *q,
+                int64_t ldq, int q_packed, float *sq, hipStream_t stream);
+
+/* k_post_ff (pipeline.py:110-114): h = bf16(res + bf16(rms(y, w_post_ff))); q, sq = quant(h). */
+int w8a8_k_post_ff(const int32_t *acc, int64_t ldacc, const float *sx, const float *sw, const uint16_t *res,
+                   int64_t ldr, const uint16_t *w_post_ff, float eps, int64_t M, int64_t N, uint16_t *h, int64_t ldh,
+                   int8_t *q, int64_t ldq, int q_packed, float *sq, hipStream_t stream);
+
+/* k_ple_gate (pipeline.py:117-121): q, sq = quant(bf16(bf16(gelu_tanh(y)) * ple)), ple bf16 [M, N]
+ * (ld = ldp; the reference passes a strided per-layer slice). */
+int w8a8_k_ple_gate(const int32_t *acc, int64_t ldacc, const float *sx, const float *sw, const uint16_t *ple,
+                    int64_t ldp, int64_t M, int64_t N, int8_t *q, int64_t ldq, int q_packed, float *sq,
+                    hipStream_t stream);
+
+/* k_ple_out (pipeline.py:124-127): out = bf16(bf16(h + bf16(rms(y, w_post_ple))) * scalar), scalar
+ * one bf16 value in device memory (the layer scalar). */
+int w8a8_k_ple_out(const int32_t *acc, int64_t ldacc, const float *sx, const float *sw, const uint16_t *h,
+                   int64_t ldh, const uint16_t *w_post_ple, const uint16_t *scalar, float eps, int64_t M, int64_t N,
+                   uint16_t *out, int64_t ldo, hipStream_t stream);
 
 /* ---- whole linear: bf16 in -> bf16 out (NPUGemm.matmul, gemma_npu.py:117-152) ------------ */
 

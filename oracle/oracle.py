@@ -39,6 +39,8 @@ def lib():
         L.oracle_rms_residual.argtypes = [p, i64, p, i64, p, f32, i64, i64, p, i64]
         L.oracle_add_residual.argtypes = [p, i64, p, i64, i64, i64, p, i64]
         L.oracle_gemv.argtypes = [p, i64, i64, p, i64, i64, i64, p, i32, p, i64]
+        L.oracle_rms_bf16.argtypes = [p, i64, p, f32, i64, i64, p, i64]
+        L.oracle_rope_rows.argtypes = [p, i64, p, p, i64, i64, i64, p, i64]
         L.oracle_f32_to_bf16.argtypes = [f32]
         L.oracle_f32_to_bf16.restype = ctypes.c_uint16
         _lib = L
@@ -194,3 +196,101 @@ def linear_bf16(x, wq, sw, epilogue="none", residual=None, rms_w=None, eps=1e-6)
     else:
         raise ValueError(epilogue)
     return out, acc, sx
+
+
+# ---- the fused kernels between the GEMMs (pipeline.py:43-127) ---------------------------
+
+def rms_bf16(x, w, eps):
+    """bf16 bits of _rms(x, w, eps).to(bfloat16) over the last axis (pipeline.py:43-46)."""
+    x = _c(x, np.uint16)
+    shape = x.shape
+    x2 = x.reshape(-1, shape[-1])
+    M, N = x2.shape
+    wp = None
+    if w is not None:
+        w = _c(w, np.uint16)
+        wp = _ptr(w)
+    out = np.empty((M, N), np.uint16)
+    lib().oracle_rms_bf16(_ptr(x2), N, wp, float(eps), M, N, _ptr(out), N)
+    return out.reshape(shape)
+
+
+def rope(x, cos, sin):
+    """bf16 bits of _rope(x, cos, sin) on bf16 tensors (pipeline.py:60-63); x [R, D], cos / sin
+    [R, D] (row r rotated by row r)."""
+    x, cos, sin = _c(x, np.uint16), _c(cos, np.uint16), _c(sin, np.uint16)
+    R, D = x.shape
+    assert cos.shape == (R, D) and sin.shape == (R, D)
+    out = np.empty((R, D), np.uint16)
+    lib().oracle_rope_rows(_ptr(x), D, _ptr(cos), _ptr(sin), D, R, D, _ptr(out), D)
+    return out
+
+
+def scale_bf16(x, scalar):
+    """bf16 bits of x * scalar on bf16 values (scalar given as bf16 bits)."""
+    prod = bits_to_f32(x) * bits_to_f32(np.asarray([scalar], np.uint16))[0]
+    return bf16_bits(prod.astype(np.float32))
+
+
+def k_in(h, w, eps):
+    """quant(bf16(rms(h, w)))  (pipeline.py:66-69) -> (q, s)."""
+    return quant_rows(rms_bf16(h, w, eps), "bf16")
+
+
+def k_qkv(acc, sx, sw, cos, sin, qw, kw, eps, H, KV, D, shared):
+    """(pipeline.py:72-85) -> q [H, T, D], k, v [KV, T, D] bf16 bits (q, q, q when shared)."""
+    y = dequant(acc, sx, sw)
+    T = y.shape[0]
+
+    def heads(col0, n, w, rotate):
+        x = y[:, col0:col0 + n * D].reshape(T, n, D).transpose(1, 0, 2)      # [n, T, D]
+        x = rms_bf16(np.ascontiguousarray(x), w, eps)
+        if rotate:
+            x = np.stack([rope(x[i], cos, sin) for i in range(n)])
+        return x
+
+    q = heads(0, H, qw, True)
+    if shared:
+        return q, q, q
+    k = heads(H * D, KV, kw, True)
+    v = heads((H + KV) * D, KV, None, False)
+    return q, k, v
+
+
+def k_attn_out(o):
+    """quant of o [H, T, D] read as rows [T, H*D]  (pipeline.py:88-92) -> (q, s)."""
+    H, T, D = o.shape
+    return quant_rows(np.ascontiguousarray(np.asarray(o).transpose(1, 0, 2).reshape(T, H * D)), "bf16")
+
+
+def k_post_attn(acc, sx, sw, res, w_post, w_pre_ff, eps):
+    """(pipeline.py:95-99) -> (h, q, s)."""
+    h = rms_residual(dequant(acc, sx, sw), res, w_post, eps)
+    q, s = quant_rows(rms_bf16(h, w_pre_ff, eps), "bf16")
+    return h, q, s
+
+
+def k_gelu(acc, sx, sw, I):
+    """(pipeline.py:102-107) on acc [T, 2I] -> (q, s)."""
+    y = dequant(acc, sx, sw)
+    return quant_rows(gelu_mul(y[:, :2 * I]), "bf16")
+
+
+def k_post_ff(acc, sx, sw, res, w_post_ff, eps):
+    """(pipeline.py:110-114) -> (h, q, s)."""
+    h = rms_residual(dequant(acc, sx, sw), res, w_post_ff, eps)
+    q, s = quant_rows(h, "bf16")
+    return h, q, s
+
+
+def k_ple_gate(acc, sx, sw, ple):
+    """(pipeline.py:117-121) -> (q, s): gelu_mul on [y | ple] is bf16(bf16(gelu(y)) * ple)."""
+    y = dequant(acc, sx, sw)
+    g = gelu_mul(np.concatenate([y, _c(ple, np.uint16)], axis=1))
+    return quant_rows(g, "bf16")
+
+
+def k_ple_out(acc, sx, sw, h, w_post_ple, scalar, eps):
+    """(pipeline.py:124-127) -> bf16 bits of bf16(bf16(h + bf16(rms(y, w))) * scalar)."""
+    t = rms_residual(dequant(acc, sx, sw), h, w_post_ple, eps)
+    return scale_bf16(t, scalar)

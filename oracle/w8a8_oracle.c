@@ -17,6 +17,11 @@
  *   gelu_mul      pipeline.py:102-107   (k_gelu: gelu_tanh(y[:, :I]) * y[:, I:])
  *   rms_residual  pipeline.py:43-46, 110-114 (k_post_ff: res + rms(y, w).to(bf16))
  *   gemv          gemma_npu.py:155-156  (torch._weight_int8pack_mm(x, w[N,K], s))
+ *   rms_bf16      pipeline.py:43-46     (_rms(x, w, eps).to(bfloat16), the norms of k_in,
+ *                                        k_qkv, k_post_attn)
+ *   rope_rows     pipeline.py:60-63     (_rope on bf16 tensors)
+ * The fused k_* functions of pipeline.py:66-127 are compositions of these; oracle.py composes
+ * them in the reference's order.
  *
  * bf16 values travel as uint16_t bit patterns.  All float arithmetic is
  * IEEE binary32 with round-to-nearest-even, matching torch's eager CPU ops
@@ -180,4 +185,42 @@ void oracle_gemv(const uint16_t *x, int64_t ldx, int64_t M, const int8_t *w, int
             float sc = sdtype == 0 ? bf16_to_f32(((const uint16_t *)s)[n]) : ((const float *)s)[n];
             y[m * ldy + n] = f32_to_bf16(acc * sc);
         }
+}
+
+/* ---- the reference's other fused element-wise kernels (pipeline.py:43-127) ---------------- */
+
+/* out = bf16(rms(x) * w), rms(x) = x * (mean(x^2) + eps)^-0.5 in fp32, w == NULL: no weight
+ * (pipeline.py:43-46 _rms followed by .to(bfloat16)).  x bf16 [M, N]. */
+void oracle_rms_bf16(const uint16_t *x, int64_t ldx, const uint16_t *w, float eps, int64_t M, int64_t N,
+                     uint16_t *out, int64_t ldo) {
+    for (int64_t m = 0; m < M; ++m) {
+        float ss = 0.0f;
+        for (int64_t n = 0; n < N; ++n) {
+            float v = bf16_to_f32(x[m * ldx + n]);
+            ss += v * v;
+        }
+        float r = 1.0f / sqrtf(ss / (float)N + eps);
+        for (int64_t n = 0; n < N; ++n) {
+            float v = bf16_to_f32(x[m * ldx + n]) * r;
+            if (w) v = v * bf16_to_f32(w[n]);
+            out[m * ldo + n] = f32_to_bf16(v);
+        }
+    }
+}
+
+/* Rotary embedding of bf16 rows x[R, D] (D even), row r with cos / sin row r (pipeline.py:60-63):
+ * rot = cat(-x[D/2:], x[:D/2]);  out = bf16(bf16(x * cos) + bf16(rot * sin)), all bf16 tensors. */
+void oracle_rope_rows(const uint16_t *x, int64_t ldx, const uint16_t *cs, const uint16_t *sn, int64_t ldcs,
+                      int64_t R, int64_t D, uint16_t *out, int64_t ldo) {
+    const int64_t h = D / 2;
+    for (int64_t r = 0; r < R; ++r) {
+        const uint16_t *xr = x + r * ldx, *cr = cs + r * ldcs, *sr = sn + r * ldcs;
+        for (int64_t d = 0; d < D; ++d) {
+            float xv = bf16_to_f32(xr[d]);
+            float rv = d < h ? -bf16_to_f32(xr[d + h]) : bf16_to_f32(xr[d - h]);
+            float a = bf16_to_f32(f32_to_bf16(xv * bf16_to_f32(cr[d])));
+            float b = bf16_to_f32(f32_to_bf16(rv * bf16_to_f32(sr[d])));
+            out[r * ldo + d] = f32_to_bf16(a + b);
+        }
+    }
 }
