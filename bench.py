@@ -15,7 +15,9 @@ inputs resident in HBM.  The JSON line also carries the roofline of the dominant
 gate_up GEMM, timed live with HIP events on the launch stream), the host CPU's torch._int_mm
 on the same GEMMs (the reference's --backend cpu-int8 path, pipeline.py:237), and `extra`:
 the eager (uncaptured) step, the full-prefill GEMM sweep at M=3658 / 4096, the M=16384
-stress GEMMs, and the decode GEMV bandwidth.
+stress GEMMs, a decoder layer's whole linear path on the device (the six GEMMs with the fused
+norm / RoPE / GELU / residual / quant kernels between them, one HIP graph), and the decode GEMV
+bandwidth.
 """
 import argparse
 import json
@@ -191,6 +193,72 @@ def gemv_bench(M, K, N, dev, reps, seed=5):
     return ms, nbytes
 
 
+def build_chain(M, dev, seed0=500):
+    """A decoder layer's whole linear path on the device (pipeline.py:244-310 without the
+    attention itself): the six GEMMs of an E2B-class layer and the fused kernels between them.
+    The attention output is stood in for by the rotated q heads."""
+    import torch
+    from w8a8 import ops, workloads
+    E, H, KV, D, I, P = workloads.HIDDEN, 8, 1, 256, 6144, 256
+    shapes = {"qkv": ((H + 2 * KV) * D, E, 0), "o": (E, H * D, 0), "gate_up": (2 * I, E, I), "down": (E, I, 0),
+              "ple_gate": (P, E, 0), "ple_proj": (E, P, 0)}
+    c = {"M": M, "H": H, "KV": KV, "D": D, "I": I, "eps": 1e-6, "pw": {}}
+    for i, (name, (N, K, inter)) in enumerate(shapes.items()):
+        w, sw = workloads.weights(N, K, seed=seed0 + i)
+        c["pw"][name] = ops.pack_weight(w.to(dev), "nk", inter, sw=sw.to(dev))
+    g = torch.Generator().manual_seed(seed0 + 99)
+    c["norm"] = {n: (torch.rand(D if n in ("qw", "kw") else E, generator=g) + 0.5).to(torch.bfloat16).to(dev)
+                 for n in ("in", "qw", "kw", "post", "pre_ff", "post_ff", "post_ple")}
+    ang = torch.arange(M).float()[:, None] * (10000.0 ** (-torch.arange(0, D, 2).float() / D))[None, :]
+    ang = torch.cat([ang, ang], dim=-1)
+    c["cos"], c["sin"] = ang.cos().to(torch.bfloat16).to(dev), ang.sin().to(torch.bfloat16).to(dev)
+    c["ple"] = workloads.activations(M, P, seed=seed0 + 98, outliers=False).to(dev)
+    c["scalar"] = torch.tensor([0.8], dtype=torch.bfloat16, device=dev)
+    c["h0"] = workloads.activations(M, E, seed=seed0 + 97).to(dev)
+    c["ops"] = sum(workloads.gemm_ops(M, N, K) for N, K, _ in shapes.values())
+    c["launches"] = 14
+    return c
+
+
+def chain_step(c):
+    """k_in -> qkv -> k_qkv -> k_attn_out -> o -> k_post_attn -> gate_up (GELU epilogue) -> quant
+    -> down -> k_post_ff -> ple_gate -> k_ple_gate -> ple_proj -> k_ple_out; returns the new h."""
+    from w8a8 import fused, ops
+    pw, nw, eps = c["pw"], c["norm"], c["eps"]
+    xq, sx = fused.k_in(c["h0"], nw["in"], eps, packed=True)
+    acc = ops.gemm_i32(xq, pw["qkv"])
+    q, k, v = fused.k_qkv(acc, sx, pw["qkv"].sw, c["cos"], c["sin"], nw["qw"], nw["kw"], eps, c["H"], c["KV"],
+                          c["D"], False)
+    xq, sx = fused.k_attn_out(q, packed=True)
+    acc = ops.gemm_i32(xq, pw["o"])
+    h, xq, sx = fused.k_post_attn(acc, sx, pw["o"].sw, c["h0"], nw["post"], nw["pre_ff"], eps, packed=True)
+    a = ops.gemm_bf16(xq, sx, pw["gate_up"], epilogue="gelu")
+    xq, sx = ops.quant_rows_packed(a)
+    acc = ops.gemm_i32(xq, pw["down"])
+    h, xq, sx = fused.k_post_ff(acc, sx, pw["down"].sw, h, nw["post_ff"], eps, packed=True)
+    acc = ops.gemm_i32(xq, pw["ple_gate"])
+    xq, sx = fused.k_ple_gate(acc, sx, pw["ple_gate"].sw, c["ple"], packed=True)
+    acc = ops.gemm_i32(xq, pw["ple_proj"])
+    c["out"] = fused.k_ple_out(acc, sx, pw["ple_proj"].sw, h, nw["post_ple"], c["scalar"], eps)
+    return c["out"]
+
+
+def time_chain(M, dev, reps):
+    """(graph-replayed us, eager us) of one chain step; the replay must equal the eager result."""
+    import torch
+    c = build_chain(M, dev)
+    ref = chain_step(c).clone()
+    graph = capture(lambda: chain_step(c), dev)
+    c["out"].zero_()
+    graph.replay()
+    torch.cuda.synchronize()
+    if not torch.equal(c["out"], ref):
+        raise RuntimeError("captured layer chain differs from eager")
+    ms = event_time_ms(graph.replay, reps, 5)
+    eager = event_time_ms(lambda: chain_step(c), reps, 5)
+    return ms, eager, c
+
+
 COPY_BYTES = 64 << 20
 
 
@@ -221,6 +289,8 @@ def main():
     ap.add_argument("--profile-kernel", action="store_true",
                     help="for counter collection: launch only the dominant GEMM (eager, --steps times) and a "
                          "64 MiB device copy that calibrates the byte counters, then exit")
+    ap.add_argument("--profile-chain", action="store_true",
+                    help="for kernel traces: run the device layer chain (--steps times, eager) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the W8A8 path runs "
@@ -233,6 +303,13 @@ def main():
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     M = 512
+    if args.profile_chain:
+        c = build_chain(M, dev)
+        for _ in range(args.steps):
+            chain_step(c)
+        torch.cuda.synchronize()
+        log(f"bench: ran the device layer chain {args.steps} times at M={M}")
+        return 0
     log(f"bench: building one E2B layer at M={M}")
     groups = build_layer(M, dev)
     if args.profile_kernel:
@@ -335,6 +412,14 @@ def main():
                                               "frac_mfma": round(t / PEAK_INT8_TOPS, 4)}
             log(f"bench: stress {name}: {extra[f'stress_m16384_{name}']}")
             del x, q, w, pw, res, out
+        ms, eager, c = time_chain(M, dev, reps=100)
+        extra[f"device_layer_chain_m{M}"] = {
+            "us": round(ms * 1e3, 1), "eager_us": round(eager * 1e3, 1), "launches": c["launches"],
+            "gemm_tops": round(c["ops"] / (ms * 1e-3) / 1e12, 1),
+            "what": "k_in, qkv GEMM, k_qkv, k_attn_out, o GEMM, k_post_attn, gate_up GEMM+GELU, quant, down GEMM, "
+                    "k_post_ff, PLE gate GEMM, k_ple_gate, PLE proj GEMM, k_ple_out (no attention), one HIP graph"}
+        log(f"bench: device layer chain M={M}: {extra[f'device_layer_chain_m{M}']}")
+        del c
         for Mg in (1, 4, 16):
             K, N = workloads.LM_HEAD
             ms, nbytes = gemv_bench(Mg, K, N, dev, reps=50)

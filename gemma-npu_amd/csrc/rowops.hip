@@ -121,10 +121,12 @@ __device__ __forceinline__ void load_in8(const RowChain& p, int row, int col, fl
 }
 
 // One block of blockDim.x (64 .. 256) threads per row; thread t holds chunks c < CH of 8
-// consecutive elements at k = 8 * (blockDim.x * c + t), so the row makes one trip from memory and
-// every statistic is a block reduction over registers.  Rows M .. gridDim.x-1 exist only for the
-// packed layout and are written as zeros, as are its columns N .. 32*KF-1.
-template <int CH, bool IN_I32>
+// consecutive elements at k = 8 * (blockDim.x * c + t).  Every operand of the row (input, up /
+// residual, norm weights, scalar) is fetched in one burst before the first reduction, so the row
+// costs one memory round trip; each statistic is then a block reduction over registers.  Rows
+// M .. gridDim.x-1 exist only for the packed layout and are written as zeros, as are its columns
+// N .. 32*KF-1.  OP is the RowOp (the loads it needs are fixed at compile time).
+template <int CH, bool IN_I32, int OP>
 __global__ __launch_bounds__(256) void row_chain_kernel(RowChain p) {
   __shared__ float red[3][4];
   const int t = threadIdx.x, nt = int(blockDim.x);
@@ -142,34 +144,49 @@ __global__ __launch_bounds__(256) void row_chain_kernel(RowChain p) {
     return;
   }
   const float sxm = IN_I32 ? p.sx[row] : 0.0f;
+  const float scl = p.scalar ? bf16_to_f32(*p.scalar) : 1.0f;
   float v[CH][8];
+  float up[OP == RC_GELU_MUL ? CH : 1][8];  // GELU_MUL multiplier
+  v4u res[OP == RC_NORM_RES ? CH : 1];     // NORM_RES residual (bf16 words)
+  v4u w1[OP == RC_NORM_RES ? CH : 1];      // NORM_RES weight
+  v4u w2[CH];                              // second-norm weight
+  const v4u one = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};  // bf16 1.0 x 8
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     const int k = 8 * (nt * c + t);
-    if (k < p.N) {
+    const bool in = k < p.N;
+    if (in) {
       load_in8<IN_I32>(p, row, k, sxm, v[c]);
     } else {
 #pragma unroll
       for (int i = 0; i < 8; ++i) v[c][i] = 0.0f;
     }
+    if constexpr (OP == RC_GELU_MUL) {
+      if (in && p.aux) {
+        unpack8(*reinterpret_cast<const v4u*>(p.aux + int64_t(row) * p.ld_aux + k), up[c]);
+      } else if (in) {
+        load_in8<IN_I32>(p, row, p.N + k, sxm, up[c]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) up[c][i] = 0.0f;
+      }
+    }
+    if constexpr (OP == RC_NORM_RES) {
+      res[c] = in ? *reinterpret_cast<const v4u*>(p.aux + int64_t(row) * p.ld_aux + k) : v4u{0u, 0u, 0u, 0u};
+      w1[c] = (in && p.w1) ? *reinterpret_cast<const v4u*>(p.w1 + k) : one;
+    }
+    w2[c] = (in && p.q && p.norm2 && p.w2) ? *reinterpret_cast<const v4u*>(p.w2 + k) : one;
   }
 
-  if (p.op == RC_GELU_MUL) {
+  if constexpr (OP == RC_GELU_MUL) {
     // bf16(bf16(gelu_tanh(y)) * up): F.gelu on a bf16 tensor rounds, and so does the product
     // (pipeline.py:106, 120).
 #pragma unroll
-    for (int c = 0; c < CH; ++c) {
-      const int k = 8 * (nt * c + t);
-      if (k >= p.N) continue;
-      float up[8];
-      if (p.aux)
-        unpack8(*reinterpret_cast<const v4u*>(p.aux + int64_t(row) * p.ld_aux + k), up);
-      else
-        load_in8<IN_I32>(p, row, p.N + k, sxm, up);
+    for (int c = 0; c < CH; ++c)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[c][i] = round_bf16(round_bf16(gelu_tanh_f32(v[c][i])) * up[i]);
-    }
-  } else if (p.op == RC_NORM_RES) {
+      for (int i = 0; i < 8; ++i) v[c][i] = round_bf16(round_bf16(gelu_tanh_f32(v[c][i])) * up[c][i]);
+  }
+  if constexpr (OP == RC_NORM_RES) {
     float ss = 0.0f;
 #pragma unroll
     for (int c = 0; c < CH; ++c)
@@ -179,25 +196,22 @@ __global__ __launch_bounds__(256) void row_chain_kernel(RowChain p) {
     const float r = 1.0f / sqrtf(ss / float(p.N) + p.eps);
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
-      const int k = 8 * (nt * c + t);
-      if (k >= p.N) continue;
-      float res[8], w[8];
-      unpack8(*reinterpret_cast<const v4u*>(p.aux + int64_t(row) * p.ld_aux + k), res);
-      if (p.w1) unpack8(*reinterpret_cast<const v4u*>(p.w1 + k), w);
+      float rv[8], wv[8];
+      unpack8(res[c], rv);
+      unpack8(w1[c], wv);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         float n = v[c][i] * r;
-        if (p.w1) n = n * w[i];
-        v[c][i] = round_bf16(res[i] + round_bf16(n));
+        if (p.w1) n = n * wv[i];
+        v[c][i] = round_bf16(rv[i] + round_bf16(n));
       }
     }
   }
   if (p.scalar) {
-    const float s = bf16_to_f32(*p.scalar);
 #pragma unroll
     for (int c = 0; c < CH; ++c)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[c][i] = round_bf16(v[c][i] * s);
+      for (int i = 0; i < 8; ++i) v[c][i] = round_bf16(v[c][i] * scl);
   }
   if (p.h) {
 #pragma unroll
@@ -218,14 +232,12 @@ __global__ __launch_bounds__(256) void row_chain_kernel(RowChain p) {
     const float r = 1.0f / sqrtf(ss / float(p.N) + p.eps);
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
-      const int k = 8 * (nt * c + t);
-      if (k >= p.N) continue;
-      float w[8];
-      if (p.w2) unpack8(*reinterpret_cast<const v4u*>(p.w2 + k), w);
+      float wv[8];
+      unpack8(w2[c], wv);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         float n = v[c][i] * r;
-        if (p.w2) n = n * w[i];
+        if (p.w2) n = n * wv[i];
         v[c][i] = round_bf16(n);
       }
     }
@@ -403,10 +415,13 @@ static int launch_row_chain(const RowChain& p, bool in_i32, hipStream_t stream, 
   const int threads = ((chunks + 63) / 64) * 64;
   const int rows = (p.q && p.KF) ? ((p.M + 31) / 32) * 32 : p.M;
   const dim3 grid{static_cast<unsigned>(rows)};
-#define W8A8_RC(C)                                                                   \
-  do {                                                                               \
-    if (in_i32) row_chain_kernel<C, true><<<grid, threads, 0, stream>>>(p);          \
-    else row_chain_kernel<C, false><<<grid, threads, 0, stream>>>(p);                \
+#define W8A8_RC(C)                                                                          \
+  do {                                                                                      \
+    if (in_i32 && p.op == RC_NORM_RES) row_chain_kernel<C, true, RC_NORM_RES><<<grid, threads, 0, stream>>>(p); \
+    else if (in_i32 && p.op == RC_GELU_MUL) row_chain_kernel<C, true, RC_GELU_MUL><<<grid, threads, 0, stream>>>(p); \
+    else if (!in_i32 && p.op == RC_NORM_RES) row_chain_kernel<C, false, RC_NORM_RES><<<grid, threads, 0, stream>>>(p); \
+    else if (!in_i32 && p.op == RC_NONE) row_chain_kernel<C, false, RC_NONE><<<grid, threads, 0, stream>>>(p); \
+    else return fail(W8A8_EINVAL, "%s: unsupported row-chain combination", what);         \
   } while (0)
   switch (CHs) {
     case 1: W8A8_RC(1); break;
