@@ -174,13 +174,17 @@ __global__ __launch_bounds__(WGM * WGN * 64, MINB) void gemm_kernel(GemmParams p
   constexpr int EARLY = NQ >= 8 ? NQ / 4 : 1;     // MFMAs issued before the next fragment reads
 
   // Slot layout: A fragments (s, mt) at (s*MT + mt) KiB, then W fragments (s, nt) at
-  // (KS*MT + s*NTB + nt) KiB, s = 0 .. KS-1 the 32-wide k-steps of the k-tile.
-  __shared__ __attribute__((aligned(1024))) char lds[NS][F * 1024];
-  // The tile's per-row scales sx (first BM) and per-packed-column scales sw (next BN), parked in
-  // LDS so the epilogue never waits on memory for them.
-  constexpr int NSCALE = EPI == EPI_I32 ? 4 : BM + BN;
-  constexpr int SCALE_PER_THREAD = (NSCALE + NW * 64 - 1) / (NW * 64);
-  __shared__ __attribute__((aligned(16))) float s_scale[NSCALE];
+  // (KS*MT + s*NTB + nt) KiB, s = 0 .. KS-1 the 32-wide k-steps of the k-tile.  After the NS
+  // slots: the tile's per-row scales sx (first BM) and per-packed-column scales sw (next BN),
+  // parked in LDS so the epilogue never waits on memory for them.  Ring and scales are one LDS
+  // object: with a second one the compiler cannot tell the ring's fragment reads from the
+  // in-flight DMA writes and waits for every outstanding load before each read, which removes
+  // the prefetch.
+  constexpr int NSCALE = EPI == EPI_I32 ? 0 : BM + BN;
+  constexpr int SCALE_PER_THREAD = NSCALE ? (NSCALE + NW * 64 - 1) / (NW * 64) : 1;
+  constexpr int RING = NS * F * 1024;
+  __shared__ __attribute__((aligned(1024))) char lds[RING + NSCALE * 4];
+  float* const s_scale = reinterpret_cast<float*>(lds + RING);
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -254,7 +258,7 @@ __global__ __launch_bounds__(WGM * WGN * 64, MINB) void gemm_kernel(GemmParams p
   // Fragments past K (a partial last k-tile) are loaded but never multiplied; loads past the
   // end of A or W read zero.
   auto issue = [&](int kt) {
-    char* slot = lds[kt % NS];
+    char* slot = lds + (kt % NS) * (F * 1024);
 #pragma unroll
     for (int i = 0; i < FA; ++i) dma16(ra, slot + (i * NW + wave) * 1024, offa[i] + uint32_t(kt) * A_STEP);
 #pragma unroll
@@ -262,7 +266,7 @@ __global__ __launch_bounds__(WGM * WGN * 64, MINB) void gemm_kernel(GemmParams p
   };
   // This wave's operand fragments of k-step s of k-tile kt.
   auto read = [&](int kt, int s, v4i (&a)[WTM], v4i (&b)[WTN]) {
-    const char* slot = lds[kt % NS];
+    const char* slot = lds + (kt % NS) * (F * 1024);
 #pragma unroll
     for (int j = 0; j < WTN; ++j)
       b[j] = *reinterpret_cast<const v4i*>(slot + (KS * MT + s * NTB + wn * WTN + j) * 1024 + lane * 16);
@@ -367,7 +371,7 @@ __global__ __launch_bounds__(WGM * WGN * 64, MINB) void gemm_kernel(GemmParams p
     __builtin_amdgcn_s_waitcnt(0);
     // The ring is idle now (every wave's reads completed before its last MFMAs), so its first
     // word carries the arrival count to the whole block.
-    int* arrived = reinterpret_cast<int*>(&lds[0][0]);
+    int* arrived = reinterpret_cast<int*>(lds);
     __syncthreads();
     if (threadIdx.x == 0)
       *arrived = __hip_atomic_fetch_add(p.counters + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
@@ -450,7 +454,7 @@ int gemm_config_count() { return kNumCfg; }
 // 256 of K; `kps` is the number of k-tiles per split.
 static int pick_splits(int tiles, int KT, int ks, int req, int& kps) {
   int s = 1;
-  if (req > 1 && tiles < 200) s = min(req, 256 / tiles);  // and so tiles < kCounterBytes / 4
+  if (req > 1 && tiles < 512) s = min(req, 1024 / tiles);  // and so tiles < kCounterBytes / 4
   if (req == 0 && tiles <= 128 && KT * ks * 32 >= 4096) s = 2;
   const int min_kt = max(1, 8 / ks);
   s = max(1, min(s, min(8, KT / min_kt)));
