@@ -454,7 +454,7 @@ int gemm_config_count() { return kNumCfg; }
 // 256 of K; `kps` is the number of k-tiles per split.
 static int pick_splits(int tiles, int KT, int ks, int req, int& kps) {
   int s = 1;
-  if (req > 1 && tiles < 512) s = min(req, 1024 / tiles);  // and so tiles < kCounterBytes / 4
+  if (req > 1 && tiles < 200) s = min(req, 256 / tiles);  // and so tiles < kCounterBytes / 4
   if (req == 0 && tiles <= 128 && KT * ks * 32 >= 4096) s = 2;
   const int min_kt = max(1, 8 / ks);
   s = max(1, min(s, min(8, KT / min_kt)));
