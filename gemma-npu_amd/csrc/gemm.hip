@@ -141,6 +141,106 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, const v16i& acc,
   }
 }
 
+// Epilogue of the wave split-K kernels.  `red` holds the KW waves' partial tiles as row-major
+// int32 [KW][BM][LDR].  Thread q of a row (TPR = BN/16 threads per row) adds the partials of 4
+// columns in each quarter of the tile, columns 4q + (BN/4)*st (st = 0..3), so in each step the
+// TPR threads of a row read and store one contiguous run.  For GELU (BN of 64 or 128) the gate
+// column c of a [gate | up] pair of 32-channel tiles sits in quarter st and its up column c + 32
+// in quarter st + 128/BN.
+template <int EPI, int BM, int BN, int KW, int NW, int LDR>
+__device__ __forceinline__ void ksplit_epilogue(const GemmParams& p, const int32_t* red, const float* s_scale,
+                                                int m0, int t0) {
+  constexpr int TPR = BN / 16;
+  constexpr int RPP = NW * 64 / TPR;
+  static_assert(EPI != EPI_GELU || BN == 64 || BN == 128, "GELU pairing needs a 64- or 128-wide tile");
+  const int q = int(threadIdx.x) % TPR;
+  for (int r = int(threadIdx.x) / TPR; r < BM; r += RPP) {
+    const int m = m0 + r;
+    if (m >= p.M) break;
+    v4i acc[4];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const int col = 4 * q + (BN / 4) * st;
+      acc[st] = *reinterpret_cast<const v4i*>(red + r * LDR + col);
+#pragma unroll
+      for (int k = 1; k < KW; ++k) acc[st] += *reinterpret_cast<const v4i*>(red + (k * BM + r) * LDR + col);
+    }
+    const float sxm = EPI == EPI_I32 ? 0.0f : s_scale[r];
+    if constexpr (EPI == EPI_I32) {
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const int n = t0 * 32 + 4 * q + (BN / 4) * st;
+        int32_t* dst = p.c + int64_t(m) * p.ldc + n;
+        if (p.vec_store && n + 3 < p.N) {
+          *reinterpret_cast<v4i*>(dst) = acc[st];
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (n + i < p.N) dst[i] = acc[st][i];
+        }
+      }
+    } else if constexpr (EPI == EPI_BF16 || EPI == EPI_RESID) {
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const int col = 4 * q + (BN / 4) * st;
+        const int n = t0 * 32 + col;
+        const v4f sw = *reinterpret_cast<const v4f*>(s_scale + BM + col);
+        float y[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) y[i] = round_bf16((float(acc[st][i]) * sxm) * sw[i]);
+        if constexpr (EPI == EPI_RESID) {
+          const uint16_t* rs = p.res + int64_t(m) * p.ldr + n;
+          if (p.res_vec && n + 3 < p.N) {
+            const v2u rv = *reinterpret_cast<const v2u*>(rs);
+            y[0] += bf16_to_f32(uint16_t(rv[0]));
+            y[1] += bf16_to_f32(uint16_t(rv[0] >> 16));
+            y[2] += bf16_to_f32(uint16_t(rv[1]));
+            y[3] += bf16_to_f32(uint16_t(rv[1] >> 16));
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (n + i < p.N) y[i] += bf16_to_f32(rs[i]);
+          }
+        }
+        uint16_t* dst = p.out + int64_t(m) * p.ldo + n;
+        if (p.vec_store && n + 3 < p.N) {
+          *reinterpret_cast<v2u*>(dst) = v2u{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (n + i < p.N) dst[i] = f32_to_bf16(y[i]);
+        }
+      }
+    } else {  // EPI_GELU
+      constexpr int UP = 128 / BN;  // quarters between a gate column and its up column
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        if ((((BN / 4) * st) / 32) % 2 != 0) continue;  // up quarter: handled with its gate quarter
+        const int su = st + UP < 4 ? st + UP : st;         // the up quarter (always st + UP here)
+        const int col = 4 * q + (BN / 4) * st;
+        const int c = ((t0 + col / 32) >> 1) * 32 + col % 32;  // gate / up channel
+        const v4f swg = *reinterpret_cast<const v4f*>(s_scale + BM + col);
+        const v4f swu = *reinterpret_cast<const v4f*>(s_scale + BM + col + 32);
+        float o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float gate = round_bf16((float(acc[st][i]) * sxm) * swg[i]);
+          const float up = round_bf16((float(acc[su][i]) * sxm) * swu[i]);
+          o[i] = round_bf16(gelu_tanh_f32(gate)) * up;
+        }
+        uint16_t* dst = p.out + int64_t(m) * p.ldo + c;
+        if (p.vec_store && c + 3 < p.I) {
+          *reinterpret_cast<v2u*>(dst) = v2u{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (c + i < p.I) dst[i] = f32_to_bf16(o[i]);
+        }
+      }
+    }
+  }
+}
+
 // Logical tile -> output tile.  Blocks are handed to the 8 XCDs round-robin (b % 8); xcd_remap
 // gives each XCD a contiguous run of logical tiles, and the logical order walks groups of `gm` row
 // tiles across all column tiles, so the ~32 blocks an XCD runs at once cover a compact
@@ -154,9 +254,9 @@ __device__ __forceinline__ void tile_coords(int t, int ntm, int ntn, int gm, int
   tn = r / gsz;
 }
 
-template <int BM, int BN, int WGM, int WGN, int KS, int NS, int EPI, bool A_PACKED, bool SPLIT, int MINB>
-__global__ __launch_bounds__(WGM * WGN * 64, MINB) void gemm_kernel(GemmParams p) {
-  constexpr int NW = WGM * WGN;
+template <int BM, int BN, int WGM, int WGN, int KW, int KS, int NS, int EPI, bool A_PACKED, bool SPLIT, int MINB>
+__global__ __launch_bounds__(WGM * WGN * KW * 64, MINB) void gemm_kernel(GemmParams p) {
+  constexpr int NW = WGM * WGN * KW;  // KW waves share each output sub-tile, splitting its k-steps
   constexpr int MT = BM / 32;         // A row-tiles per block
   constexpr int NTB = BN / 32;        // W column-tiles per block
   constexpr int F = KS * (MT + NTB);  // fragments per k-tile (one ring slot)
@@ -167,7 +267,9 @@ __global__ __launch_bounds__(WGM * WGN * 64, MINB) void gemm_kernel(GemmParams p
   constexpr int WTN = NTB / WGN;      // 32-column tiles per wave
   static_assert(WTM * WGM == MT && WTN * WGN == NTB, "wave grid must divide the block tile");
   static_assert(EPI != EPI_GELU || (WTN % 2 == 0), "GELU pairs need an even tile count per wave");
-  static_assert(KS % 2 == 0, "k-steps alternate between two register sets");
+  static_assert(KS % (2 * KW) == 0, "each wave's k-steps alternate between two register sets");
+  static_assert(KW == 1 || !SPLIT, "wave split-K and block split-K do not combine");
+  constexpr int SW = KS / KW;  // k-steps per wave per k-tile
   static_assert(NS >= 2, "the ring needs one slot being read and one landing");
   static_assert(FW * (NS - 1) < 64, "outstanding loads must fit the 6-bit vmcnt");
   constexpr int NQ = WTM * WTN;                   // MFMAs per k-step
@@ -188,7 +290,8 @@ __global__ __launch_bounds__(WGM * WGN * 64, MINB) void gemm_kernel(GemmParams p
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int wm = wave / WGN, wn = wave % WGN;
+  const int kw = wave / (WGM * WGN);  // this wave takes k-steps kw, kw + KW, ... of every k-tile
+  const int wm = (wave % (WGM * WGN)) / WGN, wn = wave % WGN;
 
   const int ntm = (p.M + BM - 1) / BM;
   const int ntn = (p.NT + NTB - 1) / NTB;
@@ -314,20 +417,21 @@ __global__ __launch_bounds__(WGM * WGN * 64, MINB) void gemm_kernel(GemmParams p
   }
 
   v4i a0[WTM], b0[WTN], a1[WTM], b1[WTN];
-  if (KT > 0) read(k_lo, 0, a0, b0);
+  if (KT > 0) read(k_lo, kw, a0, b0);
   for (int kt = 0; kt < KT; ++kt) {
     const bool more = kt + 1 < KT;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      v4i(&ca)[WTM] = (s % 2 == 0) ? a0 : a1;
-      v4i(&cb)[WTN] = (s % 2 == 0) ? b0 : b1;
-      v4i(&na)[WTM] = (s % 2 == 0) ? a1 : a0;
-      v4i(&nb)[WTN] = (s % 2 == 0) ? b1 : b0;
+    for (int j = 0; j < SW; ++j) {
+      const int s = kw + j * KW;  // k-step within the k-tile
+      v4i(&ca)[WTM] = (j % 2 == 0) ? a0 : a1;
+      v4i(&cb)[WTN] = (j % 2 == 0) ? b0 : b1;
+      v4i(&na)[WTM] = (j % 2 == 0) ? a1 : a0;
+      v4i(&nb)[WTN] = (j % 2 == 0) ? b1 : b0;
       const bool live = more || s < last_steps;  // k-step inside K
       if (live) mma(ca, cb, 0, EARLY);
       __builtin_amdgcn_sched_barrier(0);
-      if (s + 1 < KS) {
-        read(k_lo + kt, s + 1, na, nb);
+      if (j + 1 < SW) {
+        read(k_lo + kt, s + KW, na, nb);
       } else if (more) {
         // Every read of this k-tile has completed (lgkmcnt 0) and, after the barrier, on every
         // wave: its slot takes k-tile kt+NS.  k-tile kt+1 has landed once at most the NS-2
@@ -339,11 +443,36 @@ __global__ __launch_bounds__(WGM * WGN * 64, MINB) void gemm_kernel(GemmParams p
           wait_vmcnt<0>();
         __builtin_amdgcn_s_barrier();
         if (kt + NS < KT) issue(k_lo + kt + NS);
-        read(k_lo + kt + 1, 0, na, nb);
+        read(k_lo + kt + 1, kw, na, nb);
       }
       __builtin_amdgcn_sched_barrier(0);
       if (live) mma(ca, cb, EARLY, NQ);
     }
+  }
+
+  // ---- wave split-K: add the KW partial tiles through LDS, then a row-major epilogue ---------
+  if constexpr (KW > 1) {
+    constexpr int LDR = BN + 4;  // padded row (int32) of the staged tiles
+    static_assert(KW * BM * LDR * 4 <= RING, "the staged partial tiles must fit in the ring");
+    int32_t* red = reinterpret_cast<int32_t*>(lds);
+    // Every DMA has landed (the last k-tiles waited for vmcnt 0) and, after this barrier, every
+    // wave has finished reading the ring.
+    __syncthreads();
+    const int lrow = lane & 31, lcol = 4 * (lane >> 5);
+#pragma unroll
+    for (int i = 0; i < WTM; ++i)
+#pragma unroll
+      for (int j = 0; j < WTN; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int row = (wm * WTM + i) * 32 + lrow;
+          const int col = (wn * WTN + j) * 32 + 8 * g + lcol;
+          *reinterpret_cast<v4i*>(red + (kw * BM + row) * LDR + col) =
+              v4i{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+        }
+    __syncthreads();
+    ksplit_epilogue<EPI, BM, BN, KW, NW, LDR>(p, red, s_scale, m0, t0);
+    return;
   }
 
   // ---- split-K: park partial sums; the last block of the tile adds them up -------------------
@@ -423,6 +552,7 @@ __global__ __launch_bounds__(WGM * WGN * 64, MINB) void gemm_kernel(GemmParams p
 // k-tile depth 32*KS, LDS ring of NS k-tiles.
 struct TileCfg {
   int bm, bn, waves, ks, ns;
+  int kw = 1;  // waves sharing each output sub-tile, splitting its k-steps (partials added in LDS)
 };
 static constexpr TileCfg kCfg[] = {
     {256, 256, 8, 4, 2},  // 0: 64 KiB slots, 128 KiB ring
@@ -440,6 +570,14 @@ static constexpr TileCfg kCfg[] = {
     {64, 128, 4, 4, 2},   // 12: 24 KiB slots, 48 KiB ring (three blocks per CU)
     {64, 128, 4, 4, 3},   // 13: 24 KiB slots, 72 KiB ring (two blocks per CU)
     {64, 64, 2, 4, 2},    // 14: 16 KiB slots, 32 KiB ring, 2 waves (four blocks per CU)
+    {64, 64, 2, 4, 6},    // 15: 16 KiB slots, 96 KiB ring: five k-tiles in flight
+    {64, 128, 4, 4, 5},   // 16: 24 KiB slots, 120 KiB ring: four k-tiles in flight
+    {64, 64, 2, 8, 3},    // 17: 32 KiB slots (k-tile 256), 96 KiB ring
+    {64, 128, 4, 8, 3},   // 18: 48 KiB slots (k-tile 256), 144 KiB ring
+    // wave split-K: each 64x64 sub-tile is computed by kw waves taking alternate k-steps
+    {64, 64, 4, 8, 3, 4},   // 19: one sub-tile, 4 waves; 96 KiB ring
+    {64, 128, 4, 8, 3, 2},  // 20: two sub-tiles side by side, 2 waves each; 144 KiB ring
+    {128, 64, 4, 8, 3, 2},  // 21: two sub-tiles stacked, 2 waves each; 144 KiB ring
 };
 static constexpr int kNumCfg = int(sizeof(kCfg) / sizeof(kCfg[0]));
 static constexpr int64_t kCounterBytes = 4096;
@@ -452,8 +590,12 @@ int gemm_config_count() { return kNumCfg; }
 // 64x128 over K = 6144), where measured on MI355X two halves of K beat one block per tile;
 // shorter K loses more to the partial-sum exchange than it gains.  Every split keeps at least
 // 256 of K; `kps` is the number of k-tiles per split.
-static int pick_splits(int tiles, int KT, int ks, int req, int& kps) {
+static int pick_splits(int tiles, int KT, int ks, int req, int& kps, int kw = 1) {
   int s = 1;
+  if (kw > 1) {  // wave split-K kernels do not split across blocks
+    kps = KT;
+    return 1;
+  }
   if (req > 1 && tiles < 200) s = min(req, 256 / tiles);  // and so tiles < kCounterBytes / 4
   if (req == 0 && tiles <= 128 && KT * ks * 32 >= 4096) s = 2;
   const int min_kt = max(1, 8 / ks);
@@ -468,7 +610,7 @@ int64_t gemm_workspace_bytes(int M, int NP, int KF, int cfg, int split_k) {
   const TileCfg& c = kCfg[cfg];
   const int ntm = (M + c.bm - 1) / c.bm, ntn = (NP + c.bn - 1) / c.bn;
   int kps;
-  const int s = pick_splits(ntm * ntn, (KF + c.ks - 1) / c.ks, c.ks, split_k, kps);
+  const int s = pick_splits(ntm * ntn, (KF + c.ks - 1) / c.ks, c.ks, split_k, kps, c.kw);
   if (s <= 1) return 0;
   return kCounterBytes + int64_t(ntm) * ntn * s * c.bm * c.bn * 4;
 }
@@ -480,19 +622,19 @@ constexpr int blocks_per_cu() {
   return 4 * ring <= 160 * 1024 ? 4 : (3 * ring <= 160 * 1024 ? 3 : (2 * ring <= 160 * 1024 ? 2 : 1));
 }
 
-template <int BM, int BN, int WGM, int WGN, int KS, int NS, bool AP, bool SPLIT>
+template <int BM, int BN, int WGM, int WGN, int KW, int KS, int NS, bool AP, bool SPLIT>
 static void launch_kernel(const GemmParams& p, int epi, dim3 grid, hipStream_t stream) {
-  const int threads = WGM * WGN * 64;
+  const int threads = WGM * WGN * KW * 64;
   constexpr int B = blocks_per_cu<BM, BN, KS, NS>();
   switch (epi) {
-    case EPI_I32: gemm_kernel<BM, BN, WGM, WGN, KS, NS, EPI_I32, AP, SPLIT, B><<<grid, threads, 0, stream>>>(p); break;
-    case EPI_BF16: gemm_kernel<BM, BN, WGM, WGN, KS, NS, EPI_BF16, AP, SPLIT, B><<<grid, threads, 0, stream>>>(p); break;
-    case EPI_GELU: gemm_kernel<BM, BN, WGM, WGN, KS, NS, EPI_GELU, AP, SPLIT, B><<<grid, threads, 0, stream>>>(p); break;
-    case EPI_RESID: gemm_kernel<BM, BN, WGM, WGN, KS, NS, EPI_RESID, AP, SPLIT, B><<<grid, threads, 0, stream>>>(p); break;
+    case EPI_I32: gemm_kernel<BM, BN, WGM, WGN, KW, KS, NS, EPI_I32, AP, SPLIT, B><<<grid, threads, 0, stream>>>(p); break;
+    case EPI_BF16: gemm_kernel<BM, BN, WGM, WGN, KW, KS, NS, EPI_BF16, AP, SPLIT, B><<<grid, threads, 0, stream>>>(p); break;
+    case EPI_GELU: gemm_kernel<BM, BN, WGM, WGN, KW, KS, NS, EPI_GELU, AP, SPLIT, B><<<grid, threads, 0, stream>>>(p); break;
+    case EPI_RESID: gemm_kernel<BM, BN, WGM, WGN, KW, KS, NS, EPI_RESID, AP, SPLIT, B><<<grid, threads, 0, stream>>>(p); break;
   }
 }
 
-template <int BM, int BN, int WGM, int WGN, int KS, int NS, bool AP>
+template <int BM, int BN, int WGM, int WGN, int KW, int KS, int NS, bool AP>
 static void launch_epi(GemmParams p, int epi, void* ws, int64_t ws_bytes, hipStream_t stream) {
   const int ntm = (p.M + BM - 1) / BM;
   const int ntn = (p.NT * 32 + BN - 1) / BN;
@@ -500,7 +642,7 @@ static void launch_epi(GemmParams p, int epi, void* ws, int64_t ws_bytes, hipStr
   const int KT = (p.KF + KS - 1) / KS;
   p.splits = 1;
   p.kt_per_split = KT;
-  if (ws) {
+  if (ws && KW == 1) {
     int kps;
     const int s = pick_splits(ntm * ntn, KT, KS, p.split_req, kps);
     const int64_t need = kCounterBytes + int64_t(ntm) * ntn * s * BM * BN * 4;
@@ -512,33 +654,43 @@ static void launch_epi(GemmParams p, int epi, void* ws, int64_t ws_bytes, hipStr
     }
   }
   dim3 grid(unsigned(ntm * ntn * p.splits));
-  if (p.splits > 1)
-    launch_kernel<BM, BN, WGM, WGN, KS, NS, AP, true>(p, epi, grid, stream);
-  else
-    launch_kernel<BM, BN, WGM, WGN, KS, NS, AP, false>(p, epi, grid, stream);
+  if constexpr (KW == 1) {
+    if (p.splits > 1) {
+      launch_kernel<BM, BN, WGM, WGN, KW, KS, NS, AP, true>(p, epi, grid, stream);
+      return;
+    }
+  }
+  launch_kernel<BM, BN, WGM, WGN, KW, KS, NS, AP, false>(p, epi, grid, stream);
 }
 
 template <int CFG>
 static void launch(const GemmParams& p, int epi, bool a_packed, void* ws, int64_t ws_bytes, hipStream_t stream) {
   constexpr TileCfg c = kCfg[CFG];
-  // waves laid out along the longer side of the block tile: 8 waves as 4x2 (BM >= BN) or 2x4,
-  // 4 waves as 2x2, 2 waves as 2x1
-  constexpr int WGM = c.waves == 2 ? 2 : (c.waves == 4 ? 2 : (c.bm >= c.bn ? 4 : 2));
-  constexpr int WGN = c.waves / WGM;
+  // The waves / kw wave groups laid out along the longer side of the block tile: 8 as 4x2
+  // (BM >= BN) or 2x4, 4 as 2x2, 2 as 2x1 (BM >= BN) or 1x2, 1 as 1x1.
+  constexpr int WG = c.waves / c.kw;
+  constexpr int WGM = WG == 1 ? 1 : (WG == 2 ? (c.bm >= c.bn ? 2 : 1) : (WG == 4 ? 2 : (c.bm >= c.bn ? 4 : 2)));
+  constexpr int WGN = WG / WGM;
   if (a_packed)
-    launch_epi<c.bm, c.bn, WGM, WGN, c.ks, c.ns, true>(p, epi, ws, ws_bytes, stream);
+    launch_epi<c.bm, c.bn, WGM, WGN, c.kw, c.ks, c.ns, true>(p, epi, ws, ws_bytes, stream);
   else
-    launch_epi<c.bm, c.bn, WGM, WGN, c.ks, c.ns, false>(p, epi, ws, ws_bytes, stream);
+    launch_epi<c.bm, c.bn, WGM, WGN, c.kw, c.ks, c.ns, false>(p, epi, ws, ws_bytes, stream);
 }
 
 // Tile choice, from timing every configuration with the bf16 epilogues on the E2B prefill
 // shapes (M = 512, 3658, 16384).  At one 512-row micro-batch the GEMMs are bound by how fast
 // each CU streams its operands, so small tiles that spread the work over more CUs win: 64x64
 // (14) for the narrow, short-K output projection, 64x128 three blocks per CU (12) otherwise.
+// The long-K down projection has only 192 such tiles, one block per CU, whose two waves cannot
+// hide their LDS reads behind two MFMAs per k-step: four waves that each own the whole 64x64
+// tile and take every fourth k-step (19) keep all four SIMDs issuing.
 // At long M, 16 waves per CU (two 8-wave blocks) hide each block's barrier stalls behind the
 // other's MFMAs: 128x128 (7), and 128x256 (5) for the wide gate/up projection.
 int gemm_pick_config(int M, int NP, int K) {
-  if (M <= 1024) return (NP <= 2048 && K < 4096) ? 14 : 12;
+  if (M <= 1024) {
+    if (K >= 4096 && NP <= 4096) return 19;  // few 64x64 tiles, long K: four waves split the k-steps
+    return (NP <= 2048 && K < 4096) ? 14 : 12;
+  }
   return NP >= 8192 ? 5 : 7;
 }
 
@@ -561,6 +713,13 @@ int gemm_launch(const GemmParams& p, int epi, int cfg, bool a_packed, void* ws, 
     case 12: launch<12>(p, epi, a_packed, ws, ws_bytes, stream); break;
     case 13: launch<13>(p, epi, a_packed, ws, ws_bytes, stream); break;
     case 14: launch<14>(p, epi, a_packed, ws, ws_bytes, stream); break;
+    case 15: launch<15>(p, epi, a_packed, ws, ws_bytes, stream); break;
+    case 16: launch<16>(p, epi, a_packed, ws, ws_bytes, stream); break;
+    case 17: launch<17>(p, epi, a_packed, ws, ws_bytes, stream); break;
+    case 18: launch<18>(p, epi, a_packed, ws, ws_bytes, stream); break;
+    case 19: launch<19>(p, epi, a_packed, ws, ws_bytes, stream); break;
+    case 20: launch<20>(p, epi, a_packed, ws, ws_bytes, stream); break;
+    case 21: launch<21>(p, epi, a_packed, ws, ws_bytes, stream); break;
     default: return fail(W8A8_EINVAL, "gemm: unknown tile config %d", cfg);
   }
   return check_launch("gemm");
