@@ -71,7 +71,10 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const T* __restrict__ x
   }
   amax = wave_max(amax);
   const float s = fmaxf(amax, 1e-8f) / 127.0f;
+  const float rs = 1.0f / s;
   if (lane == 0) scale[row] = s;
+  // bf16 rows take the division-free step (exact for bf16 values); fp32 rows divide.
+  auto qt = [&](float v) { return sizeof(T) == 2 ? quant1_bf16(v, s, rs) : quant1(v, s); };
   if (VEC) {
     for (int k = lane * 8; k < K; k += 512) {
       float v[8];
@@ -79,13 +82,13 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const T* __restrict__ x
       uint32_t lo = 0, hi = 0;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        lo |= uint32_t(uint8_t(quant1(v[i], s))) << (8 * i);
-        hi |= uint32_t(uint8_t(quant1(v[4 + i], s))) << (8 * i);
+        lo |= uint32_t(uint8_t(qt(v[i]))) << (8 * i);
+        hi |= uint32_t(uint8_t(qt(v[4 + i]))) << (8 * i);
       }
       *reinterpret_cast<v2u*>(qr + k) = v2u{lo, hi};
     }
   } else {
-    for (int k = lane; k < K; k += 64) qr[k] = quant1(load1<T>(xr + k), s);
+    for (int k = lane; k < K; k += 64) qr[k] = qt(load1<T>(xr + k));
   }
 }
 
@@ -156,6 +159,7 @@ __global__ __launch_bounds__(256) void quant_rows_packed_kernel(const uint16_t* 
   }
   amax = wave_max(amax);
   const float s = fmaxf(amax, 1e-8f) / 127.0f;
+  const float rs = 1.0f / s;
   if (lane == 0) scale[row] = s;
   for (int k = lane * 16; k < KP; k += 1024) {
     uint32_t w[4] = {0, 0, 0, 0};
@@ -169,7 +173,7 @@ __global__ __launch_bounds__(256) void quant_rows_packed_kernel(const uint16_t* 
         for (int i = 0; i < 16; ++i) v[i] = bf16_to_f32(xr[k + i]);
       }
 #pragma unroll
-      for (int i = 0; i < 16; ++i) w[i >> 2] |= uint32_t(uint8_t(quant1(v[i], s))) << (8 * (i & 3));
+      for (int i = 0; i < 16; ++i) w[i >> 2] |= uint32_t(uint8_t(quant1_bf16(v[i], s, rs))) << (8 * (i & 3));
     }
     *reinterpret_cast<v4u*>(q + packed_act_offset(row, k, KF)) = v4u{w[0], w[1], w[2], w[3]};
   }
@@ -177,7 +181,7 @@ __global__ __launch_bounds__(256) void quant_rows_packed_kernel(const uint16_t* 
 
 // Single-pass quantisation of bf16 rows held in registers: one 256-thread block per row; thread
 // t holds chunks c = 0 .. CH-1 of 8 consecutive elements at k = 8 * (256c + t), all loaded in one
-// burst, so the row costs one memory round trip and its divisions are spread over four waves.
+// burst, so the row costs one memory round trip and its quant steps are spread over four waves.
 // The absmax is a DPP wave reduction plus one LDS exchange between the waves.  The int8 bytes
 // leave as 8-byte stores, row-major or into the packed fragment layout (half of the 16-byte
 // piece holding k: fragment (row/32, k/32), lane slot row%32 + 32 * ((k/16) % 2), byte k % 16).
@@ -222,6 +226,7 @@ __global__ __launch_bounds__(256) void quant_rows_blk_kernel(const uint16_t* __r
   __syncthreads();
   amax = fmaxf(fmaxf(wave_amax[0], wave_amax[1]), fmaxf(wave_amax[2], wave_amax[3]));
   const float s = fmaxf(amax, 1e-8f) / 127.0f;
+  const float rs = 1.0f / s;
   if (t == 0) scale[row] = s;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
@@ -231,8 +236,8 @@ __global__ __launch_bounds__(256) void quant_rows_blk_kernel(const uint16_t* __r
     if (k < K) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const uint32_t lo = uint8_t(quant1(__uint_as_float(v[c][i] << 16), s));
-        const uint32_t hi = uint8_t(quant1(__uint_as_float(v[c][i] & 0xffff0000u), s));
+        const uint32_t lo = uint8_t(quant1_bf16(__uint_as_float(v[c][i] << 16), s, rs));
+        const uint32_t hi = uint8_t(quant1_bf16(__uint_as_float(v[c][i] & 0xffff0000u), s, rs));
         w[i >> 1] |= (lo | (hi << 8)) << (16 * (i & 1));
       }
     }
@@ -270,6 +275,31 @@ __global__ __launch_bounds__(256) void pack_act_kernel(const int8_t* __restrict_
   v4u v = {0, 0, 0, 0};
   if (row < M && k < K) v = *reinterpret_cast<const v4u*>(a + int64_t(row) * lda + k);
   *reinterpret_cast<v4u*>(out + c * 16) = v;
+}
+
+// Self-check of quant1_bf16 against the IEEE-division form: one block per positive finite bf16
+// absmax a, its threads walking every bf16 v with |v| <= a.  counts[0] += pairs whose int8 codes
+// differ, counts[1] += pairs compared (1,065,402,240 in all).
+__global__ __launch_bounds__(256) void selfcheck_quant_step_kernel(unsigned long long* counts) {
+  const float a = bf16_to_f32(uint16_t(blockIdx.x));
+  const float s = fmaxf(a, 1e-8f) / 127.0f;
+  const float rs = 1.0f / s;
+  int bad = 0, n = 0;
+  for (int vh = int(threadIdx.x); vh < 65536; vh += 256) {
+    const float v = bf16_to_f32(uint16_t(vh));
+    if (!(fabsf(v) <= a)) continue;
+    ++n;
+    bad += quant1_bf16(v, s, rs) != quant1(v, s);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    bad += __shfl_xor(bad, o, 64);
+    n += __shfl_xor(n, o, 64);
+  }
+  if ((threadIdx.x & 63) == 0) {
+    atomicAdd(counts, (unsigned long long)bad);
+    atomicAdd(counts + 1, (unsigned long long)n);
+  }
 }
 
 }  // namespace w8a8
@@ -387,6 +417,13 @@ int w8a8_quant_rows_packed_bf16(const uint16_t* x, int64_t ldx, int64_t M, int64
   else
     quant_rows_packed_kernel<false><<<grid, 256, 0, stream>>>(x, ldx, int(M), Mp, int(K), KF, packed, scale);
   return check_launch("quant_rows_packed_bf16");
+}
+
+int w8a8_selfcheck_quant_step(unsigned long long* counts, hipStream_t stream) {
+  if (!counts) return fail(W8A8_EINVAL, "selfcheck_quant_step: null counts");
+  if ((uintptr_t)counts % 8 != 0) return fail(W8A8_EALIGN, "selfcheck_quant_step: counts must be 8-byte aligned");
+  selfcheck_quant_step_kernel<<<0x7f80, 256, 0, stream>>>(counts);
+  return check_launch("selfcheck_quant_step");
 }
 
 }  // extern "C"

@@ -249,6 +249,7 @@ __global__ __launch_bounds__(256) void row_chain_kernel(RowChain p) {
     for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[c][i]));
   amax = block_reduce<true>(amax, red[2]);
   const float s = fmaxf(amax, 1e-8f) / 127.0f;
+  const float rs = 1.0f / s;
   if (t == 0) p.sq[row] = s;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
@@ -257,7 +258,7 @@ __global__ __launch_bounds__(256) void row_chain_kernel(RowChain p) {
     uint32_t w[2] = {0u, 0u};
     if (k < p.N) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) w[i >> 2] |= uint32_t(uint8_t(quant1(v[c][i], s))) << (8 * (i & 3));
+      for (int i = 0; i < 8; ++i) w[i >> 2] |= uint32_t(uint8_t(quant1_bf16(v[c][i], s, rs))) << (8 * (i & 3));
     }
     *reinterpret_cast<v2u*>(qdst(k)) = v2u{w[0], w[1]};
   }

@@ -82,6 +82,21 @@ __device__ __forceinline__ int8_t quant1(float v, float s) {
   return int8_t(int(r));
 }
 
+// The same q for a bf16-valued v with |v| <= 127 s (every element of the row the scale was taken
+// from), without a division per element: rs = 1 / s (IEEE, once per row), q0 = v * rs,
+// r = fma(-q0, s, v) (exact), q1 = fma(r, rs, q0).  q1 may differ from the IEEE quotient v / s in
+// its last bit, but rint(q1) == rint(v / s) for every bf16 absmax a (s = max(a, 1e-8) / 127) and
+// every bf16 v with |v| <= a: all 1.07e9 such pairs were compared, and the library's self-check
+// (w8a8_selfcheck_quant_step) repeats that comparison on the GPU.
+__device__ __forceinline__ int8_t quant1_bf16(float v, float s, float rs) {
+  const float q0 = v * rs;
+  const float r = __builtin_fmaf(-q0, s, v);
+  const float q1 = __builtin_fmaf(r, rs, q0);
+  float q = __builtin_rintf(q1);
+  q = fminf(fmaxf(q, -127.0f), 127.0f);
+  return int8_t(int(q));
+}
+
 // ---- packed activations ----------------------------------------------------------------------
 // The GEMM reads A fastest when it is laid out like the packed weight: 1 KiB fragments of 32
 // rows x 32 k, fragment (mt, j) at (mt * KF + j) * 1024 with KF = 2 * ceil(K/64), byte 16*l + b

@@ -88,6 +88,15 @@ int w8a8_quant_rows_f32(const float *x, int64_t ldx, int64_t M, int64_t K, int8_
 int w8a8_gemm_i32(const int8_t *a, int64_t lda, const int8_t *w_packed, int64_t M, int64_t N, int64_t K,
                   int32_t *c, int64_t ldc, hipStream_t stream);
 
+/* Self-check of the division-free quant step the bf16 quant kernels use (no counterpart in the
+ * reference; for callers and tests that want to confirm the device's arithmetic): for every
+ * positive finite bf16 absmax a and every bf16 v with |v| <= a, compares
+ * clamp(rint(v / s), +-127) (IEEE division, s = max(a, 1e-8) / 127) with the kernels' form
+ * q0 = v * (1/s), q1 = fma(fma(-q0, s, v), 1/s, q0), clamp(rint(q1), +-127).  Adds the number of
+ * differing pairs to counts[0] and the number of pairs compared (1,065,402,240) to counts[1];
+ * counts is device memory, 8-byte aligned, zeroed by the caller. */
+int w8a8_selfcheck_quant_step(unsigned long long *counts, hipStream_t stream);
+
 /* ---- packed activations ----------------------------------------------------------------- */
 
 /* The GEMM streams A fastest when it is laid out like the packed weight: 1 KiB fragments of

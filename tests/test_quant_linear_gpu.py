@@ -136,3 +136,14 @@ def test_quant_weight_roundtrip():
     a = torch.randint(-127, 128, (40, 256), generator=g, dtype=torch.int8)
     c = ops.gemm_i32(a.to(DEV), pw)
     assert np.array_equal(c.cpu().numpy(), orc.int_mm_nk(a.numpy(), q_ref))
+
+
+def test_selfcheck_quant_step():
+    """The division-free quant step equals the IEEE-division step on the GPU for every bf16
+    absmax and every bf16 value not above it (1,065,402,240 pairs)."""
+    from w8a8._lib import call
+    counts = torch.zeros(2, dtype=torch.int64, device=DEV)
+    call("w8a8_selfcheck_quant_step", counts.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    bad, pairs = counts.cpu().tolist()
+    assert pairs == 1065402240
+    assert bad == 0
