@@ -95,7 +95,7 @@ int64_t w8a8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int tile_cfg,
   if (M <= 0 || N <= 0 || K <= 0 || M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) return 0;
   if (tile_cfg >= gemm_config_count()) return -1;
   const int np = int((N + 31) / 32 * 32), kf = int(2 * ((K + 63) / 64));
-  const int cfg = tile_cfg < 0 ? gemm_pick_config(int(M), np, kf * 32) : tile_cfg;
+  const int cfg = tile_cfg < 0 ? gemm_pick_config(int(M), np, kf * 32, EPI_BF16) : tile_cfg;
   return gemm_workspace_bytes(int(M), np, kf, cfg, split_k < 0 ? 0 : split_k);
 }
 

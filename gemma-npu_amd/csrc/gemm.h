@@ -32,7 +32,8 @@ struct GemmParams {
 };
 
 int gemm_config_count();
-int gemm_pick_config(int M, int NP, int K);
+// Automatic tile configuration for [M, NP, K] with epilogue epi (split-K needs never depend on epi).
+int gemm_pick_config(int M, int NP, int K, int epi);
 // ws: split-K workspace (zero-filled before first use; the kernels leave it zeroed), may be null.
 int gemm_launch(const GemmParams& p, int epi, int cfg, bool a_packed, void* ws, int64_t ws_bytes,
                 hipStream_t stream);

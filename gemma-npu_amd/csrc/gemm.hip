@@ -450,9 +450,12 @@ __global__ __launch_bounds__(WGM * WGN * KW * 64, MINB) void gemm_kernel(GemmPar
     }
   }
 
-  // ---- wave split-K: add the KW partial tiles through LDS, then a row-major epilogue ---------
-  if constexpr (KW > 1) {
-    constexpr int LDR = BN + 4;  // padded row (int32) of the staged tiles
+  // ---- row-major epilogue through LDS: wave split-K tiles add their KW partials there; other
+  // tiles whose ring can hold the whole accumulator tile stage it there too, so that every
+  // store instruction writes whole row segments instead of 16 or 32 bytes of 32 rows --------
+  constexpr int LDR = BN + 4;  // padded row (int32) of the staged tiles
+  constexpr bool STAGED = KW > 1 || (!SPLIT && BM * LDR * 4 <= RING && (EPI != EPI_GELU || BN == 64 || BN == 128));
+  if constexpr (STAGED) {
     static_assert(KW * BM * LDR * 4 <= RING, "the staged partial tiles must fit in the ring");
     int32_t* red = reinterpret_cast<int32_t*>(lds);
     // Every DMA has landed (the last k-tiles waited for vmcnt 0) and, after this barrier, every
@@ -684,19 +687,25 @@ static void launch(const GemmParams& p, int epi, bool a_packed, void* ws, int64_
 // The long-K down projection has only 192 such tiles, one block per CU, whose two waves cannot
 // hide their LDS reads behind two MFMAs per k-step: four waves that each own the whole 64x64
 // tile and take every fourth k-step (19) keep all four SIMDs issuing.
-// At long M, 16 waves per CU (two 8-wave blocks) hide each block's barrier stalls behind the
-// other's MFMAs: 128x128 (7), and 128x256 (5) for the wide gate/up projection.
-int gemm_pick_config(int M, int NP, int K) {
+// Longer M: the fused GELU epilogue, whose stores are half as wide, runs best on 128x256 with two
+// 8-wave blocks per CU (5).  Other epilogues at a few thousand rows (M = 3658, 4096): 256x256
+// tiles (0) for the wide gate/up and PLE projections and 64x128 tiles with their accumulators
+// staged through LDS for row-contiguous stores (12) for the rest; this is the fastest rule for
+// the 141-GEMM int32 prefill sweep at both sizes.  At M = 16384, 128x128 tiles of 4 waves, two
+// blocks per CU (9), are within 5% of the best on every shape.
+int gemm_pick_config(int M, int NP, int K, int epi) {
   if (M <= 1024) {
     if (K >= 4096 && NP <= 4096) return 19;  // few 64x64 tiles, long K: four waves split the k-steps
     return (NP <= 2048 && K < 4096) ? 14 : 12;
   }
-  return NP >= 8192 ? 5 : 7;
+  if (epi == EPI_GELU) return 5;
+  if (M <= 8192) return NP >= 8192 ? 0 : 12;
+  return 9;
 }
 
 int gemm_launch(const GemmParams& p, int epi, int cfg, bool a_packed, void* ws, int64_t ws_bytes,
                 hipStream_t stream) {
-  if (cfg < 0) cfg = gemm_pick_config(p.M, p.NT * 32, p.KF * 32);
+  if (cfg < 0) cfg = gemm_pick_config(p.M, p.NT * 32, p.KF * 32, epi);
   switch (cfg) {
     case 0: launch<0>(p, epi, a_packed, ws, ws_bytes, stream); break;
     case 1: launch<1>(p, epi, a_packed, ws, ws_bytes, stream); break;
