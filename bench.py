@@ -189,8 +189,11 @@ def gemv_bench(M, K, N, dev, reps, seed=5):
     s = (torch.rand(N, generator=g, device=dev) * 0.015 + 0.005).to(torch.bfloat16)
     y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
     ms = event_time_ms(lambda: ops.gemv_bf16(x, w, s, y), reps, 3)
+    pw = ops.pack_gemv_weight(w)
+    del w
+    ms_packed = event_time_ms(lambda: ops.gemv_bf16(x, pw, s, y), reps, 3)
     nbytes = K * N + 2 * N + 2 * M * K + 2 * M * N
-    return ms, nbytes
+    return ms, ms_packed, nbytes
 
 
 def build_chain(M, dev, seed0=500):
@@ -422,10 +425,13 @@ def main():
         del c
         for Mg in (1, 4, 16):
             K, N = workloads.LM_HEAD
-            ms, nbytes = gemv_bench(Mg, K, N, dev, reps=50)
+            ms_rm, ms, nbytes = gemv_bench(Mg, K, N, dev, reps=50)
             gbs = nbytes / (ms * 1e-3) / 1e9
             extra[f"gemv_lm_head_m{Mg}"] = {"us": round(ms * 1e3, 1), "gbs": round(gbs, 1),
-                                            "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
+                                            "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+                                            "weight": "GEMV fragment layout (w8a8_pack_gemv_weight)",
+                                            "row_major_us": round(ms_rm * 1e3, 1),
+                                            "row_major_gbs": round(nbytes / (ms_rm * 1e-3) / 1e9, 1)}
             log(f"bench: gemv lm head M={Mg}: {extra[f'gemv_lm_head_m{Mg}']}")
         torch.cuda.empty_cache()
 

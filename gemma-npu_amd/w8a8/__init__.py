@@ -7,6 +7,6 @@
 from . import fused  # noqa: F401
 from ._lib import LIB_PATH, W8A8Error, lib  # noqa: F401
 from .ops import (  # noqa: F401
-    PackedActivation, PackedWeight, dequant_bf16, pack_act, packed_act_bytes, quant_rows_packed, gemm_bf16, gemm_i32, gemv_bf16, linear_bf16, pack_weight, packed_weight_bytes,
+    GemvWeight, PackedActivation, PackedWeight, dequant_bf16, pack_gemv_weight, pack_act, packed_act_bytes, quant_rows_packed, gemm_bf16, gemm_i32, gemv_bf16, linear_bf16, pack_weight, packed_weight_bytes,
     quant_rows, quant_weight, rms_residual,
 )

@@ -345,22 +345,60 @@ def linear_bf16(x, w, sw=None, epilogue="none", residual=None, rms_w=None, eps=1
     return out
 
 
+class GemvWeight:
+    """An int8 weight [N, K] resident in the GEMV fragment layout (w8a8_gemv_packed_bytes): the
+    decode copy of a linear's weight (the reference's w_cpu, gemma_npu.py:81)."""
+
+    __slots__ = ("data", "N", "K")
+
+    def __init__(self, data, N, K):
+        self.data, self.N, self.K = data, int(N), int(K)
+
+    @property
+    def device(self):
+        return self.data.device
+
+    @property
+    def shape(self):
+        """(N, K), the shape of the row-major weight it holds."""
+        return (self.N, self.K)
+
+
+def pack_gemv_weight(w):
+    """int8 W [N, K] -> GemvWeight (the layout the GEMV streams fastest)."""
+    _check(w, "w", torch.int8)
+    N, K = w.shape
+    n = lib().w8a8_gemv_packed_bytes(N, K)
+    if n < 0:
+        raise ValueError(f"invalid weight shape {tuple(w.shape)}")
+    out = torch.empty(n, dtype=torch.int8, device=w.device)
+    call("w8a8_pack_gemv_weight", w.data_ptr(), _ld(w), N, K, out.data_ptr(), _stream(w))
+    return GemvWeight(out, N, K)
+
+
 def gemv_bf16(x, w, s, out=None):
     """y = bf16((x @ w^T) * s): torch._weight_int8pack_mm semantics (gemma_npu.py:155-156).
-    x bf16 [M<=16, K]; w int8 [N, K]; s bf16 or fp32 [N]."""
+    x bf16 [M<=16, K]; w int8 [N, K] or a GemvWeight; s bf16 or fp32 [N]."""
     _check(x, "x", torch.bfloat16)
-    _check(w, "w", torch.int8)
+    packed = isinstance(w, GemvWeight)
+    if not packed:
+        _check(w, "w", torch.int8)
     if s.dtype not in (torch.bfloat16, torch.float32):
         raise TypeError(f"gemv_bf16: scales must be bf16 or fp32, got {s.dtype}")
     _check(s, "s", s.dtype, 1)
     M, K = x.shape
-    N = w.shape[0]
-    if w.shape[1] != K or s.shape[0] != N:
+    N, KW = (w.N, w.K) if packed else w.shape
+    if KW != K or s.shape[0] != N:
         raise ValueError("gemv_bf16: operand shapes do not match")
     if out is None:
         out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
     _check(out, "out", torch.bfloat16)
-    _same_device(x, w, s, out)
-    call("w8a8_gemv_bf16", x.data_ptr(), _ld(x), M, w.data_ptr(), _ld(w), N, K, s.data_ptr(),
-         1 if s.dtype == torch.float32 else 0, out.data_ptr(), _ld(out), _stream(x))
+    wt = w.data if packed else w
+    _same_device(x, wt, s, out)
+    if packed:
+        call("w8a8_gemv_packed_bf16", x.data_ptr(), _ld(x), M, wt.data_ptr(), N, K, s.data_ptr(),
+             1 if s.dtype == torch.float32 else 0, out.data_ptr(), _ld(out), _stream(x))
+    else:
+        call("w8a8_gemv_bf16", x.data_ptr(), _ld(x), M, w.data_ptr(), _ld(w), N, K, s.data_ptr(),
+             1 if s.dtype == torch.float32 else 0, out.data_ptr(), _ld(out), _stream(x))
     return out

@@ -24,8 +24,9 @@
  *   k_gelu on an int32 result .............. pipeline.py:102-107       -> w8a8_k_gelu
  *   k_ple_gate / k_ple_out ................. pipeline.py:117-127       -> w8a8_k_ple_gate / w8a8_k_ple_out
  *   NPUGemm.matmul (quant->GEMM->dequant) .. gemma_npu.py:117-152      -> w8a8_linear_bf16
- *   cpu_int8_linear / Int8Head ............. gemma_npu.py:155-172      -> w8a8_gemv_bf16
- *     (torch._weight_int8pack_mm semantics)
+ *   cpu_int8_linear / Int8Head ............. gemma_npu.py:155-172      -> w8a8_gemv_bf16,
+ *     (torch._weight_int8pack_mm semantics)                               w8a8_gemv_packed_bf16
+ *   resident decode weight w_cpu ........... gemma_npu.py:81           -> w8a8_pack_gemv_weight
  */
 #ifndef W8A8_H
 #define W8A8_H
@@ -251,6 +252,22 @@ int w8a8_linear_bf16(const uint16_t *x, int64_t ldx, const int8_t *w_packed, con
  * K % 16 == 0; x and w rows 16-byte aligned.  fp32 accumulation; deterministic. */
 int w8a8_gemv_bf16(const uint16_t *x, int64_t ldx, int64_t M, const int8_t *w, int64_t ldw, int64_t N, int64_t K,
                    const void *scales, int scale_is_f32, uint16_t *y, int64_t ldy, hipStream_t stream);
+
+/* Bytes of the GEMV fragment layout of an int8 W [N, K]: ceil(N/16) * ceil(K/64) KiB; -1 if invalid.
+ * Fragment (t, kb) (n-tile t of 16 rows, k-block kb of 64) is 1 KiB at (t * ceil(K/64) + kb) * 1024
+ * whose byte 16*l + b is W[16t + l%16][64kb + 16(l/16) + b]; rows past N and k past K are zero.
+ * The resident decode copy of a weight (the reference's w_cpu [N, K], gemma_npu.py:81) can be
+ * kept in this layout: the GEMV then reads it in whole contiguous KiB with the streaming cache
+ * policy. */
+int64_t w8a8_gemv_packed_bytes(int64_t N, int64_t K);
+
+/* Row-major int8 W [N, K] (ld = ldw, 16-byte aligned rows, K % 16 == 0) -> GEMV fragment layout. */
+int w8a8_pack_gemv_weight(const int8_t *w, int64_t ldw, int64_t N, int64_t K, int8_t *packed, hipStream_t stream);
+
+/* As w8a8_gemv_bf16 with the weight in the GEMV fragment layout (w8a8_pack_gemv_weight); same
+ * results bit for bit (the same products are added in the same order). */
+int w8a8_gemv_packed_bf16(const uint16_t *x, int64_t ldx, int64_t M, const int8_t *packed, int64_t N, int64_t K,
+                          const void *scales, int scale_is_f32, uint16_t *y, int64_t ldy, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -80,3 +80,64 @@ def test_gemv_deterministic():
     y0 = ops.gemv_bf16(x, w, s)
     for _ in range(3):
         assert torch.equal(ops.gemv_bf16(x, w, s), y0)
+
+
+# ---- the GEMV fragment layout (w8a8_pack_gemv_weight) -------------------------------------
+
+def _unpack_gemv(packed, N, K):
+    """Row-major int8 [N, K] from the GEMV fragment layout: fragment (t, kb) at
+    (t * KB + kb) KiB, byte 16*l + b = W[16t + l%16][64kb + 16(l/16) + b]."""
+    KB = (K + 63) // 64
+    T = (N + 15) // 16
+    f = packed.reshape(T, KB, 4, 16, 16)           # t, kb, l/16, l%16, b
+    rows = f.transpose(0, 3, 1, 2, 4).reshape(T * 16, KB * 64)
+    return rows[:N, :K], rows
+
+
+@pytest.mark.parametrize("N,K", [(40, 80), (2560, 1536), (1000, 2064)])
+def test_pack_gemv_weight_layout(N, K):
+    g = torch.Generator().manual_seed(N + K)
+    w = torch.randint(-128, 128, (N, K), generator=g, dtype=torch.int8)
+    pw = ops.pack_gemv_weight(w.to(DEV))
+    assert pw.data.numel() == lib_bytes(N, K)
+    rows, full = _unpack_gemv(pw.data.cpu().numpy(), N, K)
+    assert np.array_equal(rows, w.numpy())
+    assert not full[N:].any() and not full[:, K:].any()
+
+
+def lib_bytes(N, K):
+    from w8a8 import lib
+    return lib().w8a8_gemv_packed_bytes(N, K)
+
+
+@pytest.mark.parametrize("M", [1, 4, 16])
+@pytest.mark.parametrize("K,N", [(1536, 2560), (6144, 1536), (80, 40), (2064, 1000), (1536, 65536)])
+def test_gemv_packed_matches_row_major(M, K, N):
+    """Same products added in the same order: the packed GEMV equals the row-major one bit for
+    bit, and the oracle within the GEMV tolerance."""
+    x = workloads.activations(M, K, seed=M * 17 + K, outliers=False)
+    w, sw = workloads.weights(N, K, seed=N + 3)
+    for s in (sw.to(torch.bfloat16), sw):
+        y_rm = ops.gemv_bf16(x.to(DEV), w.to(DEV), s.to(DEV))
+        y_pk = ops.gemv_bf16(x.to(DEV), ops.pack_gemv_weight(w.to(DEV)), s.to(DEV))
+        assert torch.equal(y_rm, y_pk)
+    if N * K <= 4_000_000:
+        s = sw.to(torch.bfloat16)
+        extra = dot_error_bound(x.float().numpy(), w.numpy(), s.float().numpy())
+        ref = orc.gemv(to_bits(x), w.numpy(), to_bits(s), "bf16")
+        assert_bf16_close(f32(to_bits(y_pk)), f32(ref), what=f"packed gemv M{M} K{K} N{N}", extra=extra)
+
+
+def test_gemv_packed_lm_head_exact_on_integer_activations():
+    """The LM-head shape (K=1536, N=262144) with integer activations: every partial sum is exact,
+    so the packed GEMV must equal bf16(int32 product * s)."""
+    g = torch.Generator().manual_seed(11)
+    K, N = 1536, 262144
+    xi = torch.randint(-4, 5, (4, K), generator=g)
+    w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    s = torch.rand(N, generator=g) * 0.01 + 0.005
+    wd = w.to(DEV)
+    y = ops.gemv_bf16(xi.to(torch.bfloat16).to(DEV), ops.pack_gemv_weight(wd), s.to(DEV))
+    acc = (xi.to(DEV).double() @ wd.double().t()).float()  # exact integers, |acc| < 2^24
+    ref = (acc * s.to(DEV)[None, :]).to(torch.bfloat16)
+    assert torch.equal(y, ref)
