@@ -292,6 +292,9 @@ def main():
     ap.add_argument("--profile-kernel", action="store_true",
                     help="for counter collection: launch only the dominant GEMM (eager, --steps times) and a "
                          "64 MiB device copy that calibrates the byte counters, then exit")
+    ap.add_argument("--profile-gemv", action="store_true",
+                    help="for kernel traces / counters: run the packed LM-head GEMV at M=1 (--steps times) and a "
+                         "64 MiB device copy that calibrates the byte counters, then exit")
     ap.add_argument("--profile-chain", action="store_true",
                     help="for kernel traces: run the device layer chain (--steps times, eager) and exit")
     args = ap.parse_args()
@@ -306,6 +309,22 @@ def main():
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     M = 512
+    if args.profile_gemv:
+        K, N = workloads.LM_HEAD
+        x = workloads.activations(1, K, seed=5, outliers=False).to(dev)
+        g = torch.Generator(device=dev).manual_seed(5)
+        pw = ops.pack_gemv_weight(torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8, device=dev))
+        s = (torch.rand(N, generator=g, device=dev) * 0.015 + 0.005).to(torch.bfloat16)
+        y = torch.empty((1, N), dtype=torch.bfloat16, device=dev)
+        src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        for _ in range(args.steps):
+            ops.gemv_bf16(x, pw, s, y)
+        torch.cuda.synchronize()
+        log(f"bench: ran the packed LM-head GEMV (M=1, K={K}, N={N}) {args.steps} times")
+        return 0
     if args.profile_chain:
         c = build_chain(M, dev)
         for _ in range(args.steps):
