@@ -2,9 +2,10 @@
 
     from w8a8 import ops          # torch-facing entry points (GEMM, quant, GEMV, linear)
     from w8a8 import fused        # the reference's fused kernels between the GEMMs (k_in ... k_ple_out)
+    from w8a8 import attention    # prefill attention (full_attention, sliding_attention, local_sdpa)
     import npu_kernels            # drop-in for the reference's npu_kernels.mm_i8
 """
-from . import fused  # noqa: F401
+from . import attention, fused  # noqa: F401
 from ._lib import LIB_PATH, W8A8Error, lib  # noqa: F401
 from .ops import (  # noqa: F401
     GemvWeight, PackedActivation, PackedWeight, dequant_bf16, pack_gemv_weight, pack_act, packed_act_bytes, quant_rows_packed, gemm_bf16, gemm_i32, gemv_bf16, linear_bf16, pack_weight, packed_weight_bytes,

@@ -1,0 +1,108 @@
+"""Prefill attention on the GPU, with the reference's function names (pipeline.py:130-180,
+local_attn.py:71-107).
+
+    full_attention(q, k_all, v_all, q_start)        -> o [H, Tq, D]      pipeline.py:140-155
+    sliding_attention(q, k_all, v_all, q_start, W)  -> o [H, Tq, D]      pipeline.py:158-180
+    local_sdpa(module, query, key, value, mask, ...) -> ([1, T, H, D], None)   local_attn.py:71-107
+    attention(q, k, v, q_start, window, scale)      -> o (and the logsumexp)
+
+q is bf16 [H, Tq, D] at positions q_start.., k_all / v_all bf16 [KV, Tk, D] holding positions
+0.. (Tk >= q_start + Tq); any strides with a contiguous last dimension.  Scale 1.0 as Gemma uses.
+The query at position p sees keys j <= p, and with a window W only those with p - j < W.  One
+kernel launch (w8a8_attention_bf16) on torch's current stream computes the whole masked softmax in
+one pass, so the reference's logsumexp merge of a prefix pass and a causal pass (`_merge`,
+pipeline.py:133-137) and its 128-query window blocks have no counterpart here; the result is the
+same function.  Unlike the reference's sliding_attention, q_start need not be a multiple of 128.
+There is no CPU fallback.
+"""
+import torch
+
+from ._lib import call
+from .ops import _stream
+
+
+def _check3(t, name):
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name}: expected a tensor, got {type(t).__name__}")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name}: expected a GPU tensor, got device {t.device}")
+    if t.dtype != torch.bfloat16:
+        raise TypeError(f"{name}: expected torch.bfloat16, got {t.dtype}")
+    if t.dim() != 3:
+        raise ValueError(f"{name}: expected [heads, rows, head_dim], got shape {tuple(t.shape)}")
+    if t.shape[2] > 1 and t.stride(2) != 1:
+        raise ValueError(f"{name}: the last dimension must be contiguous, got strides {t.stride()}")
+
+
+def _strides(t):
+    """(head stride, row stride) in elements; sizes of 1 take the natural stride."""
+    H, T, D = t.shape
+    rs = t.stride(1) if T > 1 else D
+    hs = t.stride(0) if H > 1 else max(T, 1) * rs
+    return hs, rs
+
+
+def attention(q, k, v, q_start=0, window=0, scale=1.0, out=None, return_lse=False):
+    """softmax(scale q k^T, causal [+ window]) v per head; grouped-query heads h -> h // (H // KV).
+
+    out: optional bf16 [H, Tq, D] destination (any strides with a contiguous last dimension, e.g.
+    a transposed view of a [Tq, H, D] tensor).  With return_lse, also the fp32 [H, Tq] natural-log
+    logsumexp of the scaled scores (what torch's flash kernels return beside the output)."""
+    _check3(q, "q")
+    _check3(k, "k")
+    _check3(v, "v")
+    H, Tq, D = q.shape
+    KV, Tk, Dk = k.shape
+    if tuple(v.shape) != (KV, Tk, Dk) or Dk != D:
+        raise ValueError(f"q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)} do not match")
+    if len({q.device, k.device, v.device}) != 1:
+        raise ValueError("q, k and v must be on one device")
+    if out is None:
+        out = torch.empty((H, Tq, D), dtype=torch.bfloat16, device=q.device)
+    else:
+        _check3(out, "out")
+        if tuple(out.shape) != (H, Tq, D) or out.device != q.device:
+            raise ValueError(f"out: expected shape {(H, Tq, D)} on {q.device}, got {tuple(out.shape)}")
+    lse = torch.empty((H, Tq), dtype=torch.float32, device=q.device) if return_lse else None
+    qhs, qrs = _strides(q)
+    khs, krs = _strides(k)
+    vhs, vrs = _strides(v)
+    ohs, ors = _strides(out)
+    call("w8a8_attention_bf16", q.data_ptr(), qhs, qrs, k.data_ptr(), khs, krs, v.data_ptr(), vhs, vrs, H, KV, Tq,
+         Tk, D, int(q_start), int(window), float(scale), out.data_ptr(), ohs, ors,
+         lse.data_ptr() if return_lse else None, _stream(q))
+    return (out, lse) if return_lse else out
+
+
+def full_attention(q, k_all, v_all, q_start):
+    """q [H, Tq, D] at positions q_start.. ; k/v [KV, q_start + Tq, D] -> [H, Tq, D] (causal, scale 1)."""
+    return attention(q, k_all, v_all, q_start, 0, 1.0)
+
+
+def sliding_attention(q, k_all, v_all, q_start, W):
+    """Sliding-window attention for queries at q_start.. against keys 0..q_start+Tq (scale 1)."""
+    if int(W) < 1:
+        raise ValueError(f"sliding_attention: window {W} must be positive")
+    return attention(q, k_all, v_all, q_start, int(W), 1.0)
+
+
+def local_sdpa(module, query, key, value, attention_mask, dropout=0.0, scaling=None, sliding_window=None,
+               **kwargs):
+    """The attention interface the reference registers with HF as "local_sdpa", on the GPU.
+
+    query [1, H, T, D], key / value [1, KV, Tk, D] with Tk >= T (the last T positions are the
+    queries'); returns ([1, T, H, D] contiguous, None).  Causal, and with sliding_window W only the
+    last W keys of each query, which is what HF's mask says for these layers; attention_mask is
+    therefore not read.  Decode (T == 1) is the same call with one query at position Tk - 1."""
+    if dropout:
+        raise ValueError("local_sdpa: dropout is not supported")
+    if query.dim() != 4 or query.shape[0] != 1 or key.shape[0] != 1 or value.shape[0] != 1:
+        raise ValueError("local_sdpa: batch size 1 only")
+    _, H, T, D = query.shape
+    Tk = key.shape[2]
+    if Tk < T:
+        raise ValueError(f"local_sdpa: {Tk} keys for {T} queries")
+    scale = float(scaling) if scaling is not None else D ** -0.5
+    out = torch.empty((1, T, H, D), dtype=torch.bfloat16, device=query.device)
+    attention(query[0], key[0], value[0], Tk - T, int(sliding_window or 0), scale, out=out[0].transpose(0, 1))
+    return out, None

@@ -27,6 +27,8 @@
  *   cpu_int8_linear / Int8Head ............. gemma_npu.py:155-172      -> w8a8_gemv_bf16,
  *     (torch._weight_int8pack_mm semantics)                               w8a8_gemv_packed_bf16
  *   resident decode weight w_cpu ........... gemma_npu.py:81           -> w8a8_pack_gemv_weight
+ *   full_attention / sliding_attention ..... pipeline.py:140-180,      -> w8a8_attention_bf16
+ *     (prefill sdpa of local_sdpa)             local_attn.py:71-107
  */
 #ifndef W8A8_H
 #define W8A8_H
@@ -268,6 +270,27 @@ int w8a8_pack_gemv_weight(const int8_t *w, int64_t ldw, int64_t N, int64_t K, in
  * results bit for bit (the same products are added in the same order). */
 int w8a8_gemv_packed_bf16(const uint16_t *x, int64_t ldx, int64_t M, const int8_t *packed, int64_t N, int64_t K,
                           const void *scales, int scale_is_f32, uint16_t *y, int64_t ldy, hipStream_t stream);
+
+/* ---- prefill attention ------------------------------------------------------------------ */
+
+/* o[h, i, :] = sum_j softmax_j(scale * q[h, i] . k[g, j]) v[g, j] with g = h / (H / KV), over the
+ * keys the query at position p = q_start + i may see: j <= p and, if window > 0, p - j < window.
+ * Replaces full_attention (window 0: causal over k_all[:, :q_start + Tq], pipeline.py:140-155,
+ * merging the prefix and the micro-batch's own keys in one pass) and sliding_attention
+ * (pipeline.py:158-180, local_attn.py:91-107), both with scale 1.0, and the prefill branches of
+ * local_sdpa (local_attn.py:84-107) for any positive scale.
+ *   q  bf16 [H, Tq, D]  (element strides q_head_stride, q_row_stride; last dim contiguous)
+ *   k  bf16 [KV, Tk, D] (k_head_stride, k_row_stride), v likewise; Tk >= q_start + Tq
+ *   o  bf16 [H, Tq, D]  (o_head_stride, o_row_stride): e.g. D, H*D writes HF's [T, H, D] layout
+ *   lse fp32 [H, Tq] natural-log logsumexp of the scaled scores per query, or NULL
+ * D in {128, 256, 512}; H % KV == 0 and H / KV <= 128; strides multiples of 8 elements; pointers
+ * 16-byte aligned.  Scores, softmax and sums in fp32, the softmax weights rounded to bf16 for the
+ * second product (as the CPU flash kernel does). */
+int w8a8_attention_bf16(const uint16_t *q, int64_t q_head_stride, int64_t q_row_stride, const uint16_t *k,
+                        int64_t k_head_stride, int64_t k_row_stride, const uint16_t *v, int64_t v_head_stride,
+                        int64_t v_row_stride, int64_t H, int64_t KV, int64_t Tq, int64_t Tk, int64_t D,
+                        int64_t q_start, int64_t window, float scale, uint16_t *o, int64_t o_head_stride,
+                        int64_t o_row_stride, float *lse, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -41,6 +41,8 @@ def lib():
         L.oracle_gemv.argtypes = [p, i64, i64, p, i64, i64, i64, p, i32, p, i64]
         L.oracle_rms_bf16.argtypes = [p, i64, p, f32, i64, i64, p, i64]
         L.oracle_rope_rows.argtypes = [p, i64, p, p, i64, i64, i64, p, i64]
+        L.oracle_attention.argtypes = [p, i64, i64, p, p, i64, i64, i64, i64, i64, i64, i64, i64, i64,
+                                       ctypes.c_double, p, i64, i64, p, p]
         L.oracle_f32_to_bf16.argtypes = [f32]
         L.oracle_f32_to_bf16.restype = ctypes.c_uint16
         _lib = L
@@ -294,3 +296,26 @@ def k_ple_out(acc, sx, sw, h, w_post_ple, scalar, eps):
     """(pipeline.py:124-127) -> bf16 bits of bf16(bf16(h + bf16(rms(y, w))) * scalar)."""
     t = rms_residual(dequant(acc, sx, sw), h, w_post_ple, eps)
     return scale_bf16(t, scalar)
+
+
+# ---- prefill attention (pipeline.py:141-180, local_attn.py:71-107) --------------------------
+
+def attention(q, k, v, q_start=0, window=0, scale=1.0, budget=False, lse=False):
+    """bf16 bits of softmax(scale q k^T, causal [+ window]) v per head (double precision inside).
+
+    q [H, Tq, D], k / v [KV, Tk, D] uint16 bf16 bits; the query at position q_start + i sees keys
+    j <= q_start + i, and with window W > 0 only those with q_start + i - j < W.  Returns out, then
+    with budget=True sum_j p_j |v_j| per output element (float32 [H, Tq, D]), then with lse=True
+    the logsumexp of the scaled scores (float64 [H, Tq])."""
+    q, k, v = _c(q, np.uint16), _c(k, np.uint16), _c(v, np.uint16)
+    H, Tq, D = q.shape
+    KV, Tk, D2 = k.shape
+    assert D2 == D and v.shape == k.shape and H % KV == 0 and Tk >= q_start + Tq
+    out = np.empty((H, Tq, D), np.uint16)
+    bud = np.empty((H, Tq, D), np.float32) if budget else None
+    ls = np.empty((H, Tq), np.float64) if lse else None
+    lib().oracle_attention(_ptr(q), Tq * D, D, _ptr(k), _ptr(v), Tk * D, D, H, KV, Tq, Tk, D, int(q_start),
+                           int(window), float(scale), _ptr(out), Tq * D, D, _ptr(bud) if budget else None,
+                           _ptr(ls) if lse else None)
+    res = (out,) + ((bud,) if budget else ()) + ((ls,) if lse else ())
+    return res if len(res) > 1 else out

@@ -20,6 +20,8 @@
  *   rms_bf16      pipeline.py:43-46     (_rms(x, w, eps).to(bfloat16), the norms of k_in,
  *                                        k_qkv, k_post_attn)
  *   rope_rows     pipeline.py:60-63     (_rope on bf16 tensors)
+ *   attention     pipeline.py:141-180, local_attn.py:71-107 (causal / sliding-window GQA
+ *                                        attention, scale 1, the math of torch's sdpa / flash)
  * The fused k_* functions of pipeline.py:66-127 are compositions of these; oracle.py composes
  * them in the reference's order.
  *
@@ -31,6 +33,7 @@
 #include <math.h>
 #include <stdint.h>
 #include <string.h>
+#include <stdlib.h>
 
 static inline float bf16_to_f32(uint16_t h) {
     uint32_t u = (uint32_t)h << 16;
@@ -223,4 +226,61 @@ void oracle_rope_rows(const uint16_t *x, int64_t ldx, const uint16_t *cs, const 
             out[r * ldo + d] = f32_to_bf16(a + b);
         }
     }
+}
+
+/* ---- prefill attention (pipeline.py:141-180, local_attn.py:71-107) -------------------------
+ * o[h, i, :] = sum_j softmax_j(scale * q[h, i] . k[g, j]) v[g, j]  over the keys j the query at
+ * position p = q_start + i may see: j <= p and, for a sliding layer (window W > 0), p - j < W;
+ * g = h / (H / KV) (grouped-query heads).  q [H, Tq, D], k / v [KV, Tk, D] bf16, row-major with
+ * the given strides (elements).  Scores, softmax and the weighted sum are computed in double; out
+ * receives the bf16 result, budget (optional) sum_j p_j |v[g, j, d]| per output element (the scale
+ * of the error a bf16 rounding of the weights p can make), lse (optional) the natural-log
+ * logsumexp of the scaled scores per query [H, Tq] (what sdpa's flash kernels return and _merge,
+ * pipeline.py:133-137, weighs partial results by). */
+void oracle_attention(const uint16_t *q, int64_t qhs, int64_t qrs, const uint16_t *k, const uint16_t *v,
+                      int64_t khs, int64_t krs, int64_t H, int64_t KV, int64_t Tq, int64_t Tk, int64_t D,
+                      int64_t q_start, int64_t window, double scale, uint16_t *out, int64_t ohs, int64_t ors,
+                      float *budget, double *lse) {
+    double *s = (double *)malloc((size_t)Tk * sizeof(double));
+    double *acc = (double *)malloc((size_t)D * sizeof(double));
+    double *bud = (double *)malloc((size_t)D * sizeof(double));
+    const int64_t G = H / KV;
+    for (int64_t h = 0; h < H; ++h) {
+        const int64_t g = h / G;
+        for (int64_t i = 0; i < Tq; ++i) {
+            const int64_t p = q_start + i;
+            int64_t lo = 0, hi = p < Tk - 1 ? p : Tk - 1;
+            if (window > 0 && p - window + 1 > lo) lo = p - window + 1;
+            double mx = -INFINITY;
+            for (int64_t j = lo; j <= hi; ++j) {
+                double d = 0.0;
+                for (int64_t e = 0; e < D; ++e)
+                    d += (double)bf16_to_f32(q[h * qhs + i * qrs + e]) * (double)bf16_to_f32(k[g * khs + j * krs + e]);
+                s[j] = d * scale;
+                if (s[j] > mx) mx = s[j];
+            }
+            double sum = 0.0;
+            for (int64_t j = lo; j <= hi; ++j) {
+                s[j] = exp(s[j] - mx);
+                sum += s[j];
+            }
+            for (int64_t e = 0; e < D; ++e) acc[e] = bud[e] = 0.0;
+            for (int64_t j = lo; j <= hi; ++j) {
+                const double w = s[j] / sum;
+                for (int64_t e = 0; e < D; ++e) {
+                    const double ve = (double)bf16_to_f32(v[g * khs + j * krs + e]);
+                    acc[e] += w * ve;
+                    bud[e] += w * fabs(ve);
+                }
+            }
+            if (lse) lse[h * Tq + i] = mx + log(sum);
+            for (int64_t e = 0; e < D; ++e) {
+                out[h * ohs + i * ors + e] = f32_to_bf16((float)acc[e]);
+                if (budget) budget[(h * Tq + i) * D + e] = (float)bud[e];
+            }
+        }
+    }
+    free(s);
+    free(acc);
+    free(bud);
 }

@@ -1,0 +1,178 @@
+"""GPU parity of prefill attention (w8a8_attention_bf16) against the oracle.
+
+The oracle computes each output in double and rounds it to bf16 once; the GPU rounds the softmax
+weights to bf16 for the second product (as the reference's CPU flash kernel does with bf16
+inputs) and its output once.  Tolerance per element:
+
+    |o - o_ref| <= 2^-8 * sum_j p_j |v_j| + 1 ulp_bf16(o_ref)
+
+twice the bound of the weight rounding (2^-9 relative per weight) plus the two output roundings.
+The same bound is reported for torch's CPU sdpa in bf16 on the same inputs (the routine the
+reference calls), so the two can be compared.
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from helpers import f32, to_bits, ulp_bf16
+
+import oracle.oracle as orc
+from w8a8 import W8A8Error
+from w8a8 import attention as attn
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def make(H, KV, Tq, Tk, D, seed, qscale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    q = (torch.randn(H, Tq, D, generator=g) * qscale).to(torch.bfloat16)
+    k = (torch.randn(KV, Tk, D, generator=g) * qscale).to(torch.bfloat16)
+    v = torch.randn(KV, Tk, D, generator=g).to(torch.bfloat16)
+    return q, k, v
+
+
+def reference(q, k, v, q_start, window, scale=1.0):
+    out, bud, lse = orc.attention(to_bits(q), to_bits(k), to_bits(v), q_start, window, scale, budget=True, lse=True)
+    return f32(out), bud, lse
+
+
+def check(o, ref, bud, what, strict=True):
+    """Max |err| / budget; raises if any element is outside the tolerance (strict)."""
+    got = f32(to_bits(o))
+    tol = 2.0 ** -8 * bud + ulp_bf16(ref)
+    err = np.abs(got - ref)
+    bad = err > tol
+    if strict and bad.any():
+        i = tuple(np.argwhere(bad)[0])
+        raise AssertionError(f"{what}: {bad.sum()} of {bad.size} outside tolerance; first at {i}: "
+                             f"got {got[i]!r} ref {ref[i]!r} budget {bud[i]!r}")
+    return float((err / np.maximum(bud, 1e-30)).max())
+
+
+CASES = [
+    # H, KV, Tq, Tk, D, q_start, window, scale, qscale
+    (8, 1, 512, 512, 256, 0, 512, 1.0, 1.0),     # sliding layer, first micro-batch
+    (8, 1, 512, 1024, 256, 512, 512, 1.0, 0.3),  # sliding layer, second micro-batch
+    (8, 1, 300, 400, 256, 100, 512, 1.0, 0.3),   # ragged, q_start not a multiple of 128
+    (8, 1, 77, 77, 256, 0, 16, 1.0, 1.0),        # window shorter than a key block
+    (8, 1, 256, 256, 512, 0, 0, 1.0, 0.3),       # full layer, head_dim 512
+    (8, 1, 256, 768, 512, 512, 0, 1.0, 1.0),     # full layer against earlier keys
+    (8, 1, 33, 290, 512, 257, 0, 1.0, 0.3),      # ragged full layer
+    (4, 2, 200, 200, 128, 0, 0, 0.0883883, 1.0),  # head_dim 128, 2 KV heads, HF's 1/sqrt(D)
+    (6, 2, 130, 190, 128, 60, 50, 1.0, 0.3),     # 3 heads per KV head (rows not a power of 2)
+    (2, 2, 64, 64, 256, 0, 0, 1.0, 1.0),         # no grouping (one head per KV head)
+    (16, 1, 40, 100, 256, 60, 1, 1.0, 1.0),      # window 1: each query sees only itself
+]
+
+
+@pytest.mark.parametrize("H,KV,Tq,Tk,D,q_start,window,scale,qscale", CASES)
+def test_attention_matches_oracle(H, KV, Tq, Tk, D, q_start, window, scale, qscale):
+    print(f"attention H={H} KV={KV} Tq={Tq} Tk={Tk} D={D} q_start={q_start} W={window}", flush=True)
+    q, k, v = make(H, KV, Tq, Tk, D, seed=Tq + 3 * D + window, qscale=qscale)
+    o, lse = attn.attention(q.to(DEV), k.to(DEV), v.to(DEV), q_start, window, scale, return_lse=True)
+    ref, bud, lse_ref = reference(q, k, v, q_start, window, scale)
+    check(o, ref, bud, "attention")
+    assert np.allclose(lse.cpu().numpy(), lse_ref, rtol=1e-5, atol=1e-4), "logsumexp differs"
+    if window == 1:
+        assert torch.equal(o.cpu(), v[torch.arange(H) // (H // KV), q_start:q_start + Tq]), "window 1"
+
+
+def test_micro_batches_like_the_reference_pipeline():
+    """pipeline.py:281-295: each 512-row micro-batch of a sliding layer attends to keys 0..e, each
+    256-row chunk of a full layer to keys 0..s+r1; the chunks are the pipeline's calls."""
+    T = 1300
+    q, k, v = make(8, 1, T, T, 256, seed=1, qscale=0.3)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    ref, bud, _ = reference(q, k, v, 0, 512)
+    for s in range(0, T, 512):
+        e = min(s + 512, T)
+        o = attn.sliding_attention(qd[:, s:e], kd[:, :e], vd[:, :e], s, 512)
+        check(o, ref[:, s:e], bud[:, s:e], f"sliding micro-batch {s}")
+    q, k, v = make(8, 1, T, T, 512, seed=2, qscale=0.3)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    ref, bud, _ = reference(q, k, v, 0, 0)
+    for s in range(0, T, 512):
+        e = min(s + 512, T)
+        for r0 in range(0, e - s, 256):
+            r1 = min(r0 + 256, e - s)
+            o = attn.full_attention(qd[:, s + r0:s + r1], kd[:, :s + r1], vd[:, :s + r1], s + r0)
+            check(o, ref[:, s + r0:s + r1], bud[:, s + r0:s + r1], f"full chunk {s + r0}")
+
+
+@pytest.mark.parametrize("D,window", [(256, 512), (512, 0)])
+def test_whole_prompt_3658(D, window):
+    """The 3658-token prompt in one call; rows at the start, the middle and the end against the oracle."""
+    T = 3658
+    print(f"attention whole prompt T={T} D={D} W={window}", flush=True)
+    q, k, v = make(8, 1, T, T, D, seed=D, qscale=0.3)
+    o = attn.attention(q.to(DEV), k.to(DEV), v.to(DEV), 0, window).cpu()
+    for r0 in (0, 1800, T - 40):
+        r1 = r0 + 40
+        ref, bud, _ = reference(q[:, r0:r1], k[:, :r1], v[:, :r1], r0, window)
+        check(o[:, r0:r1], ref, bud, f"rows {r0}..{r1}")
+
+
+def test_layouts_and_local_sdpa():
+    """HF hands local_sdpa query [1, H, T, D] as a transposed view of [1, T, H, D] and wants
+    [1, T, H, D] back; strided inputs and outputs give the same bits as contiguous ones."""
+    H, KV, T, D = 8, 1, 200, 256
+    q, k, v = make(H, KV, T, T, D, seed=7, qscale=0.3)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    o = attn.attention(qd, kd, vd, 0, 64)
+    q_thd = qd.transpose(0, 1).contiguous()            # [T, H, D]
+    out, none = attn.local_sdpa(None, q_thd.transpose(0, 1)[None], kd[None], vd[None], None, scaling=1.0,
+                                sliding_window=64)
+    assert none is None and out.shape == (1, T, H, D) and out.is_contiguous()
+    assert torch.equal(out[0].transpose(0, 1), o)
+    full = attn.local_sdpa(None, qd[None], kd[None], vd[None], None, scaling=1.0)[0]
+    assert torch.equal(full[0].transpose(0, 1), attn.full_attention(qd, kd, vd, 0))
+    # decode: one query at the last position against the cache (local_attn.py:74-83)
+    dec = attn.local_sdpa(None, qd[None, :, -1:], kd[None], vd[None], None, scaling=1.0, sliding_window=64)[0]
+    assert torch.equal(dec[0, 0], o[:, -1])
+    # k / v as column slices of a wider buffer
+    kv = torch.cat([kd, vd], 2)
+    o2 = attn.attention(qd, kv[:, :, :D], kv[:, :, D:], 0, 64)
+    assert torch.equal(o, o2)
+
+
+def test_deterministic():
+    q, k, v = make(8, 1, 600, 600, 512, seed=3, qscale=0.3)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    a = attn.attention(qd, kd, vd, 0, 0)
+    b = attn.attention(qd, kd, vd, 0, 0)
+    assert torch.equal(a, b)
+
+
+def test_versus_torch_cpu_flash():
+    """Error against the double-precision oracle, relative to the weight-rounding budget, of ours
+    (within the tolerance) and, for comparison, of torch's CPU sdpa in bf16 (what the reference
+    runs)."""
+    H, KV, T, D, W = 8, 1, 384, 256, 128
+    q, k, v = make(H, KV, T, T, D, seed=5, qscale=0.3)
+    ref, bud, _ = reference(q, k, v, 0, W)
+    ours = check(attn.sliding_attention(q.to(DEV), k.to(DEV), v.to(DEV), 0, W), ref, bud, "ours")
+    qp = torch.arange(T)[:, None]
+    kp = torch.arange(T)[None, :]
+    mask = (kp <= qp) & (qp - kp < W)
+    cpu = F.scaled_dot_product_attention(q[None], k[None], v[None], attn_mask=mask, scale=1.0, enable_gqa=True)[0]
+    theirs = check(cpu, ref, bud, "torch cpu bf16", strict=False)
+    print(f"max |err| / budget: ours {ours:.3g}, torch cpu {theirs:.3g}")
+
+
+def test_errors():
+    q, k, v = make(4, 2, 8, 8, 128, seed=0)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    with pytest.raises(W8A8Error, match="head_dim"):
+        attn.attention(qd[:, :, :64].contiguous(), kd[:, :, :64].contiguous(), vd[:, :, :64].contiguous())
+    with pytest.raises(W8A8Error, match="Tk >= q_start"):
+        attn.attention(qd, kd, vd, q_start=1)
+    with pytest.raises(W8A8Error, match="multiple of KV"):
+        attn.attention(qd[:3], kd, vd)
+    with pytest.raises(ValueError):
+        attn.attention(qd, kd[:, :4], vd)
+    with pytest.raises(ValueError):
+        attn.sliding_attention(qd, kd, vd, 0, 0)
+    # Tq == 0 is a no-op
+    assert attn.attention(qd[:, :0], kd, vd).shape == (4, 0, 128)
