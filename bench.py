@@ -32,6 +32,11 @@ sys.path.insert(0, ROOT)
 
 PEAK_INT8_TOPS = 5000.0   # MI355X dense int8 MFMA, published
 PEAK_HBM_GBS = 8000.0     # MI355X HBM3E, published
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, published
+# Gemma 4 E2B attention: 8 query heads on 1 KV head; 28 sliding layers (head_dim 256, window 512)
+# and 7 full layers (head_dim 512); the reference's benchmark prompt is 3658 tokens.
+ATTN_H, ATTN_KV, ATTN_T = 8, 1, 3658
+ATTN_LAYERS = {"sliding": (256, 512, 28), "full": (512, 0, 7)}
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "gemm_gate_up_m512_traffic.md")
 
 
@@ -265,6 +270,55 @@ def time_chain(M, dev, reps):
 COPY_BYTES = 64 << 20
 
 
+def attention_pairs(q_start, Tq, window):
+    """(query, key) pairs the masked softmax covers for queries q_start .. q_start + Tq - 1."""
+    n = 0
+    for i in range(Tq):
+        p = q_start + i
+        n += p + 1 if window == 0 else min(p + 1, window)
+    return n
+
+
+def attention_inputs(D, T, dev, seed):
+    import torch
+    g = torch.Generator(device=dev).manual_seed(seed)
+    q = (torch.randn(ATTN_H, T, D, generator=g, device=dev) * 0.3).to(torch.bfloat16)
+    k = (torch.randn(ATTN_KV, T, D, generator=g, device=dev) * 0.3).to(torch.bfloat16)
+    v = torch.randn(ATTN_KV, T, D, generator=g, device=dev).to(torch.bfloat16)
+    return q, k, v
+
+
+def attention_bench(dev, reps):
+    """Prefill attention of the 3658-token prompt: each layer kind in one call over the whole prompt,
+    and the reference pipeline's largest per-micro-batch calls (pipeline.py:281-295)."""
+    import torch
+    from w8a8 import attention as attn
+    T = ATTN_T
+    res, total_us = {}, 0.0
+    for name, (D, W, layers) in ATTN_LAYERS.items():
+        q, k, v = attention_inputs(D, T, dev, seed=D)
+        out = torch.empty_like(q)
+        ms = event_time_ms(lambda: attn.attention(q, k, v, 0, W, out=out), reps, 3)
+        flops = 4.0 * D * ATTN_H * attention_pairs(0, T, W)
+        tf = flops / (ms * 1e-3) / 1e12
+        e = {"us": round(ms * 1e3, 1), "tflops": round(tf, 1), "frac_mfma_bf16": round(tf / PEAK_BF16_TFLOPS, 4),
+             "head_dim": D, "window": W, "layers": layers}
+        # the reference's per-micro-batch calls at the end of the prompt: a sliding micro-batch of 512
+        # rows, a full-attention chunk of 256 rows (ATTN_ROWS) against every earlier key
+        r = 512 if W else 256
+        qs = T - r
+        ms_mb = event_time_ms(lambda: attn.attention(q[:, qs:], k, v, qs, W, out=out[:, qs:]), reps, 3)
+        e["last_micro_batch_us"] = round(ms_mb * 1e3, 1)
+        e["last_micro_batch"] = f"{r} queries at position {qs}"
+        res[name] = e
+        total_us += layers * ms * 1e3
+        del q, k, v, out
+    res["prompt_total_us"] = round(total_us, 1)
+    res["what"] = (f"E2B prefill attention at T={T}: H={ATTN_H}, KV={ATTN_KV}; flops = 4 * head_dim * H * "
+                   f"visible (query, key) pairs; prompt_total = 28 sliding + 7 full layers")
+    return res
+
+
 def profile_kernel(groups, dev, launches):
     """The dominant kernel alone, plus one plain copy of COPY_BYTES (read COPY_BYTES, write
     COPY_BYTES) whose FETCH_SIZE / WRITE_SIZE readings give the counters' byte scale."""
@@ -295,6 +349,9 @@ def main():
     ap.add_argument("--profile-gemv", action="store_true",
                     help="for kernel traces / counters: run the packed LM-head GEMV at M=1 (--steps times) and a "
                          "64 MiB device copy that calibrates the byte counters, then exit")
+    ap.add_argument("--profile-attention", action="store_true",
+                    help="for kernel traces: run the whole-prompt sliding and full attention calls at T=3658 "
+                         "(--steps times each) and exit")
     ap.add_argument("--profile-chain", action="store_true",
                     help="for kernel traces: run the device layer chain (--steps times, eager) and exit")
     args = ap.parse_args()
@@ -324,6 +381,16 @@ def main():
             ops.gemv_bf16(x, pw, s, y)
         torch.cuda.synchronize()
         log(f"bench: ran the packed LM-head GEMV (M=1, K={K}, N={N}) {args.steps} times")
+        return 0
+    if args.profile_attention:
+        from w8a8 import attention as attn
+        for name, (D, W, _) in ATTN_LAYERS.items():
+            q, k, v = attention_inputs(D, ATTN_T, dev, seed=D)
+            out = torch.empty_like(q)
+            for _ in range(args.steps):
+                attn.attention(q, k, v, 0, W, out=out)
+            torch.cuda.synchronize()
+            log(f"bench: ran {name} attention (T={ATTN_T}, head_dim {D}, window {W}) {args.steps} times")
         return 0
     if args.profile_chain:
         c = build_chain(M, dev)
@@ -452,6 +519,9 @@ def main():
                                             "row_major_us": round(ms_rm * 1e3, 1),
                                             "row_major_gbs": round(nbytes / (ms_rm * 1e-3) / 1e9, 1)}
             log(f"bench: gemv lm head M={Mg}: {extra[f'gemv_lm_head_m{Mg}']}")
+        torch.cuda.empty_cache()
+        extra["attention_prefill_t3658"] = attention_bench(dev, reps=20)
+        log(f"bench: attention: {extra['attention_prefill_t3658']}")
         torch.cuda.empty_cache()
 
     line = {

@@ -10,34 +10,34 @@
 // window reaches, masked k >= 0, k <= q, q - k < W).  One pass over the visible keys with an
 // online softmax gives the same function without the two-part merge.
 //
-// Work split.  A workgroup of 4 waves owns 128 query rows of one KV group: with G = H / KV heads
+// Work split.  A workgroup of 8 waves owns 128 query rows of one KV group: with G = H / KV heads
 // per group the rows are (position, head) pairs, G heads x 128/G consecutive positions, so the
-// group's G heads share every K / V tile the workgroup loads and the window of 128/G positions
-// wastes few masked keys.  Each wave owns 32 rows and walks the keys in blocks of BN:
+// group's G heads share every K / V block the workgroup loads and the 128/G positions waste few
+// masked keys.  Each wave owns 16 rows and walks the keys in blocks of BN:
 //
-//   S^T = K Q^T   (v_mfma_f32_32x32x16_bf16, K from LDS as the A operand, Q held in registers as
+//   S^T = K Q^T   (v_mfma_f32_16x16x32_bf16, K from LDS as the A operand, Q held in registers as
 //                  the B operand), so a lane's accumulator column is one query and the softmax
-//                  statistics are lane-local but for one exchange between the two lane halves;
+//                  statistics are lane-local but for two exchanges between the four lane groups;
 //   P^T = exp2((S^T - m) * scale * log2 e), rounded to bf16;
-//   O^T += V^T P^T  (V^T from LDS as the A operand, P^T straight from the S^T accumulator as the
+//   O^T += V^T P^T  (V^T from LDS as the A operand, P^T straight from the S^T accumulators as the
 //                  B operand), so O's rescaling by the running maximum is lane-local too.
 //
-// For P^T to be usable in place, row rho of the S^T tile holds key pi(rho), pi swapping bits 2
-// and 3: then accumulator register i of lane half hf holds key 16*(i/8) + 8*hf + i%8, which is
-// exactly the k-slot order the next MFMA's B operand expects, and the matching V^T operand is 8
-// consecutive keys, one ds_read_b128.
+// For P^T to be usable in place, the rows of each pair of 16-key S^T tiles hold their 32 keys in
+// the order that makes register i of lane group qq hold keys 8 qq + {i, 4 + i}: exactly the
+// k-slot order of the next MFMA's B operand, whose V^T operand is then 8 consecutive keys, one
+// ds_read_b128.
 //
 // Data movement.  K blocks go from HBM (mostly L2: every workgroup of a group reads the same
 // keys) straight into a 2-slot LDS ring with buffer_load ... lds, one block ahead; 16-byte chunks
 // of a key row are XOR-swizzled by the row so that the 16 rows one ds_read_b128 touches hit
 // distinct banks.  V blocks are loaded into registers one block ahead and written transposed
 // (V^T [D][BN + 8], 8-byte stores of 4 keys) into a 2-slot ring.  Loads past the end of K / V
-// read zero and are masked.
+// read zero and are masked.  One barrier per block.
 #include "w8a8_common.h"
 
 namespace w8a8 {
 
-typedef float v16f __attribute__((ext_vector_type(16)));
+constexpr int ATTN_NW = 8;  // waves per workgroup, 16 query rows each
 
 struct AttnParams {
   const uint16_t* q; int64_t qhs, qrs;  // bf16 [H, Tq, D] (element strides, last dim contiguous)
@@ -67,64 +67,38 @@ __device__ __forceinline__ int attn_xcd_remap(int b, int nblocks) {
   return (b & 7) * per + (b >> 3);
 }
 
-// Row-within-a-32-key-tile of the key held by S^T row rho (and its inverse): bits 2 and 3 swapped.
-__device__ __forceinline__ int pi_row(int rho) { return (rho & ~12) | ((rho & 4) << 1) | ((rho & 8) >> 1); }
 
-// Schedule the N operand reads (ds_read) and N MFMAs before this point as LEAD reads, then
-// MFMA / read pairs, so that few fragments are live at once.
-template <int N, int LEAD = 3>
-__device__ __forceinline__ void interleave() {
-  constexpr int L = N < LEAD ? N : LEAD;
-#pragma unroll
-  for (int i = 0; i < L; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-#pragma unroll
-  for (int i = 0; i < N - L; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-  }
-#pragma unroll
-  for (int i = 0; i < L; ++i) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-}
-
-template <int D, int BN, int DS>
-__global__ __launch_bounds__(256 * DS, 1) void attn_fwd_kernel(AttnParams p) {
+template <int D, int BN, int NW>
+__global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(AttnParams p) {
   static_assert(D == 128 || D == 256 || D == 512, "head_dim 128, 256 or 512");
-  static_assert(BN == 32 || BN == 64, "key block 32 or 64");
-  static_assert(DS == 1 || DS == 2, "head_dim split over 1 or 2 waves");
-  constexpr int NW = 4 * DS;                          // waves: 4 query groups x DS head_dim parts
+  static_assert(BN == 32 || BN == 64 || BN == 128, "key block 32, 64 or 128");
   constexpr int NT = NW * 64;
-  constexpr int DH = D / DS;                          // head_dim columns of q and o per wave
   constexpr int KCH = D / 8;                          // 16-byte chunks per key row
-  constexpr int K_SLOTS = DS == 1 ? 2 : 1;
   constexpr int K_SLOT = BN * D * 2;                  // bytes of one K block
   constexpr int VLD = BN + 8;                         // padded V^T row, elements
   constexpr int V_SLOT = D * VLD * 2;                 // bytes of one V^T block
-  constexpr int NST = BN / 32;                        // 32-key tiles per block
-  constexpr int X_BYTES = DS == 1 ? 0 : NW * NST * 16 * 64 * 4;  // partial-score exchange
+  constexpr int NKC = BN / 32;                        // 32-key chunks per block
   constexpr int KU = BN * KCH / NT;                   // K DMA instructions per wave per block
   constexpr int KG = BN / 4;                          // 4-key groups of a V block
   constexpr int VP = D * BN / (8 * 4 * NT);           // V staging passes per thread
-  constexpr int NDT = DH / 32;                        // 32-wide d tiles of this wave's O^T
+  constexpr int NDT = D / 16;                         // 16-wide d tiles of O^T
+  constexpr int NKK = D / 32;                         // k-steps of S^T
   static_assert(KU * NT == BN * KCH && VP * 8 * 4 * NT == D * BN, "tiling");
-  constexpr int V_OFF = K_SLOTS * K_SLOT, X_OFF = V_OFF + 2 * V_SLOT;
-  static_assert(X_OFF + X_BYTES <= 160 * 1024, "LDS");
-  __shared__ __attribute__((aligned(1024))) char lds[X_OFF + X_BYTES];
+  constexpr int V_OFF = 2 * K_SLOT;
+  static_assert(V_OFF + 2 * V_SLOT <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(1024))) char lds[V_OFF + 2 * V_SLOT];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int qi = lane & 31, hf = lane >> 5;
-  const int qg = wave & 3, dp = wave >> 2;  // query group, head_dim part
+  const int qi = lane & 15, qq = lane >> 4;  // query column, lane group
 
   // ---- which KV group and query rows -------------------------------------------------------
   const int nblocks = p.KV * p.ntiles;
-  int lb;
-  if (p.window > 0)
-    lb = attn_xcd_remap(blockIdx.x, nblocks);  // neighbouring tiles share their window's keys
-  else
-    lb = blockIdx.x;                           // causal: the longest tiles first, every XCD a mix
+  const int lb = p.window > 0 ? attn_xcd_remap(blockIdx.x, nblocks) : int(blockIdx.x);
   const int g = lb / p.ntiles;
+  // causal: the longest tiles first, and consecutive workgroups (other XCDs) a mix of lengths
   const int tile = p.window > 0 ? lb % p.ntiles : p.ntiles - 1 - lb % p.ntiles;
   const int i0 = tile * p.PB;
-  const int r = qg * 32 + qi;
+  const int r = wave * 16 + qi;
   const int hl = r % p.G, pl = r / p.G;
   const int qrow = i0 + pl;
   const bool valid = pl < p.PB && qrow < p.Tq;
@@ -141,28 +115,28 @@ __global__ __launch_bounds__(256 * DS, 1) void attn_fwd_kernel(AttnParams p) {
   const __amdgpu_buffer_rsrc_t rk = make_rsrc(p.k + int64_t(g) * p.khs, p.k_bytes);
   const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.v + int64_t(g) * p.vhs, p.v_bytes);
 
-  // ---- Q fragments: B operand, lane (qi, hf) holds q[row qi][dp*DH + 16 kk + 8 hf .. + 7] ----
-  v8bf qf[DH / 16];
+  // ---- Q fragments: B operand of v_mfma_f32_16x16x32_bf16, lane (qi, qq) holds
+  // q[row qi][32 kk + 8 qq .. + 7] ---------------------------------------------------------------
+  v8bf qf[NKK];
   {
-    const uint16_t* qp = p.q + int64_t(h) * p.qhs + int64_t(qrow) * p.qrs + dp * DH + 8 * hf;
+    const uint16_t* qp = p.q + int64_t(h) * p.qhs + int64_t(qrow) * p.qrs + 8 * qq;
 #pragma unroll
-    for (int kk = 0; kk < DH / 16; ++kk) {
+    for (int kk = 0; kk < NKK; ++kk) {
       v4i t = v4i{0, 0, 0, 0};
-      if (valid) t = *reinterpret_cast<const v4i*>(qp + 16 * kk);
+      if (valid) t = *reinterpret_cast<const v4i*>(qp + 32 * kk);
       qf[kk] = __builtin_bit_cast(v8bf, t);
     }
   }
 
   // ---- staging ------------------------------------------------------------------------------
   // K chunk x = (u * NW + wave) * 64 + lane of a block: key row x / KCH, stored chunk x % KCH,
-  // holding source chunk (x % KCH) ^ swz(row), swz = the row's low 4 bits with bits 2 and 3
-  // swapped.  A reader of key row pi(qi) (+ 32 st) then finds chunk c at c ^ (qi & 15).
+  // holding source chunk (x % KCH) ^ swz(row), swz(row) = (row & 3) | ((row >> 1) & 12).
   uint32_t koff[KU];
 #pragma unroll
   for (int u = 0; u < KU; ++u) {
     const int x = (u * NW + wave) * 64 + lane;
     const int row = x / KCH, cs = x % KCH;
-    const int c = cs ^ pi_row(row & 15);
+    const int c = cs ^ ((row & 3) | ((row >> 1) & 12));
     koff[u] = uint32_t(row) * uint32_t(p.krs) * 2u + uint32_t(c) * 16u;
   }
   auto issue_k = [&](int kb, int slot) {
@@ -206,22 +180,23 @@ __global__ __launch_bounds__(256 * DS, 1) void attn_fwd_kernel(AttnParams p) {
     }
   };
 
-  // This lane's K operand within a block: key row pi(qi) (+ 32 per 32-key tile), chunk
-  // 2*kk + hf of the head_dim, stored at that chunk ^ (qi & 15).  The XOR only touches a chunk's
-  // low 4 bits, so chunk 16*(kk/8) + (2*(kk%8) + hf) is found at kofs[kk % 8] + 256*(kk/8).
-  static_assert((DH / 16) % 8 == 0, "K operand offsets assume whole 16-chunk groups per wave");
-  uint32_t kofs[8];
+  // S^T tile 2c + hh (16 keys x 16 queries) row rho = 4 a + b holds key 32 c + 8 a + 4 hh + b, so
+  // register i of lane group qq of tiles 2c, 2c+1 holds keys 32 c + 8 qq + {i, 4 + i}: the k-slot
+  // order of the B operand of the O^T product.  This lane's A operand (row rho = qi) is key row
+  // 32 c + 4 hh + krow, stored chunk (4 kk + qq) ^ qi (swz of that row is qi), i.e. at
+  // kofs[kk % 4] + 256 (kk / 4) within the row.
+  const int krow = 8 * (qi >> 2) + (qi & 3);
+  uint32_t kofs[4];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) kofs[j] = uint32_t((pi_row(qi) * KCH + ((2 * j + hf) ^ (qi & 15))) * 16);
+  for (int j = 0; j < 4; ++j) kofs[j] = uint32_t(krow * KCH * 16 + (((4 * j + qq) ^ qi) * 16));
+  const uint32_t vofs = uint32_t((qi * VLD + 8 * qq) * 2);  // V^T row d = qi, keys 8 qq ..
 
   // ---- main loop -----------------------------------------------------------------------------
-  v16f o[NDT];
+  v4f o[NDT];
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) o[dt][e] = 0.0f;
+  for (int dt = 0; dt < NDT; ++dt) o[dt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
   float m = -__builtin_inff();  // running maximum of the raw scores of this lane's query
-  float l = 0.0f;               // this lane half's share of sum exp2((s - m) * c)
+  float l = 0.0f;               // this lane group's share of sum exp2((s - m) * c)
   const float c = p.c;
   const int win = p.window;
   const int Tk = p.Tk;
@@ -234,127 +209,93 @@ __global__ __launch_bounds__(256 * DS, 1) void attn_fwd_kernel(AttnParams p) {
   for (int n = 0; n < nblk; ++n) {
     const int kb = kb0 + n * BN;
     const int slot = n & 1;
-    const int kslot = K_SLOTS == 2 ? slot : 0;
     attn_wait_vmcnt<0>();
     __syncthreads();  // K and V^T of block n are in LDS; the other slots are free
-    if (DS == 1 && n + 1 < nblk) {
+    if (n + 1 < nblk) {
       issue_k(kb + BN, slot ^ 1);
       load_v(kb + BN);
     }
 
-    // S^T = K Q^T over this wave's head_dim part
-    v16f s[NST];
-    const char* kbase = lds + kslot * K_SLOT + dp * (DH / 16 / 8) * 256;
+    // S^T = K Q^T: 2 NKC independent accumulators
+    v4f s[2 * NKC];
+    const char* kbase = lds + slot * K_SLOT;
 #pragma unroll
-    for (int st = 0; st < NST; ++st) {
+    for (int t = 0; t < 2 * NKC; ++t) s[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int e = 0; e < 16; ++e) s[st][e] = 0.0f;
+    for (int kk = 0; kk < NKK; ++kk)
 #pragma unroll
-      for (int kk = 0; kk < DH / 16; ++kk) {
-        const v8bf a = *reinterpret_cast<const v8bf*>(kbase + kofs[kk % 8] + st * (32 * KCH * 16) + (kk / 8) * 256);
-        s[st] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], s[st], 0, 0, 0);
+      for (int t = 0; t < 2 * NKC; ++t) {
+        const int row0 = 32 * (t >> 1) + 4 * (t & 1);
+        const v8bf a = *reinterpret_cast<const v8bf*>(kbase + kofs[kk % 4] + row0 * (KCH * 16) + (kk / 4) * 256);
+        s[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[kk], s[t], 0, 0, 0);
       }
-    }
-    interleave<NST * (DH / 16)>();
-    if constexpr (DS == 2) {
-      // Add the partner wave's half of the dot products, in the same order on both waves.
-      // Wave w's partial tile at X_OFF + w * NST * 4 KiB, register e of lane l at (e * 64 + l) * 4.
-      const int wu = __builtin_amdgcn_readfirstlane(wave);
-      float* xw = reinterpret_cast<float*>(lds + X_OFF + wu * (NST * 4096)) + lane;
-      const float* xr = reinterpret_cast<const float*>(lds + X_OFF + (wu ^ 4) * (NST * 4096)) + lane;
-#pragma unroll
-      for (int st = 0; st < NST; ++st)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) xw[(st * 16 + e) * 64] = s[st][e];
-      __syncthreads();  // partials published; every wave is done with K block n
-      if (n + 1 < nblk) issue_k(kb + BN, 0);
-#pragma unroll
-      for (int st = 0; st < NST; ++st)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const float other = xr[(st * 16 + e) * 64];
-          s[st][e] = dp == 0 ? s[st][e] + other : other + s[st][e];
-        }
-      __builtin_amdgcn_sched_barrier(0);
-      if (n + 1 < nblk) load_v(kb + BN);
-    }
 
     // mask, block maximum, online softmax
     const bool edge = !valid || kb + BN - 1 > pmin || (win > 0 && kb < pmax - win + 1) || kb + BN > Tk;
     if (edge) {
 #pragma unroll
-      for (int st = 0; st < NST; ++st)
+      for (int t = 0; t < 2 * NKC; ++t)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int key = kb + 32 * st + 16 * (e / 8) + 8 * hf + (e % 8);
+        for (int i = 0; i < 4; ++i) {
+          const int key = kb + 32 * (t >> 1) + 8 * qq + 4 * (t & 1) + i;
           const bool vis = valid && key <= pos && key < Tk && (win == 0 || pos - key < win);
-          if (!vis) s[st][e] = -__builtin_inff();
+          if (!vis) s[t][i] = -__builtin_inff();
         }
     }
     float bm = -__builtin_inff();
 #pragma unroll
-    for (int st = 0; st < NST; ++st)
+    for (int t = 0; t < 2 * NKC; ++t)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) bm = fmaxf(bm, s[st][e]);
+      for (int i = 0; i < 4; ++i) bm = fmaxf(bm, s[t][i]);
+    bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
     bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
     const float mn = fmaxf(m, bm);
     const float ms = mn == -__builtin_inff() ? 0.0f : mn * c;
     const float alpha = __builtin_amdgcn_exp2f(__builtin_fmaf(m, c, -ms));
     m = mn;
     float bs = 0.0f;
-    v8bf pb[NST][2];
+    v8bf pb[NKC];
 #pragma unroll
-    for (int st = 0; st < NST; ++st)
+    for (int ch = 0; ch < NKC; ++ch)
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float pe = __builtin_amdgcn_exp2f(__builtin_fmaf(s[st][8 * half + e], c, -ms));
-          bs += pe;
-          pb[st][half][e] = (__bf16)pe;
-        }
+      for (int j = 0; j < 8; ++j) {
+        const float pe = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * ch + (j >> 2)][j & 3], c, -ms));
+        bs += pe;
+        pb[ch][j] = (__bf16)pe;
       }
     l = l * alpha + bs;
     if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
+      for (int dt = 0; dt < NDT; ++dt) o[dt] *= alpha;
     }
 
-    // O^T += V^T P^T over this wave's head_dim part
-    const char* vbase = lds + V_OFF + slot * V_SLOT;
+    // O^T += V^T P^T
+    const char* vbase = lds + V_OFF + slot * V_SLOT + vofs;
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
+    for (int ch = 0; ch < NKC; ++ch)
 #pragma unroll
-      for (int st = 0; st < NST; ++st)
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          const int d = dp * DH + 32 * dt + qi;
-          const v8bf a = *reinterpret_cast<const v8bf*>(vbase + (d * VLD + 32 * st + 16 * half + 8 * hf) * 2);
-          o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[st][half], o[dt], 0, 0, 0);
-        }
-    interleave<NDT * NST * 2>();
+      for (int dt = 0; dt < NDT; ++dt) {
+        const v8bf a = *reinterpret_cast<const v8bf*>(vbase + (16 * dt * VLD + 32 * ch) * 2);
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[ch], o[dt], 0, 0, 0);
+      }
 
     if (n + 1 < nblk) store_vt(slot ^ 1);
   }
 
   // ---- normalise and store --------------------------------------------------------------------
-  const float lt = l + __shfl_xor(l, 32, 64);
+  float lt = l + __shfl_xor(l, 16, 64);
+  lt += __shfl_xor(lt, 32, 64);
   if (!valid) return;
   const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-  uint16_t* op = p.o + int64_t(h) * p.ohs + int64_t(qrow) * p.ors + dp * DH;
+  uint16_t* op = p.o + int64_t(h) * p.ohs + int64_t(qrow) * p.ors + 4 * qq;
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-    for (int gq = 0; gq < 4; ++gq) {
-      const int d = 32 * dt + 8 * gq + 4 * hf;
-      v2u w;
-      w[0] = pack_bf16x2(o[dt][4 * gq] * inv, o[dt][4 * gq + 1] * inv);
-      w[1] = pack_bf16x2(o[dt][4 * gq + 2] * inv, o[dt][4 * gq + 3] * inv);
-      *reinterpret_cast<v2u*>(op + d) = w;
-    }
-  if (p.lse && hf == 0 && dp == 0)
+  for (int dt = 0; dt < NDT; ++dt) {
+    v2u w;
+    w[0] = pack_bf16x2(o[dt][0] * inv, o[dt][1] * inv);
+    w[1] = pack_bf16x2(o[dt][2] * inv, o[dt][3] * inv);
+    *reinterpret_cast<v2u*>(op + 16 * dt) = w;
+  }
+  if (p.lse && qq == 0)
     p.lse[int64_t(h) * p.Tq + qrow] = lt > 0.0f ? m * p.scale + __logf(lt) : -__builtin_inff();
 }
 
@@ -395,7 +336,7 @@ extern "C" int w8a8_attention_bf16(const uint16_t* q, int64_t q_head_stride, int
   p.o = o; p.ohs = o_head_stride; p.ors = o_row_stride;
   p.lse = lse;
   p.k_bytes = uint32_t(kb); p.v_bytes = uint32_t(vb);
-  p.H = int(H); p.KV = int(KV); p.G = int(H / KV); p.PB = 128 / p.G;
+  p.H = int(H); p.KV = int(KV); p.G = int(H / KV); p.PB = ATTN_NW * 16 / p.G;
   p.Tq = int(Tq); p.Tk = int(Tk); p.q_start = int(q_start); p.window = int(window);
   p.ntiles = int((Tq + p.PB - 1) / p.PB);
   p.scale = scale; p.c = scale * 1.4426950408889634f;
@@ -403,10 +344,10 @@ extern "C" int w8a8_attention_bf16(const uint16_t* q, int64_t q_head_stride, int
   if (nwg > INT32_MAX) return fail(W8A8_ENOTSUP, "attention: too many query tiles");
   const dim3 grid{unsigned(nwg), 1, 1};
   if (D == 128)
-    attn_fwd_kernel<128, 64, 1><<<grid, dim3{256, 1, 1}, 0, stream>>>(p);
+    attn_fwd_kernel<128, 128, ATTN_NW><<<grid, dim3{ATTN_NW * 64, 1, 1}, 0, stream>>>(p);
   else if (D == 256)
-    attn_fwd_kernel<256, 64, 1><<<grid, dim3{256, 1, 1}, 0, stream>>>(p);
+    attn_fwd_kernel<256, 64, ATTN_NW><<<grid, dim3{ATTN_NW * 64, 1, 1}, 0, stream>>>(p);
   else
-    attn_fwd_kernel<512, 32, 2><<<grid, dim3{512, 1, 1}, 0, stream>>>(p);
+    attn_fwd_kernel<512, 32, ATTN_NW><<<grid, dim3{ATTN_NW * 64, 1, 1}, 0, stream>>>(p);
   return check_launch("attention_bf16");
 }
