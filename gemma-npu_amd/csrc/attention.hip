@@ -37,6 +37,9 @@
 
 namespace w8a8 {
 
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef short v8s __attribute__((ext_vector_type(8)));
+
 constexpr int ATTN_NW = 8;  // waves per workgroup, 16 query rows each
 
 struct AttnParams {
@@ -299,6 +302,248 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(AttnParams p) {
     p.lse[int64_t(h) * p.Tq + qrow] = lt > 0.0f ? m * p.scale + __logf(lt) : -__builtin_inff();
 }
 
+// ---- decode: one query per head, keys split into chunks --------------------------------------
+//
+// The reference's decode step (local_attn.py:44-68, _split_kv_decode; local_sdpa's decode branch,
+// local_attn.py:74-83) attends one query per head to the cache (or its last W entries), splitting
+// the keys into chunks whose partial results are merged by their logsumexp.  Here
+// attn_decode_split_kernel computes, per (KV group, chunk of 32 or 64 keys), the G heads' chunk
+// maximum M, sum L = sum_j exp2((s_j - M) c) and unnormalised o = sum_j bf16(exp2((s_j - M) c)) v_j;
+// attn_decode_merge_kernel combines the chunks in chunk order (deterministic).
+//
+// Split kernel, 4 waves: the chunk's K and V rows are loaded into LDS at once by DMA.  Wave w
+// computes the 16-key S^T tile w (16x16x32 bf16 MFMA, K rows from LDS as the A operand, the G <= 16
+// query rows in registers as the B operand); the chunk's softmax goes through LDS; then wave w
+// computes O^T for head_dim columns [w D/4, (w+1) D/4) as V^T P^T, its V^T operand read from the
+// row-major V rows with ds_read_b64_tr_b16 (result lane i, slot j = lane 4j + i/4's element i%4 of a
+// 16-lane group), its P^T operand from LDS.
+// keys per chunk: 64 (32 at head_dim 512, so that two workgroups fit in a CU's LDS)
+__host__ __device__ constexpr int dec_chunk(int D) { return D >= 512 ? 32 : 64; }
+
+struct DecodeParams {
+  const uint16_t* q; int64_t qhs;       // bf16 [H, D]
+  const uint16_t* k; int64_t khs, krs;  // bf16 [KV, Tk, D]
+  const uint16_t* v; int64_t vhs, vrs;
+  uint16_t* o; int64_t ohs;             // bf16 [H, D]
+  float* lse;                           // [H] or null
+  float* part_o;                        // [KV][nchunk][G][D] unnormalised partial outputs
+  float* part_ml;                       // [KV][nchunk][G][2] chunk maximum and sum
+  uint32_t k_bytes, v_bytes;
+  int H, KV, G, Tk, klo, pos, nchunk;
+  float scale, c;
+};
+
+template <int D>
+__global__ __launch_bounds__(256, 2) void attn_decode_split_kernel(DecodeParams p) {
+  constexpr int DEC_C = dec_chunk(D);
+  constexpr int KCH = D / 8;                 // 16-byte chunks per row
+  constexpr int ROW = D * 2;                 // bytes per K / V row
+  constexpr int KV_BYTES = DEC_C * ROW;      // one chunk of K (or V)
+  constexpr int PLD = DEC_C + 8;             // padded P row, elements
+  constexpr int NKK = D / 32;
+  constexpr int NDT = D / 64;                // 16-wide d tiles per wave
+  constexpr int DMA = DEC_C * KCH / 256;     // DMA instructions per thread per operand
+  __shared__ __attribute__((aligned(1024))) char lds[2 * KV_BYTES + 16 * PLD * 2 + 2 * 4 * 16 * 4];
+  char* const kl = lds;
+  char* const vl = lds + KV_BYTES;
+  uint16_t* const pl = reinterpret_cast<uint16_t*>(lds + 2 * KV_BYTES);
+  float* const smax = reinterpret_cast<float*>(lds + 2 * KV_BYTES + 16 * PLD * 2);  // [4 waves][16]
+  float* const ssum = smax + 64;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int qi = lane & 15, qq = lane >> 4;
+  const int g = blockIdx.x / p.nchunk, chunk = blockIdx.x % p.nchunk;
+  const int kc = p.klo + chunk * DEC_C;      // first key of the chunk
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(p.k + int64_t(g) * p.khs, p.k_bytes);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.v + int64_t(g) * p.vhs, p.v_bytes);
+
+  // K chunk x of row r lands at stored chunk x ^ (r & 15); V chunk x of row r at x ^ 2 (r & 3).
+#pragma unroll
+  for (int u = 0; u < DMA; ++u) {
+    const int x = (u * 4 + wave) * 64 + lane;
+    const int r = x / KCH, cs = x % KCH;
+    const uint32_t row = uint32_t(kc + r);
+    attn_dma16(rk, kl + (u * 4 + wave) * 1024, row * uint32_t(p.krs) * 2u + uint32_t(cs ^ (r & 15)) * 16u);
+    attn_dma16(rv, vl + (u * 4 + wave) * 1024, row * uint32_t(p.vrs) * 2u + uint32_t(cs ^ (2 * (r & 3))) * 16u);
+  }
+  // Q rows (B operand): lane (qi, qq) holds q[head g*G + qi][32 kk + 8 qq .. + 7], zero past G.
+  v8bf qf[NKK];
+  {
+    const bool has = qi < p.G;
+    const uint16_t* qp = p.q + int64_t(g * p.G + (has ? qi : 0)) * p.qhs + 8 * qq;
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk) {
+      v4i t = v4i{0, 0, 0, 0};
+      if (has) t = *reinterpret_cast<const v4i*>(qp + 32 * kk);
+      qf[kk] = __builtin_bit_cast(v8bf, t);
+    }
+  }
+  attn_wait_vmcnt<0>();
+  __syncthreads();
+
+  // S^T tile: keys 16 wave + 4 qq + i (i = 0..3) of the chunk, query qi; two accumulators.
+  const bool has_tile = 16 * wave < DEC_C;
+  v4f s0 = v4f{0.0f, 0.0f, 0.0f, 0.0f}, s1 = s0;
+  if (has_tile) {
+    const int r = 16 * wave + qi;
+    const char* kr = kl + r * ROW;
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk) {
+      const v8bf a = *reinterpret_cast<const v8bf*>(kr + (((4 * kk + qq) ^ qi) * 16));
+      if (kk & 1)
+        s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[kk], s1, 0, 0, 0);
+      else
+        s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[kk], s0, 0, 0, 0);
+    }
+  }
+  float sc[4];
+  float bm = -__builtin_inff();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int key = kc + 16 * wave + 4 * qq + i;
+    sc[i] = (has_tile && key <= p.pos && key < p.Tk) ? s0[i] + s1[i] : -__builtin_inff();
+    bm = fmaxf(bm, sc[i]);
+  }
+  bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
+  bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+  if (qq == 0) smax[wave * 16 + qi] = bm;
+  __syncthreads();
+  float M = fmaxf(fmaxf(smax[qi], smax[16 + qi]), fmaxf(smax[32 + qi], smax[48 + qi]));
+  const float ms = M == -__builtin_inff() ? 0.0f : M * p.c;
+  float ls = 0.0f;
+  v4u pw;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float pe = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[i], p.c, -ms));
+    ls += pe;
+    reinterpret_cast<uint16_t*>(&pw)[i] = f32_to_bf16(pe);
+  }
+  if (has_tile) *reinterpret_cast<v2u*>(pl + qi * PLD + 16 * wave + 4 * qq) = v2u{pw[0], pw[1]};
+  ls += __shfl_xor(ls, 16, 64);
+  ls += __shfl_xor(ls, 32, 64);
+  if (qq == 0) ssum[wave * 16 + qi] = ls;
+  __syncthreads();
+
+  // O^T for d in [wave D/4, (wave+1) D/4): V^T operand by transposing reads of the V rows.
+  v4f o[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) o[dt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  const int srow = qq * 8 + (qi >> 2);  // this lane's source row (+ 32 c, + 4 for slots 4..7)
+#pragma unroll
+  for (int c = 0; c < DEC_C / 32; ++c) {
+    const v8bf b = *reinterpret_cast<const v8bf*>(pl + qi * PLD + 32 * c + 8 * qq);
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      const int d = wave * (D / 4) + 16 * dt + 4 * (qi & 3);  // this lane's 4 source columns
+      v4s lo, hi;
+      {
+        const int r = 32 * c + srow;
+        const int cs = (d >> 3) ^ (2 * (r & 3));
+        lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) v4s*)(vl + r * ROW + cs * 16 + (d & 7) * 2));
+      }
+      {
+        const int r = 32 * c + srow + 4;
+        const int cs = (d >> 3) ^ (2 * (r & 3));
+        hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) v4s*)(vl + r * ROW + cs * 16 + (d & 7) * 2));
+      }
+      const v8s a8 = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a8), b, o[dt], 0, 0, 0);
+    }
+  }
+
+  // partial results: O^T register i of lane (qi, qq) is d = wave D/4 + 16 dt + 4 qq + i, head qi
+  if (qi < p.G) {
+    const int64_t base = (int64_t(g) * p.nchunk + chunk) * p.G + qi;
+    float* po = p.part_o + base * D + wave * (D / 4) + 4 * qq;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) *reinterpret_cast<v4f*>(po + 16 * dt) = o[dt];
+    if (wave == 0 && qq == 0) {
+      const float L = ssum[qi] + ssum[16 + qi] + ssum[32 + qi] + ssum[48 + qi];
+      p.part_ml[base * 2] = M;
+      p.part_ml[base * 2 + 1] = L;
+    }
+  }
+}
+
+// Workgroups of 256 threads per (head, 64 output columns): M = max_c M_c, w_c = exp2((M_c - M) c),
+// o = sum_c w_c o_c / sum_c w_c L_c.  The chunk statistics are read in parallel into LDS, the sums
+// run in chunk order (deterministic); the two halves of the workgroup take alternate chunks of the
+// output sum and are added in a fixed order.
+constexpr int DEC_MAX_CHUNKS = 4096;
+constexpr int DEC_MCOLS = 16;  // float4 output columns per merge workgroup
+
+template <int D>
+__global__ __launch_bounds__(256) void attn_decode_merge_kernel(DecodeParams p) {
+  __shared__ float wsh[DEC_MAX_CHUNKS];
+  __shared__ float red[256];
+  const int h = blockIdx.x, g = h / p.G, hl = h % p.G;
+  const int t = threadIdx.x;
+  const float* ml = p.part_ml + (int64_t(g) * p.nchunk * p.G + hl) * 2;  // chunk c at ml[c * G * 2]
+  float mx = -__builtin_inff();
+  for (int c = t; c < p.nchunk; c += 256) {
+    const float m = ml[int64_t(c) * p.G * 2];
+    wsh[c] = m;
+    mx = fmaxf(mx, m);
+  }
+  red[t] = mx;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (t < s) red[t] = fmaxf(red[t], red[t + s]);
+    __syncthreads();
+  }
+  const float M = red[0];
+  __syncthreads();
+  const float ms = M == -__builtin_inff() ? 0.0f : M * p.c;
+  float lsum = 0.0f;
+  for (int c = t; c < p.nchunk; c += 256) {
+    const float w = __builtin_amdgcn_exp2f(__builtin_fmaf(wsh[c], p.c, -ms));
+    wsh[c] = w;
+    lsum = __builtin_fmaf(w, ml[int64_t(c) * p.G * 2 + 1], lsum);
+  }
+  red[t] = lsum;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (t < s) red[t] += red[t + s];
+    __syncthreads();
+  }
+  const float L = red[0];
+  // output columns: this workgroup's DEC_MCOLS float4 columns (blockIdx.y); thread t handles
+  // column t % DEC_MCOLS of chunks t / DEC_MCOLS, + PARTS, ..., eight loads in flight at a time
+  constexpr int COLS = DEC_MCOLS, PARTS = 256 / COLS;
+  const int col = blockIdx.y * COLS + t % COLS, part = t / COLS;
+  v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  const float* po = p.part_o + (int64_t(g) * p.nchunk * p.G + hl) * D + 4 * col;  // chunk c at po[c * G * D]
+  for (int c0 = part; c0 < p.nchunk; c0 += 8 * PARTS) {
+    v4f oc[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int c = c0 + u * PARTS;
+      oc[u] = c < p.nchunk ? *reinterpret_cast<const v4f*>(po + int64_t(c) * p.G * D) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int c = c0 + u * PARTS;
+      const float w = c < p.nchunk ? wsh[c] : 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(w, oc[u][i], acc[i]);
+    }
+  }
+  // fold the PARTS partial sums in order 0, 1, ..
+  __shared__ v4f parts[256];
+  parts[t] = acc;
+  __syncthreads();
+  if (part != 0) return;
+  for (int q = 1; q < PARTS; ++q) acc += parts[q * COLS + t % COLS];
+  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+  v2u w2;
+  w2[0] = pack_bf16x2(acc[0] * inv, acc[1] * inv);
+  w2[1] = pack_bf16x2(acc[2] * inv, acc[3] * inv);
+  *reinterpret_cast<v2u*>(p.o + int64_t(h) * p.ohs + 4 * col) = w2;
+  if (p.lse && col == 0) p.lse[h] = L > 0.0f ? M * p.scale + __logf(L) : -__builtin_inff();
+}
+
 }  // namespace w8a8
 
 using namespace w8a8;
@@ -350,4 +595,79 @@ extern "C" int w8a8_attention_bf16(const uint16_t* q, int64_t q_head_stride, int
   else
     attn_fwd_kernel<512, 32, ATTN_NW><<<grid, dim3{ATTN_NW * 64, 1, 1}, 0, stream>>>(p);
   return check_launch("attention_bf16");
+}
+
+static void decode_geometry(int64_t D, int64_t q_pos, int64_t window, int& klo, int& nchunk) {
+  klo = window > 0 ? int(q_pos - window + 1 > 0 ? q_pos - window + 1 : 0) : 0;
+  nchunk = int((q_pos - klo) / dec_chunk(int(D)) + 1);
+}
+
+extern "C" int64_t w8a8_attention_decode_workspace_bytes(int64_t H, int64_t KV, int64_t Tk, int64_t D, int64_t q_pos,
+                                                         int64_t window) {
+  if (H < 1 || KV < 1 || H % KV != 0 || H / KV > 16 || (D != 128 && D != 256 && D != 512) || Tk < 1 || q_pos < 0 ||
+      q_pos >= Tk || window < 0)
+    return -1;
+  int klo, nchunk;
+  decode_geometry(D, q_pos, window, klo, nchunk);
+  return int64_t(KV) * nchunk * (H / KV) * (D + 2) * 4;
+}
+
+extern "C" int w8a8_attention_decode_bf16(const uint16_t* q, int64_t q_head_stride, const uint16_t* k,
+                                          int64_t k_head_stride, int64_t k_row_stride, const uint16_t* v,
+                                          int64_t v_head_stride, int64_t v_row_stride, int64_t H, int64_t KV,
+                                          int64_t Tk, int64_t D, int64_t q_pos, int64_t window, float scale,
+                                          uint16_t* o, int64_t o_head_stride, float* lse, void* workspace,
+                                          int64_t workspace_bytes, hipStream_t stream) {
+  if (H < 1 || KV < 1 || H % KV != 0 || H / KV > 16)
+    return fail(W8A8_EINVAL, "attention_decode: H=%lld KV=%lld (H must be a multiple of KV, at most 16 heads per KV head)",
+                (long long)H, (long long)KV);
+  if (D != 128 && D != 256 && D != 512)
+    return fail(W8A8_ENOTSUP, "attention_decode: head_dim %lld (supported: 128, 256, 512)", (long long)D);
+  if (Tk < 1 || Tk > INT32_MAX || q_pos < 0 || q_pos >= Tk || window < 0)
+    return fail(W8A8_EINVAL, "attention_decode: Tk=%lld q_pos=%lld window=%lld (need 0 <= q_pos < Tk)", (long long)Tk,
+                (long long)q_pos, (long long)window);
+  {
+    int klo, nchunk;
+    decode_geometry(D, q_pos, window, klo, nchunk);
+    if (nchunk > DEC_MAX_CHUNKS)
+      return fail(W8A8_ENOTSUP, "attention_decode: %d key chunks of %d (at most %d)", nchunk, dec_chunk(int(D)),
+                  DEC_MAX_CHUNKS);
+  }
+  if (!(scale > 0.0f) || scale == __builtin_inff()) return fail(W8A8_EINVAL, "attention_decode: scale must be positive");
+  if (!q || !k || !v || !o || !workspace) return fail(W8A8_EINVAL, "attention_decode: null pointer");
+  const int64_t need = w8a8_attention_decode_workspace_bytes(H, KV, Tk, D, q_pos, window);
+  if (workspace_bytes < need)
+    return fail(W8A8_EINVAL, "attention_decode: workspace of %lld bytes, %lld needed", (long long)workspace_bytes,
+                (long long)need);
+  if (k_row_stride < D || v_row_stride < D || (H > 1 && (q_head_stride < D || o_head_stride < D)))
+    return fail(W8A8_EINVAL, "attention_decode: strides smaller than head_dim");
+  const int64_t strides[6] = {q_head_stride, k_head_stride, k_row_stride, v_head_stride, v_row_stride, o_head_stride};
+  for (int i = 0; i < 6; ++i)
+    if (strides[i] % 8 != 0) return fail(W8A8_EALIGN, "attention_decode: strides must be multiples of 8 elements");
+  if ((uintptr_t)q % 16 || (uintptr_t)k % 16 || (uintptr_t)v % 16 || (uintptr_t)o % 16 || (uintptr_t)workspace % 16)
+    return fail(W8A8_EALIGN, "attention_decode: q, k, v, o and the workspace must be 16-byte aligned");
+  const int64_t kb = ((Tk - 1) * k_row_stride + D) * 2, vb = ((Tk - 1) * v_row_stride + D) * 2;
+  if (kb > INT32_MAX || vb > INT32_MAX) return fail(W8A8_ENOTSUP, "attention_decode: one head's K or V above 2 GiB");
+  DecodeParams p;
+  p.q = q; p.qhs = q_head_stride; p.k = k; p.khs = k_head_stride; p.krs = k_row_stride;
+  p.v = v; p.vhs = v_head_stride; p.vrs = v_row_stride; p.o = o; p.ohs = o_head_stride; p.lse = lse;
+  p.k_bytes = uint32_t(kb); p.v_bytes = uint32_t(vb);
+  p.H = int(H); p.KV = int(KV); p.G = int(H / KV); p.Tk = int(Tk); p.pos = int(q_pos);
+  decode_geometry(D, q_pos, window, p.klo, p.nchunk);
+  p.part_o = static_cast<float*>(workspace);
+  p.part_ml = p.part_o + int64_t(KV) * p.nchunk * p.G * D;
+  p.scale = scale; p.c = scale * 1.4426950408889634f;
+  const dim3 grid{unsigned(KV * p.nchunk), 1, 1};
+  const dim3 mgrid{unsigned(H), unsigned(D / 4 / DEC_MCOLS), 1};
+  if (D == 128) {
+    attn_decode_split_kernel<128><<<grid, dim3{256, 1, 1}, 0, stream>>>(p);
+    attn_decode_merge_kernel<128><<<mgrid, dim3{256, 1, 1}, 0, stream>>>(p);
+  } else if (D == 256) {
+    attn_decode_split_kernel<256><<<grid, dim3{256, 1, 1}, 0, stream>>>(p);
+    attn_decode_merge_kernel<256><<<mgrid, dim3{256, 1, 1}, 0, stream>>>(p);
+  } else {
+    attn_decode_split_kernel<512><<<grid, dim3{256, 1, 1}, 0, stream>>>(p);
+    attn_decode_merge_kernel<512><<<mgrid, dim3{256, 1, 1}, 0, stream>>>(p);
+  }
+  return check_launch("attention_decode_bf16");
 }

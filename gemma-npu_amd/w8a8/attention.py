@@ -4,7 +4,9 @@ local_attn.py:71-107).
     full_attention(q, k_all, v_all, q_start)        -> o [H, Tq, D]      pipeline.py:140-155
     sliding_attention(q, k_all, v_all, q_start, W)  -> o [H, Tq, D]      pipeline.py:158-180
     local_sdpa(module, query, key, value, mask, ...) -> ([1, T, H, D], None)   local_attn.py:71-107
+    split_kv_decode(query, key, value, scale)        -> [1, 1, H, D]      local_attn.py:44-68
     attention(q, k, v, q_start, window, scale)      -> o (and the logsumexp)
+    decode(q, k, v, q_pos, window, scale)           -> o [H, D] (and the logsumexp)
 
 q is bf16 [H, Tq, D] at positions q_start.., k_all / v_all bf16 [KV, Tk, D] holding positions
 0.. (Tk >= q_start + Tq); any strides with a contiguous last dimension.  Scale 1.0 as Gemma uses.
@@ -15,10 +17,27 @@ pipeline.py:133-137) and its 128-query window blocks have no counterpart here; t
 same function.  Unlike the reference's sliding_attention, q_start need not be a multiple of 128.
 There is no CPU fallback.
 """
+import threading
+
 import torch
 
-from ._lib import call
+from ._lib import call, lib
 from .ops import _stream
+
+_WS = {}
+_WS_LOCK = threading.Lock()
+
+
+def _workspace(device, nbytes):
+    """Decode scratch of (device, current stream), grown to at least nbytes (calls on one stream are
+    ordered, so they can share it; nothing is kept between calls)."""
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    with _WS_LOCK:
+        buf = _WS.get(key)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
+            _WS[key] = buf
+    return buf
 
 
 def _check3(t, name):
@@ -86,6 +105,55 @@ def sliding_attention(q, k_all, v_all, q_start, W):
     return attention(q, k_all, v_all, q_start, int(W), 1.0)
 
 
+def decode(q, k, v, q_pos=None, window=0, scale=1.0, out=None, return_lse=False):
+    """One query per head at position q_pos (default: the last key) against k / v [KV, Tk, D].
+
+    q: bf16 [H, D] or [H, 1, D]; keys 0..q_pos are visible, with a window W only the last W of them.
+    Returns o [H, D] (into `out` if given), and with return_lse the fp32 [H] logsumexp."""
+    if q.dim() == 3:
+        if q.shape[1] != 1:
+            raise ValueError(f"decode: expected one query per head, got shape {tuple(q.shape)}")
+        q = q[:, 0]
+    if not isinstance(q, torch.Tensor) or q.dim() != 2 or q.dtype != torch.bfloat16 or q.device.type != "cuda":
+        raise ValueError("decode: q must be a bf16 GPU tensor [H, D]")
+    if q.shape[1] > 1 and q.stride(1) != 1:
+        raise ValueError("decode: q's last dimension must be contiguous")
+    _check3(k, "k")
+    _check3(v, "v")
+    H, D = q.shape
+    KV, Tk, Dk = k.shape
+    if tuple(v.shape) != (KV, Tk, Dk) or Dk != D:
+        raise ValueError(f"q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)} do not match")
+    if len({q.device, k.device, v.device}) != 1:
+        raise ValueError("q, k and v must be on one device")
+    pos = Tk - 1 if q_pos is None else int(q_pos)
+    if out is None:
+        out = torch.empty((H, D), dtype=torch.bfloat16, device=q.device)
+    elif out.shape != (H, D) or out.dtype != torch.bfloat16 or (D > 1 and out.stride(1) != 1):
+        raise ValueError(f"decode: out must be bf16 [{H}, {D}] with a contiguous last dimension")
+    lse = torch.empty((H,), dtype=torch.float32, device=q.device) if return_lse else None
+    need = lib().w8a8_attention_decode_workspace_bytes(H, KV, Tk, D, pos, int(window))
+    ws = _workspace(q.device, max(need, 0))
+    khs, krs = _strides(k)
+    vhs, vrs = _strides(v)
+    call("w8a8_attention_decode_bf16", q.data_ptr(), q.stride(0) if H > 1 else D, k.data_ptr(), khs, krs,
+         v.data_ptr(), vhs, vrs, H, KV, Tk, D, pos, int(window), float(scale), out.data_ptr(),
+         out.stride(0) if H > 1 else D, lse.data_ptr() if return_lse else None, ws.data_ptr(), ws.numel(),
+         _stream(q))
+    return (out, lse) if return_lse else out
+
+
+def split_kv_decode(query, key, value, scale):
+    """local_attn.py:44-68: one query per head [1, H, 1, D] against one KV head [1, 1, T, D] ->
+    [1, 1, H, D] (the reference's split over up to 16 key chunks and logsumexp merge)."""
+    if query.dim() != 4 or query.shape[0] != 1 or query.shape[2] != 1:
+        raise ValueError(f"split_kv_decode: expected query [1, H, 1, D], got {tuple(query.shape)}")
+    H, D = query.shape[1], query.shape[3]
+    out = torch.empty((1, 1, H, D), dtype=torch.bfloat16, device=query.device)
+    decode(query[0, :, 0], key[0], value[0], None, 0, scale, out=out[0, 0])
+    return out
+
+
 def local_sdpa(module, query, key, value, attention_mask, dropout=0.0, scaling=None, sliding_window=None,
                **kwargs):
     """The attention interface the reference registers with HF as "local_sdpa", on the GPU.
@@ -93,7 +161,8 @@ def local_sdpa(module, query, key, value, attention_mask, dropout=0.0, scaling=N
     query [1, H, T, D], key / value [1, KV, Tk, D] with Tk >= T (the last T positions are the
     queries'); returns ([1, T, H, D] contiguous, None).  Causal, and with sliding_window W only the
     last W keys of each query, which is what HF's mask says for these layers; attention_mask is
-    therefore not read.  Decode (T == 1) is the same call with one query at position Tk - 1."""
+    therefore not read.  Decode (T == 1) goes to the split-key decode kernels (one query at position
+    Tk - 1)."""
     if dropout:
         raise ValueError("local_sdpa: dropout is not supported")
     if query.dim() != 4 or query.shape[0] != 1 or key.shape[0] != 1 or value.shape[0] != 1:
@@ -104,5 +173,8 @@ def local_sdpa(module, query, key, value, attention_mask, dropout=0.0, scaling=N
         raise ValueError(f"local_sdpa: {Tk} keys for {T} queries")
     scale = float(scaling) if scaling is not None else D ** -0.5
     out = torch.empty((1, T, H, D), dtype=torch.bfloat16, device=query.device)
-    attention(query[0], key[0], value[0], Tk - T, int(sliding_window or 0), scale, out=out[0].transpose(0, 1))
+    if T == 1 and H // key.shape[1] <= 16:
+        decode(query[0, :, 0], key[0], value[0], Tk - 1, int(sliding_window or 0), scale, out=out[0, 0])
+    else:
+        attention(query[0], key[0], value[0], Tk - T, int(sliding_window or 0), scale, out=out[0].transpose(0, 1))
     return out, None

@@ -1,0 +1,140 @@
+"""HF transformers' Gemma 4 text decoder on the GPU with this engine underneath.
+
+The reference swaps the decoder's linears for grouped W8A8 GEMMs (`to_npu`, gemma_npu.py:208-241,
+with `NPUGemm`, gemma_npu.py:57-152, and `Slice`, gemma_npu.py:175-193), the LM head for an int8
+GEMV (`Int8Head`, gemma_npu.py:159-172), and registers its attention as "local_sdpa"
+(gemma_npu.py:253, local_attn.py:110-111).  `to_gpu` does the same on a model whose weights are on
+the GPU:
+
+    model = AutoModelForCausalLM.from_pretrained(...).to("cuda")      # or a random-init config
+    hf.to_gpu(model)
+    out = model(input_ids=ids, use_cache=True, logits_to_keep=1)      # prefill: W8A8 GEMMs
+    out = model(input_ids=nxt, past_key_values=out.past_key_values)   # decode: int8 GEMVs
+
+Groups as the reference forms them: [q; k; v] (q only on KV-shared layers), o, [gate; up], down,
+the per-layer-input gate and projection, and the per-layer model projection.  Rows < 16 (decode)
+take the weight-only int8 GEMV with bf16 scales (gemma_npu.py:120-121); more rows take per-token
+quant -> int8 GEMM -> dequant (gemma_npu.py:123-152).  Unlike the reference, the small PLE gate and
+projection stay on the GPU too.  The HF modules around them (norms, RoPE, GELU, residuals, the KV
+cache, the decode loop) run unchanged, as torch ops on the GPU.
+"""
+import torch
+
+from . import attention, ops
+
+DECODE_ROWS = 16  # rows below this go to the GEMV (gemma_npu.py:120)
+
+
+class GpuGemm(torch.nn.Module):
+    """One group of linears sharing an input, as one weight [sum of N, K] (gemma_npu.py:57-84):
+    per-channel int8 quantisation (absmax / 127), packed for the GEMM (fp32 scales) and for the
+    GEMV (bf16 scales, the reference's decode copy w_cpu / sw_cpu, gemma_npu.py:81-82)."""
+
+    def __init__(self, linears):
+        super().__init__()
+        w = torch.cat([l.weight.detach() for l in linears], 0)
+        if w.device.type != "cuda":
+            raise ValueError("to_gpu: move the model to the GPU first")
+        self.N, self.K = w.shape
+        self.sizes = [l.out_features for l in linears]
+        self.dtype = w.dtype
+        q, sw = ops.quant_rows(w.float().contiguous())
+        self.packed = ops.pack_weight(q, "nk", sw=sw)
+        self.gemv_w = ops.pack_gemv_weight(q)
+        self.sw_bf16 = sw.to(torch.bfloat16)
+        self.pending = None
+
+    def matmul(self, x2d):
+        x2d = x2d.to(torch.bfloat16).contiguous()
+        if x2d.shape[0] < DECODE_ROWS:
+            y = ops.gemv_bf16(x2d, self.gemv_w, self.sw_bf16)
+        else:
+            y = ops.linear_bf16(x2d, self.packed)
+        return y.to(self.dtype)
+
+
+class Slice(torch.nn.Module):
+    """Stands in for one linear of a GpuGemm group (gemma_npu.py:175-193): the first slice called
+    computes the whole group, its siblings reuse the result for the same input tensor."""
+
+    def __init__(self, gemm, index, in_features, out_features):
+        super().__init__()
+        self.gemm, self.index = gemm, index
+        self.in_features, self.out_features = in_features, out_features
+
+    def forward(self, x):
+        g = self.gemm
+        shape = x.shape[:-1]
+        if self.index == 0 or g.pending is None or g.pending[0] is not x:
+            y = g.matmul(x.reshape(-1, x.shape[-1]))
+            parts = torch.split(y, g.sizes, dim=-1) if len(g.sizes) > 1 else (y,)
+            g.pending = (x, parts)
+        out = g.pending[1][self.index]
+        if self.index == len(g.sizes) - 1:
+            g.pending = None
+        return out.reshape(*shape, -1)
+
+
+class Int8Head(torch.nn.Module):
+    """The LM head as a weight-only int8 GEMV (gemma_npu.py:159-172), 16 rows per launch."""
+
+    def __init__(self, linear):
+        super().__init__()
+        q, sw = ops.quant_rows(linear.weight.detach().float().contiguous())
+        self.w = ops.pack_gemv_weight(q)
+        self.sw = sw.to(torch.bfloat16)
+        self.in_features, self.out_features = linear.in_features, linear.out_features
+
+    def forward(self, x):
+        shape = x.shape[:-1]
+        x2d = x.reshape(-1, x.shape[-1]).to(torch.bfloat16).contiguous()
+        outs = [ops.gemv_bf16(x2d[r:r + DECODE_ROWS], self.w, self.sw) for r in range(0, x2d.shape[0], DECODE_ROWS)]
+        y = outs[0] if len(outs) == 1 else torch.cat(outs, 0)
+        return y.reshape(*shape, -1)
+
+
+def language_model(model):
+    """The text decoder of a Gemma 4 causal LM (multimodal or text-only)."""
+    m = model.model
+    return m.language_model if hasattr(m, "language_model") else m
+
+
+def register_attention():
+    """Registers attention.local_sdpa as HF's "local_sdpa" (local_attn.py:110-111)."""
+    from transformers import AttentionInterface
+    from transformers.masking_utils import ALL_MASK_ATTENTION_FUNCTIONS, sdpa_mask
+    AttentionInterface.register("local_sdpa", attention.local_sdpa)
+    ALL_MASK_ATTENTION_FUNCTIONS.register("local_sdpa", sdpa_mask)
+
+
+def to_gpu(model):
+    """Swap the text decoder's linears for GPU W8A8 groups, the LM head for the int8 GEMV head, and
+    the attention for local_sdpa (gemma_npu.py:208-241, 253).  Returns the groups."""
+    lm = language_model(model)
+    groups = []
+    for layer in lm.layers:
+        a, mlp = layer.self_attn, layer.mlp
+        qkv = [a.q_proj]
+        if not a.is_kv_shared_layer:
+            qkv += [a.k_proj] + ([a.v_proj] if a.v_proj is not None else [])
+        groups += [(a, ["q_proj", "k_proj", "v_proj"][: len(qkv)], qkv),
+                   (a, ["o_proj"], [a.o_proj]),
+                   (mlp, ["gate_proj", "up_proj"], [mlp.gate_proj, mlp.up_proj]),
+                   (mlp, ["down_proj"], [mlp.down_proj])]
+        if getattr(layer, "per_layer_input_gate", None) is not None:
+            groups += [(layer, ["per_layer_input_gate"], [layer.per_layer_input_gate]),
+                       (layer, ["per_layer_projection"], [layer.per_layer_projection])]
+    if getattr(lm, "per_layer_model_projection", None) is not None:
+        groups.append((lm, ["per_layer_model_projection"], [lm.per_layer_model_projection]))
+    gemms = []
+    for parent, names, linears in groups:
+        g = GpuGemm(linears)
+        g.name = "+".join(names)
+        gemms.append(g)
+        for i, (name, l) in enumerate(zip(names, linears)):
+            setattr(parent, name, Slice(g, i, l.in_features, l.out_features))
+    # tied to the input embedding, so this is a new int8 copy, not a swap
+    model.lm_head = Int8Head(model.lm_head)
+    register_attention()
+    lm.set_attn_implementation("local_sdpa")
+    return gemms

@@ -29,6 +29,7 @@
  *   resident decode weight w_cpu ........... gemma_npu.py:81           -> w8a8_pack_gemv_weight
  *   full_attention / sliding_attention ..... pipeline.py:140-180,      -> w8a8_attention_bf16
  *     (prefill sdpa of local_sdpa)             local_attn.py:71-107
+ *   _split_kv_decode / local_sdpa decode ... local_attn.py:44-83       -> w8a8_attention_decode_bf16
  */
 #ifndef W8A8_H
 #define W8A8_H
@@ -291,6 +292,28 @@ int w8a8_attention_bf16(const uint16_t *q, int64_t q_head_stride, int64_t q_row_
                         int64_t v_row_stride, int64_t H, int64_t KV, int64_t Tq, int64_t Tk, int64_t D,
                         int64_t q_start, int64_t window, float scale, uint16_t *o, int64_t o_head_stride,
                         int64_t o_row_stride, float *lse, hipStream_t stream);
+
+/* ---- decode attention ------------------------------------------------------------------- */
+
+/* Bytes of the workspace w8a8_attention_decode_bf16 needs: KV * ceil-chunks * (H/KV) * (D + 2) * 4,
+ * chunks of 64 keys (32 at head_dim 512) over the visible range; -1 if the arguments are invalid. */
+int64_t w8a8_attention_decode_workspace_bytes(int64_t H, int64_t KV, int64_t Tk, int64_t D, int64_t q_pos,
+                                              int64_t window);
+
+/* One query per head at position q_pos against keys 0..q_pos (the last `window` of them if window > 0):
+ * o[h, :] = sum_j softmax_j(scale * q[h] . k[g, j]) v[g, j], g = h / (H / KV).  Replaces
+ * _split_kv_decode (local_attn.py:44-68) and the decode branch of local_sdpa (local_attn.py:74-83):
+ * the keys are split into chunks of 64 (32 at head_dim 512) whose partial results are merged by their
+ * logsumexp (two launches; the merge runs in chunk order, so results are deterministic).
+ *   q bf16 [H, D] (q_head_stride), k / v bf16 [KV, Tk, D], o bf16 [H, D] (o_head_stride), lse fp32 [H]
+ *   or NULL; workspace: device memory of w8a8_attention_decode_workspace_bytes(...) bytes or more,
+ *   16-byte aligned, scratch (no contents are kept between calls).
+ * D in {128, 256, 512}; H / KV <= 16; strides multiples of 8 elements. */
+int w8a8_attention_decode_bf16(const uint16_t *q, int64_t q_head_stride, const uint16_t *k, int64_t k_head_stride,
+                               int64_t k_row_stride, const uint16_t *v, int64_t v_head_stride, int64_t v_row_stride,
+                               int64_t H, int64_t KV, int64_t Tk, int64_t D, int64_t q_pos, int64_t window,
+                               float scale, uint16_t *o, int64_t o_head_stride, float *lse, void *workspace,
+                               int64_t workspace_bytes, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -128,9 +128,10 @@ def test_layouts_and_local_sdpa():
     assert torch.equal(out[0].transpose(0, 1), o)
     full = attn.local_sdpa(None, qd[None], kd[None], vd[None], None, scaling=1.0)[0]
     assert torch.equal(full[0].transpose(0, 1), attn.full_attention(qd, kd, vd, 0))
-    # decode: one query at the last position against the cache (local_attn.py:74-83)
+    # decode: one query at the last position against the cache (local_attn.py:74-83) goes to the
+    # split-key decode kernels
     dec = attn.local_sdpa(None, qd[None, :, -1:], kd[None], vd[None], None, scaling=1.0, sliding_window=64)[0]
-    assert torch.equal(dec[0, 0], o[:, -1])
+    assert torch.equal(dec[0, 0], attn.decode(qd[:, -1], kd, vd, T - 1, 64))
     # k / v as column slices of a wider buffer
     kv = torch.cat([kd, vd], 2)
     o2 = attn.attention(qd, kv[:, :, :D], kv[:, :, D:], 0, 64)
@@ -176,3 +177,62 @@ def test_errors():
         attn.sliding_attention(qd, kd, vd, 0, 0)
     # Tq == 0 is a no-op
     assert attn.attention(qd[:, :0], kd, vd).shape == (4, 0, 128)
+
+
+# ---- decode (local_attn.py:44-83) -------------------------------------------------------------
+
+DECODE_CASES = [
+    # H, KV, Tk, D, q_pos, window
+    (8, 1, 3658, 512, 3657, 0),     # full layer at the end of the benchmark prompt
+    (8, 1, 3658, 256, 3657, 512),   # sliding layer: the last 512 keys
+    (8, 1, 1, 256, 0, 0),           # the first token
+    (8, 1, 65, 256, 64, 0),         # one key past a 64-key chunk
+    (8, 1, 64, 512, 63, 0),         # exactly one chunk
+    (8, 1, 500, 256, 300, 0),       # keys past the query position are ignored
+    (4, 2, 300, 128, 299, 50),      # 2 KV heads, window not a chunk multiple
+    (16, 1, 200, 256, 199, 0),      # 16 heads per KV head
+    (6, 2, 130, 128, 129, 7),       # 3 heads per KV head
+]
+
+
+@pytest.mark.parametrize("H,KV,Tk,D,q_pos,window", DECODE_CASES)
+def test_decode_matches_oracle(H, KV, Tk, D, q_pos, window):
+    print(f"decode H={H} KV={KV} Tk={Tk} D={D} q_pos={q_pos} W={window}", flush=True)
+    q, k, v = make(H, KV, 1, Tk, D, seed=Tk + D + window, qscale=0.5)
+    o, lse = attn.decode(q[:, 0].to(DEV), k.to(DEV), v.to(DEV), q_pos, window, return_lse=True)
+    ref, bud, lse_ref = reference(q, k, v, q_pos, window)
+    check(o[:, None], ref, bud, "decode")
+    assert np.allclose(lse.cpu().numpy(), lse_ref[:, 0], rtol=1e-5, atol=1e-4), "decode logsumexp differs"
+
+
+def test_decode_mirror_and_determinism():
+    """split_kv_decode takes the reference's shapes ([1, H, 1, D] against [1, 1, T, D]) and
+    returns [1, 1, H, D]; repeated calls give the same bits."""
+    H, T, D = 8, 1000, 256
+    q, k, v = make(H, 1, 1, T, D, seed=21, qscale=0.5)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    out = attn.split_kv_decode(qd.transpose(0, 1)[None].transpose(1, 2), kd[None], vd[None], 1.0)
+    assert out.shape == (1, 1, H, D)
+    a = attn.decode(qd[:, 0], kd, vd)
+    assert torch.equal(out[0, 0], a)
+    assert torch.equal(attn.decode(qd[:, 0], kd, vd), a)
+    # and the result agrees with the prefill kernel's row for the same query within the tolerance
+    ref, bud, _ = reference(q, k, v, T - 1, 0)
+    check(a[:, None], ref, bud, "decode vs oracle")
+
+
+def test_decode_errors():
+    from w8a8._lib import call
+    q, k, v = make(8, 1, 1, 100, 256, seed=0)
+    qd, kd, vd = q[:, 0].to(DEV), k.to(DEV), v.to(DEV)
+    with pytest.raises(W8A8Error, match="q_pos"):
+        attn.decode(qd, kd, vd, q_pos=100)
+    q32 = torch.zeros(32, 256, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(W8A8Error, match="16 heads per KV head"):
+        attn.decode(q32, kd, vd)
+    o = torch.empty(8, 256, dtype=torch.bfloat16, device=DEV)
+    ws = torch.empty(64, dtype=torch.uint8, device=DEV)
+    with pytest.raises(W8A8Error, match="workspace"):
+        call("w8a8_attention_decode_bf16", qd.data_ptr(), 256, kd.data_ptr(), 100 * 256, 256, vd.data_ptr(),
+             100 * 256, 256, 8, 1, 100, 256, 99, 0, 1.0, o.data_ptr(), 256, None, ws.data_ptr(), 64,
+             torch.cuda.current_stream().cuda_stream)
