@@ -288,6 +288,92 @@ def attention_inputs(D, T, dev, seed):
     return q, k, v
 
 
+def e2b_model(dev):
+    """A Gemma 4 E2B-shaped text decoder (HF transformers' own model code), random-init in bf16 on
+    the GPU, with the engine underneath (w8a8.hf.to_gpu).  Shapes: hidden 1536, 35 layers (4
+    sliding + 1 full, repeated), 8 query heads on 1 KV head, head_dim 256 / 512, window 512, the
+    last 20 layers KV-shared with double-wide MLPs, 256-wide per-layer inputs, vocab 262144."""
+    import torch
+    from transformers.models.gemma4.configuration_gemma4 import Gemma4TextConfig
+    from transformers.models.gemma4.modeling_gemma4 import Gemma4ForCausalLM
+    from w8a8 import hf
+    cfg = Gemma4TextConfig(vocab_size=262144, hidden_size=1536, intermediate_size=6144, num_hidden_layers=35,
+                           num_attention_heads=8, num_key_value_heads=1, head_dim=256, global_head_dim=512,
+                           sliding_window=512, layer_types=(["sliding_attention"] * 4 + ["full_attention"]) * 7,
+                           num_kv_shared_layers=20, use_double_wide_mlp=True, vocab_size_per_layer_input=262144,
+                           hidden_size_per_layer_input=256, final_logit_softcapping=30.0)
+    torch.manual_seed(0)
+    old = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device(dev):
+            model = Gemma4ForCausalLM(cfg).eval()
+    finally:
+        torch.set_default_dtype(old)
+    nparams = sum(p.numel() for p in model.parameters())
+    hf.to_gpu(model)
+    return model, nparams
+
+
+def e2e_bench(dev, T=ATTN_T, n_decode=32):
+    """The reference's run() (gemma_npu.py:278-300) on the GPU: a timed prefill of T tokens, then
+    greedy decode through HF's unchanged loop, one model call per token."""
+    import torch
+    model, nparams = e2b_model(dev)
+    ids = torch.randint(0, 262144, (1, T), generator=torch.Generator().manual_seed(1)).to(dev)
+    ttfts = []
+    with torch.inference_mode():
+        for _ in range(4):  # the first call pays one-time set-up
+            torch.cuda.synchronize()
+            t = time.perf_counter()
+            out = model(input_ids=ids, use_cache=True, logits_to_keep=1)
+            torch.cuda.synchronize()
+            ttfts.append(time.perf_counter() - t)
+        past, nxt = out.past_key_values, out.logits[0, -1].argmax().view(1, 1)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        for _ in range(n_decode):
+            o = model(input_ids=nxt, past_key_values=past, use_cache=True, logits_to_keep=1)
+            past, nxt = o.past_key_values, o.logits[0, -1].argmax().view(1, 1)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t
+    del model, past, out, o
+    return {"prefill_ms": round(statistics.median(ttfts[1:]) * 1e3, 1), "prompt_tokens": T,
+            "decode_tok_s": round(n_decode / dt, 1), "decode_ms_per_token": round(dt / n_decode * 1e3, 2),
+            "decode_tokens": n_decode, "params": nparams,
+            "what": "HF Gemma 4 (transformers' modeling code, unchanged) with E2B's shapes, random-init bf16 weights, "
+                    "linears through w8a8.hf.to_gpu (W8A8 GEMM prefill, int8 GEMV decode and LM head), attention "
+                    "through local_sdpa (prefill and split-key decode kernels); prefill = median of 3 timed calls "
+                    "after one warm-up (logits_to_keep=1); decode = greedy, one model call per token",
+            "reference": {"ttft_ms": 2911, "decode_tok_s": 27.4, "source": "README.md:40-45 (NPU backend, 3658 "
+                                                                          "prompt tokens, real weights)"}}
+
+
+def decode_attention_bench(dev, launches=50):
+    """Decode attention at the end of the 3658-token prompt: one query per head against the cache
+    (full layers) or its last 512 keys (sliding layers), HIP-graph replays of back-to-back calls."""
+    import torch
+    from w8a8 import attention as attn
+    res = {}
+    for name, (D, W, layers) in ATTN_LAYERS.items():
+        _, k, v = attention_inputs(D, ATTN_T, dev, seed=D + 1)
+        q = (torch.randn(ATTN_H, D, generator=torch.Generator(device=dev).manual_seed(7), device=dev) * 0.3).to(
+            torch.bfloat16)
+        out = torch.empty_like(q)
+        ws = torch.empty(attn.decode_workspace_bytes(ATTN_H, ATTN_KV, ATTN_T, D, None, W), dtype=torch.uint8,
+                         device=dev)
+        ms = graph_time_ms(lambda: attn.decode(q, k, v, ATTN_T - 1, W, out=out, workspace=ws), dev,
+                           launches=launches)
+        keys = ATTN_T if W == 0 else W
+        nbytes = 2 * keys * D * 2 * ATTN_KV
+        res[name] = {"us": round(ms * 1e3, 2), "kv_bytes": nbytes, "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                     "head_dim": D, "window": W, "layers": layers}
+    res["token_total_us"] = round(sum(r["us"] * r["layers"] for r in res.values()), 1)
+    res["what"] = ("one decode token's attention per layer kind (split-key kernel + logsumexp merge, two launches), "
+                   "HIP-graph replay; token_total = 28 sliding + 7 full layers")
+    return res
+
+
 def attention_bench(dev, reps):
     """Prefill attention of the 3658-token prompt: each layer kind in one call over the whole prompt,
     and the reference pipeline's largest per-micro-batch calls (pipeline.py:281-295)."""
@@ -352,6 +438,9 @@ def main():
     ap.add_argument("--profile-attention", action="store_true",
                     help="for kernel traces: run the whole-prompt sliding and full attention calls at T=3658 "
                          "(--steps times each) and exit")
+    ap.add_argument("--profile-e2e", action="store_true",
+                    help="for kernel traces: one prefill of the 3658-token prompt and --steps decode tokens of the "
+                         "E2B-shaped HF Gemma 4 on the engine, then exit")
     ap.add_argument("--profile-chain", action="store_true",
                     help="for kernel traces: run the device layer chain (--steps times, eager) and exit")
     args = ap.parse_args()
@@ -381,6 +470,18 @@ def main():
             ops.gemv_bf16(x, pw, s, y)
         torch.cuda.synchronize()
         log(f"bench: ran the packed LM-head GEMV (M=1, K={K}, N={N}) {args.steps} times")
+        return 0
+    if args.profile_e2e:
+        model, _ = e2b_model(dev)
+        ids = torch.randint(0, 262144, (1, ATTN_T), generator=torch.Generator().manual_seed(1)).to(dev)
+        with torch.inference_mode():
+            out = model(input_ids=ids, use_cache=True, logits_to_keep=1)
+            past, nxt = out.past_key_values, out.logits[0, -1].argmax().view(1, 1)
+            for _ in range(args.steps):
+                o = model(input_ids=nxt, past_key_values=past, use_cache=True, logits_to_keep=1)
+                past, nxt = o.past_key_values, o.logits[0, -1].argmax().view(1, 1)
+        torch.cuda.synchronize()
+        log(f"bench: ran the E2B-shaped model: prefill of {ATTN_T} tokens, {args.steps} decode tokens")
         return 0
     if args.profile_attention:
         from w8a8 import attention as attn
@@ -522,6 +623,11 @@ def main():
         torch.cuda.empty_cache()
         extra["attention_prefill_t3658"] = attention_bench(dev, reps=20)
         log(f"bench: attention: {extra['attention_prefill_t3658']}")
+        torch.cuda.empty_cache()
+        extra["decode_attention_t3658"] = decode_attention_bench(dev)
+        log(f"bench: decode attention: {extra['decode_attention_t3658']}")
+        extra["hf_gemma4_e2b_shape"] = e2e_bench(dev)
+        log(f"bench: HF Gemma 4 end to end: {extra['hf_gemma4_e2b_shape']}")
         torch.cuda.empty_cache()
 
     line = {

@@ -105,11 +105,22 @@ def sliding_attention(q, k_all, v_all, q_start, W):
     return attention(q, k_all, v_all, q_start, int(W), 1.0)
 
 
-def decode(q, k, v, q_pos=None, window=0, scale=1.0, out=None, return_lse=False):
+def decode_workspace_bytes(H, KV, Tk, D, q_pos=None, window=0):
+    """Bytes of scratch decode() needs (w8a8_attention_decode_workspace_bytes)."""
+    n = lib().w8a8_attention_decode_workspace_bytes(H, KV, Tk, D, Tk - 1 if q_pos is None else int(q_pos),
+                                                    int(window))
+    if n < 0:
+        raise ValueError(f"decode: invalid shape H={H} KV={KV} Tk={Tk} D={D}")
+    return n
+
+
+def decode(q, k, v, q_pos=None, window=0, scale=1.0, out=None, return_lse=False, workspace=None):
     """One query per head at position q_pos (default: the last key) against k / v [KV, Tk, D].
 
     q: bf16 [H, D] or [H, 1, D]; keys 0..q_pos are visible, with a window W only the last W of them.
-    Returns o [H, D] (into `out` if given), and with return_lse the fp32 [H] logsumexp."""
+    Returns o [H, D] (into `out` if given), and with return_lse the fp32 [H] logsumexp.
+    workspace: a device uint8 tensor of at least decode_workspace_bytes(...) (scratch; nothing is kept
+    between calls); by default a buffer cached per device and stream."""
     if q.dim() == 3:
         if q.shape[1] != 1:
             raise ValueError(f"decode: expected one query per head, got shape {tuple(q.shape)}")
@@ -133,7 +144,7 @@ def decode(q, k, v, q_pos=None, window=0, scale=1.0, out=None, return_lse=False)
         raise ValueError(f"decode: out must be bf16 [{H}, {D}] with a contiguous last dimension")
     lse = torch.empty((H,), dtype=torch.float32, device=q.device) if return_lse else None
     need = lib().w8a8_attention_decode_workspace_bytes(H, KV, Tk, D, pos, int(window))
-    ws = _workspace(q.device, max(need, 0))
+    ws = _workspace(q.device, max(need, 0)) if workspace is None else workspace
     khs, krs = _strides(k)
     vhs, vrs = _strides(v)
     call("w8a8_attention_decode_bf16", q.data_ptr(), q.stride(0) if H > 1 else D, k.data_ptr(), khs, krs,
