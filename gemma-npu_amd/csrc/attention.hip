@@ -50,7 +50,12 @@ struct AttnParams {
   float* lse;                           // fp32 [H, Tq] natural-log logsumexp of the scaled scores, or null
   uint32_t k_bytes, v_bytes;            // extent of one KV group's K / V rows, bytes
   int H, KV, G, PB, Tq, Tk, q_start, window;
-  int ntiles;                           // ceil(Tq / PB) workgroups per KV group
+  int ntiles;                           // ceil(Tq / PB) query tiles per KV group
+  // Key splitting of the longest causal tiles: tiles >= split_from are each computed by `split`
+  // workgroups over consecutive parts of their key blocks, the last to finish merging the parts.
+  int split, split_from;
+  float* part;                          // [KV][ntiles - split_from][split] partial tiles (lane-native)
+  int* counters;                        // [KV][ntiles - split_from] arrival counts, zero between calls
   float scale, c;                       // c = scale * log2(e)
 };
 
@@ -95,11 +100,23 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(AttnParams p) {
   const int qi = lane & 15, qq = lane >> 4;  // query column, lane group
 
   // ---- which KV group and query rows -------------------------------------------------------
-  const int nblocks = p.KV * p.ntiles;
-  const int lb = p.window > 0 ? attn_xcd_remap(blockIdx.x, nblocks) : int(blockIdx.x);
-  const int g = lb / p.ntiles;
-  // causal: the longest tiles first, and consecutive workgroups (other XCDs) a mix of lengths
-  const int tile = p.window > 0 ? lb % p.ntiles : p.ntiles - 1 - lb % p.ntiles;
+  // Workgroups per KV group: split * (ntiles - split_from) parts of split tiles, then one per
+  // remaining tile.  Sliding windows: neighbouring tiles (sharing their keys) on one XCD.  Causal:
+  // the longest tiles first, consecutive workgroups (other XCDs) a mix of lengths.
+  const int nsplit_tiles = p.ntiles - p.split_from;
+  const int per_group = p.split * nsplit_tiles + p.split_from;
+  const int lb = p.window > 0 ? attn_xcd_remap(blockIdx.x, p.KV * per_group) : int(blockIdx.x);
+  const int g = lb / per_group, b = lb % per_group;
+  int tile, part = 0;
+  if (p.window > 0) {
+    tile = b;
+  } else if (b < p.split * nsplit_tiles) {
+    tile = p.ntiles - 1 - b / p.split;
+    part = b % p.split;
+  } else {
+    tile = p.split_from - 1 - (b - p.split * nsplit_tiles);
+  }
+  const bool split_tile = p.split > 1 && tile >= p.split_from;
   const int i0 = tile * p.PB;
   const int r = wave * 16 + qi;
   const int hl = r % p.G, pl = r / p.G;
@@ -112,8 +129,13 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(AttnParams p) {
   const int pmax = p.q_start + min(i0 + p.PB, p.Tq) - 1;
   const int khi = min(pmax, p.Tk - 1);
   const int klo = p.window > 0 ? max(0, pmin - p.window + 1) : 0;
-  const int kb0 = (klo / BN) * BN;
-  const int nblk = khi >= kb0 ? (khi - kb0) / BN + 1 : 0;
+  const int kb_first = (klo / BN) * BN;
+  const int nblk_tile = khi >= kb_first ? (khi - kb_first) / BN + 1 : 0;
+  // this workgroup's key blocks: part `part` of `split` consecutive parts when the tile is split
+  const int n_lo = split_tile ? part * nblk_tile / p.split : 0;
+  const int n_hi = split_tile ? (part + 1) * nblk_tile / p.split : nblk_tile;
+  const int kb0 = kb_first + n_lo * BN;
+  const int nblk = n_hi - n_lo;
 
   const __amdgpu_buffer_rsrc_t rk = make_rsrc(p.k + int64_t(g) * p.khs, p.k_bytes);
   const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.v + int64_t(g) * p.vhs, p.v_bytes);
@@ -283,6 +305,59 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(AttnParams p) {
       }
 
     if (n + 1 < nblk) store_vt(slot ^ 1);
+  }
+
+  // ---- split tiles: park this part; the last part to arrive merges them in part order ---------
+  // The XCDs' L2 caches are not coherent with each other, so the parts go through system-scope
+  // (sc0 sc1) buffer stores and loads and the arrival count is a system-scope atomic; each
+  // thread's stores are complete (vmcnt 0) before the barrier that precedes the count.
+  if (split_tile) {
+    constexpr uint32_t LANE_BYTES = (NDT + 1) * 16;  // o[NDT] and (m, l) per lane
+    constexpr uint32_t PART_BYTES = NW * 64 * LANE_BYTES;
+    const int slot_tile = g * nsplit_tiles + (tile - p.split_from);
+    const __amdgpu_buffer_rsrc_t rp =
+        make_rsrc(p.part + size_t(slot_tile) * p.split * (PART_BYTES / 4), uint32_t(p.split) * PART_BYTES);
+    const uint32_t lane_off = uint32_t(tid) * LANE_BYTES;
+    {
+      const uint32_t base = uint32_t(part) * PART_BYTES + lane_off;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, o[dt]), rp, base + dt * 16, 0, 0x11);
+      const v4f ml = v4f{m, l, 0.0f, 0.0f};
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, ml), rp, base + NDT * 16, 0, 0x11);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    int* arrived = reinterpret_cast<int*>(lds);
+    __syncthreads();
+    if (tid == 0)
+      *arrived = __hip_atomic_fetch_add(p.counters + slot_tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __syncthreads();
+    if (*arrived != p.split - 1) return;
+    // merge: M = max of the parts' maxima, w_s = exp2((m_s - M) c), o = sum_s w_s o_s, l likewise
+    float M = -__builtin_inff();
+    for (int sp = 0; sp < p.split; ++sp) {
+      const v4f ml = __builtin_bit_cast(
+          v4f, __builtin_amdgcn_raw_buffer_load_b128(rp, uint32_t(sp) * PART_BYTES + lane_off + NDT * 16, 0, 0x11));
+      M = fmaxf(M, ml[0]);
+    }
+    const float Ms = M == -__builtin_inff() ? 0.0f : M * c;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) o[dt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    l = 0.0f;
+    for (int sp = 0; sp < p.split; ++sp) {
+      const uint32_t base = uint32_t(sp) * PART_BYTES + lane_off;
+      const v4f ml = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rp, base + NDT * 16, 0, 0x11));
+      const float w = __builtin_amdgcn_exp2f(__builtin_fmaf(ml[0], c, -Ms));
+      l = __builtin_fmaf(w, ml[1], l);
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        const v4f od = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rp, base + dt * 16, 0, 0x11));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[dt][i] = __builtin_fmaf(w, od[i], o[dt][i]);
+      }
+    }
+    m = M;
+    if (tid == 0) __hip_atomic_store(p.counters + slot_tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   }
 
   // ---- normalise and store --------------------------------------------------------------------
@@ -548,11 +623,75 @@ __global__ __launch_bounds__(256) void attn_decode_merge_kernel(DecodeParams p) 
 
 using namespace w8a8;
 
-extern "C" int w8a8_attention_bf16(const uint16_t* q, int64_t q_head_stride, int64_t q_row_stride, const uint16_t* k,
-                                   int64_t k_head_stride, int64_t k_row_stride, const uint16_t* v,
-                                   int64_t v_head_stride, int64_t v_row_stride, int64_t H, int64_t KV, int64_t Tq,
-                                   int64_t Tk, int64_t D, int64_t q_start, int64_t window, float scale, uint16_t* o,
-                                   int64_t o_head_stride, int64_t o_row_stride, float* lse, hipStream_t stream) {
+static int attn_bn(int64_t D) { return D == 128 ? 128 : (D == 256 ? 64 : 32); }
+
+static int64_t attn_part_bytes(int64_t D) { return int64_t(ATTN_NW) * 64 * (D / 16 + 1) * 16; }
+
+static int attn_cu_count() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) ==
+                                                 hipSuccess && n > 0)
+      cus = n;
+    else
+      cus = 256;
+  }
+  return cus;
+}
+
+// Key splitting for causal calls whose longest query tile has far more key blocks than the chip's
+// fair share (total blocks / CUs): the tiles past that share are split into `split` parts.
+static void attn_plan(int64_t H, int64_t KV, int64_t Tq, int64_t Tk, int64_t D, int64_t q_start, int64_t window,
+                      int& ntiles, int& split, int& split_from) {
+  const int G = int(H / KV), PB = ATTN_NW * 16 / G, BN = attn_bn(D);
+  ntiles = int((Tq + PB - 1) / PB);
+  split = 1;
+  split_from = ntiles;
+  if (window > 0 || Tq == 0) return;
+  auto nblk = [&](int t) {
+    const int64_t i0 = int64_t(t) * PB;
+    const int64_t pmax = q_start + (i0 + PB < Tq ? i0 + PB : Tq) - 1;
+    const int64_t khi = pmax < Tk - 1 ? pmax : Tk - 1;
+    return int(khi / BN + 1);
+  };
+  int64_t total = 0;
+  int mx = 0;
+  for (int t = 0; t < ntiles; ++t) {
+    const int n = nblk(t);
+    total += n;
+    mx = n > mx ? n : mx;
+  }
+  const int64_t cus = attn_cu_count();
+  const int64_t fair = (total * KV + cus - 1) / cus;
+  if (mx < 8 || 4 * int64_t(mx) <= 5 * fair) return;
+  const int64_t want = (mx + fair - 1) / fair;
+  split = int(want < 8 ? want : 8);
+  int from = ntiles;
+  while (from > 0 && nblk(from - 1) > fair) --from;
+  const int max_counters = 1024;
+  if (KV * (ntiles - from) > max_counters) from = int(ntiles - max_counters / KV);
+  split_from = from;
+  if (split_from >= ntiles) split = 1;
+}
+
+extern "C" int64_t w8a8_attention_workspace_bytes(int64_t H, int64_t KV, int64_t Tq, int64_t Tk, int64_t D,
+                                                  int64_t q_start, int64_t window) {
+  if (H < 1 || KV < 1 || H % KV != 0 || H / KV > 128 || (D != 128 && D != 256 && D != 512) || Tq < 0 ||
+      q_start < 0 || window < 0 || Tk < q_start + Tq)
+    return -1;
+  int ntiles, split, split_from;
+  attn_plan(H, KV, Tq, Tk, D, q_start, window, ntiles, split, split_from);
+  if (split <= 1) return 0;
+  return 4096 + KV * int64_t(ntiles - split_from) * split * attn_part_bytes(D);
+}
+
+static int attention_launch(const uint16_t* q, int64_t q_head_stride, int64_t q_row_stride, const uint16_t* k,
+                            int64_t k_head_stride, int64_t k_row_stride, const uint16_t* v, int64_t v_head_stride,
+                            int64_t v_row_stride, int64_t H, int64_t KV, int64_t Tq, int64_t Tk, int64_t D,
+                            int64_t q_start, int64_t window, float scale, uint16_t* o, int64_t o_head_stride,
+                            int64_t o_row_stride, float* lse, void* workspace, int64_t workspace_bytes,
+                            hipStream_t stream) {
   if (H < 1 || KV < 1 || H % KV != 0 || H / KV > 128)
     return fail(W8A8_EINVAL, "attention: H=%lld KV=%lld (H must be a multiple of KV, at most 128 heads per KV head)",
                 (long long)H, (long long)KV);
@@ -583,9 +722,26 @@ extern "C" int w8a8_attention_bf16(const uint16_t* q, int64_t q_head_stride, int
   p.k_bytes = uint32_t(kb); p.v_bytes = uint32_t(vb);
   p.H = int(H); p.KV = int(KV); p.G = int(H / KV); p.PB = ATTN_NW * 16 / p.G;
   p.Tq = int(Tq); p.Tk = int(Tk); p.q_start = int(q_start); p.window = int(window);
-  p.ntiles = int((Tq + p.PB - 1) / p.PB);
+  attn_plan(H, KV, Tq, Tk, D, q_start, window, p.ntiles, p.split, p.split_from);
+  p.part = nullptr;
+  p.counters = nullptr;
+  if (p.split > 1) {
+    const int64_t need = 4096 + KV * int64_t(p.ntiles - p.split_from) * p.split * attn_part_bytes(D);
+    if (!workspace) {
+      p.split = 1;
+      p.split_from = p.ntiles;
+    } else if (workspace_bytes < need) {
+      return fail(W8A8_EINVAL, "attention: workspace of %lld bytes, %lld needed", (long long)workspace_bytes,
+                  (long long)need);
+    } else if ((uintptr_t)workspace % 16) {
+      return fail(W8A8_EALIGN, "attention: the workspace must be 16-byte aligned");
+    } else {
+      p.counters = static_cast<int*>(workspace);
+      p.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + 4096);
+    }
+  }
   p.scale = scale; p.c = scale * 1.4426950408889634f;
-  const int64_t nwg = KV * int64_t(p.ntiles);
+  const int64_t nwg = KV * (int64_t(p.split) * (p.ntiles - p.split_from) + p.split_from);
   if (nwg > INT32_MAX) return fail(W8A8_ENOTSUP, "attention: too many query tiles");
   const dim3 grid{unsigned(nwg), 1, 1};
   if (D == 128)
@@ -595,6 +751,27 @@ extern "C" int w8a8_attention_bf16(const uint16_t* q, int64_t q_head_stride, int
   else
     attn_fwd_kernel<512, 32, ATTN_NW><<<grid, dim3{ATTN_NW * 64, 1, 1}, 0, stream>>>(p);
   return check_launch("attention_bf16");
+}
+
+extern "C" int w8a8_attention_bf16(const uint16_t* q, int64_t q_head_stride, int64_t q_row_stride, const uint16_t* k,
+                                   int64_t k_head_stride, int64_t k_row_stride, const uint16_t* v,
+                                   int64_t v_head_stride, int64_t v_row_stride, int64_t H, int64_t KV, int64_t Tq,
+                                   int64_t Tk, int64_t D, int64_t q_start, int64_t window, float scale, uint16_t* o,
+                                   int64_t o_head_stride, int64_t o_row_stride, float* lse, hipStream_t stream) {
+  return attention_launch(q, q_head_stride, q_row_stride, k, k_head_stride, k_row_stride, v, v_head_stride,
+                          v_row_stride, H, KV, Tq, Tk, D, q_start, window, scale, o, o_head_stride, o_row_stride, lse,
+                          nullptr, 0, stream);
+}
+
+extern "C" int w8a8_attention_ws_bf16(const uint16_t* q, int64_t q_head_stride, int64_t q_row_stride,
+                                      const uint16_t* k, int64_t k_head_stride, int64_t k_row_stride, const uint16_t* v,
+                                      int64_t v_head_stride, int64_t v_row_stride, int64_t H, int64_t KV, int64_t Tq,
+                                      int64_t Tk, int64_t D, int64_t q_start, int64_t window, float scale, uint16_t* o,
+                                      int64_t o_head_stride, int64_t o_row_stride, float* lse, void* workspace,
+                                      int64_t workspace_bytes, hipStream_t stream) {
+  return attention_launch(q, q_head_stride, q_row_stride, k, k_head_stride, k_row_stride, v, v_head_stride,
+                          v_row_stride, H, KV, Tq, Tk, D, q_start, window, scale, o, o_head_stride, o_row_stride, lse,
+                          workspace, workspace_bytes, stream);
 }
 
 static void decode_geometry(int64_t D, int64_t q_pos, int64_t window, int& klo, int& nchunk) {

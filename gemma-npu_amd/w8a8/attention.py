@@ -40,6 +40,22 @@ def _workspace(device, nbytes):
     return buf
 
 
+_SPLIT_WS = {}
+
+
+def _split_workspace(device, nbytes):
+    """The zero-filled workspace of (device, current stream) for split causal tiles, grown to at
+    least nbytes: its counters are zero between calls by the kernel's own contract, so it is only
+    cleared when (re)allocated."""
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    with _WS_LOCK:
+        buf = _SPLIT_WS.get(key)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+            _SPLIT_WS[key] = buf
+    return buf
+
+
 def _check3(t, name):
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"{name}: expected a tensor, got {type(t).__name__}")
@@ -87,9 +103,12 @@ def attention(q, k, v, q_start=0, window=0, scale=1.0, out=None, return_lse=Fals
     khs, krs = _strides(k)
     vhs, vrs = _strides(v)
     ohs, ors = _strides(out)
-    call("w8a8_attention_bf16", q.data_ptr(), qhs, qrs, k.data_ptr(), khs, krs, v.data_ptr(), vhs, vrs, H, KV, Tq,
-         Tk, D, int(q_start), int(window), float(scale), out.data_ptr(), ohs, ors,
-         lse.data_ptr() if return_lse else None, _stream(q))
+    need = lib().w8a8_attention_workspace_bytes(H, KV, Tq, Tk, D, int(q_start), int(window))
+    ws = _split_workspace(q.device, need) if need > 0 else None
+    call("w8a8_attention_ws_bf16", q.data_ptr(), qhs, qrs, k.data_ptr(), khs, krs, v.data_ptr(), vhs, vrs, H, KV,
+         Tq, Tk, D, int(q_start), int(window), float(scale), out.data_ptr(), ohs, ors,
+         lse.data_ptr() if return_lse else None, None if ws is None else ws.data_ptr(),
+         0 if ws is None else ws.numel(), _stream(q))
     return (out, lse) if return_lse else out
 
 

@@ -293,6 +293,27 @@ int w8a8_attention_bf16(const uint16_t *q, int64_t q_head_stride, int64_t q_row_
                         int64_t q_start, int64_t window, float scale, uint16_t *o, int64_t o_head_stride,
                         int64_t o_row_stride, float *lse, hipStream_t stream);
 
+/* Bytes of the workspace w8a8_attention_ws_bf16 uses for these arguments (0: it splits no query
+ * tile and needs none; -1: invalid arguments).  Causal calls whose longest query tiles hold far more
+ * key blocks than the chip's fair share (at T = 3658, head_dim 512: 115 blocks of 32 keys against
+ * ~52) split those tiles' keys over several workgroups, the last to finish merging the parts by
+ * their logsumexp. */
+int64_t w8a8_attention_workspace_bytes(int64_t H, int64_t KV, int64_t Tq, int64_t Tk, int64_t D, int64_t q_start,
+                                       int64_t window);
+
+/* w8a8_attention_bf16 with a workspace for splitting long causal tiles: device memory of at least
+ * w8a8_attention_workspace_bytes(...) bytes, 16-byte aligned, ZERO-FILLED BEFORE ITS FIRST USE (its
+ * first 4 KiB are arrival counters that every call leaves zero; the rest is scratch).  Calls that
+ * share a workspace must be ordered (one stream).  NULL behaves as w8a8_attention_bf16.  The parts
+ * are merged in a fixed order, so results are deterministic; they may differ from the unsplit
+ * call's in the last bits. */
+int w8a8_attention_ws_bf16(const uint16_t *q, int64_t q_head_stride, int64_t q_row_stride, const uint16_t *k,
+                           int64_t k_head_stride, int64_t k_row_stride, const uint16_t *v, int64_t v_head_stride,
+                           int64_t v_row_stride, int64_t H, int64_t KV, int64_t Tq, int64_t Tk, int64_t D,
+                           int64_t q_start, int64_t window, float scale, uint16_t *o, int64_t o_head_stride,
+                           int64_t o_row_stride, float *lse, void *workspace, int64_t workspace_bytes,
+                           hipStream_t stream);
+
 /* ---- decode attention ------------------------------------------------------------------- */
 
 /* Bytes of the workspace w8a8_attention_decode_bf16 needs: KV * ceil-chunks * (H/KV) * (D + 2) * 4,

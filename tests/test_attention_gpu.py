@@ -138,6 +138,34 @@ def test_layouts_and_local_sdpa():
     assert torch.equal(o, o2)
 
 
+def test_split_tiles_and_the_unsplit_entry():
+    """Long causal calls split their longest tiles' keys over several workgroups (the workspace
+    entry, which attention() uses); the entry without a workspace computes every tile in one
+    workgroup.  Both agree with the oracle; the split result is deterministic across calls."""
+    from w8a8 import lib
+    from w8a8._lib import call
+    T, D = 1300, 512
+    assert lib().w8a8_attention_workspace_bytes(8, 1, T, T, D, 0, 0) > 0
+    q, k, v = make(8, 1, T, T, D, seed=11, qscale=0.3)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    a, lse_a = attn.attention(qd, kd, vd, 0, 0, return_lse=True)
+    b = attn.attention(qd, kd, vd, 0, 0)
+    assert torch.equal(a, b)
+    u = torch.empty_like(a)
+    lse_u = torch.empty(8, T, dtype=torch.float32, device=DEV)
+    call("w8a8_attention_bf16", qd.data_ptr(), T * D, D, kd.data_ptr(), T * D, D, vd.data_ptr(), T * D, D, 8, 1, T, T,
+         D, 0, 0, 1.0, u.data_ptr(), T * D, D, lse_u.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    rows = list(range(0, 40)) + list(range(T - 200, T))
+    ref, bud, lse_ref = reference(q[:, rows[:40]], k[:, :40], v[:, :40], 0, 0)
+    check(a[:, :40], ref, bud, "split, first rows")
+    check(u[:, :40], ref, bud, "unsplit, first rows")
+    ref, bud, lse_ref = reference(q[:, T - 200:], k, v, T - 200, 0)
+    check(a[:, T - 200:], ref, bud, "split, last rows")
+    check(u[:, T - 200:], ref, bud, "unsplit, last rows")
+    assert np.allclose(lse_a[:, T - 200:].cpu().numpy(), lse_ref, rtol=1e-5, atol=1e-4)
+    assert np.allclose(lse_u[:, T - 200:].cpu().numpy(), lse_ref, rtol=1e-5, atol=1e-4)
+
+
 def test_deterministic():
     q, k, v = make(8, 1, 600, 600, 512, seed=3, qscale=0.3)
     qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
