@@ -690,9 +690,11 @@ static void launch(const GemmParams& p, int epi, bool a_packed, void* ws, int64_
 // Longer M: the fused GELU epilogue, whose stores are half as wide, runs best on 128x256 with two
 // 8-wave blocks per CU (5).  Other epilogues at a few thousand rows (M = 3658, 4096): 256x256
 // tiles (0) for the wide gate/up and PLE projections and 64x128 tiles with their accumulators
-// staged through LDS for row-contiguous stores (12) for the rest; this is the fastest rule for
-// the 141-GEMM int32 prefill sweep at both sizes.  At M = 16384, 128x128 tiles of 4 waves, two
-// blocks per CU (9), are within 5% of the best on every shape.
+// staged through LDS for row-contiguous stores (12) for the rest.  This is timed on the 141-GEMM
+// int32 prefill sweep itself, with a distinct weight per layer: there the 256-row tiles' halved
+// weight reads decide (gate/up 92 us in the sequence against 98 us on 128x256), while one GEMM
+// repeated on a cache-resident weight favours 128x256 (92 against 108 us).  At M = 16384, 128x256
+// (5) is the fastest on the stress shapes (gate/up + GELU 417 us, down + residual 189 us).
 int gemm_pick_config(int M, int NP, int K, int epi) {
   if (M <= 1024) {
     if (K >= 4096 && NP <= 4096) return 19;  // few 64x64 tiles, long K: four waves split the k-steps
@@ -700,7 +702,7 @@ int gemm_pick_config(int M, int NP, int K, int epi) {
   }
   if (epi == EPI_GELU) return 5;
   if (M <= 8192) return NP >= 8192 ? 0 : 12;
-  return 9;
+  return 5;
 }
 
 int gemm_launch(const GemmParams& p, int epi, int cfg, bool a_packed, void* ws, int64_t ws_bytes,
