@@ -374,9 +374,57 @@ def decode_attention_bench(dev, launches=50):
     return res
 
 
-def attention_bench(dev, reps):
+def cpu_attention_ms(D, W, T=ATTN_T, rows=512, reps=2):
+    """The reference's CPU prefill attention (torch's CPU sdpa, bf16, as pipeline.py:140-180 and
+    local_attn.py:91-107 call it) for the last `rows` queries of a T-token prompt: a sliding layer
+    as 128-query blocks against the W + 128 keys their window reaches (one batched, masked sdpa);
+    a full layer as one causal sdpa over the rows' own keys plus one non-causal sdpa over the
+    earlier keys, merged by their logsumexp.  Host threads: torch's default."""
+    import torch
+    import torch.nn.functional as F
+    g = torch.Generator().manual_seed(D)
+    q = (torch.randn(ATTN_H, rows, D, generator=g) * 0.3).to(torch.bfloat16)
+    k = (torch.randn(ATTN_KV, T, D, generator=g) * 0.3).to(torch.bfloat16)
+    v = torch.randn(ATTN_KV, T, D, generator=g).to(torch.bfloat16)
+    s = T - rows
+    flash = torch.ops.aten._scaled_dot_product_flash_attention_for_cpu
+
+    def sliding():
+        B = 128
+        nb = rows // B
+        qb = q.view(ATTN_H, nb, B, D).transpose(0, 1)
+        kw = k[:, s - W: T].unfold(1, W + B, B).permute(1, 0, 3, 2)
+        vw = v[:, s - W: T].unfold(1, W + B, B).permute(1, 0, 3, 2)
+        qp = s + torch.arange(nb)[:, None, None] * B + torch.arange(B)[None, :, None]
+        kp = qp[:, :1, :1] - W + torch.arange(W + B)[None, None, :]
+        mask = ((kp >= 0) & (kp <= qp) & (qp - kp < W))[:, None]
+        return F.scaled_dot_product_attention(qb, kw, vw, attn_mask=mask, scale=1.0, enable_gqa=True)
+
+    def full():
+        kb = k[None, :, s:].expand(1, ATTN_H, rows, D).contiguous()
+        vb = v[None, :, s:].expand(1, ATTN_H, rows, D).contiguous()
+        ob, lb = flash(q[None], kb, vb, 0.0, True, scale=1.0)
+        ka = k[None, :, :s].expand(1, ATTN_H, s, D).contiguous()
+        va = v[None, :, :s].expand(1, ATTN_H, s, D).contiguous()
+        oa, la = flash(q[None], ka, va, 0.0, False, scale=1.0)
+        m = torch.maximum(la, lb)
+        w1, w2 = torch.exp(la - m)[..., None], torch.exp(lb - m)[..., None]
+        return ((oa.float() * w1 + ob.float() * w2) / (w1 + w2)).to(torch.bfloat16)
+
+    fn = sliding if W else full
+    fn()
+    times = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t)
+    return min(times) * 1e3
+
+
+def attention_bench(dev, reps, cpu=True):
     """Prefill attention of the 3658-token prompt: each layer kind in one call over the whole prompt,
-    and the reference pipeline's largest per-micro-batch calls (pipeline.py:281-295)."""
+    and the reference pipeline's largest per-micro-batch calls (pipeline.py:281-295); with cpu, the
+    reference's CPU attention for the same last micro-batch beside them."""
     import torch
     from w8a8 import attention as attn
     T = ATTN_T
@@ -396,6 +444,11 @@ def attention_bench(dev, reps):
         ms_mb = event_time_ms(lambda: attn.attention(q[:, qs:], k, v, qs, W, out=out[:, qs:]), reps, 3)
         e["last_micro_batch_us"] = round(ms_mb * 1e3, 1)
         e["last_micro_batch"] = f"{r} queries at position {qs}"
+        if cpu:
+            cms = cpu_attention_ms(D, W, rows=r)
+            e["cpu_last_micro_batch_ms"] = round(cms, 2)
+            e["cpu_threads"] = torch.get_num_threads()
+            e["speedup_vs_cpu_last_micro_batch"] = round(cms / (ms_mb * 1e3) * 1e3, 1)
         res[name] = e
         total_us += layers * ms * 1e3
         del q, k, v, out
@@ -621,7 +674,7 @@ def main():
                                             "row_major_gbs": round(nbytes / (ms_rm * 1e-3) / 1e9, 1)}
             log(f"bench: gemv lm head M={Mg}: {extra[f'gemv_lm_head_m{Mg}']}")
         torch.cuda.empty_cache()
-        extra["attention_prefill_t3658"] = attention_bench(dev, reps=20)
+        extra["attention_prefill_t3658"] = attention_bench(dev, reps=20, cpu=not args.no_cpu)
         log(f"bench: attention: {extra['attention_prefill_t3658']}")
         torch.cuda.empty_cache()
         extra["decode_attention_t3658"] = decode_attention_bench(dev)
