@@ -494,6 +494,9 @@ def main():
     ap.add_argument("--profile-e2e", action="store_true",
                     help="for kernel traces: one prefill of the 3658-token prompt and --steps decode tokens of the "
                          "E2B-shaped HF Gemma 4 on the engine, then exit")
+    ap.add_argument("--profile-decode", action="store_true",
+                    help="for kernel traces: decode attention at the end of the 3658-token prompt for each layer "
+                         "kind (--steps calls each, eager) and exit")
     ap.add_argument("--profile-chain", action="store_true",
                     help="for kernel traces: run the device layer chain (--steps times, eager) and exit")
     args = ap.parse_args()
@@ -535,6 +538,18 @@ def main():
                 past, nxt = o.past_key_values, o.logits[0, -1].argmax().view(1, 1)
         torch.cuda.synchronize()
         log(f"bench: ran the E2B-shaped model: prefill of {ATTN_T} tokens, {args.steps} decode tokens")
+        return 0
+    if args.profile_decode:
+        from w8a8 import attention as attn
+        for name, (D, W, _) in ATTN_LAYERS.items():
+            _, k, v = attention_inputs(D, ATTN_T, dev, seed=D + 1)
+            q = (torch.randn(ATTN_H, D, generator=torch.Generator(device=dev).manual_seed(7), device=dev) * 0.3).to(
+                torch.bfloat16)
+            out = torch.empty_like(q)
+            for _ in range(args.steps):
+                attn.decode(q, k, v, ATTN_T - 1, W, out=out)
+            torch.cuda.synchronize()
+            log(f"bench: ran {name} decode attention (keys {ATTN_T}, head_dim {D}, window {W}) {args.steps} times")
         return 0
     if args.profile_attention:
         from w8a8 import attention as attn

@@ -106,3 +106,55 @@ def test_python_layer_raises():
         ops.quant_rows(torch.zeros(2, 16, dtype=torch.bfloat16))
     with pytest.raises(TypeError):
         ops.gemm_i32(torch.zeros(2, 16, dtype=torch.int8), object())
+
+
+def test_attention_workspace_and_errors():
+    """Attention workspace sizing (closed forms) and argument errors, all decided on the host."""
+    L = _lib.lib()
+    part512 = 8 * 64 * (512 // 16 + 1) * 16      # one split part of a 128-row tile at head_dim 512
+    # sliding windows and short causal calls need no workspace
+    assert L.w8a8_attention_workspace_bytes(8, 1, 3658, 3658, 256, 0, 512) == 0
+    assert L.w8a8_attention_workspace_bytes(8, 1, 200, 200, 128, 0, 0) == 0
+    # 256 queries at the end of the 3658-token prompt, head_dim 512: 16 tiles of 115 key blocks,
+    # fair share 8 blocks per CU -> every tile split into 8 parts (8-part cap)
+    assert L.w8a8_attention_workspace_bytes(8, 1, 256, 3658, 512, 3402, 0) == 4096 + 16 * 8 * part512
+    ws = L.w8a8_attention_workspace_bytes(8, 1, 3658, 3658, 512, 0, 0)
+    assert ws > 4096 and (ws - 4096) % (3 * part512) == 0   # the longest tiles in 3 parts
+    assert L.w8a8_attention_workspace_bytes(8, 3, 16, 16, 256, 0, 0) == -1     # H % KV
+    assert L.w8a8_attention_workspace_bytes(8, 1, 16, 8, 256, 0, 0) == -1      # Tk < Tq
+    assert L.w8a8_attention_workspace_bytes(8, 1, 16, 16, 64, 0, 0) == -1      # head_dim
+    # decode: chunks of 64 keys (32 at head_dim 512) over the visible range
+    assert L.w8a8_attention_decode_workspace_bytes(8, 1, 3658, 512, 3657, 0) == 115 * 8 * 514 * 4
+    assert L.w8a8_attention_decode_workspace_bytes(8, 1, 3658, 256, 3657, 512) == 8 * 8 * 258 * 4
+    assert L.w8a8_attention_decode_workspace_bytes(8, 1, 1, 256, 0, 0) == 1 * 8 * 258 * 4
+    assert L.w8a8_attention_decode_workspace_bytes(32, 1, 100, 256, 99, 0) == -1   # > 16 heads per KV head
+    assert L.w8a8_attention_decode_workspace_bytes(8, 1, 100, 256, 100, 0) == -1   # q_pos past the keys
+    fake = ctypes.c_void_p(0x100000)
+    rc, msg = _status("w8a8_attention_bf16", fake, 64 * 8, 64, fake, 64 * 8, 64, fake, 64 * 8, 64, 1, 1, 8, 8, 64, 0,
+                      0, 1.0, fake, 64 * 8, 64, None, None)
+    assert rc == _lib.W8A8_ENOTSUP and "head_dim" in msg
+    rc, msg = _status("w8a8_attention_bf16", fake, 256 * 8, 256, fake, 256 * 8, 256, fake, 256 * 8, 256, 1, 1, 8, 4,
+                      256, 0, 0, 1.0, fake, 256 * 8, 256, None, None)
+    assert rc == _lib.W8A8_EINVAL and "Tk >= q_start" in msg
+    rc, msg = _status("w8a8_attention_bf16", fake, 256 * 8, 256, fake, 256 * 8, 256, fake, 256 * 8, 256, 1, 1, 8, 8,
+                      256, 0, 0, -1.0, fake, 256 * 8, 256, None, None)
+    assert rc == _lib.W8A8_EINVAL and "scale" in msg
+    rc, msg = _status("w8a8_attention_bf16", fake, 256 * 8, 260, fake, 256 * 8, 256, fake, 256 * 8, 256, 1, 1, 8, 8,
+                      256, 0, 0, 1.0, fake, 256 * 8, 256, None, None)
+    assert rc == _lib.W8A8_EALIGN
+    rc, msg = _status("w8a8_attention_decode_bf16", fake, 256, fake, 100 * 256, 256, fake, 100 * 256, 256, 8, 1, 100,
+                      256, 99, 0, 1.0, fake, 256, None, fake, 16, None)
+    assert rc == _lib.W8A8_EINVAL and "workspace" in msg
+    rc, msg = _status("w8a8_attention_decode_bf16", fake, 256, fake, 100 * 256, 256, fake, 100 * 256, 256, 8, 1, 100,
+                      256, 100, 0, 1.0, fake, 256, None, fake, 1 << 20, None)
+    assert rc == _lib.W8A8_EINVAL and "q_pos" in msg
+
+
+def test_attention_python_layer_raises():
+    import torch
+    from w8a8 import attention
+    with pytest.raises(ValueError, match="GPU tensor"):
+        attention.attention(*(torch.zeros(1, 4, 128, dtype=torch.bfloat16) for _ in range(3)))
+    with pytest.raises(ValueError, match="batch size 1"):
+        attention.local_sdpa(None, torch.zeros(2, 1, 4, 128), torch.zeros(2, 1, 4, 128), torch.zeros(2, 1, 4, 128),
+                             None)
