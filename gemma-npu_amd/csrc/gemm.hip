@@ -44,13 +44,6 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, void* lds, uint3
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
 }
 
-// Logical tile of block b: each of the 8 XCDs gets a contiguous run.
-__device__ __forceinline__ int xcd_remap(int b, int nblocks) {
-  const int full = nblocks & ~7;
-  if (b >= full) return b;
-  const int per = full >> 3;
-  return (b & 7) * per + (b >> 3);
-}
 
 // Epilogue for one 32x32 accumulator tile.  Lane l holds row m and, for register group
 // g = 0..3, packed columns t*32 + 8g + lcol + r (r = 0..3, lcol = 4*(l/32)).  sxm is the row's
@@ -152,6 +145,7 @@ __device__ __forceinline__ void ksplit_epilogue(const GemmParams& p, const int32
                                                 int m0, int t0) {
   constexpr int TPR = BN / 16;
   constexpr int RPP = NW * 64 / TPR;
+  static_assert(RPP * TPR == NW * 64, "each row is covered by whole threads");
   static_assert(EPI != EPI_GELU || BN == 64 || BN == 128, "GELU pairing needs a 64- or 128-wide tile");
   const int q = int(threadIdx.x) % TPR;
   for (int r = int(threadIdx.x) / TPR; r < BM; r += RPP) {
@@ -454,7 +448,8 @@ __global__ __launch_bounds__(WGM * WGN * KW * 64, MINB) void gemm_kernel(GemmPar
   // tiles whose ring can hold the whole accumulator tile stage it there too, so that every
   // store instruction writes whole row segments instead of 16 or 32 bytes of 32 rows --------
   constexpr int LDR = BN + 4;  // padded row (int32) of the staged tiles
-  constexpr bool STAGED = KW > 1 || (!SPLIT && BM * LDR * 4 <= RING && (EPI != EPI_GELU || BN == 64 || BN == 128));
+  constexpr bool STAGED = KW > 1 || (!SPLIT && BM * LDR * 4 <= RING && (NW * 64) % (BN / 16) == 0 &&
+                                     (EPI != EPI_GELU || BN == 64 || BN == 128));
   if constexpr (STAGED) {
     static_assert(KW * BM * LDR * 4 <= RING, "the staged partial tiles must fit in the ring");
     int32_t* red = reinterpret_cast<int32_t*>(lds);
@@ -583,6 +578,7 @@ static constexpr TileCfg kCfg[] = {
     {128, 64, 4, 8, 3, 2},  // 21: two sub-tiles stacked, 2 waves each; 144 KiB ring
 };
 static constexpr int kNumCfg = int(sizeof(kCfg) / sizeof(kCfg[0]));
+static_assert(kNumCfg == 22, "every configuration needs its case in gemm_launch");
 static constexpr int64_t kCounterBytes = 4096;
 
 int gemm_config_count() { return kNumCfg; }
@@ -682,11 +678,15 @@ static void launch(const GemmParams& p, int epi, bool a_packed, void* ws, int64_
 
 // Tile choice, from timing every configuration with the bf16 epilogues on the E2B prefill
 // shapes (M = 512, 3658, 16384).  At one 512-row micro-batch the GEMMs are bound by how fast
-// each CU streams its operands, so small tiles that spread the work over more CUs win: 64x64
-// (14) for the narrow, short-K output projection, 64x128 three blocks per CU (12) otherwise.
-// The long-K down projection has only 192 such tiles, one block per CU, whose two waves cannot
-// hide their LDS reads behind two MFMAs per k-step: four waves that each own the whole 64x64
-// tile and take every fourth k-step (19) keep all four SIMDs issuing.
+// each CU streams its operands, so small tiles that spread the work over more CUs win: 64x128
+// three blocks per CU (12) for the wide and short-K GEMMs, 64x64 (14) for narrow short-K ones.
+// The narrow long-K GEMMs (the output projection, K = 2048, and the down projection, K = 6144,
+// both N = 1536) have only 192 such tiles, one block per CU, whose two waves cannot hide their
+// LDS reads behind two MFMAs per k-step: four waves that each own the whole 64x64 tile and take
+// every fourth k-step (19) keep all four SIMDs issuing (output projection 7.3 us against 9.5 us
+// on 64x64 with two waves, down 16.1 us against 21.6 us or more).  A 128x192 tile, one per CU
+// for the gate/up GEMM (256 tiles), measured slower than 12 there (17.2 against 15.9 us): its one
+// wave per SIMD leaves the LDS reads exposed.
 // Longer M: the fused GELU epilogue, whose stores are half as wide, runs best on 128x256 with two
 // 8-wave blocks per CU (5).  Other epilogues at a few thousand rows (M = 3658, 4096): 256x256
 // tiles (0) for the wide gate/up and PLE projections and 64x128 tiles with their accumulators
@@ -697,8 +697,8 @@ static void launch(const GemmParams& p, int epi, bool a_packed, void* ws, int64_
 // (5) is the fastest on the stress shapes (gate/up + GELU 417 us, down + residual 189 us).
 int gemm_pick_config(int M, int NP, int K, int epi) {
   if (M <= 1024) {
-    if (K >= 4096 && NP <= 4096) return 19;  // few 64x64 tiles, long K: four waves split the k-steps
-    return (NP <= 2048 && K < 4096) ? 14 : 12;
+    if (K >= 2048 && NP <= 4096) return 19;  // few 64x64 tiles, long K: four waves split the k-steps
+    return NP <= 2048 ? 14 : 12;
   }
   if (epi == EPI_GELU) return 5;
   if (M <= 8192) return NP >= 8192 ? 0 : 12;

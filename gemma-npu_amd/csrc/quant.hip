@@ -135,7 +135,8 @@ __global__ __launch_bounds__(256) void quant_rows_packed_kernel(const uint16_t* 
                                                                 int Mp, int K, int KF, int8_t* __restrict__ q,
                                                                 float* __restrict__ scale) {
   const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  // Blocks in XCD order, so the 8 rows sharing each 128-byte line of q are written in one L2.
+  const int row = xcd_remap(int(blockIdx.x), int(gridDim.x)) * 4 + (threadIdx.x >> 6);
   if (row >= Mp) return;
   const int KP = KF * 32;
   if (row >= M) {
@@ -192,7 +193,10 @@ __global__ __launch_bounds__(256) void quant_rows_blk_kernel(const uint16_t* __r
                                                              float* __restrict__ scale) {
   __shared__ float wave_amax[4];
   const int t = threadIdx.x;
-  const int row = blockIdx.x;
+  // Packed output: the 16-byte pieces of 8 consecutive rows share each 128-byte line, so rows
+  // are dealt out XCD by XCD and every line is assembled in one L2 (round-robin rows would leave
+  // a dirty eighth of every line in each of the 8 L2s).
+  const int row = PACKED ? xcd_remap(int(blockIdx.x), int(gridDim.x)) : int(blockIdx.x);
   const int KP = PACKED ? KF * 32 : K;
   auto dst = [&](int k) -> int8_t* {
     if constexpr (PACKED)

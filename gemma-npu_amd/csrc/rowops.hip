@@ -130,7 +130,9 @@ template <int CH, bool IN_I32, int OP>
 __global__ __launch_bounds__(256) void row_chain_kernel(RowChain p) {
   __shared__ float red[3][4];
   const int t = threadIdx.x, nt = int(blockDim.x);
-  const int row = blockIdx.x;
+  // Packed q: 8 consecutive rows share each 128-byte line of the layout, so rows are dealt out XCD
+  // by XCD and each line is assembled in one L2.
+  const int row = p.KF ? xcd_remap(int(blockIdx.x), int(gridDim.x)) : int(blockIdx.x);
   const int KQ = p.KF ? p.KF * 32 : p.N;  // q columns written
   auto qdst = [&](int k) -> int8_t* {
     return p.KF ? p.q + packed_act_offset(row, k & ~15, p.KF) + (k & 15) : p.q + int64_t(row) * p.ldq + k;

@@ -97,6 +97,17 @@ __device__ __forceinline__ int8_t quant1_bf16(float v, float s, float rs) {
   return int8_t(int(q));
 }
 
+// ---- XCD-aware block order ---------------------------------------------------------------------
+// Workgroups are dealt to the 8 XCDs round-robin (block b runs on XCD b % 8), each XCD with its
+// own L2.  xcd_remap(b) gives each XCD a contiguous run of logical indices (the last nblocks % 8
+// blocks keep their own index).
+__device__ __forceinline__ int xcd_remap(int b, int nblocks) {
+  const int full = nblocks & ~7;
+  if (b >= full) return b;
+  const int per = full >> 3;
+  return (b & 7) * per + (b >> 3);
+}
+
 // ---- packed activations ----------------------------------------------------------------------
 // The GEMM reads A fastest when it is laid out like the packed weight: 1 KiB fragments of 32
 // rows x 32 k, fragment (mt, j) at (mt * KF + j) * 1024 with KF = 2 * ceil(K/64), byte 16*l + b
