@@ -293,7 +293,10 @@ def e2b_model(dev):
     """A Gemma 4 E2B-shaped text decoder (HF transformers' own model code), random-init in bf16 on
     the GPU, with the engine underneath (w8a8.hf.to_gpu).  Shapes: hidden 1536, 35 layers (4
     sliding + 1 full, repeated), 8 query heads on 1 KV head, head_dim 256 / 512, window 512, the
-    last 20 layers KV-shared with double-wide MLPs, 256-wide per-layer inputs, vocab 262144."""
+    last 20 layers KV-shared with double-wide MLPs, 256-wide per-layer inputs, vocab 262144.  The q /
+    k norm weights are head_dim^-1/4, as a trained model's small norm weights keep the (scale 1.0)
+    scores near unit variance; with the init's 1.0 the random model's softmax is nearly one-hot and
+    any rounding difference grows layer by layer, which would make logit comparisons meaningless."""
     import torch
     from transformers.models.gemma4.configuration_gemma4 import Gemma4TextConfig
     from transformers.models.gemma4.modeling_gemma4 import Gemma4ForCausalLM
@@ -311,9 +314,43 @@ def e2b_model(dev):
             model = Gemma4ForCausalLM(cfg).eval()
     finally:
         torch.set_default_dtype(old)
+    with torch.no_grad():
+        for layer in model.model.layers:
+            a = layer.self_attn
+            a.q_norm.weight.fill_(a.head_dim ** -0.25)
+            if getattr(a, "k_norm", None) is not None:
+                a.k_norm.weight.fill_(a.head_dim ** -0.25)
     nparams = sum(p.numel() for p in model.parameters())
     hf.to_gpu(model)
     return model, nparams
+
+
+def pipeline_prefill_bench(model, ids, hf_logits, reps=3):
+    """The reference's prefill pipeline (pipeline.py:224-339) on the GPU, w8a8.pipeline.Prefill, on
+    the same model and prompt: whole-prompt layers (the default) and the reference's 512-row
+    micro-batches; each the median of `reps` timed calls after one warm-up.  Its logits are compared
+    with the HF-driven engine's (relative L2 difference of the last-token logits)."""
+    import torch
+    from w8a8.pipeline import Prefill
+    res = {}
+    for name, step in (("whole_prompt", None), ("row_step_512", 512)):
+        pre = Prefill(model, row_step=step)
+        times = []
+        for _ in range(reps + 1):
+            torch.cuda.synchronize()
+            t = time.perf_counter()
+            logits, _ = pre(ids)
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - t)
+        diff = ((logits - hf_logits).norm() / hf_logits.norm()).item()
+        res[name] = {"ms": round(statistics.median(times[1:]) * 1e3, 2), "logits_rel_diff_vs_hf_engine": round(diff, 4)}
+        log(f"bench: pipeline prefill {name}: {res[name]}")
+    res["what"] = ("w8a8.pipeline.Prefill: embedding/PLE/RoPE tables from the model, then per layer k_in, qkv "
+                   "GEMM, k_qkv, attention, k_attn_out, o GEMM, k_post_attn, gate/up GEMM, k_gelu, down GEMM, "
+                   "k_post_ff, PLE gate GEMM, k_ple_gate, PLE projection GEMM, k_ple_out (int32 GEMMs + fused "
+                   "kernels + attention kernels), final norm and the int8 LM head GEMV; returns the logits and "
+                   "the filled DynamicCache")
+    return res
 
 
 def e2e_bench(dev, T=ATTN_T, n_decode=32):
@@ -338,8 +375,10 @@ def e2e_bench(dev, T=ATTN_T, n_decode=32):
             past, nxt = o.past_key_values, o.logits[0, -1].argmax().view(1, 1)
         torch.cuda.synchronize()
         dt = time.perf_counter() - t
+        pipe = pipeline_prefill_bench(model, ids, out.logits[0, -1].float())
     del model, past, out, o
     return {"prefill_ms": round(statistics.median(ttfts[1:]) * 1e3, 1), "prompt_tokens": T,
+            "pipeline_prefill": pipe,
             "decode_tok_s": round(n_decode / dt, 1), "decode_ms_per_token": round(dt / n_decode * 1e3, 2),
             "decode_tokens": n_decode, "params": nparams,
             "what": "HF Gemma 4 (transformers' modeling code, unchanged) with E2B's shapes, random-init bf16 weights, "
@@ -495,6 +534,9 @@ def main():
     ap.add_argument("--profile-e2e", action="store_true",
                     help="for kernel traces: one prefill of the 3658-token prompt and --steps decode tokens of the "
                          "E2B-shaped HF Gemma 4 on the engine, then exit")
+    ap.add_argument("--profile-pipeline", action="store_true",
+                    help="for kernel traces: --steps whole-prompt prefills of the 3658-token prompt through "
+                         "w8a8.pipeline.Prefill on the E2B-shaped HF Gemma 4, then exit")
     ap.add_argument("--profile-decode", action="store_true",
                     help="for kernel traces: decode attention at the end of the 3658-token prompt for each layer "
                          "kind (--steps calls each, eager) and exit")
@@ -539,6 +581,16 @@ def main():
                 past, nxt = o.past_key_values, o.logits[0, -1].argmax().view(1, 1)
         torch.cuda.synchronize()
         log(f"bench: ran the E2B-shaped model: prefill of {ATTN_T} tokens, {args.steps} decode tokens")
+        return 0
+    if args.profile_pipeline:
+        from w8a8.pipeline import Prefill
+        model, _ = e2b_model(dev)
+        ids = torch.randint(0, 262144, (1, ATTN_T), generator=torch.Generator().manual_seed(1)).to(dev)
+        pre = Prefill(model)
+        for _ in range(args.steps):
+            pre(ids)
+        torch.cuda.synchronize()
+        log(f"bench: ran {args.steps} whole-prompt pipeline prefills of {ATTN_T} tokens on the E2B-shaped model")
         return 0
     if args.profile_decode:
         from w8a8 import attention as attn

@@ -668,7 +668,11 @@ static void launch(const GemmParams& p, int epi, bool a_packed, void* ws, int64_
   // The waves / kw wave groups laid out along the longer side of the block tile: 8 as 4x2
   // (BM >= BN) or 2x4, 4 as 2x2, 2 as 2x1 (BM >= BN) or 1x2, 1 as 1x1.
   constexpr int WG = c.waves / c.kw;
-  constexpr int WGM = WG == 1 ? 1 : (WG == 2 ? (c.bm >= c.bn ? 2 : 1) : (WG == 4 ? 2 : (c.bm >= c.bn ? 4 : 2)));
+  constexpr int WGM = WG == 1 ? 1
+                    : WG == 2 ? (c.bm >= c.bn ? 2 : 1)
+                    : WG == 4 ? 2
+                    : WG == 8 ? (c.bm >= c.bn ? 4 : 2)
+                              : (c.bm >= c.bn ? 8 : 2);
   constexpr int WGN = WG / WGM;
   if (a_packed)
     launch_epi<c.bm, c.bn, WGM, WGN, c.kw, c.ks, c.ns, true>(p, epi, ws, ws_bytes, stream);

@@ -2,7 +2,9 @@
 
     from w8a8 import ops          # torch-facing entry points (GEMM, quant, GEMV, linear)
     from w8a8 import fused        # the reference's fused kernels between the GEMMs (k_in ... k_ple_out)
-    from w8a8 import attention    # prefill attention (full_attention, sliding_attention, local_sdpa)
+    from w8a8 import attention    # prefill and decode attention (full_attention, sliding_attention, local_sdpa)
+    from w8a8 import hf           # HF Gemma 4 on the engine (to_gpu, the reference's to_npu)
+    from w8a8.pipeline import Prefill   # the reference's whole-prompt prefill, every step on the GPU
     import npu_kernels            # drop-in for the reference's npu_kernels.mm_i8
 """
 from . import attention, fused  # noqa: F401

@@ -30,7 +30,7 @@ class GpuGemm(torch.nn.Module):
     per-channel int8 quantisation (absmax / 127), packed for the GEMM (fp32 scales) and for the
     GEMV (bf16 scales, the reference's decode copy w_cpu / sw_cpu, gemma_npu.py:81-82)."""
 
-    def __init__(self, linears):
+    def __init__(self, linears, gelu_pair=False):
         super().__init__()
         w = torch.cat([l.weight.detach() for l in linears], 0)
         if w.device.type != "cuda":
@@ -39,7 +39,11 @@ class GpuGemm(torch.nn.Module):
         self.sizes = [l.out_features for l in linears]
         self.dtype = w.dtype
         q, sw = ops.quant_rows(w.float().contiguous())
+        self.sw = sw
         self.packed = ops.pack_weight(q, "nk", sw=sw)
+        # [gate; up]: a second copy packed for the GEMM's fused gelu(gate) * up epilogue, which the
+        # whole-prompt pipeline uses in place of the int32 result and k_gelu
+        self.packed_gelu = ops.pack_weight(q, "nk", self.N // 2, sw=sw) if gelu_pair else None
         self.gemv_w = ops.pack_gemv_weight(q)
         self.sw_bf16 = sw.to(torch.bfloat16)
         self.pending = None
@@ -109,10 +113,13 @@ def register_attention():
 
 def to_gpu(model):
     """Swap the text decoder's linears for GPU W8A8 groups, the LM head for the int8 GEMV head, and
-    the attention for local_sdpa (gemma_npu.py:208-241, 253).  Returns the groups."""
+    the attention for local_sdpa (gemma_npu.py:208-241, 253).  Returns the groups; model.layer_gemms
+    holds each layer's groups by name ("qkv", "o", "gate_up", "down", "ple_gate", "ple_proj") for
+    w8a8.pipeline.Prefill."""
     lm = language_model(model)
     groups = []
-    for layer in lm.layers:
+    per_layer = []  # (layer index, group key) of each group, as the reference's layer_gemms keys
+    for li, layer in enumerate(lm.layers):
         a, mlp = layer.self_attn, layer.mlp
         qkv = [a.q_proj]
         if not a.is_kv_shared_layer:
@@ -121,18 +128,24 @@ def to_gpu(model):
                    (a, ["o_proj"], [a.o_proj]),
                    (mlp, ["gate_proj", "up_proj"], [mlp.gate_proj, mlp.up_proj]),
                    (mlp, ["down_proj"], [mlp.down_proj])]
+        per_layer += [(li, "qkv"), (li, "o"), (li, "gate_up"), (li, "down")]
         if getattr(layer, "per_layer_input_gate", None) is not None:
             groups += [(layer, ["per_layer_input_gate"], [layer.per_layer_input_gate]),
                        (layer, ["per_layer_projection"], [layer.per_layer_projection])]
+            per_layer += [(li, "ple_gate"), (li, "ple_proj")]
     if getattr(lm, "per_layer_model_projection", None) is not None:
         groups.append((lm, ["per_layer_model_projection"], [lm.per_layer_model_projection]))
     gemms = []
     for parent, names, linears in groups:
-        g = GpuGemm(linears)
+        g = GpuGemm(linears, gelu_pair=names == ["gate_proj", "up_proj"])
         g.name = "+".join(names)
         gemms.append(g)
         for i, (name, l) in enumerate(zip(names, linears)):
             setattr(parent, name, Slice(g, i, l.in_features, l.out_features))
+    # the per-layer groups by name, for the whole-prompt pipeline (gemma_npu.py:238-239)
+    model.layer_gemms = [{} for _ in lm.layers]
+    for (li, key), g in zip(per_layer, gemms):
+        model.layer_gemms[li][key] = g
     # tied to the input embedding, so this is a new int8 copy, not a swap
     model.lm_head = Int8Head(model.lm_head)
     register_attention()
