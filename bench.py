@@ -117,6 +117,34 @@ def graph_time_ms(fn, dev, launches=50, reps=10):
     return s.elapsed_time(e) / (reps * launches)
 
 
+def clock_during(fn, dev, launches=100, window_ms=1.0):
+    """Engine clock (GHz) while fn's kernels run: `launches` copies of fn captured in one graph and
+    replayed on the current stream, while w8a8_clock_probe's one wave on a second stream (default
+    priority) counts core cycles against the real-time counter over `window_ms` inside the replay."""
+    import ctypes
+    import torch
+    from w8a8._lib import call
+    out = torch.zeros(2, dtype=torch.int64, device=dev)
+    khz = ctypes.c_int(0)
+    side = torch.cuda.Stream(dev)
+    call("w8a8_clock_probe", out.data_ptr(), 100, ctypes.byref(khz), side.cuda_stream)
+    torch.cuda.synchronize(dev)
+
+    def many():
+        for _ in range(launches):
+            fn()
+    graph = capture(many, dev)
+    replay_ms = event_time_ms(graph.replay, 1, 1)
+    window_ms = min(window_ms, 0.6 * replay_ms)
+    ticks = max(1, int(khz.value * window_ms))
+    torch.cuda.synchronize(dev)
+    graph.replay()
+    call("w8a8_clock_probe", out.data_ptr(), ticks, ctypes.byref(khz), side.cuda_stream)
+    torch.cuda.synchronize(dev)
+    cycles, real = out.tolist()
+    return cycles / (real / (khz.value * 1e3)) / 1e9
+
+
 def read_traffic():
     """HBM bytes per launch of the dominant kernel, from the committed rocprofv3 counter summary
     (FETCH_SIZE + WRITE_SIZE, each calibrated on a 64 MiB copy); None if it is absent."""
@@ -676,10 +704,15 @@ def main():
     gu_ms = per_ms["gate_up"]
     achieved = gu_ops / (gu_ms * 1e-3) / 1e12
     traffic = read_traffic()
+    clock = clock_during(lambda: ops.gemm_bf16(gu["q"], gu["sx"], gu["pw"], epilogue="gelu", out=gu["out"]), dev)
+    peak_at_clock = 256 * 8192 * clock / 1e3  # TOP/s: 256 CUs x 8192 int8 op/clk/CU at the measured clock
     roofline = {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": traffic,
                 "kernel": "gemm_kernel<EPI_GELU> gate_up M=512 K=1536 N=12288, packed A",
-                "avg_launch_us": round(gu_ms * 1e3, 2)}
+                "avg_launch_us": round(gu_ms * 1e3, 2), "clock_ghz": round(clock, 3),
+                "frac_at_clock": round(achieved / peak_at_clock, 4)}
+    log(f"bench: gate_up runs at {clock:.3f} GHz: {achieved:.0f} TOP/s = {achieved / peak_at_clock:.3f} of the "
+        f"MFMA peak at that clock ({peak_at_clock:.0f} TOP/s)")
     log(f"bench: per-GEMM us: " + ", ".join(f"{k} {v * 1e3:.1f}" for k, v in per_ms.items()))
 
     # ---- host CPU baseline: torch._int_mm on the same four GEMMs -------------------------

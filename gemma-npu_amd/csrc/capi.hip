@@ -79,6 +79,25 @@ int64_t w8a8_packed_weight_bytes_internal(int64_t N, int64_t K, int64_t interlea
   return nt * 2 * ((K + 63) / 64) * 1024;
 }
 
+// Shader-clock probe: one wave reads the core-clock counter (s_memtime) and the constant-rate
+// real-time counter (s_memrealtime) at the start and at the end of a window of `ticks` real-time
+// ticks, sleeping between reads; the ratio is the engine clock over the window, whatever else
+// runs on the device meanwhile.  The loop also ends after 2^22 reads, so it always terminates.
+__global__ __launch_bounds__(64) void clock_probe_kernel(unsigned long long* out, unsigned ticks) {
+  const unsigned long long r0 = __builtin_amdgcn_s_memrealtime();
+  const unsigned long long c0 = __builtin_amdgcn_s_memtime();
+  unsigned long long r = r0;
+  for (int n = 0; r - r0 < ticks && n < (1 << 22); ++n) {
+    __builtin_amdgcn_s_sleep(8);
+    r = __builtin_amdgcn_s_memrealtime();
+  }
+  const unsigned long long c1 = __builtin_amdgcn_s_memtime();
+  if (threadIdx.x == 0) {
+    out[0] = c1 - c0;
+    out[1] = r - r0;
+  }
+}
+
 }  // namespace w8a8
 
 using namespace w8a8;
@@ -86,6 +105,17 @@ using namespace w8a8;
 extern "C" {
 
 const char* w8a8_last_error(void) { return g_err; }
+
+int w8a8_clock_probe(unsigned long long* out, unsigned ticks, int* wall_clock_khz, hipStream_t stream) {
+  if (!out || !wall_clock_khz) return fail(W8A8_EINVAL, "clock_probe: null pointer");
+  if (ticks == 0 || ticks > 100000000u) return fail(W8A8_EINVAL, "clock_probe: ticks %u out of range", ticks);
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(wall_clock_khz, hipDeviceAttributeWallClockRate, dev);
+  if (e != hipSuccess) return fail(W8A8_EHIP, "clock_probe: %s", hipGetErrorString(e));
+  clock_probe_kernel<<<1, 64, 0, stream>>>(out, ticks);
+  return check_launch("clock_probe");
+}
 
 int w8a8_abi_version(void) { return 1; }
 

@@ -101,6 +101,15 @@ int w8a8_gemm_i32(const int8_t *a, int64_t lda, const int8_t *w_packed, int64_t 
  * counts is device memory, 8-byte aligned, zeroed by the caller. */
 int w8a8_selfcheck_quant_step(unsigned long long *counts, hipStream_t stream);
 
+/* Engine-clock probe (no counterpart in the reference; for benchmarks that state the clock a
+ * kernel ran at): launches one wave on `stream` that reads the core-clock counter and the
+ * constant-rate real-time counter at the start and the end of a window of `ticks` real-time ticks
+ * (ticks in 1 .. 1e8) and writes out[0] = core cycles and out[1] = real-time ticks elapsed (device
+ * memory, 8-byte aligned).  *wall_clock_khz (host) receives the real-time counter's rate, so the
+ * clock over the window is out[0] / out[1] * wall_clock_khz kHz.  Launched on a second stream while
+ * other kernels run, it measures the clock they run at. */
+int w8a8_clock_probe(unsigned long long *out, unsigned ticks, int *wall_clock_khz, hipStream_t stream);
+
 /* ---- packed activations ----------------------------------------------------------------- */
 
 /* The GEMM streams A fastest when it is laid out like the packed weight: 1 KiB fragments of

@@ -158,3 +158,14 @@ def test_attention_python_layer_raises():
     with pytest.raises(ValueError, match="batch size 1"):
         attention.local_sdpa(None, torch.zeros(2, 1, 4, 128), torch.zeros(2, 1, 4, 128), torch.zeros(2, 1, 4, 128),
                              None)
+
+
+def test_clock_probe_rejects_bad_arguments_on_the_host():
+    fake = ctypes.c_void_p(0x100000)
+    khz = ctypes.c_int(0)
+    rc, msg = _status("w8a8_clock_probe", fake, 0, ctypes.byref(khz), None)
+    assert rc == _lib.W8A8_EINVAL and "ticks" in msg
+    rc, msg = _status("w8a8_clock_probe", fake, 200000000, ctypes.byref(khz), None)
+    assert rc == _lib.W8A8_EINVAL and "ticks" in msg
+    rc, msg = _status("w8a8_clock_probe", None, 100, ctypes.byref(khz), None)
+    assert rc == _lib.W8A8_EINVAL and "null" in msg

@@ -296,3 +296,26 @@ def test_split_k_repeated_launches_fresh_inputs():
         refs.append(torch._int_mm(a, wt))
     for it, (c, r) in enumerate(zip(outs, refs)):
         assert torch.equal(c.cpu(), r), f"launch {it}"
+
+
+def test_clock_probe_reads_a_plausible_engine_clock():
+    """w8a8_clock_probe (the bench's clock reading): the core-clock / real-time ratio over a window
+    is a clock between 0.5 and 3 GHz (MI355X tops out at 2.4 GHz), idle and with GEMMs running on
+    another stream, and the window it reports is the one asked for."""
+    import ctypes
+    import bench
+    from w8a8._lib import call
+    out = torch.zeros(2, dtype=torch.int64, device=DEV)
+    khz = ctypes.c_int(0)
+    call("w8a8_clock_probe", out.data_ptr(), 20000, ctypes.byref(khz), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    cycles, real = out.tolist()
+    assert 10_000 <= khz.value <= 1_000_000
+    assert 20000 <= real < 20000 + 5000
+    idle = cycles / (real / (khz.value * 1e3)) / 1e9
+    a = ops.pack_act(rand_i8((512, 1536), seed=1).to(DEV))
+    w = packed_from_nk(rand_i8((12288, 1536), seed=2))
+    c = torch.empty((512, 12288), dtype=torch.int32, device=DEV)
+    busy = bench.clock_during(lambda: ops.gemm_i32(a, w, c=c), torch.device(DEV), launches=40)
+    print(f"engine clock: idle {idle:.3f} GHz, under int8 GEMMs {busy:.3f} GHz")
+    assert 0.5 < idle < 3.0 and 0.5 < busy < 3.0
