@@ -708,7 +708,7 @@ def main():
     peak_at_clock = 256 * 8192 * clock / 1e3  # TOP/s: 256 CUs x 8192 int8 op/clk/CU at the measured clock
     roofline = {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": traffic,
-                "kernel": "gemm_kernel<EPI_GELU> gate_up M=512 K=1536 N=12288, packed A",
+                "kernel": "gemm_dw_kernel<EPI_GELU> (direct-W 64x256 tiles) gate_up M=512 K=1536 N=12288, packed A",
                 "avg_launch_us": round(gu_ms * 1e3, 2), "clock_ghz": round(clock, 3),
                 "frac_at_clock": round(achieved / peak_at_clock, 4)}
     log(f"bench: gate_up runs at {clock:.3f} GHz: {achieved:.0f} TOP/s = {achieved / peak_at_clock:.3f} of the "

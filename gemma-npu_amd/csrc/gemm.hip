@@ -544,6 +544,189 @@ __global__ __launch_bounds__(WGM * WGN * KW * 64, MINB) void gemm_kernel(GemmPar
   }
 }
 
+
+// ---- direct-W kernel ----------------------------------------------------------------------------
+// NWN waves side by side along N, each owning all BM rows of the block tile and WTN 32-column
+// tiles.  Only A goes through LDS (two slots of KS k-steps, DMA'd one k-tile ahead, shared by all
+// waves); each wave loads its own W fragments straight into registers from the packed layout --
+// a fragment is 1 KiB of contiguous 16-byte lane slices, the MFMA operand as it lies in memory --
+// PW k-steps ahead of their MFMAs.  LDS then carries A only, and a barrier comes once per KS
+// k-steps, in a k-tile's last k-step: it publishes the next k-tile's A (DMA'd a k-tile earlier)
+// and frees the current slot for the k-tile after next.
+template <int BM, int NWN, int WTN, int KS, int PW, int EPI, bool A_PACKED, int MINB>
+__global__ __launch_bounds__(NWN * 64, MINB) void gemm_dw_kernel(GemmParams p) {
+  constexpr int NW = NWN;
+  constexpr int MT = BM / 32;
+  constexpr int NTB = NWN * WTN;
+  constexpr int BN = NTB * 32;
+  constexpr int FA = KS * MT / NW;  // A fragments each wave DMAs per k-tile
+  static_assert(FA * NW == KS * MT, "each wave moves whole A fragments");
+  static_assert(KS % PW == 0 && PW >= 1, "the W register ring must divide the k-tile");
+  static_assert(EPI != EPI_GELU || WTN % 2 == 0, "GELU pairs need an even tile count per wave");
+  static_assert(FA + (KS > PW ? KS : PW) * WTN < 64, "outstanding loads must fit the 6-bit vmcnt");
+  static_assert(KS % 2 == 0, "k-steps alternate between two A register sets");
+  constexpr int SLOT = KS * MT * 1024;
+  constexpr int NSCALE = EPI == EPI_I32 ? 0 : BM + BN;
+  constexpr int SCALE_PER_THREAD = NSCALE ? (NSCALE + NW * 64 - 1) / (NW * 64) : 1;
+  __shared__ __attribute__((aligned(1024))) char lds[2 * SLOT + NSCALE * 4];
+  float* const s_scale = reinterpret_cast<float*>(lds + 2 * SLOT);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int ntm = (p.M + BM - 1) / BM;
+  const int ntn = (p.NT + NTB - 1) / NTB;
+  const int lb = xcd_remap(blockIdx.x, ntm * ntn);
+  int tm, tn;
+  tile_coords(lb, ntm, ntn, p.gm, tm, tn);
+  const int m0 = tm * BM;
+  const int t0 = tn * NTB;
+  const int KT = (p.KF + KS - 1) / KS;
+  const int last_steps = p.KF - (KT - 1) * KS;
+
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a, p.a_bytes);
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.wp, p.w_bytes);
+
+  float scale_v[SCALE_PER_THREAD];
+#pragma unroll
+  for (int u = 0; u < SCALE_PER_THREAD; ++u) {
+    scale_v[u] = 0.0f;
+    if constexpr (EPI != EPI_I32) {
+      const int i = int(threadIdx.x) + u * NW * 64;
+      if (i < BM) {
+        if (m0 + i < p.M) scale_v[u] = p.sx[m0 + i];
+      } else if (i < BM + BN) {
+        const int pc = i - BM, tt = t0 + pc / 32;
+        if constexpr (EPI == EPI_GELU) {
+          const int c = (tt >> 1) * 32 + pc % 32;
+          if (c < p.I) scale_v[u] = p.sw[(tt & 1 ? p.I : 0) + c];
+        } else {
+          const int n = tt * 32 + pc % 32;
+          if (n < p.N) scale_v[u] = p.sw[n];
+        }
+      }
+    }
+  }
+
+  uint32_t offa[FA];
+#pragma unroll
+  for (int i = 0; i < FA; ++i) {
+    const int f = i * NW + wave;
+    const int s = f / MT, mt = f % MT;
+    if constexpr (A_PACKED)
+      offa[i] = (uint32_t(m0 / 32 + mt) * uint32_t(p.KF) + uint32_t(s)) * 1024u + uint32_t(lane) * 16u;
+    else
+      offa[i] = uint32_t(m0 + mt * 32 + (lane & 31)) * uint32_t(p.lda) + uint32_t(s * 32 + (lane >> 5) * 16);
+  }
+  constexpr uint32_t A_STEP = A_PACKED ? KS * 1024u : KS * 32u;
+  // W fragment (t, g) of this wave's tile j: packed fragment t0 + wave*WTN + j, k-step g.  Tiles
+  // past NT read past the buffer (zero); k-steps past KF read the next tile's data and are never
+  // multiplied.
+  uint32_t offw[WTN];
+#pragma unroll
+  for (int j = 0; j < WTN; ++j)
+    offw[j] = uint32_t(t0 + wave * WTN + j) * uint32_t(p.KF) * 1024u + uint32_t(lane) * 16u;
+
+  auto issue_a = [&](int kt) {
+    char* slot = lds + (kt & 1) * SLOT;
+#pragma unroll
+    for (int i = 0; i < FA; ++i) dma16(ra, slot + (i * NW + wave) * 1024, offa[i] + uint32_t(kt) * A_STEP);
+  };
+  auto load_w = [&](int g, v4i (&w)[WTN]) {
+#pragma unroll
+    for (int j = 0; j < WTN; ++j) w[j] = buf_load16(rw, offw[j] + uint32_t(g) * 1024u);
+  };
+  auto read_a = [&](int kt, int s, v4i (&a)[MT]) {
+    const char* slot = lds + (kt & 1) * SLOT;
+#pragma unroll
+    for (int i = 0; i < MT; ++i) a[i] = *reinterpret_cast<const v4i*>(slot + (s * MT + i) * 1024 + lane * 16);
+  };
+
+  v16i acc[MT][WTN];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int j = 0; j < WTN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+  v4i wr[PW][WTN];
+  issue_a(0);
+  if (KT > 1) issue_a(1);
+#pragma unroll
+  for (int u = 0; u < PW; ++u) load_w(u, wr[u]);
+  // A(0) landed once at most A(1) and the PW k-steps of W are outstanding
+  if (KT > 1)
+    wait_vmcnt<FA + PW * WTN>();
+  else
+    wait_vmcnt<PW * WTN>();
+  __builtin_amdgcn_s_barrier();
+  if constexpr (EPI != EPI_I32) {
+#pragma unroll
+    for (int u = 0; u < SCALE_PER_THREAD; ++u) {
+      const int i = int(threadIdx.x) + u * NW * 64;
+      if (i < NSCALE) s_scale[i] = scale_v[u];
+    }
+  }
+
+  // Each step reads the next step's A fragments before its own MFMAs.  In a k-tile's last step,
+  // once every read of this k-tile's slot has completed (lgkmcnt 0) and this wave's part of the
+  // next k-tile's A has landed, a barrier publishes that A and frees this slot, which then takes
+  // the DMA of the k-tile after next; the next k-tile's first fragments are read after it.
+  v4i a0[MT], a1[MT];
+  read_a(0, 0, a0);
+  for (int kt = 0; kt < KT; ++kt) {
+    const bool more = kt + 1 < KT;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      v4i(&ca)[MT] = (s % 2 == 0) ? a0 : a1;
+      v4i(&na)[MT] = (s % 2 == 0) ? a1 : a0;
+      if (s + 1 < KS) {
+        read_a(kt, s + 1, na);
+      } else if (more) {
+        // A(kt+1) was issued before at least KS*WTN W loads (the last k-step of the previous
+        // k-tile and the KS-1 before this one, or the prologue's PW and KS-1 here)
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+        wait_vmcnt<KS * WTN>();
+        __builtin_amdgcn_s_barrier();
+        if (kt + 2 < KT) issue_a(kt + 2);
+        read_a(kt + 1, 0, na);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      const bool live = more || s < last_steps;
+      if (live) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+          for (int j = 0; j < WTN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wr[s % PW][j], ca[i], acc[i][j], 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      load_w(kt * KS + s + PW, wr[s % PW]);
+    }
+  }
+
+  if constexpr (EPI != EPI_I32) __syncthreads();  // s_scale is visible to every wave
+  const int lrow = lane & 31;
+  const int lcol = 4 * (lane >> 5);
+#pragma unroll
+  for (int i = 0; i < MT; ++i) {
+    const int ml = i * 32 + lrow;
+    const int m = m0 + ml;
+    if (m >= p.M) continue;
+    const float sxm = EPI == EPI_I32 ? 0.0f : s_scale[ml];
+    const float* swt = s_scale + (EPI == EPI_I32 ? 0 : BM) + wave * WTN * 32 + lcol;
+    if constexpr (EPI == EPI_GELU) {
+#pragma unroll
+      for (int j = 0; j < WTN; j += 2)
+        store_tile<EPI>(p, acc[i][j], &acc[i][j + 1], m, t0 + wave * WTN + j, lcol, sxm, swt + j * 32);
+    } else {
+#pragma unroll
+      for (int j = 0; j < WTN; ++j)
+        store_tile<EPI>(p, acc[i][j], nullptr, m, t0 + wave * WTN + j, lcol, sxm, swt + j * 32);
+    }
+  }
+}
+
 // ---- host-side launch ----------------------------------------------------------------------
 
 // Tile configurations: block tile BM x BN, waves (WGM x WGN, one wave per 32-multiple sub-tile),
@@ -578,10 +761,22 @@ static constexpr TileCfg kCfg[] = {
     {128, 64, 4, 8, 3, 2},  // 21: two sub-tiles stacked, 2 waves each; 144 KiB ring
 };
 static constexpr int kNumCfg = int(sizeof(kCfg) / sizeof(kCfg[0]));
-static_assert(kNumCfg == 22, "every configuration needs its case in gemm_launch");
+
+// Direct-W configurations (gemm_dw_kernel), numbered after kCfg: block tile BM x (NWN*WTN*32),
+// A k-tiles of 32*KS, W register ring of PW k-steps.
+struct DwCfg {
+  int bm, nwn, wtn, ks, pw;
+};
+static constexpr DwCfg kDw[] = {
+    {64, 4, 2, 8, 4},   // 22: 64x256, k-tile 256, W 4 k-steps ahead, two blocks per CU
+    {128, 4, 2, 8, 8},  // 23: 128x256, k-tile 256, W 8 k-steps ahead
+    {128, 4, 2, 4, 4},  // 24: 128x256, k-tile 128, W 4 k-steps ahead
+};
+static constexpr int kNumDw = int(sizeof(kDw) / sizeof(kDw[0]));
+static_assert(kNumCfg == 22 && kNumDw == 3, "every configuration needs its case in gemm_launch");
 static constexpr int64_t kCounterBytes = 4096;
 
-int gemm_config_count() { return kNumCfg; }
+int gemm_config_count() { return kNumCfg + kNumDw; }
 
 // Split-K: blocks per output tile along K.  Explicit requests (req = n >= 1) split into at most
 // n parts, only when there are few output tiles.  Automatic selection (req = 0) splits the
@@ -606,6 +801,7 @@ static int pick_splits(int tiles, int KT, int ks, int req, int& kps, int kw = 1)
 // Split-K workspace: kCounterBytes of arrival counters (one int per output tile; zero before
 // and after every call) followed by the partial sums (scratch).
 int64_t gemm_workspace_bytes(int M, int NP, int KF, int cfg, int split_k) {
+  if (cfg >= kNumCfg) return 0;  // direct-W kernels never split K across blocks
   const TileCfg& c = kCfg[cfg];
   const int ntm = (M + c.bm - 1) / c.bm, ntn = (NP + c.bn - 1) / c.bn;
   int kps;
@@ -680,6 +876,34 @@ static void launch(const GemmParams& p, int epi, bool a_packed, void* ws, int64_
     launch_epi<c.bm, c.bn, WGM, WGN, c.kw, c.ks, c.ns, false>(p, epi, ws, ws_bytes, stream);
 }
 
+
+template <int BM, int NWN, int WTN, int KS, int PW, bool AP>
+static void launch_dw_epi(GemmParams p, int epi, hipStream_t stream) {
+  constexpr int BN = NWN * WTN * 32;
+  constexpr int MINB = BM <= 64 ? 2 : 1;
+  const int ntm = (p.M + BM - 1) / BM;
+  const int ntn = (p.NT * 32 + BN - 1) / BN;
+  p.gm = min(ntm, BM >= BN ? 4 : 8);
+  p.splits = 1;
+  const dim3 grid{unsigned(ntm * ntn)};
+  const int threads = NWN * 64;
+  switch (epi) {
+    case EPI_I32: gemm_dw_kernel<BM, NWN, WTN, KS, PW, EPI_I32, AP, MINB><<<grid, threads, 0, stream>>>(p); break;
+    case EPI_BF16: gemm_dw_kernel<BM, NWN, WTN, KS, PW, EPI_BF16, AP, MINB><<<grid, threads, 0, stream>>>(p); break;
+    case EPI_GELU: gemm_dw_kernel<BM, NWN, WTN, KS, PW, EPI_GELU, AP, MINB><<<grid, threads, 0, stream>>>(p); break;
+    case EPI_RESID: gemm_dw_kernel<BM, NWN, WTN, KS, PW, EPI_RESID, AP, MINB><<<grid, threads, 0, stream>>>(p); break;
+  }
+}
+
+template <int D>
+static void launch_dw(const GemmParams& p, int epi, bool a_packed, hipStream_t stream) {
+  constexpr DwCfg c = kDw[D];
+  if (a_packed)
+    launch_dw_epi<c.bm, c.nwn, c.wtn, c.ks, c.pw, true>(p, epi, stream);
+  else
+    launch_dw_epi<c.bm, c.nwn, c.wtn, c.ks, c.pw, false>(p, epi, stream);
+}
+
 // Tile choice, from timing every configuration with the bf16 epilogues on the E2B prefill
 // shapes (M = 512, 3658, 16384).  At one 512-row micro-batch the GEMMs are bound by how fast
 // each CU streams its operands, so small tiles that spread the work over more CUs win: 64x128
@@ -688,9 +912,14 @@ static void launch(const GemmParams& p, int epi, bool a_packed, void* ws, int64_
 // both N = 1536) have only 192 such tiles, one block per CU, whose two waves cannot hide their
 // LDS reads behind two MFMAs per k-step: four waves that each own the whole 64x64 tile and take
 // every fourth k-step (19) keep all four SIMDs issuing (output projection 7.3 us against 9.5 us
-// on 64x64 with two waves, down 16.1 us against 21.6 us or more).  A 128x192 tile, one per CU
-// for the gate/up GEMM (256 tiles), measured slower than 12 there (17.2 against 15.9 us): its one
-// wave per SIMD leaves the LDS reads exposed.
+// on 64x64 with two waves, down 16.1 us against 21.6 us or more).  The gate/up GEMM with its GELU
+// epilogue runs best on the direct-W 64x256 tile, two blocks per CU (22): 14.8 us against
+// 16.1-18.0 us on 12 for N = 12288, 26.5 against 32.5 us for the double-wide N = 24576.  A 128x192
+// tile, one per CU (256 tiles), measured slower than 12 (17.2 against 15.9 us): its one wave per
+// SIMD leaves the LDS reads exposed.
+// At a few thousand rows the long-K narrow down projections (K = 6144 / 12288, N = 1536) take the
+// direct-W 128x256 tile with W 8 k-steps ahead (23): 43 against 49 us at K = 6144 (the int32
+// sweep 7.02 -> 6.83 ms at M = 3658, 7.89 -> 7.61 ms at M = 4096), 78 against 89 us at K = 12288.
 // Longer M: the fused GELU epilogue, whose stores are half as wide, runs best on 128x256 with two
 // 8-wave blocks per CU (5).  Other epilogues at a few thousand rows (M = 3658, 4096): 256x256
 // tiles (0) for the wide gate/up and PLE projections and 64x128 tiles with their accumulators
@@ -702,10 +931,14 @@ static void launch(const GemmParams& p, int epi, bool a_packed, void* ws, int64_
 int gemm_pick_config(int M, int NP, int K, int epi) {
   if (M <= 1024) {
     if (K >= 2048 && NP <= 4096) return 19;  // few 64x64 tiles, long K: four waves split the k-steps
+    if (epi == EPI_GELU) return 22;          // direct-W 64x256, two blocks per CU
     return NP <= 2048 ? 14 : 12;
   }
   if (epi == EPI_GELU) return 5;
-  if (M <= 8192) return NP >= 8192 ? 0 : 12;
+  if (M <= 8192) {
+    if (K >= 4096 && NP <= 2048) return 23;  // long-K narrow (down): direct-W 128x256
+    return NP >= 8192 ? 0 : 12;
+  }
   return 5;
 }
 
@@ -735,6 +968,9 @@ int gemm_launch(const GemmParams& p, int epi, int cfg, bool a_packed, void* ws, 
     case 19: launch<19>(p, epi, a_packed, ws, ws_bytes, stream); break;
     case 20: launch<20>(p, epi, a_packed, ws, ws_bytes, stream); break;
     case 21: launch<21>(p, epi, a_packed, ws, ws_bytes, stream); break;
+    case 22: launch_dw<0>(p, epi, a_packed, stream); break;
+    case 23: launch_dw<1>(p, epi, a_packed, stream); break;
+    case 24: launch_dw<2>(p, epi, a_packed, stream); break;
     default: return fail(W8A8_EINVAL, "gemm: unknown tile config %d", cfg);
   }
   return check_launch("gemm");

@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
     missing = [n for n in declared_functions() if not hasattr(L, n)]
     assert not missing, f"not exported: {missing}"
     assert L.w8a8_abi_version() == 1
-    assert L.w8a8_gemm_tile_configs() == 22
+    assert L.w8a8_gemm_tile_configs() == 25
 
 
 def test_packed_weight_bytes():
