@@ -553,6 +553,9 @@ def main():
     ap.add_argument("--profile-kernel", action="store_true",
                     help="for counter collection: launch only the dominant GEMM (eager, --steps times) and a "
                          "64 MiB device copy that calibrates the byte counters, then exit")
+    ap.add_argument("--profile-gemm", metavar="M,K,N,EPI",
+                    help="for counter collection: launch one bf16-out GEMM of that shape (EPI none / gelu / residual; "
+                         "random data, the automatic tile) --steps times, then exit")
     ap.add_argument("--profile-gemv", action="store_true",
                     help="for kernel traces / counters: run the packed LM-head GEMV at M=1 (--steps times) and a "
                          "64 MiB device copy that calibrates the byte counters, then exit")
@@ -609,6 +612,22 @@ def main():
                 past, nxt = o.past_key_values, o.logits[0, -1].argmax().view(1, 1)
         torch.cuda.synchronize()
         log(f"bench: ran the E2B-shaped model: prefill of {ATTN_T} tokens, {args.steps} decode tokens")
+        return 0
+    if args.profile_gemm:
+        Mg, Kg, Ng, epi = args.profile_gemm.split(",")
+        Mg, Kg, Ng = int(Mg), int(Kg), int(Ng)
+        if epi not in ("none", "gelu", "residual"):
+            raise SystemExit(f"--profile-gemm: epilogue {epi!r} is not none, gelu or residual")
+        x = workloads.activations(Mg, Kg, seed=9).to(dev)
+        q, sx = ops.quant_rows_packed(x)
+        w, sw = workloads.weights(Ng, Kg, seed=10)
+        pw = ops.pack_weight(w.to(dev), "nk", Ng // 2 if epi == "gelu" else 0, sw=sw.to(dev))
+        res = workloads.activations(Mg, Ng, seed=11, outliers=False).to(dev) if epi == "residual" else None
+        out = torch.empty((Mg, Ng // 2 if epi == "gelu" else Ng), dtype=torch.bfloat16, device=dev)
+        for _ in range(args.steps):
+            ops.gemm_bf16(q, sx, pw, epilogue=epi, residual=res, out=out)
+        torch.cuda.synchronize()
+        log(f"bench: ran the {epi} GEMM M={Mg} K={Kg} N={Ng} {args.steps} times")
         return 0
     if args.profile_pipeline:
         from w8a8.pipeline import Prefill
