@@ -18,9 +18,11 @@
 //   S^T = K Q^T   (v_mfma_f32_16x16x32_bf16, K from LDS as the A operand, Q held in registers as
 //                  the B operand), so a lane's accumulator column is one query and the softmax
 //                  statistics are lane-local but for two exchanges between the four lane groups;
-//   P^T = exp2((S^T - m) * scale * log2 e), rounded to bf16;
+//   P^T = exp2(S^T * scale * log2 e - ms), rounded to bf16, where the reference ms trails the
+//                  running maximum of S^T * scale * log2 e by at most 8 (it moves only when a
+//                  block exceeds it by more than that);
 //   O^T += V^T P^T  (V^T from LDS as the A operand, P^T straight from the S^T accumulators as the
-//                  B operand), so O's rescaling by the running maximum is lane-local too.
+//                  B operand), so O's rescaling when ms moves is lane-local too.
 //
 // For P^T to be usable in place, the rows of each pair of 16-key S^T tiles hold their 32 keys in
 // the order that makes register i of lane group qq hold keys 8 qq + {i, 4 + i}: exactly the
@@ -220,8 +222,13 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(AttnParams p) {
   v4f o[NDT];
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) o[dt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-  float m = -__builtin_inff();  // running maximum of the raw scores of this lane's query
-  float l = 0.0f;               // this lane group's share of sum exp2((s - m) * c)
+  // Reference exponent of this lane's query, in log2 units: p = exp2(s * c - ms).  It follows the
+  // running maximum of s * c lazily, moving only when a block's maximum exceeds it by more than 8
+  // (so p <= 2^8: the same relative bf16 / fp32 rounding, far from any overflow), which keeps the
+  // rescale of O to the few blocks where the maximum jumps; when it moves, O and l are rescaled
+  // by exactly exp2(ms_old - ms_new), the ratio of the references the sums were taken against.
+  float ms = -__builtin_inff();
+  float l = 0.0f;  // this lane group's share of sum exp2(s * c - ms)
   const float c = p.c;
   const int win = p.window;
   const int Tk = p.Tk;
@@ -274,17 +281,18 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(AttnParams p) {
       for (int i = 0; i < 4; ++i) bm = fmaxf(bm, s[t][i]);
     bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
     bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
-    const float mn = fmaxf(m, bm);
-    const float ms = mn == -__builtin_inff() ? 0.0f : mn * c;
-    const float alpha = __builtin_amdgcn_exp2f(__builtin_fmaf(m, c, -ms));
-    m = mn;
+    const float bmc = bm * c;
+    const bool grow = bmc > ms + 8.0f;  // false while every key so far is masked (bmc = -inf)
+    const float alpha = !grow ? 1.0f : (ms == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(ms - bmc));
+    if (grow) ms = bmc;
+    const float mref = ms == -__builtin_inff() ? 0.0f : ms;
     float bs = 0.0f;
     v8bf pb[NKC];
 #pragma unroll
     for (int ch = 0; ch < NKC; ++ch)
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const float pe = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * ch + (j >> 2)][j & 3], c, -ms));
+        const float pe = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * ch + (j >> 2)][j & 3], c, -mref));
         bs += pe;
         pb[ch][j] = (__bf16)pe;
       }
@@ -323,7 +331,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(AttnParams p) {
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt)
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, o[dt]), rp, base + dt * 16, 0, 0x11);
-      const v4f ml = v4f{m, l, 0.0f, 0.0f};
+      const v4f ml = v4f{ms, l, 0.0f, 0.0f};
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, ml), rp, base + NDT * 16, 0, 0x11);
     }
     __builtin_amdgcn_s_waitcnt(0);
@@ -333,21 +341,21 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(AttnParams p) {
       *arrived = __hip_atomic_fetch_add(p.counters + slot_tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     __syncthreads();
     if (*arrived != p.split - 1) return;
-    // merge: M = max of the parts' maxima, w_s = exp2((m_s - M) c), o = sum_s w_s o_s, l likewise
+    // merge: M = max of the parts' references, w_s = exp2(ms_s - M), o = sum_s w_s o_s, l likewise
     float M = -__builtin_inff();
     for (int sp = 0; sp < p.split; ++sp) {
       const v4f ml = __builtin_bit_cast(
           v4f, __builtin_amdgcn_raw_buffer_load_b128(rp, uint32_t(sp) * PART_BYTES + lane_off + NDT * 16, 0, 0x11));
       M = fmaxf(M, ml[0]);
     }
-    const float Ms = M == -__builtin_inff() ? 0.0f : M * c;
+    const float Ms = M == -__builtin_inff() ? 0.0f : M;
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) o[dt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     l = 0.0f;
     for (int sp = 0; sp < p.split; ++sp) {
       const uint32_t base = uint32_t(sp) * PART_BYTES + lane_off;
       const v4f ml = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rp, base + NDT * 16, 0, 0x11));
-      const float w = __builtin_amdgcn_exp2f(__builtin_fmaf(ml[0], c, -Ms));
+      const float w = __builtin_amdgcn_exp2f(ml[0] - Ms);
       l = __builtin_fmaf(w, ml[1], l);
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) {
@@ -356,7 +364,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(AttnParams p) {
         for (int i = 0; i < 4; ++i) o[dt][i] = __builtin_fmaf(w, od[i], o[dt][i]);
       }
     }
-    m = M;
+    ms = M;
     if (tid == 0) __hip_atomic_store(p.counters + slot_tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   }
 
@@ -374,7 +382,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(AttnParams p) {
     *reinterpret_cast<v2u*>(op + 16 * dt) = w;
   }
   if (p.lse && qq == 0)
-    p.lse[int64_t(h) * p.Tq + qrow] = lt > 0.0f ? m * p.scale + __logf(lt) : -__builtin_inff();
+    p.lse[int64_t(h) * p.Tq + qrow] = lt > 0.0f ? ms * 0.69314718055994531f + __logf(lt) : -__builtin_inff();
 }
 
 // ---- decode: one query per head, keys split into chunks --------------------------------------
