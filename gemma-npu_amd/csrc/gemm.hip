@@ -766,11 +766,12 @@ static constexpr int kNumCfg = int(sizeof(kCfg) / sizeof(kCfg[0]));
 // A k-tiles of 32*KS, W register ring of PW k-steps.
 struct DwCfg {
   int bm, nwn, wtn, ks, pw;
+  int minb = 1;  // blocks per CU the registers are budgeted for
 };
 static constexpr DwCfg kDw[] = {
-    {64, 4, 2, 8, 4},   // 22: 64x256, k-tile 256, W 4 k-steps ahead, two blocks per CU
-    {128, 4, 2, 8, 8},  // 23: 128x256, k-tile 256, W 8 k-steps ahead
-    {128, 4, 2, 4, 4},  // 24: 128x256, k-tile 128, W 4 k-steps ahead
+    {64, 4, 2, 8, 4, 2},   // 22: 64x256, k-tile 256, W 4 k-steps ahead, two blocks per CU
+    {128, 4, 2, 8, 8},     // 23: 128x256, k-tile 256, W 8 k-steps ahead, one block per CU
+    {128, 4, 2, 8, 4, 2},  // 24: 128x256, k-tile 256, W 4 k-steps ahead, two blocks per CU
 };
 static constexpr int kNumDw = int(sizeof(kDw) / sizeof(kDw[0]));
 static_assert(kNumCfg == 22 && kNumDw == 3, "every configuration needs its case in gemm_launch");
@@ -877,10 +878,9 @@ static void launch(const GemmParams& p, int epi, bool a_packed, void* ws, int64_
 }
 
 
-template <int BM, int NWN, int WTN, int KS, int PW, bool AP>
+template <int BM, int NWN, int WTN, int KS, int PW, int MINB, bool AP>
 static void launch_dw_epi(GemmParams p, int epi, hipStream_t stream) {
   constexpr int BN = NWN * WTN * 32;
-  constexpr int MINB = BM <= 64 ? 2 : 1;
   const int ntm = (p.M + BM - 1) / BM;
   const int ntn = (p.NT * 32 + BN - 1) / BN;
   p.gm = min(ntm, BM >= BN ? 4 : 8);
@@ -899,9 +899,9 @@ template <int D>
 static void launch_dw(const GemmParams& p, int epi, bool a_packed, hipStream_t stream) {
   constexpr DwCfg c = kDw[D];
   if (a_packed)
-    launch_dw_epi<c.bm, c.nwn, c.wtn, c.ks, c.pw, true>(p, epi, stream);
+    launch_dw_epi<c.bm, c.nwn, c.wtn, c.ks, c.pw, c.minb, true>(p, epi, stream);
   else
-    launch_dw_epi<c.bm, c.nwn, c.wtn, c.ks, c.pw, false>(p, epi, stream);
+    launch_dw_epi<c.bm, c.nwn, c.wtn, c.ks, c.pw, c.minb, false>(p, epi, stream);
 }
 
 // Tile choice, from timing every configuration with the bf16 epilogues on the E2B prefill
@@ -920,26 +920,29 @@ static void launch_dw(const GemmParams& p, int epi, bool a_packed, hipStream_t s
 // At a few thousand rows the long-K narrow down projections (K = 6144 / 12288, N = 1536) take the
 // direct-W 128x256 tile with W 8 k-steps ahead (23): 43 against 49 us at K = 6144 (the int32
 // sweep 7.02 -> 6.83 ms at M = 3658, 7.89 -> 7.61 ms at M = 4096), 78 against 89 us at K = 12288.
-// Longer M: the fused GELU epilogue, whose stores are half as wide, runs best on 128x256 with two
-// 8-wave blocks per CU (5).  Other epilogues at a few thousand rows (M = 3658, 4096): 256x256
-// tiles (0) for the wide gate/up and PLE projections and 64x128 tiles with their accumulators
-// staged through LDS for row-contiguous stores (12) for the rest.  This is timed on the 141-GEMM
-// int32 prefill sweep itself, with a distinct weight per layer: there the 256-row tiles' halved
-// weight reads decide (gate/up 92 us in the sequence against 98 us on 128x256), while one GEMM
-// repeated on a cache-resident weight favours 128x256 (92 against 108 us).  At M = 16384, 128x256
-// (5) is the fastest on the stress shapes (gate/up + GELU 417 us, down + residual 189 us).
+// Past 1024 rows the GELU epilogue, and everything past 8192 rows, take the direct-W 128x256 tile
+// with two blocks per CU (24): gate/up + GELU 76-78 against 90 us on the 8-wave 128x256 tile (5)
+// at M = 3658 (N = 12288), 142 against 164 us for N = 24576, 308 against 352 us at M = 16384; down
+// + residual at M = 16384 141 against 167 us.
+// The other int32 GEMMs at a few thousand rows (M = 3658, 4096) keep 256x256 tiles (0) for the
+// wide gate/up and PLE projections and 64x128 tiles with their accumulators staged through LDS
+// for row-contiguous stores (12) for the rest.  This is timed on the 141-GEMM int32 prefill sweep
+// itself, with a distinct weight per layer: there the 256-row tiles' halved weight reads decide
+// (gate/up 92 us in the sequence against 98 us on 128x256), while one GEMM repeated on a
+// cache-resident weight favours 128x256 (92 against 108 us); the direct-W tiles change the sweep
+// by less than 1% there.
 int gemm_pick_config(int M, int NP, int K, int epi) {
   if (M <= 1024) {
     if (K >= 2048 && NP <= 4096) return 19;  // few 64x64 tiles, long K: four waves split the k-steps
     if (epi == EPI_GELU) return 22;          // direct-W 64x256, two blocks per CU
     return NP <= 2048 ? 14 : 12;
   }
-  if (epi == EPI_GELU) return 5;
+  if (epi == EPI_GELU) return 24;  // direct-W 128x256, two blocks per CU
   if (M <= 8192) {
     if (K >= 4096 && NP <= 2048) return 23;  // long-K narrow (down): direct-W 128x256
     return NP >= 8192 ? 0 : 12;
   }
-  return 5;
+  return 24;
 }
 
 int gemm_launch(const GemmParams& p, int epi, int cfg, bool a_packed, void* ws, int64_t ws_bytes,
