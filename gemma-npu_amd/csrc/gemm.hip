@@ -923,7 +923,8 @@ static void launch_dw(const GemmParams& p, int epi, bool a_packed, hipStream_t s
 // Past 1024 rows the GELU epilogue, and everything past 8192 rows, take the direct-W 128x256 tile
 // with two blocks per CU (24): gate/up + GELU 76-78 against 90 us on the 8-wave 128x256 tile (5)
 // at M = 3658 (N = 12288), 142 against 164 us for N = 24576, 308 against 352 us at M = 16384; down
-// + residual at M = 16384 141 against 167 us.
+// + residual at M = 16384 141 against 167 us.  64x256 with three or four blocks per CU, and
+// 128x256 with W only 2 k-steps ahead, measured slower on all of these.
 // The other int32 GEMMs at a few thousand rows (M = 3658, 4096) keep 256x256 tiles (0) for the
 // wide gate/up and PLE projections and 64x128 tiles with their accumulators staged through LDS
 // for row-contiguous stores (12) for the rest.  This is timed on the 141-GEMM int32 prefill sweep
