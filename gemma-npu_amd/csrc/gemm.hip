@@ -759,6 +759,7 @@ static constexpr TileCfg kCfg[] = {
     {64, 64, 4, 8, 3, 4},   // 19: one sub-tile, 4 waves; 96 KiB ring
     {64, 128, 4, 8, 3, 2},  // 20: two sub-tiles side by side, 2 waves each; 144 KiB ring
     {128, 64, 4, 8, 3, 2},  // 21: two sub-tiles stacked, 2 waves each; 144 KiB ring
+    {64, 64, 4, 16, 2, 4},  // 22: one sub-tile, 4 waves; k-tile 512, 128 KiB ring
 };
 static constexpr int kNumCfg = int(sizeof(kCfg) / sizeof(kCfg[0]));
 
@@ -769,12 +770,12 @@ struct DwCfg {
   int minb = 1;  // blocks per CU the registers are budgeted for
 };
 static constexpr DwCfg kDw[] = {
-    {64, 4, 2, 8, 4, 2},   // 22: 64x256, k-tile 256, W 4 k-steps ahead, two blocks per CU
-    {128, 4, 2, 8, 8},     // 23: 128x256, k-tile 256, W 8 k-steps ahead, one block per CU
-    {128, 4, 2, 8, 4, 2},  // 24: 128x256, k-tile 256, W 4 k-steps ahead, two blocks per CU
+    {64, 4, 2, 8, 4, 2},   // 23: 64x256, k-tile 256, W 4 k-steps ahead, two blocks per CU
+    {128, 4, 2, 8, 8},     // 24: 128x256, k-tile 256, W 8 k-steps ahead, one block per CU
+    {128, 4, 2, 8, 4, 2},  // 25: 128x256, k-tile 256, W 4 k-steps ahead, two blocks per CU
 };
 static constexpr int kNumDw = int(sizeof(kDw) / sizeof(kDw[0]));
-static_assert(kNumCfg == 22 && kNumDw == 3, "every configuration needs its case in gemm_launch");
+static_assert(kNumCfg == 23 && kNumDw == 3, "every configuration needs its case in gemm_launch");
 static constexpr int64_t kCounterBytes = 4096;
 
 int gemm_config_count() { return kNumCfg + kNumDw; }
@@ -911,17 +912,19 @@ static void launch_dw(const GemmParams& p, int epi, bool a_packed, hipStream_t s
 // The narrow long-K GEMMs (the output projection, K = 2048, and the down projection, K = 6144,
 // both N = 1536) have only 192 such tiles, one block per CU, whose two waves cannot hide their
 // LDS reads behind two MFMAs per k-step: four waves that each own the whole 64x64 tile and take
-// every fourth k-step (19) keep all four SIMDs issuing (output projection 7.3 us against 9.5 us
-// on 64x64 with two waves, down 16.1 us against 21.6 us or more).  The gate/up GEMM with its GELU
-// epilogue runs best on the direct-W 64x256 tile, two blocks per CU (22): 14.8 us against
+// every fourth k-step keep all four SIMDs issuing (output projection 7.3 us against 9.5 us on
+// 64x64 with two waves, down 16.1 us against 21.6 us or more, with 256-deep k-tiles in a 3-slot
+// ring (19)); 512-deep k-tiles in a 2-slot ring (22) keep more bytes in flight per CU: 6.7 and
+// 14.9 us.  The gate/up GEMM with its GELU
+// epilogue runs best on the direct-W 64x256 tile, two blocks per CU (23): 14.8 us against
 // 16.1-18.0 us on 12 for N = 12288, 26.5 against 32.5 us for the double-wide N = 24576.  A 128x192
 // tile, one per CU (256 tiles), measured slower than 12 (17.2 against 15.9 us): its one wave per
 // SIMD leaves the LDS reads exposed.
 // At a few thousand rows the long-K narrow down projections (K = 6144 / 12288, N = 1536) take the
-// direct-W 128x256 tile with W 8 k-steps ahead (23): 43 against 49 us at K = 6144 (the int32
+// direct-W 128x256 tile with W 8 k-steps ahead (24): 43 against 49 us at K = 6144 (the int32
 // sweep 7.02 -> 6.83 ms at M = 3658, 7.89 -> 7.61 ms at M = 4096), 78 against 89 us at K = 12288.
 // Past 1024 rows the GELU epilogue, and everything past 8192 rows, take the direct-W 128x256 tile
-// with two blocks per CU (24): gate/up + GELU 76-78 against 90 us on the 8-wave 128x256 tile (5)
+// with two blocks per CU (25): gate/up + GELU 76-78 against 90 us on the 8-wave 128x256 tile (5)
 // at M = 3658 (N = 12288), 142 against 164 us for N = 24576, 308 against 352 us at M = 16384; down
 // + residual at M = 16384 141 against 167 us.  64x256 with three or four blocks per CU, and
 // 128x256 with W only 2 k-steps ahead, measured slower on all of these.
@@ -934,16 +937,16 @@ static void launch_dw(const GemmParams& p, int epi, bool a_packed, hipStream_t s
 // by less than 1% there.
 int gemm_pick_config(int M, int NP, int K, int epi) {
   if (M <= 1024) {
-    if (K >= 2048 && NP <= 4096) return 19;  // few 64x64 tiles, long K: four waves split the k-steps
-    if (epi == EPI_GELU) return 22;          // direct-W 64x256, two blocks per CU
+    if (K >= 2048 && NP <= 4096) return 22;  // few 64x64 tiles, long K: four waves split the k-steps
+    if (epi == EPI_GELU) return 23;          // direct-W 64x256, two blocks per CU
     return NP <= 2048 ? 14 : 12;
   }
-  if (epi == EPI_GELU) return 24;  // direct-W 128x256, two blocks per CU
+  if (epi == EPI_GELU) return 25;  // direct-W 128x256, two blocks per CU
   if (M <= 8192) {
-    if (K >= 4096 && NP <= 2048) return 23;  // long-K narrow (down): direct-W 128x256
+    if (K >= 4096 && NP <= 2048) return 24;  // long-K narrow (down): direct-W 128x256
     return NP >= 8192 ? 0 : 12;
   }
-  return 24;
+  return 25;
 }
 
 int gemm_launch(const GemmParams& p, int epi, int cfg, bool a_packed, void* ws, int64_t ws_bytes,
@@ -972,9 +975,10 @@ int gemm_launch(const GemmParams& p, int epi, int cfg, bool a_packed, void* ws, 
     case 19: launch<19>(p, epi, a_packed, ws, ws_bytes, stream); break;
     case 20: launch<20>(p, epi, a_packed, ws, ws_bytes, stream); break;
     case 21: launch<21>(p, epi, a_packed, ws, ws_bytes, stream); break;
-    case 22: launch_dw<0>(p, epi, a_packed, stream); break;
-    case 23: launch_dw<1>(p, epi, a_packed, stream); break;
-    case 24: launch_dw<2>(p, epi, a_packed, stream); break;
+    case 22: launch<22>(p, epi, a_packed, ws, ws_bytes, stream); break;
+    case 23: launch_dw<0>(p, epi, a_packed, stream); break;
+    case 24: launch_dw<1>(p, epi, a_packed, stream); break;
+    case 25: launch_dw<2>(p, epi, a_packed, stream); break;
     default: return fail(W8A8_EINVAL, "gemm: unknown tile config %d", cfg);
   }
   return check_launch("gemm");

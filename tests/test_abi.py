@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
     missing = [n for n in declared_functions() if not hasattr(L, n)]
     assert not missing, f"not exported: {missing}"
     assert L.w8a8_abi_version() == 1
-    assert L.w8a8_gemm_tile_configs() == 25
+    assert L.w8a8_gemm_tile_configs() == 26
 
 
 def test_packed_weight_bytes():
@@ -58,6 +58,9 @@ def test_linear_workspace_bytes():
     # automatic tile for the long-K down projection at M=512: wave split-K, never split across blocks
     assert L.w8a8_gemm_workspace_bytes(512, 1536, 6144, -1, 0) == 0
     assert L.w8a8_gemm_workspace_bytes(512, 1536, 6144, 19, 4) == 0
+    assert L.w8a8_gemm_workspace_bytes(512, 1536, 6144, 22, 4) == 0
+    assert L.w8a8_gemm_workspace_bytes(3658, 1536, 6144, 24, 4) == 0       # direct-W: never split
+    assert L.w8a8_gemm_workspace_bytes(3658, 1536, 6144, 26, 0) == -1      # past the last configuration
     assert L.w8a8_linear_workspace_bytes(512, 1536, 6144) == 4096 + 512 * 6144 + 512 * 4
     assert L.w8a8_linear_workspace_bytes(512, 1536, 2048) == 4096 + 512 * 2048 + 512 * 4
     assert L.w8a8_linear_workspace_bytes(3, 64, 64) == 4096 + 32 * 64 + 256  # counters kept; rows to 32
