@@ -412,7 +412,10 @@ static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) =
 // has validated shapes and alignment.
 static int launch_row_chain(const RowChain& p, bool in_i32, hipStream_t stream, const char* what) {
   const int KQ = p.KF ? p.KF * 32 : p.N;
-  const int ch = (KQ + 2047) / 2048;
+  // Rows up to 64 * 8 * 6 = 3072 elements go to one wave each: every reduction is then a DPP
+  // reduction with no LDS exchange or barrier, and a CU holds many more rows at once.  Longer
+  // rows spread over up to four waves.
+  const int ch = KQ <= 3072 ? (KQ + 511) / 512 : (KQ + 2047) / 2048;
   const int CHs = ch <= 1 ? 1 : ch <= 2 ? 2 : ch <= 3 ? 3 : ch <= 4 ? 4 : 6;
   const int chunks = (KQ + 8 * CHs - 1) / (8 * CHs);
   const int threads = ((chunks + 63) / 64) * 64;

@@ -22,7 +22,7 @@ import threading
 import torch
 
 from ._lib import call, lib
-from .ops import _stream
+from .ops import _stream, current_stream_handle
 
 _WS = {}
 _WS_LOCK = threading.Lock()
@@ -31,7 +31,7 @@ _WS_LOCK = threading.Lock()
 def _workspace(device, nbytes):
     """Decode scratch of (device, current stream), grown to at least nbytes (calls on one stream are
     ordered, so they can share it; nothing is kept between calls)."""
-    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    key = (device.index, current_stream_handle(device))
     with _WS_LOCK:
         buf = _WS.get(key)
         if buf is None or buf.numel() < nbytes:
@@ -47,7 +47,7 @@ def _split_workspace(device, nbytes):
     """The zero-filled workspace of (device, current stream) for split causal tiles, grown to at
     least nbytes: its counters are zero between calls by the kernel's own contract, so it is only
     cleared when (re)allocated."""
-    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    key = (device.index, current_stream_handle(device))
     with _WS_LOCK:
         buf = _SPLIT_WS.get(key)
         if buf is None or buf.numel() < nbytes:

@@ -11,8 +11,23 @@ from ._lib import call, lib
 EPILOGUES = {"none": 0, "gelu": 1, "residual": 2, "residual_rms": 3}
 
 
+# torch's current HIP stream of a device as a raw handle.  torch.cuda.current_stream() builds a
+# Python Stream object on every call (~2 us); the raw-handle accessor it is built on does not.
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def current_stream_handle(device):
+    """The raw hipStream_t of torch's current stream on `device` (a torch.device or index)."""
+    index = device if isinstance(device, int) else device.index
+    if index is None:
+        index = torch.cuda.current_device()
+    if _RAW_STREAM is not None:
+        return _RAW_STREAM(index)
+    return torch.cuda.current_stream(index).cuda_stream
+
+
 def _stream(t):
-    return torch.cuda.current_stream(t.device).cuda_stream
+    return current_stream_handle(t.device)
 
 
 def _check(t, name, dtype, ndim=2):
@@ -42,7 +57,7 @@ def workspace(device, nbytes):
     least nbytes.  Calls on one stream are ordered, so they can share it; its first 4 KiB of
     counters are zero between calls by the kernels' own contract."""
     device = torch.device(device)
-    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    key = (device.index, current_stream_handle(device))
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.zeros(max(int(nbytes), 1 << 20), dtype=torch.uint8, device=device)
