@@ -180,10 +180,10 @@ __global__ __launch_bounds__(256) void quant_rows_packed_kernel(const uint16_t* 
   }
 }
 
-// Single-pass quantisation of bf16 rows held in registers: one block of nt = 64 or 256 threads per
-// row; thread t holds chunks c = 0 .. CH-1 of 8 consecutive elements at k = 8 * (nt c + t), all
-// loaded in one burst, so the row costs one memory round trip.  The absmax is a DPP wave reduction,
-// plus one LDS exchange between the waves of a 256-thread block.  The int8 bytes
+// Single-pass quantisation of bf16 rows held in registers: one 256-thread block per row; thread
+// t holds chunks c = 0 .. CH-1 of 8 consecutive elements at k = 8 * (256c + t), all loaded in one
+// burst, so the row costs one memory round trip and its quant steps are spread over four waves.
+// The absmax is a DPP wave reduction plus one LDS exchange between the waves.  The int8 bytes
 // leave as 8-byte stores, row-major or into the packed fragment layout (half of the 16-byte
 // piece holding k: fragment (row/32, k/32), lane slot row%32 + 32 * ((k/16) % 2), byte k % 16).
 // PACKED also zero-fills rows M .. Mp-1 and k K .. 32*KF-1.
@@ -192,7 +192,7 @@ __global__ __launch_bounds__(256) void quant_rows_blk_kernel(const uint16_t* __r
                                                              int K, int KF, int8_t* __restrict__ q, int64_t ldq,
                                                              float* __restrict__ scale) {
   __shared__ float wave_amax[4];
-  const int t = threadIdx.x, nt = int(blockDim.x);
+  const int t = threadIdx.x;
   // Packed output: the 16-byte pieces of 8 consecutive rows share each 128-byte line, so rows
   // are dealt out XCD by XCD and every line is assembled in one L2 (round-robin rows would leave
   // a dirty eighth of every line in each of the 8 L2s).
@@ -207,7 +207,7 @@ __global__ __launch_bounds__(256) void quant_rows_blk_kernel(const uint16_t* __r
   if (row >= M) {  // PACKED only: padding rows are zero
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
-      const int k = 8 * (nt * c + t);
+      const int k = 8 * (256 * c + t);
       if (k < KP) *reinterpret_cast<v2u*>(dst(k)) = v2u{0u, 0u};
     }
     return;
@@ -216,7 +216,7 @@ __global__ __launch_bounds__(256) void quant_rows_blk_kernel(const uint16_t* __r
   v4u v[CH];
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
-    const int k = 8 * (nt * c + t);
+    const int k = 8 * (256 * c + t);
     v[c] = k < K ? *reinterpret_cast<const v4u*>(xr + k) : v4u{0u, 0u, 0u, 0u};
   }
   float amax = 0.0f;
@@ -226,18 +226,15 @@ __global__ __launch_bounds__(256) void quant_rows_blk_kernel(const uint16_t* __r
     for (int i = 0; i < 4; ++i)
       amax = fmaxf(amax, fmaxf(fabsf(__uint_as_float(v[c][i] << 16)), fabsf(__uint_as_float(v[c][i] & 0xffff0000u))));
   amax = wave_max_dpp(amax);
-  if (nt > 64) {
-    if ((t & 63) == 0) wave_amax[t >> 6] = amax;
-    __syncthreads();
-    amax = wave_amax[0];
-    for (int w = 1; w < (nt >> 6); ++w) amax = fmaxf(amax, wave_amax[w]);
-  }
+  if ((t & 63) == 0) wave_amax[t >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(wave_amax[0], wave_amax[1]), fmaxf(wave_amax[2], wave_amax[3]));
   const float s = fmaxf(amax, 1e-8f) / 127.0f;
   const float rs = 1.0f / s;
   if (t == 0) scale[row] = s;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
-    const int k = 8 * (nt * c + t);
+    const int k = 8 * (256 * c + t);
     if (k >= KP) continue;
     uint32_t w[2] = {0u, 0u};
     if (k < K) {
@@ -256,14 +253,9 @@ __global__ __launch_bounds__(256) void quant_rows_blk_kernel(const uint16_t* __r
 template <bool PACKED>
 static bool launch_quant_reg(const uint16_t* x, int64_t ldx, int M, int Mp, int K, int KF, int8_t* q, int64_t ldq,
                              float* scale, hipStream_t stream) {
-  // Rows up to 64 * 8 * 6 = 3072 elements (packed: the padded width) take one wave each, whose
-  // absmax is a DPP reduction alone; longer rows take four waves and one LDS exchange.
-  const int KP = PACKED ? KF * 32 : K;
-  const bool wave = KP <= 3072;
-  const int threads = wave ? 64 : 256;
-  const int ch = wave ? (KP + 511) / 512 : (K + 2047) / 2048;
+  const int ch = (K + 2047) / 2048;
   const dim3 grid{static_cast<unsigned>(Mp)};
-#define W8A8_QBLK(N) quant_rows_blk_kernel<N, PACKED><<<grid, threads, 0, stream>>>(x, ldx, M, K, KF, q, ldq, scale)
+#define W8A8_QBLK(N) quant_rows_blk_kernel<N, PACKED><<<grid, 256, 0, stream>>>(x, ldx, M, K, KF, q, ldq, scale)
   if (ch <= 1) W8A8_QBLK(1);
   else if (ch <= 2) W8A8_QBLK(2);
   else if (ch <= 3) W8A8_QBLK(3);
