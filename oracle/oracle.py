@@ -1,7 +1,7 @@
 """numpy front end of the C oracle -- TEST INFRASTRUCTURE ONLY.
 
 Only the test suite, the smoke check and the benchmark's CPU-baseline leg use
-this module, and only as the checker; the product library never loads it.
+this module, and only to check results against; the product library never loads it.
 Every function takes and returns numpy arrays.  bf16 data is carried as
 uint16 bit patterns (see `bf16_bits` / `bits_to_f32`).
 
