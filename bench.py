@@ -355,9 +355,10 @@ def e2b_model(dev):
 
 def pipeline_prefill_bench(model, ids, hf_logits, reps=3):
     """The reference's prefill pipeline (pipeline.py:224-339) on the GPU, w8a8.pipeline.Prefill, on
-    the same model and prompt: whole-prompt layers (the default) and the reference's 512-row
-    micro-batches; each the median of `reps` timed calls after one warm-up.  Its logits are compared
-    with the HF-driven engine's (relative L2 difference of the last-token logits)."""
+    the same model and prompt: whole-prompt layers (the default), the reference's 512-row
+    micro-batches, and the whole-prompt layers captured in one HIP graph (Prefill.capture); each the
+    median of `reps` timed calls after one warm-up.  Logits are compared with the HF-driven engine's
+    (relative L2 difference of the last-token logits); the captured form must equal the eager one."""
     import torch
     from w8a8.pipeline import Prefill
     res = {}
@@ -373,6 +374,24 @@ def pipeline_prefill_bench(model, ids, hf_logits, reps=3):
         diff = ((logits - hf_logits).norm() / hf_logits.norm()).item()
         res[name] = {"ms": round(statistics.median(times[1:]) * 1e3, 2), "logits_rel_diff_vs_hf_engine": round(diff, 4)}
         log(f"bench: pipeline prefill {name}: {res[name]}")
+    # the layers captured in one HIP graph (Prefill.capture), checked against the eager call on the
+    # same prompt: the whole-prompt order is GPU-bound already, the micro-batch order host-bound
+    for name, step in (("whole_prompt_graph", None), ("row_step_512_graph", 512)):
+        pre = Prefill(model, row_step=step)
+        want, _ = pre(ids)
+        run = pre.capture(ids.shape[1])
+        times = []
+        for _ in range(reps + 1):
+            torch.cuda.synchronize()
+            t = time.perf_counter()
+            logits, _ = run(ids)
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - t)
+        if not torch.equal(logits, want):
+            raise RuntimeError(f"captured prefill ({name}) differs from the eager prefill")
+        res[name] = {"ms": round(statistics.median(times[1:]) * 1e3, 2), "identical_to_eager": True}
+        log(f"bench: pipeline prefill {name}: {res[name]}")
+        del run
     res["what"] = ("w8a8.pipeline.Prefill: embedding/PLE/RoPE tables from the model, then per layer k_in, qkv "
                    "GEMM, k_qkv, attention, k_attn_out, o GEMM, k_post_attn, gate/up GEMM, k_gelu, down GEMM, "
                    "k_post_ff, PLE gate GEMM, k_ple_gate, PLE projection GEMM, k_ple_out (int32 GEMMs + fused "

@@ -4,6 +4,8 @@
     prefill = Prefill(model)                 # pipeline.py:224-231
     logits, cache = prefill(ids)             # pipeline.py:312-339: fp32 last-token logits, DynamicCache
     out = model(input_ids=nxt, past_key_values=cache, use_cache=True)   # HF's decode loop continues
+    run = prefill.capture(T)                 # the same, captured in one HIP graph for T-token prompts
+    logits, cache = run(ids)
 
 A decoder layer is the reference's step sequence (pipeline.py:244-310): k_in -> qkv GEMM -> k_qkv
 -> attention -> k_attn_out -> o GEMM -> k_post_attn -> gate/up GEMM -> k_gelu -> down GEMM ->
@@ -99,7 +101,7 @@ class Prefill:
                     k_all = torch.cat([p[0] for p in prev], 1)
                     v_all = torch.cat([p[1] for p in prev], 1)
                 if slot == ctx["last"]:
-                    ctx["cache"].update(k_all[None], v_all[None], i)
+                    ctx["layer_kv"].append((i, k_all, v_all))
                 if a.store_full_length_kv:
                     kv[("shared", lt, slot)] = (k_all, v_all)
             if a.sliding_window:
@@ -129,33 +131,110 @@ class Prefill:
                                 ctx["scalar"][i], eps)
         return h
 
+    def _check_ids(self, ids):
+        if ids.dim() != 2 or ids.shape[0] != 1 or ids.shape[1] < 1:
+            raise ValueError(f"Prefill: expected ids [1, T], got {tuple(ids.shape)}")
+        return ids.to(self.lm.embed_tokens.weight.device)
+
+    def _inputs(self, ids):
+        """The model's own embedding, per-layer inputs (PLE) and RoPE tables for ids [1, T]
+        (pipeline.py:318-321): (h0 [T, hidden], ple [T, layers, P], {layer type: (cos, sin)})."""
+        lm, cfg = self.lm, self.cfg
+        T = ids.shape[1]
+        emb = lm.embed_tokens(ids)
+        ple = lm.project_per_layer_inputs(emb, lm.get_per_layer_inputs(ids, emb))[0]
+        pos = torch.arange(T, device=ids.device)[None]
+        rope = {lt: tuple(t[0] for t in lm.rotary_emb(emb, pos, lt)) for lt in set(cfg.layer_types)}
+        return emb[0], ple, rope
+
+    def _layers(self, h0, ple, rope, scalar):
+        """Every layer over the prompt, in micro-batches of row_step rows (all at once by default):
+        (the final rows [T, hidden] before the last norm, [(layer, k, v)] of the non-shared layers)."""
+        T = h0.shape[0]
+        step = self.row_step or T
+        mbs = [(s, min(s + step, T), j) for j, s in enumerate(range(0, T, step))]
+        ctx = dict(h0=h0, ple=ple, rope=rope, kv={}, layer_kv=[], last=len(mbs) - 1, scalar=scalar)
+        out = [self.steps(mb, ctx) for mb in mbs]
+        return (out[0] if len(out) == 1 else torch.cat(out)), ctx["layer_kv"]
+
+    def _scalars(self):
+        return [layer.layer_scalar.to(torch.bfloat16) for layer in self.lm.layers]
+
+    def _head(self, h_last):
+        """Final norm, LM head and logit softcap of the last row (pipeline.py:334-338)."""
+        h = self.lm.norm(h_last[None])
+        logits = self.model.lm_head(h)[0, -1].float()
+        cap = self.cfg.final_logit_softcapping
+        if cap:
+            logits = torch.tanh(logits / cap) * cap
+        return logits
+
+    def _cache(self, layer_kv, copy):
+        """A DynamicCache holding each non-shared layer's keys and values (pipeline.py:273-274)."""
+        from transformers import DynamicCache
+        cache = DynamicCache(config=self.cfg)
+        for i, k, v in layer_kv:
+            cache.update((k.clone() if copy else k)[None], (v.clone() if copy else v)[None], i)
+        return cache
+
     @torch.inference_mode()
     def __call__(self, ids, all_hidden=False):
         """ids [1, T] -> (last-token logits [vocab] fp32, DynamicCache) (pipeline.py:312-339).
 
         With all_hidden, the final-norm hidden states [T, hidden] instead of the logits."""
-        from transformers import DynamicCache
-        lm, cfg = self.lm, self.cfg
-        if ids.dim() != 2 or ids.shape[0] != 1 or ids.shape[1] < 1:
-            raise ValueError(f"Prefill: expected ids [1, T], got {tuple(ids.shape)}")
-        dev = lm.embed_tokens.weight.device
-        ids = ids.to(dev)
-        T = ids.shape[1]
-        emb = lm.embed_tokens(ids)
-        ple = lm.project_per_layer_inputs(emb, lm.get_per_layer_inputs(ids, emb))[0]
-        pos = torch.arange(T, device=dev)[None]
-        rope = {lt: tuple(t[0] for t in lm.rotary_emb(emb, pos, lt)) for lt in set(cfg.layer_types)}
-        cache = DynamicCache(config=cfg)
-        step = self.row_step or T
-        mbs = [(s, min(s + step, T), j) for j, s in enumerate(range(0, T, step))]
-        scalar = [layer.layer_scalar.to(torch.bfloat16) for layer in lm.layers]
-        ctx = dict(h0=emb[0], ple=ple, rope=rope, kv={}, cache=cache, last=len(mbs) - 1, scalar=scalar)
-        out = [self.steps(mb, ctx) for mb in mbs]
+        h0, ple, rope = self._inputs(self._check_ids(ids))
+        rows, layer_kv = self._layers(h0, ple, rope, self._scalars())
         if all_hidden:
-            return lm.norm(torch.cat(out)[None])[0], cache
-        h = lm.norm(out[-1][-1:][None])
-        logits = self.model.lm_head(h)[0, -1].float()
-        cap = cfg.final_logit_softcapping
-        if cap:
-            logits = torch.tanh(logits / cap) * cap
-        return logits, cache
+            return self.lm.norm(rows[None])[0], self._cache(layer_kv, copy=False)
+        return self._head(rows[-1:]), self._cache(layer_kv, copy=False)
+
+    @torch.inference_mode()
+    def capture(self, T):
+        """This prefill for prompts of T tokens, captured once in a HIP graph: returns a callable
+        ids [1, T] -> (logits, DynamicCache) that replays it.  The launches of a whole prefill
+        (~600 for E2B) then cost one graph launch on the host."""
+        return CapturedPrefill(self, int(T))
+
+
+class CapturedPrefill:
+    """Prefill.capture(T): the layers of one prompt length's prefill as a HIP graph.
+
+    The graph holds every layer's launches (GEMMs, fused kernels, attention) over static input
+    buffers.  A call runs the model's own embedding and per-layer-input modules eagerly, copies
+    their results into those buffers, replays the graph, and runs the final norm, LM head and
+    softcap of the last row eagerly; the RoPE tables depend on T only and are computed once.  The
+    returned logits and cache hold their own copies, so a later replay does not change them.  An
+    eager run on the capture stream before the capture creates every cached workspace outside the
+    graph, so the graph allocates and clears nothing itself."""
+
+    def __init__(self, prefill, T):
+        if T < 1:
+            raise ValueError(f"Prefill.capture: T={T} must be positive")
+        self.prefill, self.T = prefill, T
+        dev = prefill.lm.embed_tokens.weight.device
+        ids = torch.zeros((1, T), dtype=torch.long, device=dev)
+        h0, ple, rope = prefill._inputs(ids)
+        self.h0, self.ple, self.rope = h0.clone(), ple.clone(), rope
+        self.scalar = prefill._scalars()
+        self.stream = torch.cuda.Stream(dev)
+        self.stream.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(self.stream):
+            prefill._layers(self.h0, self.ple, self.rope, self.scalar)
+        torch.cuda.current_stream(dev).wait_stream(self.stream)
+        torch.cuda.synchronize(dev)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph, stream=self.stream):
+            self.rows, self.layer_kv = prefill._layers(self.h0, self.ple, self.rope, self.scalar)
+        torch.cuda.synchronize(dev)
+
+    @torch.inference_mode()
+    def __call__(self, ids):
+        p = self.prefill
+        ids = p._check_ids(ids)
+        if ids.shape[1] != self.T:
+            raise ValueError(f"CapturedPrefill: captured for {self.T} tokens, got {ids.shape[1]}")
+        h0, ple, _ = p._inputs(ids)
+        self.h0.copy_(h0)
+        self.ple.copy_(ple)
+        self.graph.replay()
+        return p._head(self.rows[-1:]), p._cache(self.layer_kv, copy=True)

@@ -146,3 +146,32 @@ def test_fused_gelu_route_matches_reference_route():
     a, _ = Prefill(ours)(ids, all_hidden=True)
     b, _ = Prefill(ours, fuse_gelu=False)(ids, all_hidden=True)
     assert torch.equal(a, b)
+
+
+@torch.inference_mode()
+def test_captured_prefill_replays_match_eager():
+    """Prefill.capture(T): every replay, with eager work and synchronisations between replays, gives
+    the eager prefill's logits and cache bit for bit, and HF's decode loop continues from its cache."""
+    from w8a8.pipeline import Prefill
+    ours = engine_model(build(seed=13))
+    pre = Prefill(ours)
+    T = 37
+    run = pre.capture(T)
+    for seed in (14, 15, 16):
+        ids = torch.randint(0, 512, (1, T), generator=torch.Generator().manual_seed(seed))
+        want, want_cache = pre(ids)
+        torch.cuda.synchronize()
+        got, cache = run(ids)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"replay for seed {seed} differs from the eager prefill"
+        assert cache.get_seq_length() == T
+        for lw, lg in zip(want_cache.layers, cache.layers):
+            if getattr(lw, "keys", None) is not None and getattr(lw, "keys").numel():
+                assert torch.equal(lw.keys, lg.keys) and torch.equal(lw.values, lg.values)
+        _ = torch.ones(1000, device=DEV).sum().item()  # eager work between replays
+    nxt = got.argmax().view(1, 1).to(DEV)
+    a = ours(input_ids=nxt, past_key_values=cache, use_cache=True).logits[0, -1]
+    b = ours(input_ids=nxt, past_key_values=want_cache, use_cache=True).logits[0, -1]
+    assert torch.equal(a, b)
+    with pytest.raises(ValueError, match="captured for 37"):
+        run(torch.zeros((1, 36), dtype=torch.long))
