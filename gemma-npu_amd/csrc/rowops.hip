@@ -174,7 +174,7 @@ __global__ __launch_bounds__(256) void row_chain_kernel(RowChain p) {
       }
     }
     if constexpr (OP == RC_NORM_RES) {
-      res[c] = in ? *reinterpret_cast<const v4u*>(p.aux + int64_t(row) * p.ld_aux + k) : v4u{0u, 0u, 0u, 0u};
+      res[c] = (in && p.aux) ? *reinterpret_cast<const v4u*>(p.aux + int64_t(row) * p.ld_aux + k) : v4u{0u, 0u, 0u, 0u};
       w1[c] = (in && p.w1) ? *reinterpret_cast<const v4u*>(p.w1 + k) : one;
     }
     w2[c] = (in && p.q && p.norm2 && p.w2) ? *reinterpret_cast<const v4u*>(p.w2 + k) : one;
@@ -205,7 +205,7 @@ __global__ __launch_bounds__(256) void row_chain_kernel(RowChain p) {
       for (int i = 0; i < 8; ++i) {
         float n = v[c][i] * r;
         if (p.w1) n = n * wv[i];
-        v[c][i] = round_bf16(rv[i] + round_bf16(n));
+        v[c][i] = p.aux ? round_bf16(rv[i] + round_bf16(n)) : round_bf16(n);  // no residual: the norm alone
       }
     }
   }
@@ -519,14 +519,14 @@ int w8a8_rms_residual_bf16(const uint16_t* y, int64_t ldy, const uint16_t* res, 
   if ((q == nullptr) != (sq == nullptr)) return fail(W8A8_EINVAL, "rms_residual: q and its scale go together");
   W8A8_TRY(check_rows(what, M, N));
   W8A8_TRY(check_bf16_rows(what, "y", y, ldy, N));
-  W8A8_TRY(check_bf16_rows(what, "res", res, ldr, N));
+  if (res) W8A8_TRY(check_bf16_rows(what, "res", res, ldr, N));
   W8A8_TRY(check_bf16_rows(what, "h", h, ldh, N));
   W8A8_TRY(check_vec16(what, "w", w));
   RowChain p{};
   if (q) W8A8_TRY(set_q(what, p, q, ldq, 0, sq, N));
   if (M == 0) return W8A8_OK;
   p.in = y; p.ld_in = ldy; p.head_stride = N; p.head_len = int(N);
-  p.op = RC_NORM_RES; p.aux = res; p.ld_aux = ldr; p.w1 = w;
+  p.op = RC_NORM_RES; p.aux = res; p.ld_aux = res ? ldr : 0; p.w1 = w;
   p.h = h; p.ldh = ldh;
   p.eps = eps; p.M = int(M); p.N = int(N);
   return launch_row_chain(p, false, stream, "rms_residual_bf16");

@@ -15,7 +15,8 @@ Groups as the reference forms them: [q; k; v] (q only on KV-shared layers), o, [
 the per-layer-input gate and projection, and the per-layer model projection.  Rows < 16 (decode)
 take the weight-only int8 GEMV with bf16 scales (gemma_npu.py:120-121); more rows take per-token
 quant -> int8 GEMM -> dequant (gemma_npu.py:123-152).  Unlike the reference, the small PLE gate and
-projection stay on the GPU too.  The HF modules around them (norms, RoPE, GELU, residuals, the KV
+projection stay on the GPU too.  Every RMSNorm module of the text decoder becomes one launch of the
+engine's row kernel (GpuRMSNorm); the other HF modules around them (RoPE, GELU, residuals, the KV
 cache, the decode loop) run unchanged, as torch ops on the GPU.
 """
 import torch
@@ -97,6 +98,33 @@ class Int8Head(torch.nn.Module):
         return y.reshape(*shape, -1)
 
 
+class GpuRMSNorm(torch.nn.Module):
+    """HF Gemma 4's RMSNorm on bf16 GPU rows through the engine's row kernel
+    (w8a8_rms_residual_bf16 without a residual): x * (mean(x^2) + eps)^-0.5 * w in fp32, rounded to
+    bf16 once, as the module computes it (the reference's decode runs these modules around every
+    decoder layer, gemma_npu.py:278-300).  One launch instead of the module's ~6 elementwise and
+    reduction launches.  Inputs the kernel does not take (not bf16, rows not a multiple of 8 or
+    above 12288 elements) go to the model's own module."""
+
+    def __init__(self, norm):
+        super().__init__()
+        self.orig = norm
+        self.eps = float(norm.eps)
+        w = getattr(norm, "weight", None) if getattr(norm, "with_scale", True) else None
+        self.weight = w
+
+    def forward(self, x):
+        N = x.shape[-1]
+        w = self.weight
+        if (x.dtype != torch.bfloat16 or x.device.type != "cuda" or N % 8 or N > 12288 or x.numel() == 0
+                or (w is not None and (w.dtype != torch.bfloat16 or w.device != x.device))):
+            return self.orig(x)
+        x2 = x.reshape(-1, N)
+        if not x2.is_contiguous() or x2.data_ptr() % 16:
+            x2 = x2.clone(memory_format=torch.contiguous_format)
+        return ops.rms_residual(x2, None, w, self.eps).reshape(x.shape)
+
+
 def language_model(model):
     """The text decoder of a Gemma 4 causal LM (multimodal or text-only)."""
     m = model.model
@@ -146,6 +174,11 @@ def to_gpu(model):
     model.layer_gemms = [{} for _ in lm.layers]
     for (li, key), g in zip(per_layer, gemms):
         model.layer_gemms[li][key] = g
+    # every RMSNorm of the text decoder on the row kernel
+    for parent in list(lm.modules()):
+        for name, child in list(parent.named_children()):
+            if type(child).__name__ == "Gemma4RMSNorm":
+                setattr(parent, name, GpuRMSNorm(child))
     # tied to the input embedding, so this is a new int8 copy, not a swap
     model.lm_head = Int8Head(model.lm_head)
     register_attention()

@@ -293,12 +293,13 @@ def dequant_bf16(acc, sx, sw, out=None):
 
 def rms_residual(y, res, w, eps, out=None, quant=False):
     """h = res + bf16(rms(y) * w)  (k_post_ff, pipeline.py:110-114); with quant=True also
-    returns the int8 rows and scales of h."""
+    returns the int8 rows and scales of h.  res=None: h = bf16(rms(y) * w), an RMSNorm."""
     _check(y, "y", torch.bfloat16)
-    _check(res, "res", torch.bfloat16)
     M, N = y.shape
-    if tuple(res.shape) != (M, N):
-        raise ValueError("rms_residual: shapes differ")
+    if res is not None:
+        _check(res, "res", torch.bfloat16)
+        if tuple(res.shape) != (M, N):
+            raise ValueError("rms_residual: shapes differ")
     wp = None
     if w is not None:
         _check(w, "w", torch.bfloat16, 1)
@@ -311,7 +312,8 @@ def rms_residual(y, res, w, eps, out=None, quant=False):
         q = torch.empty((M, N), dtype=torch.int8, device=y.device)
         sq = torch.empty((M,), dtype=torch.float32, device=y.device)
     _same_device(y, res, w, out)
-    call("w8a8_rms_residual_bf16", y.data_ptr(), _ld(y), res.data_ptr(), _ld(res), wp, float(eps), M, N,
+    call("w8a8_rms_residual_bf16", y.data_ptr(), _ld(y), None if res is None else res.data_ptr(),
+         0 if res is None else _ld(res), wp, float(eps), M, N,
          out.data_ptr(), _ld(out), q.data_ptr() if quant else None, N if quant else 0,
          sq.data_ptr() if quant else None, _stream(y))
     return (out, q, sq) if quant else out

@@ -171,9 +171,11 @@ int w8a8_dequant_bf16(const int32_t *acc, int64_t ldacc, const float *sx, const 
                       uint16_t *out, int64_t ldo, hipStream_t stream);
 
 /* h = bf16(res + bf16(y * (mean(y^2) + eps)^-0.5 * w))  (k_post_ff, pipeline.py:110-114) on a
- * bf16 y; w may be NULL (no weight, pipeline.py:46).  If q / sq are given, also the int8 rows
- * (row-major, ld = ldq) and scales of h (the `_quant(h)` of k_post_ff).  h may alias y or res.
- * N % 8 == 0, N <= 12288, 16-byte aligned rows and w. */
+ * bf16 y; w may be NULL (no weight, pipeline.py:46).  res may be NULL: then h = bf16(y *
+ * (mean(y^2) + eps)^-0.5 * w), the RMSNorm module of HF's Gemma 4 text model on bf16 rows (the
+ * norms around every decoder layer of the reference's HF-driven decode, gemma_npu.py:278-300).
+ * If q / sq are given, also the int8 rows (row-major, ld = ldq) and scales of h (the `_quant(h)` of
+ * k_post_ff).  h may alias y or res.  N % 8 == 0, N <= 12288, 16-byte aligned rows and w. */
 int w8a8_rms_residual_bf16(const uint16_t *y, int64_t ldy, const uint16_t *res, int64_t ldr, const uint16_t *w,
                            float eps, int64_t M, int64_t N, uint16_t *h, int64_t ldh, int8_t *q, int64_t ldq,
                            float *sq, hipStream_t stream);

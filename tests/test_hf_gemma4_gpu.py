@@ -72,3 +72,32 @@ def test_decode_past_the_window():
         past_ref, past = o_ref.past_key_values, o.past_key_values
     print(f"decode to position 29: max relative logits error {worst:.4f}")
     assert worst < 0.05
+
+
+@torch.inference_mode()
+def test_gpu_rmsnorm_matches_the_module():
+    """GpuRMSNorm (the row kernel) against HF's Gemma4RMSNorm on the same bf16 rows, with and without
+    a weight, on decoder-shaped inputs (hidden rows, per-head rows, one decode row): within one bf16
+    ulp everywhere, bit for bit on nearly all elements (the sum of squares is added in another
+    order than torch's mean)."""
+    from transformers.models.gemma4.modeling_gemma4 import Gemma4RMSNorm
+    from w8a8 import hf
+    g = torch.Generator().manual_seed(21)
+    for shape, with_scale in (((1, 40, 256), True), ((1, 40, 4, 128), True), ((1, 1, 4, 256), False),
+                              ((1, 1, 1536), True), ((3, 7, 64), True)):
+        N = shape[-1]
+        norm = Gemma4RMSNorm(N, eps=1e-6, with_scale=with_scale)
+        if with_scale:
+            with torch.no_grad():
+                norm.weight.copy_(torch.rand(N, generator=g) + 0.5)
+        norm = norm.to(torch.bfloat16).to(DEV)
+        x = (torch.randn(shape, generator=g) * 3).to(torch.bfloat16).to(DEV)
+        want = norm(x)
+        got = hf.GpuRMSNorm(norm)(x)
+        assert got.shape == want.shape and got.dtype == torch.bfloat16
+        gi = got.view(torch.int16).int().cpu()
+        wi = want.view(torch.int16).int().cpu()
+        assert (gi - wi).abs().max().item() <= 1, f"{shape}: more than one bf16 ulp apart"
+        assert (gi == wi).float().mean().item() > 0.97, f"{shape}: too few bit-exact elements"
+    f32 = torch.randn(2, 8, 64, device=DEV)
+    assert torch.equal(hf.GpuRMSNorm(Gemma4RMSNorm(64).to(DEV))(f32), Gemma4RMSNorm(64).to(DEV)(f32))
