@@ -16,8 +16,9 @@ the per-layer-input gate and projection, and the per-layer model projection.  Ro
 take the weight-only int8 GEMV with bf16 scales (gemma_npu.py:120-121); more rows take per-token
 quant -> int8 GEMM -> dequant (gemma_npu.py:123-152).  Unlike the reference, the small PLE gate and
 projection stay on the GPU too.  Every RMSNorm module of the text decoder becomes one launch of the
-engine's row kernel (GpuRMSNorm); the other HF modules around them (RoPE, GELU, residuals, the KV
-cache, the decode loop) run unchanged, as torch ops on the GPU.
+engine's row kernel (GpuRMSNorm), and for prefill rows each MLP's GELU-tanh * up runs in the gate/up
+GEMM's epilogue (GpuMLP); the other HF modules around them (RoPE, residuals, the KV cache, the decode
+loop) run unchanged, as torch ops on the GPU.
 """
 import torch
 
@@ -125,6 +126,28 @@ class GpuRMSNorm(torch.nn.Module):
         return ops.rms_residual(x2, None, w, self.eps).reshape(x.shape)
 
 
+class GpuMLP(torch.nn.Module):
+    """Gemma 4's MLP, down(gelu_tanh(gate(x)) * up(x)), with the activation and product fused into
+    the gate/up GEMM's epilogue for prefill rows: the epilogue computes bf16(bf16(gelu_tanh(gate)) * up)
+    on the bf16 gate and up the unfused GEMM would have written (k_gelu's arithmetic, pipeline.py:
+    102-107), so the [T, 2I] gate/up result never goes to HBM.  Decode rows (< 16) and activations
+    other than GELU-tanh keep the module's own steps."""
+
+    def __init__(self, mlp, gate_up, down):
+        super().__init__()
+        self.orig = mlp
+        self.gate_up, self.down = gate_up, down
+        self.fused = (getattr(mlp.config, "hidden_activation", None) == "gelu_pytorch_tanh"
+                      and gate_up.packed_gelu is not None)
+
+    def forward(self, x):
+        x2 = x.reshape(-1, x.shape[-1])
+        if not self.fused or x2.shape[0] < DECODE_ROWS:
+            return self.orig(x)
+        a = ops.linear_bf16(x2.to(torch.bfloat16).contiguous(), self.gate_up.packed_gelu, epilogue="gelu")
+        return self.down.matmul(a).reshape(*x.shape[:-1], -1)
+
+
 def language_model(model):
     """The text decoder of a Gemma 4 causal LM (multimodal or text-only)."""
     m = model.model
@@ -174,6 +197,11 @@ def to_gpu(model):
     model.layer_gemms = [{} for _ in lm.layers]
     for (li, key), g in zip(per_layer, gemms):
         model.layer_gemms[li][key] = g
+    # the MLPs with the GELU-tanh * up step in the gate/up GEMM's epilogue for prefill rows
+    for li, layer in enumerate(lm.layers):
+        G = model.layer_gemms[li]
+        if "gate_up" in G and "down" in G:
+            layer.mlp = GpuMLP(layer.mlp, G["gate_up"], G["down"])
     # every RMSNorm of the text decoder on the row kernel
     for parent in list(lm.modules()):
         for name, child in list(parent.named_children()):

@@ -101,3 +101,34 @@ def test_gpu_rmsnorm_matches_the_module():
         assert (gi == wi).float().mean().item() > 0.97, f"{shape}: too few bit-exact elements"
     f32 = torch.randn(2, 8, 64, device=DEV)
     assert torch.equal(hf.GpuRMSNorm(Gemma4RMSNorm(64).to(DEV))(f32), Gemma4RMSNorm(64).to(DEV)(f32))
+
+
+@torch.inference_mode()
+def test_gpu_mlp_matches_the_module_path():
+    """GpuMLP (GELU-tanh * up in the gate/up GEMM's epilogue) against the same MLP run through the
+    engine's separate gate/up GEMM and HF's activation and product: the same bf16 gate and up feed
+    the same arithmetic, so the activations agree to one bf16 ulp (torch's tanh against the
+    epilogue's exp2 form) and mostly bit for bit; after the down GEMM's per-token quant the MLP
+    outputs agree to quantisation noise.  Decode rows take the module's own path, bit for bit."""
+    from w8a8 import hf, ops
+    ours = copy.deepcopy(build(seed=17)).to(torch.bfloat16).to(DEV)
+    hf.to_gpu(ours)
+    mlp = ours.model.layers[6].mlp
+    assert isinstance(mlp, hf.GpuMLP) and mlp.fused
+    g = torch.Generator().manual_seed(18)
+    for rows in (40, 300, 3):
+        x = torch.randn(1, rows, 256, generator=g).to(torch.bfloat16).to(DEV)
+        got = mlp(x)
+        want = mlp.orig(x)
+        assert got.shape == want.shape == (1, rows, 256)
+        if rows < 16:
+            assert torch.equal(got, want)
+            continue
+        x2 = x.reshape(rows, 256)
+        a_fused = ops.linear_bf16(x2, mlp.gate_up.packed_gelu, epilogue="gelu")
+        o = mlp.orig
+        a_ref = o.act_fn(o.gate_proj(x2)) * o.up_proj(x2)
+        ai, ri = a_fused.view(torch.int16).int().cpu(), a_ref.view(torch.int16).int().cpu()
+        assert (ai - ri).abs().max().item() <= 1
+        assert (ai == ri).float().mean().item() > 0.99
+        assert rel_err(got[0], want[0]) < 2e-2
