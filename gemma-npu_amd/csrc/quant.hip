@@ -64,13 +64,13 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const T* __restrict__ x
       float v[8];
       load8<T>(xr + k, v);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+      for (int i = 0; i < 8; ++i) amax = absmax2(amax, fabsf(v[i]));
     }
   } else {
-    for (int k = lane; k < K; k += 64) amax = fmaxf(amax, fabsf(load1<T>(xr + k)));
+    for (int k = lane; k < K; k += 64) amax = absmax2(amax, fabsf(load1<T>(xr + k)));
   }
-  amax = wave_max(amax);
-  const float s = fmaxf(amax, 1e-8f) / 127.0f;
+  amax = wave_absmax(amax);
+  const float s = quant_scale(amax);
   const float rs = 1.0f / s;
   if (lane == 0) scale[row] = s;
   // bf16 rows take the division-free step (exact for bf16 values); fp32 rows divide.
@@ -156,10 +156,10 @@ __global__ __launch_bounds__(256) void quant_rows_packed_kernel(const uint16_t* 
       for (int i = 0; i < 16; ++i) v[i] = bf16_to_f32(xr[k + i]);
     }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    for (int i = 0; i < 16; ++i) amax = absmax2(amax, fabsf(v[i]));
   }
-  amax = wave_max(amax);
-  const float s = fmaxf(amax, 1e-8f) / 127.0f;
+  amax = wave_absmax(amax);
+  const float s = quant_scale(amax);
   const float rs = 1.0f / s;
   if (lane == 0) scale[row] = s;
   for (int k = lane * 16; k < KP; k += 1024) {
@@ -224,12 +224,12 @@ __global__ __launch_bounds__(256) void quant_rows_blk_kernel(const uint16_t* __r
   for (int c = 0; c < CH; ++c)
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      amax = fmaxf(amax, fmaxf(fabsf(__uint_as_float(v[c][i] << 16)), fabsf(__uint_as_float(v[c][i] & 0xffff0000u))));
-  amax = wave_max_dpp(amax);
+      amax = absmax2(amax, absmax2(fabsf(__uint_as_float(v[c][i] << 16)), fabsf(__uint_as_float(v[c][i] & 0xffff0000u))));
+  amax = wave_absmax_dpp(amax);
   if ((t & 63) == 0) wave_amax[t >> 6] = amax;
   __syncthreads();
-  amax = fmaxf(fmaxf(wave_amax[0], wave_amax[1]), fmaxf(wave_amax[2], wave_amax[3]));
-  const float s = fmaxf(amax, 1e-8f) / 127.0f;
+  amax = absmax2(absmax2(wave_amax[0], wave_amax[1]), absmax2(wave_amax[2], wave_amax[3]));
+  const float s = quant_scale(amax);
   const float rs = 1.0f / s;
   if (t == 0) scale[row] = s;
 #pragma unroll

@@ -62,13 +62,13 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
 // is 4 floats of LDS used by this reduction only.
 template <bool MAX>
 __device__ __forceinline__ float block_reduce(float v, float* slot) {
-  v = MAX ? wave_max_dpp(v) : wave_sum_dpp(v);
+  v = MAX ? wave_absmax_dpp(v) : wave_sum_dpp(v);
   const int nw = int(blockDim.x >> 6);
   if (nw == 1) return v;
   if ((threadIdx.x & 63) == 0) slot[threadIdx.x >> 6] = v;
   __syncthreads();
   float r = slot[0];
-  for (int i = 1; i < nw; ++i) r = MAX ? fmaxf(r, slot[i]) : r + slot[i];
+  for (int i = 1; i < nw; ++i) r = MAX ? absmax2(r, slot[i]) : r + slot[i];
   return r;
 }
 
@@ -248,9 +248,9 @@ __global__ __launch_bounds__(256) void row_chain_kernel(RowChain p) {
 #pragma unroll
   for (int c = 0; c < CH; ++c)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[c][i]));
+    for (int i = 0; i < 8; ++i) amax = absmax2(amax, fabsf(v[c][i]));
   amax = block_reduce<true>(amax, red[2]);
-  const float s = fmaxf(amax, 1e-8f) / 127.0f;
+  const float s = quant_scale(amax);
   const float rs = 1.0f / s;
   if (t == 0) p.sq[row] = s;
 #pragma unroll

@@ -38,16 +38,23 @@ __device__ __forceinline__ v4i buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t vof
 }
 
 // ---- wave reductions (wave64) --------------------------------------------------------------
-__device__ __forceinline__ float wave_max(float v) {
+// Row absmax as torch.amax(|x|) computes it (pipeline.py:51): NaN propagates.  For sign-cleared
+// fp32 bit patterns the unsigned order is the numeric order with every NaN above +Inf, so an
+// unsigned max of |x| keeps a NaN where fmaxf would drop it.  Every input is an |x| (or 0).
+__device__ __forceinline__ float absmax2(float a, float b) {
+  return __uint_as_float(max(__float_as_uint(a), __float_as_uint(b)));
+}
+
+__device__ __forceinline__ float wave_absmax(float v) {
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  for (int o = 32; o > 0; o >>= 1) v = absmax2(v, __shfl_xor(v, o, 64));
   return v;
 }
-// Wave maximum of v broadcast to every lane, through DPP lane moves (no LDS round trips):
-// butterflies inside each row of 16 lanes, then row_bcast:15 / row_bcast:31 carry the row maxima
-// up to lane 63, which is read back as a scalar.
-__device__ __forceinline__ float wave_max_dpp(float v) {
-  auto dpp = [](float x, int ctrl, int row_mask) {
+// Wave absmax (as absmax2) of v broadcast to every lane, through DPP lane moves (no LDS round
+// trips): butterflies inside each row of 16 lanes, then row_bcast:15 / row_bcast:31 carry the row
+// maxima up to lane 63, which is read back as a scalar.
+__device__ __forceinline__ float wave_absmax_dpp(float v) {
+  auto dpp = [](float x, int ctrl) {
     const int xi = __builtin_bit_cast(int, x);
     switch (ctrl) {
       case 0xB1: return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(xi, xi, 0xB1, 0xF, 0xF, false));
@@ -57,14 +64,13 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
       case 0x142: return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(xi, xi, 0x142, 0xA, 0xF, false));
       default: return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(xi, xi, 0x143, 0xC, 0xF, false));
     }
-    (void)row_mask;
   };
-  v = fmaxf(v, dpp(v, 0xB1, 0xF));   // quad_perm [1,0,3,2]
-  v = fmaxf(v, dpp(v, 0x4E, 0xF));   // quad_perm [2,3,0,1]
-  v = fmaxf(v, dpp(v, 0x141, 0xF));  // row_half_mirror: 8 lanes
-  v = fmaxf(v, dpp(v, 0x140, 0xF));  // row_mirror: 16 lanes
-  v = fmaxf(v, dpp(v, 0x142, 0xA));  // row_bcast:15 into rows 1, 3
-  v = fmaxf(v, dpp(v, 0x143, 0xC));  // row_bcast:31 into rows 2, 3
+  v = absmax2(v, dpp(v, 0xB1));   // quad_perm [1,0,3,2]
+  v = absmax2(v, dpp(v, 0x4E));   // quad_perm [2,3,0,1]
+  v = absmax2(v, dpp(v, 0x141));  // row_half_mirror: 8 lanes
+  v = absmax2(v, dpp(v, 0x140));  // row_mirror: 16 lanes
+  v = absmax2(v, dpp(v, 0x142));  // row_bcast:15 into rows 1, 3
+  v = absmax2(v, dpp(v, 0x143));  // row_bcast:31 into rows 2, 3
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
@@ -75,12 +81,21 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 // ---- per-row int8 quantisation step (pipeline.py:51) -----------------------------------------
-// q = clamp(rint(v / s), +-127): IEEE fp32 division, round half to even.
-__device__ __forceinline__ int8_t quant1(float v, float s) {
-  float r = __builtin_rintf(v / s);
-  r = fminf(fmaxf(r, -127.0f), 127.0f);
-  return int8_t(int(r));
+// s = amax.clamp(min=1e-8) / 127 from a row absmax (pipeline.py:51); a NaN absmax stays NaN, as
+// torch's clamp keeps it.
+__device__ __forceinline__ float quant_scale(float amax) {
+  return (amax != amax ? amax : fmaxf(amax, 1e-8f)) / 127.0f;
 }
+
+// clamp(r, +-127) -> int8, with NaN -> 0: torch's float -> int8 conversion on the host gives 0
+// for NaN, which is what a row holding NaN (scale NaN) or +-Inf (scale Inf, Inf / Inf) quantises
+// to in the reference (fminf / fmaxf alone would turn NaN into -127).
+__device__ __forceinline__ int8_t clamp_q(float r) {
+  return r != r ? int8_t(0) : int8_t(int(fminf(fmaxf(r, -127.0f), 127.0f)));
+}
+
+// q = clamp(rint(v / s), +-127): IEEE fp32 division, round half to even.
+__device__ __forceinline__ int8_t quant1(float v, float s) { return clamp_q(__builtin_rintf(v / s)); }
 
 // The same q for a bf16-valued v with |v| <= 127 s (every element of the row the scale was taken
 // from), without a division per element: rs = 1 / s (IEEE, once per row), q0 = v * rs,
@@ -92,9 +107,7 @@ __device__ __forceinline__ int8_t quant1_bf16(float v, float s, float rs) {
   const float q0 = v * rs;
   const float r = __builtin_fmaf(-q0, s, v);
   const float q1 = __builtin_fmaf(r, rs, q0);
-  float q = __builtin_rintf(q1);
-  q = fminf(fmaxf(q, -127.0f), 127.0f);
-  return int8_t(int(q));
+  return clamp_q(__builtin_rintf(q1));
 }
 
 // ---- XCD-aware block order ---------------------------------------------------------------------

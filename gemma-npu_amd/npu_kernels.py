@@ -10,9 +10,14 @@ Same names and call signature:
 `b` is normally the PackedWeight returned by `resident.to_npu(w, static=True)` (the weight
 stays resident in HBM in the MFMA layout); a plain int8 [K, N] tensor also works and is
 packed on every call.  `a` and `c` may be host tensors (the reference's host-visible
-resident buffers): rows are copied to the GPU, multiplied, and copied back before
-mm_i8 returns, matching the reference's synchronous launch.  With GPU tensors the call is
-ordered on torch's current stream instead.
+resident buffers) or GPU tensors.
+
+Completion is synchronous, as in the reference: its launch returns when C is ready, and the
+worker thread that made it hands C to another thread straight away (pipeline.py:202-216;
+gemma_npu.py:99-115).  So when mm_i8 returns, c holds the product and a may be refilled,
+whichever thread called it and whatever stream the thread that reads c uses.  A caller that
+reads c on the stream that launched it can pass wait=False to skip the final wait; the GEMM
+is then ordered on torch's current stream like any other GPU op.
 
 Importing this module also makes `from triton.backends.amd_triton_npu import resident`
 resolve to `w8a8.resident`, so gemma_npu.py's NPUGemm runs on it unchanged.
@@ -43,11 +48,12 @@ def _device():
     return torch.device("cuda", _DEVICE_INDEX)
 
 
-def mm_i8(a, b, c):
+def mm_i8(a, b, c, *, wait=True):
     """c[M, N] = a[M, K] @ b[K, N] (int8 x int8 -> int32, exact).  Returns c.
 
     Unlike the reference (npu_kernels.py:59-64), any M and N work, and a shape mismatch
-    raises instead of truncating to multiples of 512.
+    raises instead of truncating to multiples of 512.  With wait=True (the reference's
+    contract) c is complete and a is no longer read when this returns.
     """
     if a.dtype != torch.int8 or a.dim() != 2:
         raise TypeError(f"mm_i8: a must be int8 [M, K], got {a.dtype} {tuple(a.shape)}")
@@ -69,15 +75,19 @@ def mm_i8(a, b, c):
     if M == 0:
         return c
     w = b if isinstance(b, PackedWeight) else ops.pack_weight(b.to(dev), layout="kn")
-    a_d = a if a.is_cuda else a.to(dev, non_blocking=a.is_pinned())
+    # A host `a` is copied synchronously: the caller may refill its staging rows as soon as
+    # mm_i8 returns (gemma_npu.py:94-97, pipeline.py:241), even when c stays on the GPU.
+    a_d = a if a.is_cuda else a.to(dev)
     if a_d.stride(1) != 1 or a_d.stride(0) % 16 or a_d.data_ptr() % 16:
         a_d = a_d.contiguous()
     if c.is_cuda and c.stride(1) == 1 and c.stride(0) % 4 == 0 and c.data_ptr() % 16 == 0:
         ops.gemm_i32(a_d, w, c)
-        return c
-    c_d = torch.empty((M, N), dtype=torch.int32, device=dev)
-    ops.gemm_i32(a_d, w, c_d)
-    c.copy_(c_d)  # blocking for host c: the result is there when mm_i8 returns
+    else:
+        c_d = torch.empty((M, N), dtype=torch.int32, device=dev)
+        ops.gemm_i32(a_d, w, c_d)
+        c.copy_(c_d)  # a host c: this copy waits for the GEMM
+    if wait and c.is_cuda:
+        torch.cuda.current_stream(c.device).synchronize()
     return c
 
 

@@ -31,6 +31,7 @@ SIGNATURES = {
     "w8a8_clock_probe": (_i32, [_p, ctypes.c_uint, _p, _p]),
     "w8a8_gemm_i32": (_i32, [_p, _i64, _p, _i64, _i64, _i64, _p, _i64, _p]),
     "w8a8_gemm_tile_configs": (_i32, []),
+    "w8a8_gemm_pick_tile_config": (_i32, [_i64, _i64, _i64, _i32]),
     "w8a8_gemm_workspace_bytes": (_i64, [_i64, _i64, _i64, _i32, _i32]),
     "w8a8_gemm_i32_ex": (_i32, [_p, _i64, _i32, _p, _i64, _i64, _i64, _p, _i64, _i32, _i32, _p, _i64, _p]),
     "w8a8_packed_act_bytes": (_i64, [_i64, _i64]),

@@ -129,12 +129,20 @@ int w8a8_quant_rows_packed_bf16(const uint16_t *x, int64_t ldx, int64_t M, int64
 /* Number of explicit tile configurations the _ex GEMMs accept (tile_cfg 0 .. n-1). */
 int w8a8_gemm_tile_configs(void);
 
+/* The tile configuration the automatic choice (tile_cfg = -1) takes for [M, N, K] with
+ * epilogue 0 (int32 out or dequant), 1 (GELU) or 2 (residual); -1 for an invalid shape.  No
+ * counterpart in the reference (its single Triton kernel has one schedule, npu_kernels.py:29-37);
+ * for tests and benchmarks that report which kernel ran. */
+int w8a8_gemm_pick_tile_config(int64_t M, int64_t N, int64_t K, int epilogue);
+
 /* Split-K workspace the _ex GEMMs use for [M, N, K] with tile_cfg (-1 = automatic) and split_k
- * (0 = automatic, which currently never splits; n >= 1 = at most n blocks per output tile
- * along K, used only when there are few output tiles): 0 when no split will happen.  Its first 4 KiB
- * hold arrival counters that must be zero before a call and are zero again after it (zero-fill
- * a new workspace once); the rest is scratch, so one workspace serves any shapes.  Calls that
- * overlap in time need separate workspaces. */
+ * (n >= 1 = at most n blocks per output tile along K, only when there are fewer than 200 output
+ * tiles; 0 = automatic: two blocks per output tile when a block-split tile configuration has at
+ * most 128 output tiles and K >= 4096, otherwise none -- the automatic tile choice currently
+ * takes no such configuration, so with tile_cfg = -1 this is 0).  0 when no split will happen.
+ * Its first 4 KiB hold arrival counters that must be zero before a call and are zero again after
+ * it (zero-fill a new workspace once); the rest is scratch, so one workspace serves any shapes.
+ * Calls that overlap in time need separate workspaces. */
 int64_t w8a8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int tile_cfg, int split_k);
 
 /* As w8a8_gemm_i32 with A given either row-major (a_packed = 0, lda used) or packed

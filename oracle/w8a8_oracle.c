@@ -107,7 +107,9 @@ void oracle_quant_rows(const void *x, int dtype, int64_t ldx, int64_t M, int64_t
             float r = nearbyintf(v / s);
             if (r > 127.0f) r = 127.0f;
             if (r < -127.0f) r = -127.0f;
-            q[m * ldq + k] = (int8_t)r;
+            /* A NaN quotient (a row holding NaN: s is NaN; a row holding +-Inf: Inf / Inf) is
+             * what torch's float -> int8 conversion turns into 0 on the host. */
+            q[m * ldq + k] = isnan(r) ? 0 : (int8_t)r;
         }
     }
 }

@@ -32,6 +32,23 @@ def test_library_exports_every_declared_symbol():
     assert L.w8a8_gemm_tile_configs() == 26
 
 
+def test_pick_tile_config_is_a_valid_configuration():
+    """The automatic choice names a real configuration for every prefill shape, differs between
+    one micro-batch and a whole prompt where the tiles do, and rejects invalid shapes."""
+    L = _lib.lib()
+    n = L.w8a8_gemm_tile_configs()
+    shapes = [(1536, 2560), (2048, 1536), (1536, 12288), (6144, 1536), (1536, 8960), (12288, 1536),
+              (1536, 24576)]
+    for M in (1, 77, 512, 3658, 4096, 16384):
+        for K, N in shapes:
+            for epi in (0, 1, 2):
+                cfg = L.w8a8_gemm_pick_tile_config(M, N, K, epi)
+                assert 0 <= cfg < n, (M, N, K, epi, cfg)
+    assert L.w8a8_gemm_pick_tile_config(512, 12288, 1536, 1) != L.w8a8_gemm_pick_tile_config(3658, 12288, 1536, 1)
+    assert L.w8a8_gemm_pick_tile_config(0, 64, 64, 0) == -1
+    assert L.w8a8_gemm_pick_tile_config(64, 64, 64, 3) == -1
+
+
 def test_packed_weight_bytes():
     L = _lib.lib()
     assert L.w8a8_packed_weight_bytes(6144, 1536, 0) == 6144 * 1536

@@ -91,6 +91,36 @@ def test_quant_known_answers():
     assert (np.abs(q) <= 127).all()
 
 
+def nan_inf_rows():
+    """bf16 rows holding NaN and +-Inf next to ordinary and zero rows."""
+    nan, inf = float("nan"), float("inf")
+    x = torch.randn(6, 48, generator=torch.Generator().manual_seed(3))
+    x[1, 5] = nan
+    x[2, 7] = inf
+    x[3, 0] = -inf
+    x[4] = 0.0
+    x[5, 9], x[5, 30] = inf, nan
+    return x.to(torch.bfloat16)
+
+
+def test_quant_nan_and_inf_rows_follow_torch():
+    """torch.amax propagates NaN (pipeline.py:51): a row holding NaN gets a NaN scale, a row
+    holding +-Inf an Inf scale, and both quantise to 0 everywhere (x / NaN and Inf / Inf are NaN,
+    which torch's float -> int8 conversion makes 0; finite / Inf is 0).  Checked against the
+    reference expression run by torch itself."""
+    x = nan_inf_rows()
+    xf = x.float()
+    s_t = xf.abs().amax(dim=-1, keepdim=True).clamp(min=1e-8) / 127
+    q_t = torch.round(xf / s_t).clamp(-127, 127).to(torch.int8)
+    q, s = orc.quant_rows(to_bits(x), "bf16")
+    s_ref = s_t[:, 0].numpy()
+    assert np.array_equal(np.isnan(s), np.isnan(s_ref)) and np.isnan(s[[1, 5]]).all()
+    fin = ~np.isnan(s_ref)
+    assert np.array_equal(s[fin], s_ref[fin]) and np.isinf(s[[2, 3]]).all()
+    assert np.array_equal(q, q_t.numpy())
+    assert not q[1:6].any() and q[0].any()
+
+
 # ---- dequant (pipeline.py:55-57) -----------------------------------------------------------
 
 def test_dequant_golden(gold):

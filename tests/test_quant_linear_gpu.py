@@ -48,6 +48,58 @@ def test_quant_rows_ties_and_zero_rows():
     assert q[1, :8].tolist() == [127, 64, 0, -127, 2, 2, -2, 0]
 
 
+def _nan_inf_rows(K, dtype=torch.bfloat16):
+    nan, inf = float("nan"), float("inf")
+    x = torch.randn(6, K, generator=torch.Generator().manual_seed(K))
+    x[1, K // 3] = nan
+    x[2, K - 1] = inf
+    x[3, 0] = -inf
+    x[4] = 0.0
+    x[5, 1], x[5, K // 2] = inf, nan
+    return x.to(dtype)
+
+
+def _assert_scales(s, s_ref):
+    s = s.cpu().numpy()
+    assert np.array_equal(np.isnan(s), np.isnan(s_ref)) and np.isnan(s[[1, 5]]).all()
+    fin = ~np.isnan(s_ref)
+    assert np.array_equal(s[fin], s_ref[fin]) and np.isinf(s[[2, 3]]).all()
+
+
+@pytest.mark.parametrize("K", [48, 100, 12800])
+def test_quant_nan_and_inf_rows_follow_torch(K):
+    """Rows holding NaN get a NaN scale and rows holding +-Inf an Inf scale, as torch.amax and
+    clamp give them (pipeline.py:51), and both quantise to 0 everywhere, as the oracle (pinned
+    against torch's own output on the host) does.  Every quant kernel: the block-per-row kernel
+    (K = 48), the wave-per-row kernel without (K = 100) and with (K = 12800) vector loads, their
+    packed-layout forms, fp32 rows, and the fused k_in row kernel."""
+    x = _nan_inf_rows(K)
+    q_ref, s_ref = orc.quant_rows(to_bits(x), "bf16")
+    assert not q_ref[1:].any()
+    q, s = ops.quant_rows(x.to(DEV))
+    _assert_scales(s, s_ref)
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+    if K % 16 == 0:
+        from test_gemm_gpu import unpack_act
+        for xd in (x.to(DEV), torch.cat([x, x[:, :1]], 1).to(DEV)[:, :K]):  # vector and odd-stride rows
+            pa, sp = ops.quant_rows_packed(xd)
+            _assert_scales(sp, s_ref)
+            assert np.array_equal(unpack_act(pa.data.cpu().numpy(), 6, K)[:6, :K], q_ref)
+    xf = _nan_inf_rows(K, torch.float32)
+    qf_ref, sf_ref = orc.quant_rows(xf.numpy(), "f32")
+    qf, sf = ops.quant_rows(xf.to(DEV))
+    _assert_scales(sf, sf_ref)
+    assert np.array_equal(qf.cpu().numpy(), qf_ref) and not qf_ref[1:].any()
+    if K % 8 == 0 and K <= 12288:
+        from w8a8 import fused
+        w = torch.ones(K, dtype=torch.bfloat16)
+        qk, sk = fused.k_in(x.to(DEV), w.to(DEV), 1e-6)
+        qk_ref, sk_ref = orc.k_in(to_bits(x), to_bits(w), 1e-6)
+        sk = sk.cpu().numpy()
+        assert np.array_equal(np.isnan(sk), np.isnan(sk_ref)) and np.isnan(sk[[1, 2, 3, 5]]).all()
+        assert np.array_equal(qk.cpu().numpy()[1:], qk_ref[1:]) and not qk_ref[1:4].any()
+
+
 def test_quant_rows_f32_weights():
     """Per-output-channel weight quant (gemma_npu.py:68-69) is the same kernel on fp32 rows."""
     g = torch.Generator().manual_seed(9)
