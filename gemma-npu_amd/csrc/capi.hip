@@ -2,9 +2,12 @@
 //
 // Every entry point takes plain device pointers, sizes and a hipStream_t, launches on that
 // stream and returns 0 or a W8A8_E* status; w8a8_last_error() gives the message for the
-// calling thread.  Nothing here allocates device memory or synchronises the stream.
+// calling thread.  Nothing here allocates device memory or synchronises the stream; the one
+// file-scope device array (the scratch of w8a8_linear_bf16_noalloc) is part of the code object.
 #include <stdarg.h>
 #include <stdio.h>
+
+#include <mutex>
 
 #include "gemm.h"
 #include "w8a8_common.h"
@@ -227,31 +230,35 @@ int64_t w8a8_linear_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   return linear_gemm_part(g) + align256(a) + align256(M * 4);
 }
 
-int w8a8_linear_bf16(const uint16_t* x, int64_t ldx, const int8_t* w_packed, const float* sw, int64_t M, int64_t N,
-                     int64_t K, int epilogue, int64_t interleave, const uint16_t* res, int64_t ldr,
-                     const uint16_t* rms_w, float eps, uint16_t* out, int64_t ldo, void* workspace,
-                     int64_t workspace_bytes, hipStream_t stream) {
-  if (!x && M > 0) return fail(W8A8_EINVAL, "linear_bf16: null x");
-  if (K % 16 != 0) return fail(W8A8_ENOTSUP, "linear_bf16: K=%lld must be a multiple of 16", (long long)K);
-  if (epilogue < 0 || epilogue > 3) return fail(W8A8_EINVAL, "linear_bf16: unknown epilogue %d", epilogue);
-  const int64_t need = w8a8_linear_workspace_bytes(M, N, K);
-  if (need < 0) return fail(W8A8_EINVAL, "linear_bf16: bad shape");
-  if (M == 0) return W8A8_OK;
-  if (!workspace || workspace_bytes < need || (uintptr_t)workspace % 256 != 0)
-    return fail(W8A8_EINVAL, "linear_bf16: workspace needs %lld bytes, 256-byte aligned", (long long)need);
-  if (epilogue == 3) {
-    if (!res) return fail(W8A8_EINVAL, "linear_bf16: residual_rms epilogue without a residual");
+}  // extern "C"
+
+namespace w8a8 {
+
+// Argument checks shared by the two whole-linear entry points (everything but the workspace).
+static int check_linear(const char* fn, const uint16_t* x, int64_t M, int64_t N, int64_t K, int epilogue,
+                        const uint16_t* res, int64_t ldr, const uint16_t* rms_w, const uint16_t* out, int64_t ldo) {
+  if (!x && M > 0) return fail(W8A8_EINVAL, "%s: null x", fn);
+  if (K % 16 != 0) return fail(W8A8_ENOTSUP, "%s: K=%lld must be a multiple of 16", fn, (long long)K);
+  if (epilogue < 0 || epilogue > 3) return fail(W8A8_EINVAL, "%s: unknown epilogue %d", fn, epilogue);
+  if (w8a8_packed_act_bytes(M, K) < 0 || N <= 0) return fail(W8A8_EINVAL, "%s: bad shape", fn);
+  if (M > 0 && epilogue == 3) {
+    if (!res) return fail(W8A8_EINVAL, "%s: residual_rms epilogue without a residual", fn);
     if (N % 8 != 0 || N > 12288)
-      return fail(W8A8_ENOTSUP, "linear_bf16: the RMSNorm residual needs N %% 8 == 0 and N <= 12288 (N=%lld)",
+      return fail(W8A8_ENOTSUP, "%s: the RMSNorm residual needs N %% 8 == 0 and N <= 12288 (N=%lld)", fn,
                   (long long)N);
     if ((uintptr_t)out % 16 || ldo % 8 || (uintptr_t)res % 16 || ldr % 8 || (uintptr_t)rms_w % 16)
-      return fail(W8A8_EALIGN, "linear_bf16: the RMSNorm residual needs 16-byte aligned out / res rows and rms_w");
+      return fail(W8A8_EALIGN, "%s: the RMSNorm residual needs 16-byte aligned out / res rows and rms_w", fn);
   }
-  char* base = static_cast<char*>(workspace);
-  const int64_t gbytes = linear_gemm_part(w8a8_gemm_workspace_bytes(M, N, K, -1, 0));
-  void* gws = base;
-  int8_t* q = reinterpret_cast<int8_t*>(base + gbytes);
-  float* sx = reinterpret_cast<float*>(base + gbytes + align256(w8a8_packed_act_bytes(M, K)));
+  return W8A8_OK;
+}
+
+// quant_rows(x) into the packed rows q and scales sx, then the GEMM with its epilogue.  gws: the
+// GEMM's split-K workspace, or null (the automatic tile choice never splits K, so both give the
+// same kernels and the same bits).
+static int run_linear(const uint16_t* x, int64_t ldx, const int8_t* w_packed, const float* sw, int64_t M, int64_t N,
+                      int64_t K, int epilogue, int64_t interleave, const uint16_t* res, int64_t ldr,
+                      const uint16_t* rms_w, float eps, uint16_t* out, int64_t ldo, int8_t* q, float* sx, void* gws,
+                      int64_t gbytes, hipStream_t stream) {
   int rc = w8a8_quant_rows_packed_bf16(x, ldx, M, K, q, sx, stream);
   if (rc) return rc;
   if (epilogue == 3) {
@@ -263,6 +270,83 @@ int w8a8_linear_bf16(const uint16_t* x, int64_t ldx, const int8_t* w_packed, con
   }
   return w8a8_gemm_bf16_ex(q, 0, 1, sx, w_packed, sw, M, N, K, epilogue, interleave, res, ldr, out, ldo, -1, 0, gws,
                            gbytes, stream);
+}
+
+// ---- scratch of the linear that allocates nothing -----------------------------------------------
+// Packed int8 rows, then per-row scales, for w8a8_linear_bf16_noalloc.  The array lives in the
+// code object's zero-initialised data: each GPU the library runs on holds its own copy until the
+// process ends.  In host code `scratch` only names the symbol; its device address (one per GPU)
+// comes from hipGetSymbolAddress with that GPU current, and only that address is ever passed to
+// a kernel.
+static constexpr int64_t kNoAllocScratchBytes = int64_t(64) << 20;
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+static constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices] = {};
+
+static int scratch_of_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(W8A8_EHIP, "linear_bf16_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(W8A8_ENOTSUP, "linear_bf16_noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(W8A8_EHIP, "linear_bf16_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                  e != hipSuccess ? hipGetErrorString(e) : "null address");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return W8A8_OK;
+}
+
+}  // namespace w8a8
+
+extern "C" {
+
+int w8a8_linear_bf16(const uint16_t* x, int64_t ldx, const int8_t* w_packed, const float* sw, int64_t M, int64_t N,
+                     int64_t K, int epilogue, int64_t interleave, const uint16_t* res, int64_t ldr,
+                     const uint16_t* rms_w, float eps, uint16_t* out, int64_t ldo, void* workspace,
+                     int64_t workspace_bytes, hipStream_t stream) {
+  int rc = check_linear("linear_bf16", x, M, N, K, epilogue, res, ldr, rms_w, out, ldo);
+  if (rc) return rc;
+  const int64_t need = w8a8_linear_workspace_bytes(M, N, K);
+  if (need < 0) return fail(W8A8_EINVAL, "linear_bf16: bad shape");
+  if (M == 0) return W8A8_OK;
+  if (!workspace || workspace_bytes < need || (uintptr_t)workspace % 256 != 0)
+    return fail(W8A8_EINVAL, "linear_bf16: workspace needs %lld bytes, 256-byte aligned", (long long)need);
+  char* base = static_cast<char*>(workspace);
+  const int64_t gbytes = linear_gemm_part(w8a8_gemm_workspace_bytes(M, N, K, -1, 0));
+  int8_t* q = reinterpret_cast<int8_t*>(base + gbytes);
+  float* sx = reinterpret_cast<float*>(base + gbytes + align256(w8a8_packed_act_bytes(M, K)));
+  return run_linear(x, ldx, w_packed, sw, M, N, K, epilogue, interleave, res, ldr, rms_w, eps, out, ldo, q, sx, base,
+                    gbytes, stream);
+}
+
+int w8a8_linear_bf16_noalloc(const uint16_t* x, int64_t ldx, const int8_t* w_packed, const float* sw, int64_t M,
+                             int64_t N, int64_t K, int epilogue, int64_t interleave, const uint16_t* res, int64_t ldr,
+                             const uint16_t* rms_w, float eps, uint16_t* out, int64_t ldo, hipStream_t stream) {
+  int rc = check_linear("linear_bf16_noalloc", x, M, N, K, epilogue, res, ldr, rms_w, out, ldo);
+  if (rc) return rc;
+  if (M == 0) return W8A8_OK;
+  const int64_t abytes = align256(w8a8_packed_act_bytes(M, K));
+  const int64_t need = abytes + align256(M * 4);
+  if (need > kNoAllocScratchBytes)
+    return fail(W8A8_ENOTSUP,
+                "linear_bf16_noalloc: M=%lld rows of K=%lld need %lld bytes of scratch, more than the library's "
+                "%lld (%lld MiB); split the rows or call w8a8_linear_bf16 with a workspace",
+                (long long)M, (long long)K, (long long)need, (long long)kNoAllocScratchBytes,
+                (long long)(kNoAllocScratchBytes >> 20));
+  void* base = nullptr;
+  rc = scratch_of_current_device(&base);
+  if (rc) return rc;
+  int8_t* q = static_cast<int8_t*>(base);
+  float* sx = reinterpret_cast<float*>(static_cast<char*>(base) + abytes);
+  return run_linear(x, ldx, w_packed, sw, M, N, K, epilogue, interleave, res, ldr, rms_w, eps, out, ldo, q, sx,
+                    nullptr, 0, stream);
 }
 
 }  // extern "C"

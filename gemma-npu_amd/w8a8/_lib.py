@@ -55,6 +55,8 @@ SIGNATURES = {
     "w8a8_linear_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "w8a8_linear_bf16": (_i32, [_p, _i64, _p, _p, _i64, _i64, _i64, _i32, _i64, _p, _i64, _p, _f32, _p, _i64, _p,
                                 _i64, _p]),
+    "w8a8_linear_bf16_noalloc": (_i32, [_p, _i64, _p, _p, _i64, _i64, _i64, _i32, _i64, _p, _i64, _p, _f32, _p,
+                                        _i64, _p]),
     "w8a8_gemv_bf16": (_i32, [_p, _i64, _i64, _p, _i64, _i64, _i64, _p, _i32, _p, _i64, _p]),
     "w8a8_gemv_packed_bytes": (_i64, [_i64, _i64]),
     "w8a8_pack_gemv_weight": (_i32, [_p, _i64, _i64, _i64, _p, _p]),

@@ -267,6 +267,20 @@ int w8a8_linear_bf16(const uint16_t *x, int64_t ldx, const int8_t *w_packed, con
                      const uint16_t *rms_w, float eps, uint16_t *out, int64_t ldo, void *workspace,
                      int64_t workspace_bytes, hipStream_t stream);
 
+/* w8a8_linear_bf16 without a workspace and without allocating anything.  No counterpart in the
+ * reference; it is for callers that cannot allocate device memory: code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc.  The packed int8 rows and the
+ * per-row scales go to a 64 MiB scratch array that the library holds on each GPU it runs on
+ * until the process ends, so align256(w8a8_packed_act_bytes(M, K)) + align256(4 * M) must not
+ * exceed 64 MiB (e.g. M = 8192 at K = 6144, M = 16384 at K = 2048): larger calls fail with
+ * W8A8_ENOTSUP before launching.  The same kernels and the same results as w8a8_linear_bf16.
+ * Every call on one GPU shares that scratch: calls that overlap in time on one GPU (two streams,
+ * two threads) race; calls ordered on one stream do not.  Nothing needs clearing between calls. */
+int w8a8_linear_bf16_noalloc(const uint16_t *x, int64_t ldx, const int8_t *w_packed, const float *sw, int64_t M,
+                             int64_t N, int64_t K, int epilogue, int64_t interleave, const uint16_t *res,
+                             int64_t ldr, const uint16_t *rms_w, float eps, uint16_t *out, int64_t ldo,
+                             hipStream_t stream);
+
 /* ---- decode GEMV (gemma_npu.py:155-172, torch._weight_int8pack_mm) ---------------------- */
 
 /* y[m, n] = bf16((sum_k x[m, k] * w[n, k]) * s[n]),  x bf16 [M, K] with 1 <= M <= 16,

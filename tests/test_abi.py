@@ -119,6 +119,24 @@ def test_errors_are_reported_without_launching():
     assert rc == _lib.W8A8_EINVAL
 
 
+def test_noalloc_linear_refuses_before_touching_the_device():
+    """The allocation-free linear checks its arguments and the size of its fixed scratch before
+    any HIP call, so the refusals are decided on the host."""
+    fake = ctypes.c_void_p(0x100000)
+    rc, msg = _status("w8a8_linear_bf16_noalloc", fake, 6144, fake, fake, 16384, 1536, 6144, 0, 0, None, 0, None,
+                      1e-6, fake, 1536, None)
+    assert rc == _lib.W8A8_ENOTSUP and "scratch" in msg and "64 MiB" in msg
+    rc, msg = _status("w8a8_linear_bf16_noalloc", fake, 100, fake, fake, 4, 64, 100, 0, 0, None, 0, None,
+                      1e-6, fake, 64, None)
+    assert rc == _lib.W8A8_ENOTSUP and "multiple of 16" in msg
+    rc, msg = _status("w8a8_linear_bf16_noalloc", fake, 64, fake, fake, 4, 64, 64, 3, 0, None, 0, None,
+                      1e-6, fake, 64, None)
+    assert rc == _lib.W8A8_EINVAL and "residual" in msg
+    rc, msg = _status("w8a8_linear_bf16_noalloc", fake, 64, fake, fake, 4, 64, 64, 7, 0, None, 0, None,
+                      1e-6, fake, 64, None)
+    assert rc == _lib.W8A8_EINVAL and "epilogue" in msg
+
+
 def test_python_layer_raises():
     import torch
     from w8a8 import ops
