@@ -126,8 +126,8 @@ int w8a8_gemm_tile_configs(void) { return gemm_config_count(); }
 
 int w8a8_gemm_pick_tile_config(int64_t M, int64_t N, int64_t K, int epilogue) {
   if (M <= 0 || N <= 0 || K <= 0 || M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) return -1;
-  if (epilogue < 0 || epilogue > 2) return -1;
-  const int epi = epilogue == 1 ? EPI_GELU : (epilogue == 2 ? EPI_RESID : EPI_BF16);
+  if (epilogue < -1 || epilogue > 2) return -1;
+  const int epi = epilogue == 1 ? EPI_GELU : (epilogue == 2 ? EPI_RESID : (epilogue == 0 ? EPI_BF16 : EPI_I32));
   return gemm_pick_config(int(M), int((N + 31) / 32 * 32), int(2 * ((K + 63) / 64)) * 32, epi);
 }
 

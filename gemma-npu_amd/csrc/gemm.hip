@@ -727,6 +727,267 @@ __global__ __launch_bounds__(NWN * 64, MINB) void gemm_dw_kernel(GemmParams p) {
   }
 }
 
+// ---- software-pipelined persistent kernel, one wave per SIMD ---------------------------------------
+// Four waves in a 2 x 2 grid, each owning a (BM/2) x (BN/2) quarter of the block tile as 32 x 32 MFMA
+// tiles (sixteen 16-register accumulators for 256 x 256, held in the accumulator registers).
+// k-tiles are 64 deep (two k-steps): the packed layouts pad K to 64, so every k-step of every
+// k-tile is live and the loop has no branches.  A and W fragments go HBM -> LDS by DMA into an
+// NS-slot ring, NS-1 k-tiles ahead of the multiply.  With one wave per SIMD nothing else fills a
+// gap in a wave's MFMA stream, so each LDS read and each DMA issue is placed right behind an MFMA
+// (sched_barrier fences fix the order) and issues while that MFMA runs.
+//
+// Persistent: block b multiplies the logical tiles xcd_remap(b) + i * gridDim.x, and the ring runs
+// as one stream of k-tiles across them (stream index g = i * KT + kt), so the first k-tiles of a
+// tile land while the previous tile's last k-tiles are multiplied and its epilogue stores go out.
+// Per k-tile:
+//   k-step 0: MFMAs on register set 0 (k-step 0 of g), reading k-step 1 of g into set 1;
+//   k-step 1: once set 1 has landed (so this wave reads slot g no more) and this wave's DMAs of
+//             g+1 have landed, one barrier; then MFMAs on set 1, reading k-step 0 of g+1 into
+//             set 0 and DMA-ing stream k-tile g+NS into the slot of g, which no wave reads again.
+// DMAs past the block's last k-tile go through a buffer resource with no records: they return
+// zeros and touch no memory, and every k-tile keeps the same count of loads in flight.
+template <int BM, int BN, int NS, int EPI, bool A_PACKED, int MINB>
+__global__ __launch_bounds__(256, MINB) void gemm_pipe_kernel(GemmParams p) {
+  constexpr int KS = 2, NW = 4;
+  constexpr int MT = BM / 32, NTB = BN / 32;
+  constexpr int WTM = MT / 2, WTN = NTB / 2;
+  constexpr int NQ = WTM * WTN;
+  constexpr int F = KS * (MT + NTB);
+  constexpr int FA = KS * MT / NW, FB = KS * NTB / NW, FW = FA + FB;
+  static_assert(FA * NW == KS * MT && FB * NW == KS * NTB, "each wave moves whole A and W fragments");
+  static_assert(FW * (NS - 1) < 64, "outstanding loads must fit the 6-bit vmcnt");
+  static_assert(NS >= 3, "one slot read, one landing, at least one in flight");
+  static_assert(EPI != EPI_GELU || WTN % 2 == 0, "GELU pairs need an even tile count per wave");
+  constexpr int NSCALE = EPI == EPI_I32 ? 0 : BM + BN;
+  constexpr int SCALE_PER_THREAD = NSCALE ? (NSCALE + 255) / 256 : 1;
+  constexpr int SLOT = F * 1024;
+  constexpr int RING = NS * SLOT;
+  __shared__ __attribute__((aligned(1024))) char lds[RING + NSCALE * 4];
+  float* const s_scale = reinterpret_cast<float*>(lds + RING);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int ntm = (p.M + BM - 1) / BM;
+  const int ntn = (p.NT + NTB - 1) / NTB;
+  const int ntiles = ntm * ntn;
+  const int G = int(gridDim.x);
+  const int r0 = xcd_remap(int(blockIdx.x), G);
+  const int my_tiles = r0 < ntiles ? (ntiles - 1 - r0) / G + 1 : 0;
+  const int KT = p.KF / KS;  // KF is even: K is padded to 64
+  const int total = my_tiles * KT;
+
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a, p.a_bytes);
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.wp, p.w_bytes);
+  const __amdgpu_buffer_rsrc_t ra_dead = make_rsrc(p.a, 0);
+  const __amdgpu_buffer_rsrc_t rw_dead = make_rsrc(p.wp, 0);
+
+  // First row and first 32-column tile of this block's tile i.
+  auto tile_origin = [&](int i, int& m0, int& t0) {
+    int tm, tn;
+    tile_coords(r0 + i * G, ntm, ntn, p.gm, tm, tn);
+    m0 = tm * BM;
+    t0 = tn * NTB;
+  };
+
+  // Lane parts of the DMA offsets (fragment f = i * NW + wave of a k-tile: A (s, mt) =
+  // (f / MT, f % MT), W (s, nt) = (f / NTB, f % NTB)); the tile and k-tile parts are uniform.
+  uint32_t la[FA], lw[FB];
+#pragma unroll
+  for (int i = 0; i < FA; ++i) {
+    const int f = i * NW + wave;
+    const int s = f / MT, mt = f % MT;
+    if constexpr (A_PACKED)
+      la[i] = (uint32_t(mt) * uint32_t(p.KF) + uint32_t(s)) * 1024u + uint32_t(lane) * 16u;
+    else
+      la[i] = uint32_t(mt * 32 + (lane & 31)) * uint32_t(p.lda) + uint32_t(s * 32 + (lane >> 5) * 16);
+  }
+#pragma unroll
+  for (int i = 0; i < FB; ++i) {
+    const int f = i * NW + wave;
+    const int s = f / NTB, nt = f % NTB;
+    lw[i] = (uint32_t(nt) * uint32_t(p.KF) + uint32_t(s)) * 1024u + uint32_t(lane) * 16u;
+  }
+  constexpr uint32_t A_STEP = A_PACKED ? KS * 1024u : KS * 32u;
+  constexpr uint32_t W_STEP = KS * 1024u;
+
+  // Uniform DMA state of stream k-tile h: its A / W base offsets and resources (dead past the end).
+  struct DmaBase {
+    uint32_t a, w;
+    __amdgpu_buffer_rsrc_t ra, rw;
+  };
+  auto dma_base = [&](int h) {
+    DmaBase d;
+    const bool live = h < total;
+    const int i = live ? h / KT : 0;
+    const int kk = live ? h - i * KT : 0;
+    int m0, t0;
+    tile_origin(i, m0, t0);
+    if constexpr (A_PACKED)
+      d.a = uint32_t(m0 / 32) * uint32_t(p.KF) * 1024u + uint32_t(kk) * A_STEP;
+    else
+      d.a = uint32_t(m0) * uint32_t(p.lda) + uint32_t(kk) * A_STEP;
+    d.w = uint32_t(t0) * uint32_t(p.KF) * 1024u + uint32_t(kk) * W_STEP;
+    d.ra = live ? ra : ra_dead;
+    d.rw = live ? rw : rw_dead;
+    return d;
+  };
+  // One DMA (fragment d < FA of A, else of W) of stream k-tile h into its ring slot.
+  auto dma_one = [&](int d, int h, const DmaBase& b) {
+    char* slot = lds + (h % NS) * SLOT;
+    if (d < FA)
+      dma16(b.ra, slot + (d * NW + wave) * 1024, la[d] + b.a);
+    else
+      dma16(b.rw, slot + (KS * MT + (d - FA) * NW + wave) * 1024, lw[d - FA] + b.w);
+  };
+  // One fragment read (r < WTN: W fragment r, else A fragment r - WTN) of k-step s of stream k-tile g.
+  auto read_one = [&](int r, int g, int s, v4i (&a)[WTM], v4i (&b)[WTN]) {
+    const char* slot = lds + (g % NS) * SLOT;
+    if (r < WTN)
+      b[r] = *reinterpret_cast<const v4i*>(slot + (KS * MT + s * NTB + wn * WTN + r) * 1024 + lane * 16);
+    else
+      a[r - WTN] = *reinterpret_cast<const v4i*>(slot + (s * MT + wm * WTM + r - WTN) * 1024 + lane * 16);
+  };
+
+  // This thread's per-row / per-column scales of tile i (fetched at the start of the tile's main
+  // loop, parked in LDS just before its epilogue).
+  float scale_v[SCALE_PER_THREAD];
+  auto fetch_scales = [&](int i) {
+    int m0, t0;
+    tile_origin(i, m0, t0);
+#pragma unroll
+    for (int u = 0; u < SCALE_PER_THREAD; ++u) {
+      scale_v[u] = 0.0f;
+      if constexpr (EPI != EPI_I32) {
+        const int e = int(threadIdx.x) + u * 256;
+        if (e < BM) {
+          if (m0 + e < p.M) scale_v[u] = p.sx[m0 + e];
+        } else if (e < BM + BN) {
+          const int pc = e - BM, tt = t0 + pc / 32;
+          if constexpr (EPI == EPI_GELU) {
+            const int c = (tt >> 1) * 32 + pc % 32;
+            if (c < p.I) scale_v[u] = p.sw[(tt & 1 ? p.I : 0) + c];
+          } else {
+            const int n = tt * 32 + pc % 32;
+            if (n < p.N) scale_v[u] = p.sw[n];
+          }
+        }
+      }
+    }
+  };
+
+  v16i acc[WTM][WTN];
+  auto zero_acc = [&]() {
+#pragma unroll
+    for (int i = 0; i < WTM; ++i)
+#pragma unroll
+      for (int j = 0; j < WTN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+  };
+  auto mma_one = [&](int q, const v4i (&a)[WTM], const v4i (&b)[WTN]) {
+    acc[q / WTN][q % WTN] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b[q % WTN], a[q / WTN], acc[q / WTN][q % WTN], 0, 0, 0);
+  };
+
+  constexpr int NR = WTM + WTN;          // fragment reads per k-step
+  constexpr int PRE = NQ >= 4 ? 2 : 1;   // MFMAs of k-step 1 issued before its barrier
+  static_assert(NR <= NQ, "k-step 0 places at most one read behind each MFMA");
+
+  if (my_tiles == 0) return;
+  fetch_scales(0);
+#pragma unroll
+  for (int h = 0; h < NS; ++h) {
+    const DmaBase b = dma_base(h);
+#pragma unroll
+    for (int d = 0; d < FW; ++d) dma_one(d, h, b);
+  }
+  wait_vmcnt<FW * (NS - 1)>();
+  __builtin_amdgcn_s_barrier();
+
+  v4i a0[WTM], b0[WTN], a1[WTM], b1[WTN];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) read_one(r, 0, 0, a0, b0);
+  const int lrow = lane & 31;
+  const int lcol = 4 * (lane >> 5);
+  int g = 0;  // stream k-tile
+  for (int it = 0; it < my_tiles; ++it) {
+    zero_acc();
+    for (int kt = 0; kt < KT; ++kt, ++g) {
+      // k-step 0: MFMA q on set 0, then read q of k-step 1 into set 1
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): set 0 has landed
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        mma_one(q, a0, b0);
+        __builtin_amdgcn_sched_barrier(0);
+        if (q < NR) read_one(q, g, 1, a1, b1);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // k-step 1: PRE MFMAs on set 1, the barrier, then the remaining MFMAs each followed by its
+      // share of the NR reads of k-step 0 of g+1 (into set 0) and the FW DMAs of g+NS.
+      const DmaBase nb = dma_base(g + NS);
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // set 1 has landed: this wave reads slot g no more
+#pragma unroll
+      for (int q = 0; q < PRE; ++q) {
+        mma_one(q, a1, b1);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      wait_vmcnt<FW * (NS - 2)>();  // this wave's part of g+1 has landed
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      constexpr int NOPS = NR + FW, SLOTS = NQ - PRE;
+#pragma unroll
+      for (int q = PRE; q < NQ; ++q) {
+        mma_one(q, a1, b1);
+        __builtin_amdgcn_sched_barrier(0);
+        const int lo = (q - PRE) * NOPS / SLOTS, hi = (q - PRE + 1) * NOPS / SLOTS;
+#pragma unroll
+        for (int o = 0; o < NOPS; ++o) {
+          if (o < lo || o >= hi) continue;
+          if (o < NR)
+            read_one(o, g + 1, 0, a0, b0);  // past the block's last k-tile: stale, never multiplied
+          else
+            dma_one(o - NR, g + NS, nb);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+
+    // ---- epilogue of tile it, while the next tile's first k-tiles land in the ring ----
+    int m0, t0;
+    tile_origin(it, m0, t0);
+    if constexpr (EPI != EPI_I32) {
+      // Every wave finished the previous epilogue's reads of s_scale long ago (KT barriers since).
+#pragma unroll
+      for (int u = 0; u < SCALE_PER_THREAD; ++u) {
+        const int e = int(threadIdx.x) + u * 256;
+        if (e < NSCALE) s_scale[e] = scale_v[u];
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < WTM; ++i) {
+      const int ml = (wm * WTM + i) * 32 + lrow;
+      const int m = m0 + ml;
+      if (m >= p.M) continue;
+      const float sxm = EPI == EPI_I32 ? 0.0f : s_scale[ml];
+      const float* swt = s_scale + (EPI == EPI_I32 ? 0 : BM) + wn * WTN * 32 + lcol;
+      if constexpr (EPI == EPI_GELU) {
+#pragma unroll
+        for (int j = 0; j < WTN; j += 2)
+          store_tile<EPI>(p, acc[i][j], &acc[i][j + 1], m, t0 + wn * WTN + j, lcol, sxm, swt + j * 32);
+      } else {
+#pragma unroll
+        for (int j = 0; j < WTN; ++j)
+          store_tile<EPI>(p, acc[i][j], nullptr, m, t0 + wn * WTN + j, lcol, sxm, swt + j * 32);
+      }
+    }
+    // The epilogue's loads and stores are behind the ring's DMAs in the count of loads in
+    // flight: drain them so the counts the main loop waits for hold again.
+    wait_vmcnt<0>();
+    if (it + 1 < my_tiles) fetch_scales(it + 1);
+  }
+}
+
 // ---- host-side launch ----------------------------------------------------------------------
 
 // Tile configurations: block tile BM x BN, waves (WGM x WGN, one wave per 32-multiple sub-tile),
@@ -775,10 +1036,20 @@ static constexpr DwCfg kDw[] = {
     {128, 4, 2, 8, 4, 2},  // 25: 128x256, k-tile 256, W 4 k-steps ahead, two blocks per CU
 };
 static constexpr int kNumDw = int(sizeof(kDw) / sizeof(kDw[0]));
-static_assert(kNumCfg == 23 && kNumDw == 3, "every configuration needs its case in gemm_launch");
+
+// Software-pipelined configurations (gemm_pipe_kernel), numbered after kDw: block tile BM x BN,
+// NS-slot ring of 64-deep k-tiles, blocks per CU the registers are budgeted for.
+struct PipeCfg {
+  int bm, bn, ns, minb;
+};
+static constexpr PipeCfg kPipe[] = {
+    {256, 256, 4, 1},  // 26: 128x128 per wave, 32 KiB slots, 128 KiB ring
+};
+static constexpr int kNumPipe = int(sizeof(kPipe) / sizeof(kPipe[0]));
+static_assert(kNumCfg == 23 && kNumDw == 3 && kNumPipe == 1, "every configuration needs its case in gemm_launch");
 static constexpr int64_t kCounterBytes = 4096;
 
-int gemm_config_count() { return kNumCfg + kNumDw; }
+int gemm_config_count() { return kNumCfg + kNumDw + kNumPipe; }
 
 // Split-K: blocks per output tile along K.  Explicit requests (req = n >= 1) split into at most
 // n parts, only when there are few output tiles.  Automatic selection (req = 0) splits the
@@ -803,7 +1074,7 @@ static int pick_splits(int tiles, int KT, int ks, int req, int& kps, int kw = 1)
 // Split-K workspace: kCounterBytes of arrival counters (one int per output tile; zero before
 // and after every call) followed by the partial sums (scratch).
 int64_t gemm_workspace_bytes(int M, int NP, int KF, int cfg, int split_k) {
-  if (cfg >= kNumCfg) return 0;  // direct-W kernels never split K across blocks
+  if (cfg >= kNumCfg) return 0;  // direct-W and pipelined kernels never split K across blocks
   const TileCfg& c = kCfg[cfg];
   const int ntm = (M + c.bm - 1) / c.bm, ntn = (NP + c.bn - 1) / c.bn;
   int kps;
@@ -905,6 +1176,41 @@ static void launch_dw(const GemmParams& p, int epi, bool a_packed, hipStream_t s
     launch_dw_epi<c.bm, c.nwn, c.wtn, c.ks, c.pw, c.minb, false>(p, epi, stream);
 }
 
+// Blocks of the persistent kernels: one per CU per block the registers allow, at most one per tile.
+static int persistent_blocks(int tiles, int per_cu) {
+  static int cus = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    return n;
+  }();
+  return min(tiles, cus * per_cu);
+}
+
+template <int BM, int BN, int NS, int MINB, bool AP>
+static void launch_pipe_epi(GemmParams p, int epi, hipStream_t stream) {
+  const int ntm = (p.M + BM - 1) / BM;
+  const int ntn = (p.NT * 32 + BN - 1) / BN;
+  p.gm = min(ntm, BM >= BN ? 4 : 8);
+  p.splits = 1;
+  const dim3 grid{unsigned(persistent_blocks(ntm * ntn, MINB))};
+  switch (epi) {
+    case EPI_I32: gemm_pipe_kernel<BM, BN, NS, EPI_I32, AP, MINB><<<grid, 256, 0, stream>>>(p); break;
+    case EPI_BF16: gemm_pipe_kernel<BM, BN, NS, EPI_BF16, AP, MINB><<<grid, 256, 0, stream>>>(p); break;
+    case EPI_GELU: gemm_pipe_kernel<BM, BN, NS, EPI_GELU, AP, MINB><<<grid, 256, 0, stream>>>(p); break;
+    case EPI_RESID: gemm_pipe_kernel<BM, BN, NS, EPI_RESID, AP, MINB><<<grid, 256, 0, stream>>>(p); break;
+  }
+}
+
+template <int D>
+static void launch_pipe(const GemmParams& p, int epi, bool a_packed, hipStream_t stream) {
+  constexpr PipeCfg c = kPipe[D];
+  if (a_packed)
+    launch_pipe_epi<c.bm, c.bn, c.ns, c.minb, true>(p, epi, stream);
+  else
+    launch_pipe_epi<c.bm, c.bn, c.ns, c.minb, false>(p, epi, stream);
+}
+
 // Tile choice, from timing every configuration with the bf16 epilogues on the E2B prefill
 // shapes (M = 512, 3658, 16384).  At one 512-row micro-batch the GEMMs are bound by how fast
 // each CU streams its operands, so small tiles that spread the work over more CUs win: 64x128
@@ -934,7 +1240,10 @@ static void launch_dw(const GemmParams& p, int epi, bool a_packed, hipStream_t s
 // itself, with a distinct weight per layer: there the 256-row tiles' halved weight reads decide
 // (gate/up 92 us in the sequence against 98 us on 128x256), while one GEMM repeated on a
 // cache-resident weight favours 128x256 (92 against 108 us); the direct-W tiles change the sweep
-// by less than 1% there.
+// by less than 1% there.  The wide int32 GEMMs (N >= 8192) past one micro-batch take the
+// software-pipelined persistent 256x256 kernel (26): gate/up at M = 16384 393 against 440 us, the
+// 141-GEMM sweep 6.92 -> 6.78 ms at M = 3658 and 7.64 -> 7.31 ms at M = 4096.  It is tried for
+// int32 only: its bf16 epilogues run on one wave per SIMD and lose to the two-blocks-per-CU tiles.
 int gemm_pick_config(int M, int NP, int K, int epi) {
   if (M <= 1024) {
     if (K >= 2048 && NP <= 4096) return 22;  // few 64x64 tiles, long K: four waves split the k-steps
@@ -944,9 +1253,10 @@ int gemm_pick_config(int M, int NP, int K, int epi) {
   if (epi == EPI_GELU) return 25;  // direct-W 128x256, two blocks per CU
   if (M <= 8192) {
     if (K >= 4096 && NP <= 2048) return 24;  // long-K narrow (down): direct-W 128x256
-    return NP >= 8192 ? 0 : 12;
+    if (NP >= 8192) return epi == EPI_I32 ? 26 : 0;  // wide: pipelined persistent 256x256
+    return 12;
   }
-  return 25;
+  return NP >= 8192 && epi == EPI_I32 ? 26 : 25;
 }
 
 int gemm_launch(const GemmParams& p, int epi, int cfg, bool a_packed, void* ws, int64_t ws_bytes,
@@ -979,6 +1289,7 @@ int gemm_launch(const GemmParams& p, int epi, int cfg, bool a_packed, void* ws, 
     case 23: launch_dw<0>(p, epi, a_packed, stream); break;
     case 24: launch_dw<1>(p, epi, a_packed, stream); break;
     case 25: launch_dw<2>(p, epi, a_packed, stream); break;
+    case 26: launch_pipe<0>(p, epi, a_packed, stream); break;
     default: return fail(W8A8_EINVAL, "gemm: unknown tile config %d", cfg);
   }
   return check_launch("gemm");

@@ -129,8 +129,9 @@ int w8a8_quant_rows_packed_bf16(const uint16_t *x, int64_t ldx, int64_t M, int64
 /* Number of explicit tile configurations the _ex GEMMs accept (tile_cfg 0 .. n-1). */
 int w8a8_gemm_tile_configs(void);
 
-/* The tile configuration the automatic choice (tile_cfg = -1) takes for [M, N, K] with
- * epilogue 0 (int32 out or dequant), 1 (GELU) or 2 (residual); -1 for an invalid shape.  No
+/* The tile configuration the automatic choice (tile_cfg = -1) takes for [M, N, K] with int32
+ * output (epilogue -1) or the bf16 epilogue 0 (dequant), 1 (GELU) or 2 (residual); -1 for an
+ * invalid shape or epilogue.  No
  * counterpart in the reference (its single Triton kernel has one schedule, npu_kernels.py:29-37);
  * for tests and benchmarks that report which kernel ran. */
 int w8a8_gemm_pick_tile_config(int64_t M, int64_t N, int64_t K, int epilogue);

@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
     missing = [n for n in declared_functions() if not hasattr(L, n)]
     assert not missing, f"not exported: {missing}"
     assert L.w8a8_abi_version() == 1
-    assert L.w8a8_gemm_tile_configs() == 26
+    assert L.w8a8_gemm_tile_configs() == 27
 
 
 def test_pick_tile_config_is_a_valid_configuration():
@@ -41,12 +41,13 @@ def test_pick_tile_config_is_a_valid_configuration():
               (1536, 24576)]
     for M in (1, 77, 512, 3658, 4096, 16384):
         for K, N in shapes:
-            for epi in (0, 1, 2):
+            for epi in (-1, 0, 1, 2):
                 cfg = L.w8a8_gemm_pick_tile_config(M, N, K, epi)
                 assert 0 <= cfg < n, (M, N, K, epi, cfg)
     assert L.w8a8_gemm_pick_tile_config(512, 12288, 1536, 1) != L.w8a8_gemm_pick_tile_config(3658, 12288, 1536, 1)
     assert L.w8a8_gemm_pick_tile_config(0, 64, 64, 0) == -1
     assert L.w8a8_gemm_pick_tile_config(64, 64, 64, 3) == -1
+    assert L.w8a8_gemm_pick_tile_config(64, 64, 64, -2) == -1
 
 
 def test_packed_weight_bytes():
@@ -77,7 +78,8 @@ def test_linear_workspace_bytes():
     assert L.w8a8_gemm_workspace_bytes(512, 1536, 6144, 19, 4) == 0
     assert L.w8a8_gemm_workspace_bytes(512, 1536, 6144, 22, 4) == 0
     assert L.w8a8_gemm_workspace_bytes(3658, 1536, 6144, 24, 4) == 0       # direct-W: never split
-    assert L.w8a8_gemm_workspace_bytes(3658, 1536, 6144, 26, 0) == -1      # past the last configuration
+    assert L.w8a8_gemm_workspace_bytes(3658, 12288, 1536, 26, 4) == 0      # pipelined: never split
+    assert L.w8a8_gemm_workspace_bytes(3658, 1536, 6144, 27, 0) == -1      # past the last configuration
     assert L.w8a8_linear_workspace_bytes(512, 1536, 6144) == 4096 + 512 * 6144 + 512 * 4
     assert L.w8a8_linear_workspace_bytes(512, 1536, 2048) == 4096 + 512 * 2048 + 512 * 4
     assert L.w8a8_linear_workspace_bytes(3, 64, 64) == 4096 + 32 * 64 + 256  # counters kept; rows to 32

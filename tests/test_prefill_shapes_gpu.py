@@ -91,7 +91,7 @@ def _sweep_inputs(M, K, N, layer, gi):
 def test_sweep_gemm_at_prefill_length(name, M):
     K, N, gi = SWEEP[name]
     layers = (0, 34) if name != "ple_proj" else (-1,)
-    cfg = lib().w8a8_gemm_pick_tile_config(M, N, K, 0)
+    cfg = lib().w8a8_gemm_pick_tile_config(M, N, K, -1)
     for layer in layers:
         pa, q, w = _sweep_inputs(M, K, N, layer, gi)
         c = ops.gemm_i32(pa, ops.pack_weight(w, "nk"))
@@ -132,7 +132,7 @@ def test_stress_m16384_int32(name, stress_inputs):
     q_ref, sx_ref = orc.quant_rows(to_bits(x[rows]), "bf16")
     assert np.array_equal(q[rows.to(DEV)].cpu().numpy(), q_ref), "quant prologue differs from the oracle"
     assert np.array_equal(sx[rows.to(DEV)].cpu().numpy(), sx_ref)
-    cfg = lib().w8a8_gemm_pick_tile_config(M, N, K, 0)
+    cfg = lib().w8a8_gemm_pick_tile_config(M, N, K, -1)
     c = ops.gemm_i32(pa, ops.pack_weight(wd, "nk"))
     ref = torch._int_mm(q, wd.t())
     assert torch.equal(c, ref), f"{name} M={M} tile {cfg}: {(c != ref).sum().item()} mismatches"
