@@ -187,6 +187,105 @@ def cpu_int_mm_ms(shapes, M, warm=3, reps=5, budget_s=None):
     return {s: statistics.median(v) * 1e3 for s, v in ts.items()}, rounds
 
 
+TILE_NAMES = {
+    12: "gemm_kernel 64x128 tiles, three blocks per CU",
+    14: "gemm_kernel 64x64 tiles, two waves",
+    22: "gemm_kernel 64x64 tiles with 4-wave split-K, 512-deep k-tiles",
+    0: "gemm_kernel 256x256 tiles, 8 waves",
+    23: "gemm_dw_kernel (direct-W) 64x256 tiles, two blocks per CU",
+    24: "gemm_dw_kernel (direct-W) 128x256 tiles, W 8 k-steps ahead",
+    25: "gemm_dw_kernel (direct-W) 128x256 tiles, two blocks per CU",
+    26: "gemm_pipe_kernel (software-pipelined, persistent) 256x256 tiles",
+}
+
+
+def tile_name(cfg):
+    return TILE_NAMES.get(cfg, f"tile configuration {cfg}")
+
+
+def cpu_identity():
+    """nproc, the CPU model string and the int8 / bf16 matrix ISA flags of the host (Linux)."""
+    model, flags = "unknown", set()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name") and model == "unknown":
+                    model = line.split(":", 1)[1].strip()
+                elif line.startswith("flags") and not flags:
+                    flags = set(line.split(":", 1)[1].split())
+    except OSError:
+        pass
+    isa = [x for x in ("amx_int8", "amx_bf16", "avx512_vnni", "avx_vnni", "avx512_bf16", "avx512f") if x in flags]
+    return {"nproc": os.cpu_count(), "cpu_model": model, "isa": isa}
+
+
+def cpu_gemv_ms(M, K, N, warm=3, reps=5, seed=5):
+    """Median ms of torch._weight_int8pack_mm on the host (the reference's decode linear and int8
+    LM head, gemma_npu.py:155-156): x bf16 [M, K], w int8 [N, K], bf16 per-channel scales."""
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    s = (torch.rand(N, generator=g) * 0.015 + 0.005).to(torch.bfloat16)
+    for _ in range(warm):
+        torch._weight_int8pack_mm(x, w, s)
+    ts = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        torch._weight_int8pack_mm(x, w, s)
+        ts.append(time.perf_counter() - t)
+    return statistics.median(ts) * 1e3
+
+
+def gemv_layers(dev, reps, cpu=True):
+    """Decode GEMVs of one E2B-class layer's linears (qkv, o, gate_up, down) at M = 1 / 4 / 16, int8
+    weights in the GEMV fragment layout, bf16 scales as the reference's decode copy (gemma_npu.py:82):
+      hot   each shape alone, the same weight replayed from one graph (it stays in the 256 MB MALL);
+      cold  one decode token's linears: 35 layers x 4 groups with distinct weights (1.24 GB, five
+            times the MALL) back to back, as the decode loop streams them.
+    Bytes per GEMV = K*N + 2N + 2MK + 2MN; the host leg is torch._weight_int8pack_mm per shape."""
+    import torch
+    from w8a8 import ops, workloads
+    out = {}
+    groups = list(workloads.LAYER_GROUPS.items())
+    layers = []
+    for layer in range(workloads.N_LAYERS):
+        row = []
+        for gi, (name, (K, N, _)) in enumerate(groups):
+            g = torch.Generator(device=dev).manual_seed(workloads.layer_seed(layer, gi))
+            w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8, device=dev)
+            s = (torch.rand(N, generator=g, device=dev) * 0.015 + 0.005).to(torch.bfloat16)
+            row.append((name, K, N, ops.pack_gemv_weight(w), s))
+            del w
+        layers.append(row)
+    for M in (1, 4, 16):
+        xs = {K: workloads.activations(M, K, seed=K, outliers=False).to(dev) for _, (K, _, _) in groups}
+        ys = {N: torch.empty((M, N), dtype=torch.bfloat16, device=dev) for _, (_, N, _) in groups}
+        entry = {}
+        for name, K, N, pw, s in layers[0]:
+            ms = graph_time_ms(lambda: ops.gemv_bf16(xs[K], pw, s, ys[N]), dev)
+            nbytes = K * N + 2 * N + 2 * M * K + 2 * M * N
+            e = {"us": round(ms * 1e3, 2), "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1), "bytes": nbytes}
+            if cpu:
+                cms = cpu_gemv_ms(M, K, N)
+                e["cpu_us"] = round(cms * 1e3, 1)
+                e["speedup_vs_cpu"] = round(cms / ms, 1)
+            entry[name] = e
+
+        def token():
+            for row in layers:
+                for name, K, N, pw, s in row:
+                    ops.gemv_bf16(xs[K], pw, s, ys[N])
+        ms = event_time_ms(token, reps, 2)
+        nbytes = sum(K * N + 2 * N + 2 * M * K + 2 * M * N for row in layers for _, K, N, _, _ in row)
+        entry["cold_token_all_layers"] = {
+            "us": round(ms * 1e3, 1), "gemvs": 4 * len(layers), "bytes": nbytes,
+            "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1), "frac_hbm": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+        out[f"m{M}"] = entry
+        log(f"bench: decode layer GEMVs M={M}: {entry}")
+    return out
+
+
 def sweep(M, dev, reps):
     """All prefill GEMMs of one prompt: 35 layers x 4 groups + the PLE projection, int8 A ->
     int32 C (the reference's NPU launches, gemma_npu.py:99-115), distinct weights per layer."""
@@ -211,7 +310,7 @@ def sweep(M, dev, reps):
     ms = event_time_ms(run, reps, 2)
     total_ops = sum(workloads.gemm_ops(M, N, K) for _, _, _, K, N in shapes)
     wbytes = sum(K * N for _, _, _, K, N in shapes)
-    return ms, total_ops, wbytes, [(K, N) for _, _, _, K, N in shapes]
+    return ms, total_ops, wbytes, [(K, N) for _, _, _, K, N in shapes], run
 
 
 def gemv_bench(M, K, N, dev, reps, seed=5):
@@ -572,9 +671,9 @@ def main():
     ap.add_argument("--profile-kernel", action="store_true",
                     help="for counter collection: launch only the dominant GEMM (eager, --steps times) and a "
                          "64 MiB device copy that calibrates the byte counters, then exit")
-    ap.add_argument("--profile-gemm", metavar="M,K,N,EPI",
-                    help="for counter collection: launch one bf16-out GEMM of that shape (EPI none / gelu / residual; "
-                         "random data, the automatic tile) --steps times, then exit")
+    ap.add_argument("--profile-gemm", metavar="M,K,N,EPI[,TILE]",
+                    help="for counter collection: launch one GEMM of that shape (EPI i32 / none / gelu / residual; "
+                         "random data, the automatic tile or configuration TILE) --steps times, then exit")
     ap.add_argument("--profile-gemv", action="store_true",
                     help="for kernel traces / counters: run the packed LM-head GEMV at M=1 (--steps times) and a "
                          "64 MiB device copy that calibrates the byte counters, then exit")
@@ -590,6 +689,9 @@ def main():
     ap.add_argument("--profile-decode", action="store_true",
                     help="for kernel traces: decode attention at the end of the 3658-token prompt for each layer "
                          "kind (--steps calls each, eager) and exit")
+    ap.add_argument("--profile-sweep", action="store_true",
+                    help="for kernel traces: run the 141-GEMM int32 prefill sweep at M=3658 (--steps + 2 times) "
+                         "and exit")
     ap.add_argument("--profile-chain", action="store_true",
                     help="for kernel traces: run the device layer chain (--steps times, eager) and exit")
     args = ap.parse_args()
@@ -599,11 +701,16 @@ def main():
         return 2
 
     import torch
-    from w8a8 import ops, workloads
+    from w8a8 import lib, ops, workloads
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     M = 512
+    if args.profile_sweep:
+        for Ms in (3658,):
+            sweep(Ms, dev, reps=args.steps)
+        log(f"bench: ran the 141-GEMM int32 prefill sweep at M=3658 {args.steps} + 2 times")
+        return 0
     if args.profile_gemv:
         K, N = workloads.LM_HEAD
         x = workloads.activations(1, K, seed=5, outliers=False).to(dev)
@@ -633,20 +740,27 @@ def main():
         log(f"bench: ran the E2B-shaped model: prefill of {ATTN_T} tokens, {args.steps} decode tokens")
         return 0
     if args.profile_gemm:
-        Mg, Kg, Ng, epi = args.profile_gemm.split(",")
-        Mg, Kg, Ng = int(Mg), int(Kg), int(Ng)
-        if epi not in ("none", "gelu", "residual"):
-            raise SystemExit(f"--profile-gemm: epilogue {epi!r} is not none, gelu or residual")
+        fields = args.profile_gemm.split(",")
+        Mg, Kg, Ng, epi = int(fields[0]), int(fields[1]), int(fields[2]), fields[3]
+        tile = int(fields[4]) if len(fields) > 4 else -1
+        if epi not in ("i32", "none", "gelu", "residual"):
+            raise SystemExit(f"--profile-gemm: epilogue {epi!r} is not i32, none, gelu or residual")
         x = workloads.activations(Mg, Kg, seed=9).to(dev)
         q, sx = ops.quant_rows_packed(x)
         w, sw = workloads.weights(Ng, Kg, seed=10)
         pw = ops.pack_weight(w.to(dev), "nk", Ng // 2 if epi == "gelu" else 0, sw=sw.to(dev))
+        del w
         res = workloads.activations(Mg, Ng, seed=11, outliers=False).to(dev) if epi == "residual" else None
-        out = torch.empty((Mg, Ng // 2 if epi == "gelu" else Ng), dtype=torch.bfloat16, device=dev)
-        for _ in range(args.steps):
-            ops.gemm_bf16(q, sx, pw, epilogue=epi, residual=res, out=out)
+        if epi == "i32":
+            out = torch.empty((Mg, Ng), dtype=torch.int32, device=dev)
+            for _ in range(args.steps):
+                ops.gemm_i32(q, pw, out, tile_cfg=tile)
+        else:
+            out = torch.empty((Mg, Ng // 2 if epi == "gelu" else Ng), dtype=torch.bfloat16, device=dev)
+            for _ in range(args.steps):
+                ops.gemm_bf16(q, sx, pw, epilogue=epi, residual=res, out=out, tile_cfg=tile)
         torch.cuda.synchronize()
-        log(f"bench: ran the {epi} GEMM M={Mg} K={Kg} N={Ng} {args.steps} times")
+        log(f"bench: ran the {epi} GEMM M={Mg} K={Kg} N={Ng} (tile {tile}) {args.steps} times")
         return 0
     if args.profile_pipeline:
         from w8a8.pipeline import Prefill
@@ -739,6 +853,7 @@ def main():
             lambda g=g: ops.gemm_bf16(g["q"], g["sx"], g["pw"], epilogue=g["epi"], residual=g["res"],
                                       out=g["out"]), dev)
     gu_ops = workloads.gemm_ops(M, gu["N"], gu["K"])
+    gu_cfg = lib().w8a8_gemm_pick_tile_config(M, gu["N"], gu["K"], 1)
     gu_ms = per_ms["gate_up"]
     achieved = gu_ops / (gu_ms * 1e-3) / 1e12
     traffic = read_traffic()
@@ -746,7 +861,7 @@ def main():
     peak_at_clock = 256 * 8192 * clock / 1e3  # TOP/s: 256 CUs x 8192 int8 op/clk/CU at the measured clock
     roofline = {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": traffic,
-                "kernel": "gemm_dw_kernel<EPI_GELU> (direct-W 64x256 tiles) gate_up M=512 K=1536 N=12288, packed A",
+                "kernel": f"{tile_name(gu_cfg)} gate_up M=512 K=1536 N=12288 with the GELU epilogue, packed A",
                 "avg_launch_us": round(gu_ms * 1e3, 2), "clock_ghz": round(clock, 3),
                 "frac_at_clock": round(achieved / peak_at_clock, 4)}
     log(f"bench: gate_up runs at {clock:.3f} GHz: {achieved:.0f} TOP/s = {achieved / peak_at_clock:.3f} of the "
@@ -760,7 +875,7 @@ def main():
         cm, rounds = cpu_int_mm_ms([(g["K"], g["N"]) for g in groups], M, budget_s=10.0)
         cpu_ms = sum(cm.values())
         cpu = {"value": round(step_ops / (cpu_ms * 1e-3) / 1e12, 3), "unit": "TOP/s",
-               "cores": torch.get_num_threads(), "kind": "reference",
+               "cores": torch.get_num_threads(), "kind": "reference", **cpu_identity(),
                "sample": f"torch._int_mm (the reference's --backend cpu-int8 GEMM, pipeline.py:237) on the same "
                          f"layer's 4 GEMMs at M={M} (int8 in, int32 out): 3 warm-up calls each, then {rounds} "
                          f"rounds over the 4 (~10 s), median per GEMM summed: {cpu_ms:.1f} ms per layer"}
@@ -770,14 +885,21 @@ def main():
              "gemm_us_m512": {k: round(v * 1e3, 2) for k, v in per_ms.items()}}
     if not args.no_extra:
         for Ms in (3658, 4096):
-            ms, tops_ops, wbytes, shp = sweep(Ms, dev, reps=5)
-            entry = {"ms": round(ms, 3), "gemms": len(shp), "tops": round(tops_ops / (ms * 1e-3) / 1e12, 1),
-                     "frac_mfma": round(tops_ops / (ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4)}
+            ms, tops_ops, wbytes, shp, run = sweep(Ms, dev, reps=5)
+            tops = tops_ops / (ms * 1e-3) / 1e12
+            clk = clock_during(run, dev, launches=2, window_ms=4.0)
+            entry = {"ms": round(ms, 3), "gemms": len(shp), "tops": round(tops, 1),
+                     "frac_mfma": round(tops / PEAK_INT8_TOPS, 4), "clock_ghz": round(clk, 3),
+                     "frac_at_clock": round(tops / (256 * 8192 * clk / 1e3), 4),
+                     "weights": f"cold: {wbytes / 1e9:.2f} GB of distinct per-layer weights, int32 out"}
             if not args.no_cpu and Ms == 3658:
                 uniq = sorted(set(shp))
-                cm, _ = cpu_int_mm_ms(uniq, Ms, warm=2, reps=3)
+                cm, _ = cpu_int_mm_ms(uniq, Ms, warm=3, reps=5)
                 cpu_total = sum(cm[s] for s in shp)
                 entry["cpu_int_mm_ms"] = round(cpu_total, 1)
+                entry["cpu"] = dict(cpu_identity(), threads=torch.get_num_threads(),
+                                    sample="torch._int_mm per distinct shape, 3 warm-up calls then the median of 5, "
+                                           "summed over the 141 GEMMs")
                 entry["speedup_vs_cpu"] = round(cpu_total / ms, 1)
             extra[f"prefill_sweep_m{Ms}"] = entry
             log(f"bench: sweep M={Ms}: {entry}")
@@ -812,12 +934,18 @@ def main():
             K, N = workloads.LM_HEAD
             ms_rm, ms, nbytes = gemv_bench(Mg, K, N, dev, reps=50)
             gbs = nbytes / (ms * 1e-3) / 1e9
-            extra[f"gemv_lm_head_m{Mg}"] = {"us": round(ms * 1e3, 1), "gbs": round(gbs, 1),
-                                            "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
-                                            "weight": "GEMV fragment layout (w8a8_pack_gemv_weight)",
-                                            "row_major_us": round(ms_rm * 1e3, 1),
-                                            "row_major_gbs": round(nbytes / (ms_rm * 1e-3) / 1e9, 1)}
-            log(f"bench: gemv lm head M={Mg}: {extra[f'gemv_lm_head_m{Mg}']}")
+            entry = {"us": round(ms * 1e3, 1), "gbs": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+                     "weight": "GEMV fragment layout (w8a8_pack_gemv_weight); cold: 403 MB, more than the 256 MB MALL",
+                     "row_major_us": round(ms_rm * 1e3, 1),
+                     "row_major_gbs": round(nbytes / (ms_rm * 1e-3) / 1e9, 1)}
+            if not args.no_cpu:
+                cms = cpu_gemv_ms(Mg, K, N)
+                entry.update(cpu_us=round(cms * 1e3, 1), cpu_gbs=round(nbytes / (cms * 1e-3) / 1e9, 1),
+                             speedup_vs_cpu=round(cms / ms, 1))
+            extra[f"gemv_lm_head_m{Mg}"] = entry
+            log(f"bench: gemv lm head M={Mg}: {entry}")
+        torch.cuda.empty_cache()
+        extra["gemv_decode_layers"] = gemv_layers(dev, reps=10, cpu=not args.no_cpu)
         torch.cuda.empty_cache()
         extra["attention_prefill_t3658"] = attention_bench(dev, reps=20, cpu=not args.no_cpu)
         log(f"bench: attention: {extra['attention_prefill_t3658']}")
@@ -836,7 +964,9 @@ def main():
                                  "int8 U[-127,127] weights)",
         "config": {"workload": "one E2B-class decoder layer's prefill linears, M=512 micro-batch, bf16 in -> bf16 "
                                "out with fused per-token quant and dequant/GELU/residual epilogues",
-                   "M": M, "groups": {g["name"]: [g["K"], g["N"], g["epi"]] for g in groups}},
+                   "M": M, "groups": {g["name"]: [g["K"], g["N"], g["epi"]] for g in groups},
+                   "weights": "hot: the step's 31.5 MB of packed weights are reused every step and stay in "
+                              "the 256 MB MALL (the sweep's 1.25 GB and the LM head's 403 MB are cold)"},
         "roofline": roofline, "cpu_baseline": cpu, "extra": extra,
     }
     print(json.dumps(line), flush=True)
