@@ -1,24 +1,30 @@
 """HF transformers' Gemma 4 text decoder on the GPU with this engine underneath.
 
-The reference swaps the decoder's linears for grouped W8A8 GEMMs (`to_npu`, gemma_npu.py:208-241,
-with `NPUGemm`, gemma_npu.py:57-152, and `Slice`, gemma_npu.py:175-193), the LM head for an int8
-GEMV (`Int8Head`, gemma_npu.py:159-172), and registers its attention as "local_sdpa"
-(gemma_npu.py:253, local_attn.py:110-111).  `to_gpu` does the same on a model whose weights are on
-the GPU:
+What the reference does to the model on its NPU path -- its linears become grouped W8A8 GEMMs
+(gemma_npu.py:57-152, 175-241), the LM head an int8 GEMV (gemma_npu.py:159-172), attention the
+registered "local_sdpa" (gemma_npu.py:253, local_attn.py:110-111) -- `to_gpu` does on a model whose
+weights are on the GPU:
 
     model = AutoModelForCausalLM.from_pretrained(...).to("cuda")      # or a random-init config
     hf.to_gpu(model)
     out = model(input_ids=ids, use_cache=True, logits_to_keep=1)      # prefill: W8A8 GEMMs
     out = model(input_ids=nxt, past_key_values=out.past_key_values)   # decode: int8 GEMVs
 
-Groups as the reference forms them: [q; k; v] (q only on KV-shared layers), o, [gate; up], down,
-the per-layer-input gate and projection, and the per-layer model projection.  Rows < 16 (decode)
-take the weight-only int8 GEMV with bf16 scales (gemma_npu.py:120-121); more rows take per-token
-quant -> int8 GEMM -> dequant (gemma_npu.py:123-152).  Unlike the reference, the small PLE gate and
-projection stay on the GPU too.  Every RMSNorm module of the text decoder becomes one launch of the
-engine's row kernel (GpuRMSNorm), and for prefill rows each MLP's GELU-tanh * up runs in the gate/up
-GEMM's epilogue (GpuMLP); the other HF modules around them (RoPE, residuals, the KV cache, the decode
-loop) run unchanged, as torch ops on the GPU.
+Linears that read the same input share one quantized weight ([q; k; v] -- q alone on KV-shared
+layers --, [gate; up]), as the reference groups them (gemma_npu.py:213-224); o, down, the per-layer
+input gate and projection and the per-layer model projection are groups of one.  Each original
+linear is replaced by a QuantizedLinear, a view of its group's output columns.  The group's
+output is computed once per input:
+  * attention: a forward pre-hook on the attention module runs the [q; k; v] GEMM on the module's
+    hidden states and parks each projection's columns on it; the projections return them, and a
+    forward hook drops them when the module returns;
+  * MLP: GpuMLP runs the [gate; up] weight in one launch itself -- for prefill rows with
+    gelu_tanh(gate) * up in the GEMM's epilogue (k_gelu's arithmetic, pipeline.py:102-107), for
+    decode rows as one GEMV followed by the module's own activation.
+Rows < 16 (decode) take the weight-only int8 GEMV with bf16 scales (gemma_npu.py:120-121), more
+rows per-token quant -> int8 GEMM -> dequant (gemma_npu.py:123-152).  Every RMSNorm module becomes
+one launch of the engine's row kernel (GpuRMSNorm).  RoPE, residuals, the KV cache and the decode
+loop stay HF's own torch ops on the GPU.
 """
 import torch
 
@@ -27,76 +33,110 @@ from . import attention, ops
 DECODE_ROWS = 16  # rows below this go to the GEMV (gemma_npu.py:120)
 
 
-class GpuGemm(torch.nn.Module):
-    """One group of linears sharing an input, as one weight [sum of N, K] (gemma_npu.py:57-84):
-    per-channel int8 quantisation (absmax / 127), packed for the GEMM (fp32 scales) and for the
-    GEMV (bf16 scales, the reference's decode copy w_cpu / sw_cpu, gemma_npu.py:81-82)."""
+class QuantizedWeight:
+    """The weights of linears that read one input, stacked along N into [sum N_i, K] and quantized
+    per output channel once (absmax / 127, gemma_npu.py:68-69).
 
-    def __init__(self, linears, gelu_pair=False):
-        super().__init__()
-        w = torch.cat([l.weight.detach() for l in linears], 0)
+    Kept in the forms its callers read: `packed` (the GEMM's fragment layout, fp32 scales `sw`) for
+    prefill rows, `gemv_w` / `sw_bf16` (the GEMV's layout and bf16 scales, the reference's decode copy,
+    gemma_npu.py:81-82) for decode rows, and for a [gate; up] pair `packed_gelu`, packed for the GEMM's
+    fused GELU epilogue.  With gemm=False only the GEMV form exists (the LM head) and every row goes
+    through it, 16 rows per launch.  The plain GEMM packing of a [gate; up] pair is made on first
+    use: the fused path does not need it."""
+
+    def __init__(self, weights, gemm=True, gelu_pair=False):
+        w = torch.cat([t.detach() for t in weights], 0)
         if w.device.type != "cuda":
             raise ValueError("to_gpu: move the model to the GPU first")
         self.N, self.K = w.shape
-        self.sizes = [l.out_features for l in linears]
+        self.sizes = [t.shape[0] for t in weights]
         self.dtype = w.dtype
         q, sw = ops.quant_rows(w.float().contiguous())
-        self.sw = sw
-        self.packed = ops.pack_weight(q, "nk", sw=sw)
-        # [gate; up]: a second copy packed for the GEMM's fused gelu(gate) * up epilogue, which the
-        # whole-prompt pipeline uses in place of the int32 result and k_gelu
-        self.packed_gelu = ops.pack_weight(q, "nk", self.N // 2, sw=sw) if gelu_pair else None
+        del w
+        self.sw, self.sw_bf16 = sw, sw.to(torch.bfloat16)
         self.gemv_w = ops.pack_gemv_weight(q)
-        self.sw_bf16 = sw.to(torch.bfloat16)
-        self.pending = None
+        self.has_gemm = bool(gemm)
+        self._q = q if (gemm and gelu_pair) else None  # kept until the plain packing is asked for
+        self._packed = ops.pack_weight(q, "nk", sw=sw) if (gemm and not gelu_pair) else None
+        self.packed_gelu = ops.pack_weight(q, "nk", self.N // 2, sw=sw) if (gemm and gelu_pair) else None
+        self.name = ""
 
-    def matmul(self, x2d):
+    @property
+    def packed(self):
+        if self._packed is None:
+            if not self.has_gemm:
+                raise AttributeError("this weight is kept for the GEMV only")
+            self._packed = ops.pack_weight(self._q, "nk", sw=self.sw)
+            self._q = None
+        return self._packed
+
+    def apply(self, x2d):
+        """y [rows, N] in the model's dtype for rows x2d [rows, K]."""
         x2d = x2d.to(torch.bfloat16).contiguous()
-        if x2d.shape[0] < DECODE_ROWS:
+        rows = x2d.shape[0]
+        if rows < DECODE_ROWS:
             y = ops.gemv_bf16(x2d, self.gemv_w, self.sw_bf16)
-        else:
+        elif self.has_gemm:
             y = ops.linear_bf16(x2d, self.packed)
+        else:
+            y = torch.empty((rows, self.N), dtype=torch.bfloat16, device=x2d.device)
+            for r in range(0, rows, DECODE_ROWS):
+                ops.gemv_bf16(x2d[r:r + DECODE_ROWS], self.gemv_w, self.sw_bf16, y[r:r + DECODE_ROWS])
         return y.to(self.dtype)
 
 
-class Slice(torch.nn.Module):
-    """Stands in for one linear of a GpuGemm group (gemma_npu.py:175-193): the first slice called
-    computes the whole group, its siblings reuse the result for the same input tensor."""
+class QuantizedLinear(torch.nn.Module):
+    """One original linear: output columns [c0, c1) of a QuantizedWeight.  Returns the columns
+    parked on it for this very input if there are any (a group computed once for its members),
+    otherwise runs the group and keeps its own columns."""
 
-    def __init__(self, gemm, index, in_features, out_features):
+    def __init__(self, weight, c0=0, c1=None):
         super().__init__()
-        self.gemm, self.index = gemm, index
-        self.in_features, self.out_features = in_features, out_features
+        self.weight_q = weight
+        self.c0, self.c1 = c0, weight.N if c1 is None else c1
+        self.in_features, self.out_features = weight.K, self.c1 - self.c0
+        self.parked = None  # (input tensor, its output columns)
 
     def forward(self, x):
-        g = self.gemm
-        shape = x.shape[:-1]
-        if self.index == 0 or g.pending is None or g.pending[0] is not x:
-            y = g.matmul(x.reshape(-1, x.shape[-1]))
-            parts = torch.split(y, g.sizes, dim=-1) if len(g.sizes) > 1 else (y,)
-            g.pending = (x, parts)
-        out = g.pending[1][self.index]
-        if self.index == len(g.sizes) - 1:
-            g.pending = None
-        return out.reshape(*shape, -1)
+        p = self.parked
+        if p is not None and p[0] is x:
+            return p[1]
+        y = self.weight_q.apply(x.reshape(-1, x.shape[-1]))
+        if self.c0 != 0 or self.c1 != self.weight_q.N:
+            y = y[:, self.c0:self.c1]
+        return y.reshape(*x.shape[:-1], self.out_features)
 
 
-class Int8Head(torch.nn.Module):
-    """The LM head as a weight-only int8 GEMV (gemma_npu.py:159-172), 16 rows per launch."""
+def _column_views(weight, names):
+    """QuantizedLinear views of a group's members, in stacking order, by name."""
+    views, c = {}, 0
+    for name, n in zip(names, weight.sizes):
+        views[name] = QuantizedLinear(weight, c, c + n)
+        c += n
+    return views
 
-    def __init__(self, linear):
-        super().__init__()
-        q, sw = ops.quant_rows(linear.weight.detach().float().contiguous())
-        self.w = ops.pack_gemv_weight(q)
-        self.sw = sw.to(torch.bfloat16)
-        self.in_features, self.out_features = linear.in_features, linear.out_features
 
-    def forward(self, x):
-        shape = x.shape[:-1]
-        x2d = x.reshape(-1, x.shape[-1]).to(torch.bfloat16).contiguous()
-        outs = [ops.gemv_bf16(x2d[r:r + DECODE_ROWS], self.w, self.sw) for r in range(0, x2d.shape[0], DECODE_ROWS)]
-        y = outs[0] if len(outs) == 1 else torch.cat(outs, 0)
-        return y.reshape(*shape, -1)
+def share_input(module, weight, views):
+    """Run `weight` once per forward of `module` on its hidden states and park each view's columns
+    on it for the duration of that forward (the views are the module's projections of that input)."""
+    sizes = [v.out_features for v in views]
+
+    def before(mod, args, kwargs):
+        hs = kwargs.get("hidden_states", args[0] if args else None)
+        if hs is None or hs.shape[-1] != weight.K:
+            return None
+        y = weight.apply(hs.reshape(-1, weight.K))
+        for v, part in zip(views, torch.split(y, sizes, dim=-1)):
+            v.parked = (hs, part.reshape(*hs.shape[:-1], v.out_features))
+        return None
+
+    def after(mod, args, kwargs, output):
+        for v in views:
+            v.parked = None
+        return None
+
+    module.register_forward_pre_hook(before, with_kwargs=True)
+    module.register_forward_hook(after, with_kwargs=True)
 
 
 class GpuRMSNorm(torch.nn.Module):
@@ -127,25 +167,30 @@ class GpuRMSNorm(torch.nn.Module):
 
 
 class GpuMLP(torch.nn.Module):
-    """Gemma 4's MLP, down(gelu_tanh(gate(x)) * up(x)), with the activation and product fused into
-    the gate/up GEMM's epilogue for prefill rows: the epilogue computes bf16(bf16(gelu_tanh(gate)) * up)
-    on the bf16 gate and up the unfused GEMM would have written (k_gelu's arithmetic, pipeline.py:
-    102-107), so the [T, 2I] gate/up result never goes to HBM.  Decode rows (< 16) and activations
-    other than GELU-tanh keep the module's own steps."""
+    """Gemma 4's MLP, down(act(gate(x)) * up(x)), with gate and up from one launch of their stacked
+    weight.  Prefill rows with the GELU-tanh activation take the GEMM's GELU epilogue, which computes
+    bf16(bf16(gelu_tanh(gate)) * up) on the bf16 gate and up the plain GEMM would have written (k_gelu's
+    arithmetic, pipeline.py:102-107), so the [T, 2I] result never goes to HBM.  Decode rows take one
+    GEMV for [gate; up] and the module's own activation and product on its columns."""
 
     def __init__(self, mlp, gate_up, down):
         super().__init__()
         self.orig = mlp
         self.gate_up, self.down = gate_up, down
+        self.act = mlp.act_fn
         self.fused = (getattr(mlp.config, "hidden_activation", None) == "gelu_pytorch_tanh"
                       and gate_up.packed_gelu is not None)
 
     def forward(self, x):
         x2 = x.reshape(-1, x.shape[-1])
-        if not self.fused or x2.shape[0] < DECODE_ROWS:
-            return self.orig(x)
-        a = ops.linear_bf16(x2.to(torch.bfloat16).contiguous(), self.gate_up.packed_gelu, epilogue="gelu")
-        return self.down.matmul(a).reshape(*x.shape[:-1], -1)
+        I = self.gate_up.N // 2
+        if self.fused and x2.shape[0] >= DECODE_ROWS:
+            a = ops.linear_bf16(x2.to(torch.bfloat16).contiguous(), self.gate_up.packed_gelu, epilogue="gelu")
+            a = a.to(self.gate_up.dtype)
+        else:
+            y = self.gate_up.apply(x2)
+            a = self.act(y[:, :I]) * y[:, I:]
+        return self.down.apply(a).reshape(*x.shape[:-1], -1)
 
 
 def language_model(model):
@@ -162,53 +207,60 @@ def register_attention():
     ALL_MASK_ATTENTION_FUNCTIONS.register("local_sdpa", sdpa_mask)
 
 
+def _single(module, name):
+    """Replace module.<name> (a linear) by a QuantizedLinear over its own quantized weight."""
+    w = QuantizedWeight([getattr(module, name).weight])
+    w.name = name
+    setattr(module, name, QuantizedLinear(w))
+    return w
+
+
+def _convert_layer(layer):
+    """One decoder layer's linears and MLP on the engine; returns its weights by pipeline role."""
+    attn, mlp = layer.self_attn, layer.mlp
+    names = ["q_proj"]
+    if not attn.is_kv_shared_layer:
+        names += [n for n in ("k_proj", "v_proj") if getattr(attn, n, None) is not None]
+    qkv = QuantizedWeight([getattr(attn, n).weight for n in names])
+    qkv.name = "+".join(names)
+    views = _column_views(qkv, names)
+    for n, v in views.items():
+        setattr(attn, n, v)
+    share_input(attn, qkv, [views[n] for n in names])
+    roles = {"qkv": qkv, "o": _single(attn, "o_proj")}
+
+    gate_up = QuantizedWeight([mlp.gate_proj.weight, mlp.up_proj.weight], gelu_pair=True)
+    gate_up.name = "gate_proj+up_proj"
+    for n, v in _column_views(gate_up, ["gate_proj", "up_proj"]).items():
+        setattr(mlp, n, v)
+    down = _single(mlp, "down_proj")
+    layer.mlp = GpuMLP(mlp, gate_up, down)
+    roles.update(gate_up=gate_up, down=down)
+    if getattr(layer, "per_layer_input_gate", None) is not None:
+        roles["ple_gate"] = _single(layer, "per_layer_input_gate")
+        roles["ple_proj"] = _single(layer, "per_layer_projection")
+    return roles
+
+
 def to_gpu(model):
-    """Swap the text decoder's linears for GPU W8A8 groups, the LM head for the int8 GEMV head, and
-    the attention for local_sdpa (gemma_npu.py:208-241, 253).  Returns the groups; model.layer_gemms
-    holds each layer's groups by name ("qkv", "o", "gate_up", "down", "ple_gate", "ple_proj") for
-    w8a8.pipeline.Prefill."""
+    """Put the text decoder's linears, MLPs, RMSNorms and LM head on the engine and its attention on
+    local_sdpa (what gemma_npu.py:208-241, 253 does for the NPU).  Returns every quantized weight;
+    model.layer_gemms holds each layer's by pipeline role ("qkv", "o", "gate_up", "down", "ple_gate",
+    "ple_proj") for w8a8.pipeline.Prefill."""
     lm = language_model(model)
-    groups = []
-    per_layer = []  # (layer index, group key) of each group, as the reference's layer_gemms keys
-    for li, layer in enumerate(lm.layers):
-        a, mlp = layer.self_attn, layer.mlp
-        qkv = [a.q_proj]
-        if not a.is_kv_shared_layer:
-            qkv += [a.k_proj] + ([a.v_proj] if a.v_proj is not None else [])
-        groups += [(a, ["q_proj", "k_proj", "v_proj"][: len(qkv)], qkv),
-                   (a, ["o_proj"], [a.o_proj]),
-                   (mlp, ["gate_proj", "up_proj"], [mlp.gate_proj, mlp.up_proj]),
-                   (mlp, ["down_proj"], [mlp.down_proj])]
-        per_layer += [(li, "qkv"), (li, "o"), (li, "gate_up"), (li, "down")]
-        if getattr(layer, "per_layer_input_gate", None) is not None:
-            groups += [(layer, ["per_layer_input_gate"], [layer.per_layer_input_gate]),
-                       (layer, ["per_layer_projection"], [layer.per_layer_projection])]
-            per_layer += [(li, "ple_gate"), (li, "ple_proj")]
+    model.layer_gemms = [_convert_layer(layer) for layer in lm.layers]
+    weights = [w for roles in model.layer_gemms for w in roles.values()]
     if getattr(lm, "per_layer_model_projection", None) is not None:
-        groups.append((lm, ["per_layer_model_projection"], [lm.per_layer_model_projection]))
-    gemms = []
-    for parent, names, linears in groups:
-        g = GpuGemm(linears, gelu_pair=names == ["gate_proj", "up_proj"])
-        g.name = "+".join(names)
-        gemms.append(g)
-        for i, (name, l) in enumerate(zip(names, linears)):
-            setattr(parent, name, Slice(g, i, l.in_features, l.out_features))
-    # the per-layer groups by name, for the whole-prompt pipeline (gemma_npu.py:238-239)
-    model.layer_gemms = [{} for _ in lm.layers]
-    for (li, key), g in zip(per_layer, gemms):
-        model.layer_gemms[li][key] = g
-    # the MLPs with the GELU-tanh * up step in the gate/up GEMM's epilogue for prefill rows
-    for li, layer in enumerate(lm.layers):
-        G = model.layer_gemms[li]
-        if "gate_up" in G and "down" in G:
-            layer.mlp = GpuMLP(layer.mlp, G["gate_up"], G["down"])
-    # every RMSNorm of the text decoder on the row kernel
+        weights.append(_single(lm, "per_layer_model_projection"))
     for parent in list(lm.modules()):
         for name, child in list(parent.named_children()):
             if type(child).__name__ == "Gemma4RMSNorm":
                 setattr(parent, name, GpuRMSNorm(child))
-    # tied to the input embedding, so this is a new int8 copy, not a swap
-    model.lm_head = Int8Head(model.lm_head)
+    # the LM head is tied to the input embedding: this is a new int8 copy, kept for the GEMV only
+    head = QuantizedWeight([model.lm_head.weight], gemm=False)
+    head.name = "lm_head"
+    model.lm_head = QuantizedLinear(head)
+    weights.append(head)
     register_attention()
     lm.set_attn_implementation("local_sdpa")
-    return gemms
+    return weights

@@ -1,40 +1,119 @@
 """The reference's prefill pipeline (pipeline.py:224-339) with every step on the GPU.
 
-    gemms = hf.to_gpu(model)                 # groups + model.layer_gemms (gemma_npu.py:208-241)
-    prefill = Prefill(model)                 # pipeline.py:224-231
-    logits, cache = prefill(ids)             # pipeline.py:312-339: fp32 last-token logits, DynamicCache
+    gemms = hf.to_gpu(model)                 # weights + model.layer_gemms (gemma_npu.py:208-241)
+    prefill = Prefill(model)
+    logits, cache = prefill(ids)             # fp32 last-token logits, DynamicCache (pipeline.py:312-339)
     out = model(input_ids=nxt, past_key_values=cache, use_cache=True)   # HF's decode loop continues
     run = prefill.capture(T)                 # the same, captured in one HIP graph for T-token prompts
     logits, cache = run(ids)
 
-A decoder layer is the reference's step sequence (pipeline.py:244-310): k_in -> qkv GEMM -> k_qkv
--> attention -> k_attn_out -> o GEMM -> k_post_attn -> gate/up GEMM -> k_gelu -> down GEMM ->
-k_post_ff -> PLE gate GEMM -> k_ple_gate -> PLE projection GEMM -> k_ple_out.  The GEMMs are the
-engine's int32 W8A8 GEMMs on the packed per-channel int8 weights of hf.to_gpu, the steps between
-them the fused kernels of w8a8.fused, attention the kernels of w8a8.attention; all of it is issued
-on torch's current stream, and activations stay on the device from the embedding to the logits.
+Per decoder layer the arithmetic is the reference's (pipeline.py:244-310): input norm + quant (k_in),
+the [q; k; v] GEMM, q/k norm + RoPE (k_qkv), attention, quant of its output (k_attn_out), the o GEMM,
+residual + norms + quant (k_post_attn), the gate/up GEMM with GELU-tanh * up and quant (k_gelu),
+the down GEMM, residual + norm + quant (k_post_ff), the per-layer-input gate GEMM (k_ple_gate) and
+projection GEMM (k_ple_out).  GEMMs are the engine's int32 W8A8 GEMMs on hf.to_gpu's packed weights,
+the steps between them w8a8.fused's kernels, attention w8a8.attention's; everything is issued on
+torch's current stream and activations stay on the device from the embedding to the logits.
 
-The reference cuts the prompt into 512-row micro-batches so that its CPU and NPU work overlap
-(pipeline.py:322-330, 341-392).  One GPU gains nothing from that overlap, so by default every
-layer runs over the whole prompt at once (row_step=None), which hands the GEMMs their long-M
-shapes and attention one call per layer.  row_step=512 runs the reference's micro-batches
-instead, each through every layer in prompt order, attending to the keys of the micro-batches
-before it (pipeline.py:266-276).  Every step but attention is row-wise, so the two orders differ
-only by attention's summation order.
+How it is organised here:
+  * each layer's weights, norm weights, attention geometry and key/value source are resolved once,
+    at construction, into a LayerPlan;
+  * keys and values live in a KVStore: one [KV heads, T, head_dim] tensor pair per layer that owns
+    keys; a layer that shares keys (KV-shared layers, which read the last earlier layer of their
+    attention kind that stores full-length keys) reads its source's pair; rows are written where
+    they belong and attention reads the prefix it may see;
+  * the prompt runs as one row range through all layers by default (row_step=None): one GPU has no
+    CPU work to overlap, and the whole prompt gives the GEMMs their long-M shapes and attention one
+    call per layer.  row_step=512 runs the reference's 512-row micro-batch order instead (pipeline.py:
+    322-330), each range through every layer in prompt order against the keys of the ranges before
+    it.  Every step but attention is row-wise, so the orders differ only by attention's summation
+    order.
 
-k_gelu's arithmetic -- dequant, bf16(bf16(gelu_tanh(gate)) * up), per-token quant -- also exists as
-the GEMM's fused GELU epilogue followed by the quant kernel, which never writes the int32 [T, 2I]
-result; with fuse_gelu (the default) the gate/up step takes that form, on the interleaved copy of
-the gate/up weight that hf.to_gpu packs for it.  Both forms give the same int8 rows and scales.
-
-The embedding, the per-layer-input (PLE) tables, RoPE tables, the final norm and the logit
-softcap are the model's own modules, as in the reference (pipeline.py:318-338); the PLE model
-projection inside them and the LM head are the engine's GEMM and GEMV after hf.to_gpu.
+The gate/up step takes the GEMM's fused GELU epilogue followed by the quant kernel by default
+(fuse_gelu): the same int8 rows and scales as k_gelu on the int32 result, without writing the
+[T, 2I] int32 result.  The embedding, per-layer-input tables, RoPE tables, final norm and logit
+softcap are the model's own modules (pipeline.py:318-338); inside them the per-layer model
+projection and the LM head run on the engine after hf.to_gpu.
 """
 import torch
 
 from . import attention, fused, ops
 from .hf import language_model
+
+ROLES = ("qkv", "o", "gate_up", "down", "ple_gate", "ple_proj")
+
+
+class LayerPlan:
+    """One decoder layer's prefill, resolved once: weights by role, norm weights, attention geometry
+    and the layer whose keys and values it attends to (itself unless it shares them)."""
+
+    def __init__(self, index, layer, cfg, weights, kv_source):
+        a = layer.self_attn
+        self.index = index
+        self.weights = weights
+        self.kind = cfg.layer_types[index]
+        self.window = int(a.sliding_window or 0)
+        self.heads = cfg.num_attention_heads
+        self.kv_heads = cfg.per_layer_config[index].num_key_value_heads
+        self.head_dim = a.head_dim
+        self.shares_kv = bool(a.is_kv_shared_layer)
+        self.kv_source = kv_source
+        self.norm_in = layer.input_layernorm.weight
+        self.norm_q = a.q_norm.weight
+        self.norm_k = None if self.shares_kv else a.k_norm.weight
+        self.norm_post_attn = layer.post_attention_layernorm.weight
+        self.norm_pre_ff = layer.pre_feedforward_layernorm.weight
+        self.norm_post_ff = layer.post_feedforward_layernorm.weight
+        self.norm_post_ple = layer.post_per_layer_input_norm.weight
+
+
+class KVStore:
+    """Keys and values of the prompt, per layer that owns them: [KV heads, T, head_dim] each.  A row
+    range is written where it belongs; `visible(layer, end)` is the prefix rows [0, end)."""
+
+    def __init__(self, T):
+        self.T = T
+        self.kv = {}
+
+    def write(self, layer, start, k, v):
+        n = k.shape[1]
+        if start == 0 and n == self.T:  # the whole prompt at once: keep the tensors themselves
+            self.kv[layer] = (k, v)
+            return
+        if layer not in self.kv:
+            self.kv[layer] = (k.new_empty((k.shape[0], self.T, k.shape[2])),
+                              v.new_empty((v.shape[0], self.T, v.shape[2])))
+        kb, vb = self.kv[layer]
+        kb[:, start:start + n].copy_(k)
+        vb[:, start:start + n].copy_(v)
+
+    def visible(self, layer, end):
+        kb, vb = self.kv[layer]
+        return kb[:, :end], vb[:, :end]
+
+    def to_cache(self, cfg, copy):
+        """A DynamicCache with every owning layer's keys and values (what HF's decode loop reads)."""
+        from transformers import DynamicCache
+        cache = DynamicCache(config=cfg)
+        for layer in sorted(self.kv):
+            k, v = self.kv[layer]
+            if copy:
+                k, v = k.clone(), v.clone()
+            cache.update(k[None], v[None], layer)
+        return cache
+
+
+def prompt_inputs(lm, ids):
+    """The model's own inputs to its decoder layers for ids [1, T]: the token embeddings [T, hidden],
+    the per-layer inputs [T, layers, P] and the RoPE (cos, sin) rows [T, head_dim] per attention kind."""
+    emb = lm.embed_tokens(ids)
+    per_layer = lm.project_per_layer_inputs(emb, lm.get_per_layer_inputs(ids, emb))[0]
+    positions = torch.arange(ids.shape[1], device=ids.device)[None]
+    rope = {}
+    for kind in dict.fromkeys(lm.config.layer_types):
+        cos, sin = lm.rotary_emb(emb, positions, kind)
+        rope[kind] = (cos[0], sin[0])
+    return emb[0], per_layer, rope
 
 
 class Prefill:
@@ -43,150 +122,107 @@ class Prefill:
     def __init__(self, model, layer_gemms=None, row_step=None, fuse_gelu=True):
         self.model = model
         self.lm = language_model(model)
-        self.cfg = self.lm.config
-        self.layer_gemms = layer_gemms if layer_gemms is not None else getattr(model, "layer_gemms", None)
-        if self.layer_gemms is None:
+        self.cfg = cfg = self.lm.config
+        weights = layer_gemms if layer_gemms is not None else getattr(model, "layer_gemms", None)
+        if weights is None:
             raise ValueError("Prefill: run w8a8.hf.to_gpu(model) first (it builds model.layer_gemms)")
         if row_step is not None and int(row_step) < 1:
             raise ValueError(f"Prefill: row_step {row_step} must be positive")
         self.row_step = None if row_step is None else int(row_step)
         self.fuse_gelu = bool(fuse_gelu)
-        if getattr(self.cfg, "enable_moe_block", False):
+        if getattr(cfg, "enable_moe_block", False):
             raise NotImplementedError("Prefill: MoE decoder layers are not on the reference's path")
-        if not self.cfg.hidden_size_per_layer_input:
+        if not cfg.hidden_size_per_layer_input:
             raise NotImplementedError("Prefill: the reference's pipeline needs per-layer inputs (PLE)")
+        self.plans = []
+        full_length = {}  # attention kind -> the last layer so far that stores full-length keys
         for i, layer in enumerate(self.lm.layers):
             a = layer.self_attn
             if not a.is_kv_shared_layer and a.v_proj is None:
                 raise NotImplementedError(f"Prefill: layer {i} derives v from k (attention_k_eq_v); the "
                                           "reference's k_qkv expects a v projection")
-            if set(self.layer_gemms[i]) != {"qkv", "o", "gate_up", "down", "ple_gate", "ple_proj"}:
-                raise ValueError(f"Prefill: layer {i} lacks GEMM groups, got {sorted(self.layer_gemms[i])}")
+            if set(weights[i]) != set(ROLES):
+                raise ValueError(f"Prefill: layer {i} lacks GEMM groups, got {sorted(weights[i])}")
+            kind = cfg.layer_types[i]
+            source = full_length[kind] if a.is_kv_shared_layer else i
+            if not a.is_kv_shared_layer and a.store_full_length_kv:
+                full_length[kind] = i
+            self.plans.append(LayerPlan(i, layer, cfg, weights[i], source))
+        self.layer_scalars = None
 
-    @staticmethod
-    def gemm(g, xq):
-        """The int32 GEMM result [T, N] of group g on int8 rows xq (pipeline.py:233-242)."""
-        return ops.gemm_i32(xq, g.packed)
+    def _scalars(self):
+        if self.layer_scalars is None:
+            self.layer_scalars = [layer.layer_scalar.to(torch.bfloat16) for layer in self.lm.layers]
+        return self.layer_scalars
 
-    def steps(self, mb, ctx):
-        """One micro-batch (s, e, slot) through every layer (pipeline.py:244-310); returns its rows."""
-        lm, cfg = self.lm, self.cfg
-        s, e, slot = mb
-        eps = cfg.rms_norm_eps
-        h = ctx["h0"][s:e]
-        kv = ctx["kv"]
-        for i, layer in enumerate(lm.layers):
-            G = self.layer_gemms[i]
-            a = layer.self_attn
-            lt = cfg.layer_types[i]
-            cos, sin = ctx["rope"][lt]
-            cos, sin = cos[s:e], sin[s:e]
-            H, D = cfg.num_attention_heads, a.head_dim
-            KV = cfg.per_layer_config[i].num_key_value_heads
-            shared = a.is_kv_shared_layer
+    def _layer(self, p, h, start, end, per_layer, rope, store, scalar):
+        """Rows [start, end) of the prompt through decoder layer p; returns their new hidden rows."""
+        eps = self.cfg.rms_norm_eps
+        W = p.weights
+        cos, sin = (t[start:end] for t in rope[p.kind])
+        xq, sx = fused.k_in(h, p.norm_in, eps, packed=True)
+        acc = ops.gemm_i32(xq, W["qkv"].packed)
+        q, k, v = fused.k_qkv(acc, sx, W["qkv"].sw, cos, sin, p.norm_q, p.norm_k, eps, p.heads, p.kv_heads,
+                              p.head_dim, p.shares_kv)
+        if not p.shares_kv:
+            store.write(p.index, start, k, v)
+        keys, values = store.visible(p.kv_source, end)
+        o = attention.attention(q, keys, values, start, p.window, 1.0)
 
-            xq, sx = fused.k_in(h, layer.input_layernorm.weight, eps, packed=True)
-            acc = self.gemm(G["qkv"], xq)
-            q, k, v = fused.k_qkv(acc, sx, G["qkv"].sw, cos, sin, a.q_norm.weight,
-                                  None if shared else a.k_norm.weight, eps, H, KV, D, shared)
-            if shared:
-                k_all, v_all = kv[("shared", lt, slot)]
-            else:
-                # every earlier micro-batch has run all its layers, so its keys are here
-                kv[(i, slot)] = (k, v)
-                if slot == 0:
-                    k_all, v_all = k, v
-                else:
-                    prev = [kv[(i, j)] for j in range(slot + 1)]
-                    k_all = torch.cat([p[0] for p in prev], 1)
-                    v_all = torch.cat([p[1] for p in prev], 1)
-                if slot == ctx["last"]:
-                    ctx["layer_kv"].append((i, k_all, v_all))
-                if a.store_full_length_kv:
-                    kv[("shared", lt, slot)] = (k_all, v_all)
-            if a.sliding_window:
-                o = attention.sliding_attention(q, k_all, v_all, s, a.sliding_window)
-            else:
-                o = attention.full_attention(q, k_all, v_all, s)
+        xq, sx = fused.k_attn_out(o, packed=True)
+        acc = ops.gemm_i32(xq, W["o"].packed)
+        h, xq, sx = fused.k_post_attn(acc, sx, W["o"].sw, h, p.norm_post_attn, p.norm_pre_ff, eps, packed=True)
+        gu = W["gate_up"]
+        if self.fuse_gelu and getattr(gu, "packed_gelu", None) is not None:
+            # the GEMM's GELU epilogue writes k_gelu's bf16 bf16(gelu(gate)) * up, then its quant
+            xq, sx = ops.quant_rows_packed(ops.gemm_bf16(xq, sx, gu.packed_gelu, epilogue="gelu"))
+        else:
+            xq, sx = fused.k_gelu(ops.gemm_i32(xq, gu.packed), sx, gu.sw, gu.N // 2, packed=True)
+        acc = ops.gemm_i32(xq, W["down"].packed)
+        h, xq, sx = fused.k_post_ff(acc, sx, W["down"].sw, h, p.norm_post_ff, eps, packed=True)
+        acc = ops.gemm_i32(xq, W["ple_gate"].packed)
+        xq, sx = fused.k_ple_gate(acc, sx, W["ple_gate"].sw, per_layer[start:end, p.index], packed=True)
+        acc = ops.gemm_i32(xq, W["ple_proj"].packed)
+        return fused.k_ple_out(acc, sx, W["ple_proj"].sw, h, p.norm_post_ple, scalar[p.index], eps)
 
-            xq, sx = fused.k_attn_out(o, packed=True)
-            acc = self.gemm(G["o"], xq)
-            h, xq, sx = fused.k_post_attn(acc, sx, G["o"].sw, h, layer.post_attention_layernorm.weight,
-                                          layer.pre_feedforward_layernorm.weight, eps, packed=True)
-            gu = G["gate_up"]
-            if self.fuse_gelu and getattr(gu, "packed_gelu", None) is not None:
-                # the GEMM's GELU epilogue writes k_gelu's bf16 bf16(gelu(gate)) * up, then its quant
-                a_ = ops.gemm_bf16(xq, sx, gu.packed_gelu, epilogue="gelu")
-                xq, sx = ops.quant_rows_packed(a_)
-            else:
-                acc = self.gemm(gu, xq)
-                xq, sx = fused.k_gelu(acc, sx, gu.sw, gu.N // 2, packed=True)
-            acc = self.gemm(G["down"], xq)
-            h, xq, sx = fused.k_post_ff(acc, sx, G["down"].sw, h, layer.post_feedforward_layernorm.weight, eps,
-                                        packed=True)
-            acc = self.gemm(G["ple_gate"], xq)
-            xq, sx = fused.k_ple_gate(acc, sx, G["ple_gate"].sw, ctx["ple"][s:e, i], packed=True)
-            acc = self.gemm(G["ple_proj"], xq)
-            h = fused.k_ple_out(acc, sx, G["ple_proj"].sw, h, layer.post_per_layer_input_norm.weight,
-                                ctx["scalar"][i], eps)
-        return h
+    def run_layers(self, h0, per_layer, rope, scalar=None):
+        """Every decoder layer over the prompt: (final hidden rows [T, hidden] before the last norm,
+        the KVStore of the prompt's keys and values)."""
+        scalar = self._scalars() if scalar is None else scalar
+        T = h0.shape[0]
+        store = KVStore(T)
+        step = self.row_step or T
+        rows = []
+        for start in range(0, T, step):  # prompt order: each range sees the keys of those before it
+            end = min(start + step, T)
+            h = h0[start:end]
+            for p in self.plans:
+                h = self._layer(p, h, start, end, per_layer, rope, store, scalar)
+            rows.append(h)
+        return (rows[0] if len(rows) == 1 else torch.cat(rows)), store
 
-    def _check_ids(self, ids):
+    def check_ids(self, ids):
         if ids.dim() != 2 or ids.shape[0] != 1 or ids.shape[1] < 1:
             raise ValueError(f"Prefill: expected ids [1, T], got {tuple(ids.shape)}")
         return ids.to(self.lm.embed_tokens.weight.device)
 
-    def _inputs(self, ids):
-        """The model's own embedding, per-layer inputs (PLE) and RoPE tables for ids [1, T]
-        (pipeline.py:318-321): (h0 [T, hidden], ple [T, layers, P], {layer type: (cos, sin)})."""
-        lm, cfg = self.lm, self.cfg
-        T = ids.shape[1]
-        emb = lm.embed_tokens(ids)
-        ple = lm.project_per_layer_inputs(emb, lm.get_per_layer_inputs(ids, emb))[0]
-        pos = torch.arange(T, device=ids.device)[None]
-        rope = {lt: tuple(t[0] for t in lm.rotary_emb(emb, pos, lt)) for lt in set(cfg.layer_types)}
-        return emb[0], ple, rope
-
-    def _layers(self, h0, ple, rope, scalar):
-        """Every layer over the prompt, in micro-batches of row_step rows (all at once by default):
-        (the final rows [T, hidden] before the last norm, [(layer, k, v)] of the non-shared layers)."""
-        T = h0.shape[0]
-        step = self.row_step or T
-        mbs = [(s, min(s + step, T), j) for j, s in enumerate(range(0, T, step))]
-        ctx = dict(h0=h0, ple=ple, rope=rope, kv={}, layer_kv=[], last=len(mbs) - 1, scalar=scalar)
-        out = [self.steps(mb, ctx) for mb in mbs]
-        return (out[0] if len(out) == 1 else torch.cat(out)), ctx["layer_kv"]
-
-    def _scalars(self):
-        return [layer.layer_scalar.to(torch.bfloat16) for layer in self.lm.layers]
-
-    def _head(self, h_last):
-        """Final norm, LM head and logit softcap of the last row (pipeline.py:334-338)."""
-        h = self.lm.norm(h_last[None])
-        logits = self.model.lm_head(h)[0, -1].float()
+    def last_token_logits(self, rows):
+        """The model's final norm, LM head and logit softcap on the last hidden row (pipeline.py:334-338)."""
+        logits = self.model.lm_head(self.lm.norm(rows[-1:][None]))[0, -1].float()
         cap = self.cfg.final_logit_softcapping
-        if cap:
-            logits = torch.tanh(logits / cap) * cap
-        return logits
-
-    def _cache(self, layer_kv, copy):
-        """A DynamicCache holding each non-shared layer's keys and values (pipeline.py:273-274)."""
-        from transformers import DynamicCache
-        cache = DynamicCache(config=self.cfg)
-        for i, k, v in layer_kv:
-            cache.update((k.clone() if copy else k)[None], (v.clone() if copy else v)[None], i)
-        return cache
+        return torch.tanh(logits / cap) * cap if cap else logits
 
     @torch.inference_mode()
     def __call__(self, ids, all_hidden=False):
         """ids [1, T] -> (last-token logits [vocab] fp32, DynamicCache) (pipeline.py:312-339).
 
         With all_hidden, the final-norm hidden states [T, hidden] instead of the logits."""
-        h0, ple, rope = self._inputs(self._check_ids(ids))
-        rows, layer_kv = self._layers(h0, ple, rope, self._scalars())
+        h0, per_layer, rope = prompt_inputs(self.lm, self.check_ids(ids))
+        rows, store = self.run_layers(h0, per_layer, rope)
+        cache = store.to_cache(self.cfg, copy=False)
         if all_hidden:
-            return self.lm.norm(rows[None])[0], self._cache(layer_kv, copy=False)
-        return self._head(rows[-1:]), self._cache(layer_kv, copy=False)
+            return self.lm.norm(rows[None])[0], cache
+        return self.last_token_logits(rows), cache
 
     @torch.inference_mode()
     def capture(self, T):
@@ -212,29 +248,28 @@ class CapturedPrefill:
             raise ValueError(f"Prefill.capture: T={T} must be positive")
         self.prefill, self.T = prefill, T
         dev = prefill.lm.embed_tokens.weight.device
-        ids = torch.zeros((1, T), dtype=torch.long, device=dev)
-        h0, ple, rope = prefill._inputs(ids)
-        self.h0, self.ple, self.rope = h0.clone(), ple.clone(), rope
-        self.scalar = prefill._scalars()
+        h0, per_layer, rope = prompt_inputs(prefill.lm, torch.zeros((1, T), dtype=torch.long, device=dev))
+        self.h0, self.per_layer, self.rope = h0.clone(), per_layer.clone(), rope
+        scalar = prefill._scalars()
         self.stream = torch.cuda.Stream(dev)
         self.stream.wait_stream(torch.cuda.current_stream(dev))
         with torch.cuda.stream(self.stream):
-            prefill._layers(self.h0, self.ple, self.rope, self.scalar)
+            prefill.run_layers(self.h0, self.per_layer, self.rope, scalar)
         torch.cuda.current_stream(dev).wait_stream(self.stream)
         torch.cuda.synchronize(dev)
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph, stream=self.stream):
-            self.rows, self.layer_kv = prefill._layers(self.h0, self.ple, self.rope, self.scalar)
+            self.rows, self.store = prefill.run_layers(self.h0, self.per_layer, self.rope, scalar)
         torch.cuda.synchronize(dev)
 
     @torch.inference_mode()
     def __call__(self, ids):
         p = self.prefill
-        ids = p._check_ids(ids)
+        ids = p.check_ids(ids)
         if ids.shape[1] != self.T:
             raise ValueError(f"CapturedPrefill: captured for {self.T} tokens, got {ids.shape[1]}")
-        h0, ple, _ = p._inputs(ids)
+        h0, per_layer, _ = prompt_inputs(p.lm, ids)
         self.h0.copy_(h0)
-        self.ple.copy_(ple)
+        self.per_layer.copy_(per_layer)
         self.graph.replay()
-        return p._head(self.rows[-1:]), p._cache(self.layer_kv, copy=True)
+        return p.last_token_logits(self.rows), self.store.to_cache(p.cfg, copy=True)

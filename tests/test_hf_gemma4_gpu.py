@@ -28,7 +28,7 @@ def test_prefill_and_decode_loop():
     ref = dequantized_reference(base)
     ours = copy.deepcopy(base).to(torch.bfloat16).to(DEV)
     gemms = hf.to_gpu(ours)
-    assert len(gemms) == 10 * 6 + 1
+    assert len(gemms) == 10 * 6 + 2  # six groups per layer, the PLE model projection, the LM head
     T = 40
     ids = torch.randint(0, 512, (1, T), generator=torch.Generator().manual_seed(1))
 
@@ -132,3 +132,34 @@ def test_gpu_mlp_matches_the_module_path():
         assert (ai - ri).abs().max().item() <= 1
         assert (ai == ri).float().mean().item() > 0.99
         assert rel_err(got[0], want[0]) < 2e-2
+
+
+@torch.inference_mode()
+def test_projection_groups_run_once_per_call():
+    """The [q; k; v] weight runs once per attention call and its columns are handed to the three
+    projections (w8a8.hf.share_input), nothing stays parked after the call, and the plain GEMM
+    packing of a [gate; up] weight is never made when the MLP takes the fused GELU epilogue."""
+    from w8a8 import hf
+    ours = copy.deepcopy(build(seed=19)).to(torch.bfloat16).to(DEV)
+    hf.to_gpu(ours)
+    calls = {}
+    for i, roles in enumerate(ours.layer_gemms):
+        w = roles["qkv"]
+        orig = w.apply
+
+        def counted(x2d, orig=orig, i=i):
+            calls[i] = calls.get(i, 0) + 1
+            return orig(x2d)
+        w.apply = counted
+    ids = torch.randint(0, 512, (1, 24), generator=torch.Generator().manual_seed(20))
+    out = ours(input_ids=ids.to(DEV), use_cache=True)
+    assert calls == {i: 1 for i in range(len(ours.layer_gemms))}
+    nxt = out.logits[0, -1].argmax().view(1, 1)
+    ours(input_ids=nxt, past_key_values=out.past_key_values, use_cache=True)
+    assert calls == {i: 2 for i in range(len(ours.layer_gemms))}
+    for layer in ours.model.layers:
+        for name in ("q_proj", "k_proj", "v_proj"):
+            proj = getattr(layer.self_attn, name, None)
+            if isinstance(proj, hf.QuantizedLinear):
+                assert proj.parked is None
+        assert layer.mlp.gate_up._packed is None
