@@ -728,35 +728,46 @@ __global__ __launch_bounds__(NWN * 64, MINB) void gemm_dw_kernel(GemmParams p) {
 }
 
 // ---- software-pipelined persistent kernel, one wave per SIMD ---------------------------------------
-// Four waves in a 2 x 2 grid, each owning a (BM/2) x (BN/2) quarter of the block tile as 32 x 32 MFMA
-// tiles (sixteen 16-register accumulators for 256 x 256, held in the accumulator registers).
+// Four waves in a WGM x (4/WGM) grid, each owning a (BM/WGM) x (BN*WGM/4) part of the block tile as
+// 32 x 32 MFMA tiles held in the accumulator registers (256 x 256 on 2 x 2: sixteen 16-register
+// accumulators per wave).
 // k-tiles are 64 deep (two k-steps): the packed layouts pad K to 64, so every k-step of every
 // k-tile is live and the loop has no branches.  A and W fragments go HBM -> LDS by DMA into an
-// NS-slot ring, NS-1 k-tiles ahead of the multiply.  With one wave per SIMD nothing else fills a
-// gap in a wave's MFMA stream, so each LDS read and each DMA issue is placed right behind an MFMA
-// (sched_barrier fences fix the order) and issues while that MFMA runs.
+// NS-slot ring.  With one wave per SIMD nothing else fills a gap in a wave's MFMA stream, so the
+// LDS reads and DMA issues are placed behind the MFMAs (sched_barrier fences fix the order) and
+// issue while those run.
 //
 // Persistent: block b multiplies the logical tiles xcd_remap(b) + i * gridDim.x, and the ring runs
 // as one stream of k-tiles across them (stream index g = i * KT + kt), so the first k-tiles of a
 // tile land while the previous tile's last k-tiles are multiplied and its epilogue stores go out.
 // Per k-tile:
-//   k-step 0: MFMAs on register set 0 (k-step 0 of g), reading k-step 1 of g into set 1;
+//   k-step 0: MFMAs on register set 0 (k-step 0 of g), reading k-step 1 of g into set 1 and issuing
+//             the second half of the DMAs of stream k-tile g - 1 + NS;
 //   k-step 1: once set 1 has landed (so this wave reads slot g no more) and this wave's DMAs of
 //             g+1 have landed, one barrier; then MFMAs on set 1, reading k-step 0 of g+1 into
-//             set 0 and DMA-ing stream k-tile g+NS into the slot of g, which no wave reads again.
+//             set 0 and issuing the first half of the DMAs of g + NS into the slot of g, which no
+//             wave reads again.
+// The DMAs are spread that way, evenly among the reads, because the path from L2 into a CU moves
+// about 30 bytes per clock (measured on MI355X with every CU loading): a wave that issues its
+// loads back to back fills the request queue and then stalls its MFMA stream behind it.
 // DMAs past the block's last k-tile go through a buffer resource with no records: they return
 // zeros and touch no memory, and every k-tile keeps the same count of loads in flight.
-template <int BM, int BN, int NS, int EPI, bool A_PACKED, int MINB>
+template <int BM, int BN, int WGM, int NS, int EPI, bool A_PACKED, int MINB>
 __global__ __launch_bounds__(256, MINB) void gemm_pipe_kernel(GemmParams p) {
-  constexpr int KS = 2, NW = 4;
+  constexpr int KS = 2, NW = 4, WGN = NW / WGM;
   constexpr int MT = BM / 32, NTB = BN / 32;
-  constexpr int WTM = MT / 2, WTN = NTB / 2;
+  constexpr int WTM = MT / WGM, WTN = NTB / WGN;
   constexpr int NQ = WTM * WTN;
   constexpr int F = KS * (MT + NTB);
   constexpr int FA = KS * MT / NW, FB = KS * NTB / NW, FW = FA + FB;
+  constexpr int FH = FW / 2;             // DMAs of a k-tile issued right after the barrier that frees its slot
+  constexpr int NR = WTM + WTN;          // fragment reads per k-step
+  constexpr int PRE = NQ >= 4 ? 2 : 1;   // MFMAs of k-step 1 issued before its barrier
+  static_assert(WGM * WGN == NW && WTM * WGM == MT && WTN * WGN == NTB, "waves tile the block");
   static_assert(FA * NW == KS * MT && FB * NW == KS * NTB, "each wave moves whole A and W fragments");
   static_assert(FW * (NS - 1) < 64, "outstanding loads must fit the 6-bit vmcnt");
   static_assert(NS >= 3, "one slot read, one landing, at least one in flight");
+  static_assert(PRE < NQ, "k-step 1 has MFMAs after its barrier");
   static_assert(EPI != EPI_GELU || WTN % 2 == 0, "GELU pairs need an even tile count per wave");
   constexpr int NSCALE = EPI == EPI_I32 ? 0 : BM + BN;
   constexpr int SCALE_PER_THREAD = NSCALE ? (NSCALE + 255) / 256 : 1;
@@ -767,7 +778,7 @@ __global__ __launch_bounds__(256, MINB) void gemm_pipe_kernel(GemmParams p) {
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WGN, wn = wave % WGN;
   const int ntm = (p.M + BM - 1) / BM;
   const int ntn = (p.NT + NTB - 1) / NTB;
   const int ntiles = ntm * ntn;
@@ -775,7 +786,6 @@ __global__ __launch_bounds__(256, MINB) void gemm_pipe_kernel(GemmParams p) {
   const int r0 = xcd_remap(int(blockIdx.x), G);
   const int my_tiles = r0 < ntiles ? (ntiles - 1 - r0) / G + 1 : 0;
   const int KT = p.KF / KS;  // KF is even: K is padded to 64
-  const int total = my_tiles * KT;
 
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a, p.a_bytes);
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.wp, p.w_bytes);
@@ -811,25 +821,35 @@ __global__ __launch_bounds__(256, MINB) void gemm_pipe_kernel(GemmParams p) {
   constexpr uint32_t A_STEP = A_PACKED ? KS * 1024u : KS * 32u;
   constexpr uint32_t W_STEP = KS * 1024u;
 
-  // Uniform DMA state of stream k-tile h: its A / W base offsets and resources (dead past the end).
+  // Uniform DMA state of a stream k-tile: its A / W base offsets and resources (dead past the end).
   struct DmaBase {
     uint32_t a, w;
     __amdgpu_buffer_rsrc_t ra, rw;
   };
-  auto dma_base = [&](int h) {
-    DmaBase d;
-    const bool live = h < total;
-    const int i = live ? h / KT : 0;
-    const int kk = live ? h - i * KT : 0;
+  // DMA cursor: stream k-tiles are DMA'd in order, each once, so the next one's tile (di), k-tile
+  // in that tile (dk) and the tile's base offsets advance without divisions.
+  int di = 0, dk = 0;
+  uint32_t da0 = 0, dw0 = 0;
+  auto cursor_tile = [&]() {
     int m0, t0;
-    tile_origin(i, m0, t0);
+    tile_origin(di, m0, t0);
     if constexpr (A_PACKED)
-      d.a = uint32_t(m0 / 32) * uint32_t(p.KF) * 1024u + uint32_t(kk) * A_STEP;
+      da0 = uint32_t(m0 / 32) * uint32_t(p.KF) * 1024u;
     else
-      d.a = uint32_t(m0) * uint32_t(p.lda) + uint32_t(kk) * A_STEP;
-    d.w = uint32_t(t0) * uint32_t(p.KF) * 1024u + uint32_t(kk) * W_STEP;
+      da0 = uint32_t(m0) * uint32_t(p.lda);
+    dw0 = uint32_t(t0) * uint32_t(p.KF) * 1024u;
+  };
+  auto next_dma = [&]() {
+    DmaBase d;
+    const bool live = di < my_tiles;
+    d.a = da0 + uint32_t(dk) * A_STEP;
+    d.w = dw0 + uint32_t(dk) * W_STEP;
     d.ra = live ? ra : ra_dead;
     d.rw = live ? rw : rw_dead;
+    if (++dk == KT) {
+      dk = 0;
+      if (++di < my_tiles) cursor_tile();
+    }
     return d;
   };
   // One DMA (fragment d < FA of A, else of W) of stream k-tile h into its ring slot.
@@ -888,20 +908,35 @@ __global__ __launch_bounds__(256, MINB) void gemm_pipe_kernel(GemmParams p) {
   auto mma_one = [&](int q, const v4i (&a)[WTM], const v4i (&b)[WTN]) {
     acc[q / WTN][q % WTN] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b[q % WTN], a[q / WTN], acc[q / WTN][q % WTN], 0, 0, 0);
   };
-
-  constexpr int NR = WTM + WTN;          // fragment reads per k-step
-  constexpr int PRE = NQ >= 4 ? 2 : 1;   // MFMAs of k-step 1 issued before its barrier
-  static_assert(NR <= NQ, "k-step 0 places at most one read behind each MFMA");
+  // The n ops of a k-step, nd of them DMAs placed evenly among the reads: op o is a DMA when the
+  // running count (o * nd) / n steps up at o, and the op's index among its kind is that count (DMA)
+  // or o minus it (read).  The ops are then dealt evenly over the k-step's MFMA slots.
+  auto run_ops = [&](int slot, int nslots, int nd, auto&& read, auto&& dma) {
+    const int n = NR + nd;
+    const int lo = slot * n / nslots, hi = (slot + 1) * n / nslots;
+#pragma unroll
+    for (int o = 0; o < NR + FW; ++o) {
+      if (o < lo || o >= hi || o >= n) continue;
+      const int before = o * nd / n;
+      if ((o + 1) * nd / n != before)
+        dma(before);
+      else
+        read(o - before);
+    }
+  };
 
   if (my_tiles == 0) return;
   fetch_scales(0);
+  cursor_tile();
+  DmaBase pend;  // the stream k-tile whose second half of DMAs is still to go out
 #pragma unroll
   for (int h = 0; h < NS; ++h) {
-    const DmaBase b = dma_base(h);
+    const DmaBase b = next_dma();
 #pragma unroll
-    for (int d = 0; d < FW; ++d) dma_one(d, h, b);
+    for (int d = 0; d < (h + 1 < NS ? FW : FH); ++d) dma_one(d, h, b);
+    if (h + 1 == NS) pend = b;
   }
-  wait_vmcnt<FW * (NS - 1)>();
+  wait_vmcnt<FW * (NS - 1) - (FW - FH)>();
   __builtin_amdgcn_s_barrier();
 
   v4i a0[WTM], b0[WTN], a1[WTM], b1[WTN];
@@ -913,18 +948,21 @@ __global__ __launch_bounds__(256, MINB) void gemm_pipe_kernel(GemmParams p) {
   for (int it = 0; it < my_tiles; ++it) {
     zero_acc();
     for (int kt = 0; kt < KT; ++kt, ++g) {
-      // k-step 0: MFMA q on set 0, then read q of k-step 1 into set 1
+      // k-step 0: MFMAs on set 0; reads of k-step 1 of g into set 1 and the second half of the
+      // DMAs of g - 1 + NS (its slot was freed at the barrier of g - 1)
       __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): set 0 has landed
 #pragma unroll
       for (int q = 0; q < NQ; ++q) {
         mma_one(q, a0, b0);
         __builtin_amdgcn_sched_barrier(0);
-        if (q < NR) read_one(q, g, 1, a1, b1);
+        run_ops(q, NQ, FW - FH, [&](int r) { read_one(r, g, 1, a1, b1); },
+                [&](int d) { dma_one(FH + d, g - 1 + NS, pend); });
         __builtin_amdgcn_sched_barrier(0);
       }
-      // k-step 1: PRE MFMAs on set 1, the barrier, then the remaining MFMAs each followed by its
-      // share of the NR reads of k-step 0 of g+1 (into set 0) and the FW DMAs of g+NS.
-      const DmaBase nb = dma_base(g + NS);
+      // k-step 1: PRE MFMAs on set 1, the barrier, then the remaining MFMAs with the reads of
+      // k-step 0 of g+1 (into set 0; past the block's last k-tile they are stale and never
+      // multiplied) and the first half of the DMAs of g + NS.
+      const DmaBase nb = next_dma();  // stream k-tile g + NS
       __builtin_amdgcn_s_waitcnt(0xc07f);  // set 1 has landed: this wave reads slot g no more
 #pragma unroll
       for (int q = 0; q < PRE; ++q) {
@@ -934,22 +972,15 @@ __global__ __launch_bounds__(256, MINB) void gemm_pipe_kernel(GemmParams p) {
       wait_vmcnt<FW * (NS - 2)>();  // this wave's part of g+1 has landed
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
-      constexpr int NOPS = NR + FW, SLOTS = NQ - PRE;
 #pragma unroll
       for (int q = PRE; q < NQ; ++q) {
         mma_one(q, a1, b1);
         __builtin_amdgcn_sched_barrier(0);
-        const int lo = (q - PRE) * NOPS / SLOTS, hi = (q - PRE + 1) * NOPS / SLOTS;
-#pragma unroll
-        for (int o = 0; o < NOPS; ++o) {
-          if (o < lo || o >= hi) continue;
-          if (o < NR)
-            read_one(o, g + 1, 0, a0, b0);  // past the block's last k-tile: stale, never multiplied
-          else
-            dma_one(o - NR, g + NS, nb);
-        }
+        run_ops(q - PRE, NQ - PRE, FH, [&](int r) { read_one(r, g + 1, 0, a0, b0); },
+                [&](int d) { dma_one(d, g + NS, nb); });
         __builtin_amdgcn_sched_barrier(0);
       }
+      pend = nb;
     }
 
     // ---- epilogue of tile it, while the next tile's first k-tiles land in the ring ----
@@ -1038,12 +1069,13 @@ static constexpr DwCfg kDw[] = {
 static constexpr int kNumDw = int(sizeof(kDw) / sizeof(kDw[0]));
 
 // Software-pipelined configurations (gemm_pipe_kernel), numbered after kDw: block tile BM x BN,
-// NS-slot ring of 64-deep k-tiles, blocks per CU the registers are budgeted for.
+// waves along M (the other 4 / wgm along N), NS-slot ring of 64-deep k-tiles, blocks per CU the
+// registers are budgeted for.
 struct PipeCfg {
-  int bm, bn, ns, minb;
+  int bm, bn, wgm, ns, minb;
 };
 static constexpr PipeCfg kPipe[] = {
-    {256, 256, 4, 1},  // 26: 128x128 per wave, 32 KiB slots, 128 KiB ring
+    {256, 256, 2, 4, 1},  // 26: 128x128 per wave, 32 KiB slots, 128 KiB ring
 };
 static constexpr int kNumPipe = int(sizeof(kPipe) / sizeof(kPipe[0]));
 static_assert(kNumCfg == 23 && kNumDw == 3 && kNumPipe == 1, "every configuration needs its case in gemm_launch");
@@ -1187,7 +1219,7 @@ static int persistent_blocks(int tiles, int per_cu) {
   return min(tiles, cus * per_cu);
 }
 
-template <int BM, int BN, int NS, int MINB, bool AP>
+template <int BM, int BN, int WGM, int NS, int MINB, bool AP>
 static void launch_pipe_epi(GemmParams p, int epi, hipStream_t stream) {
   const int ntm = (p.M + BM - 1) / BM;
   const int ntn = (p.NT * 32 + BN - 1) / BN;
@@ -1195,10 +1227,10 @@ static void launch_pipe_epi(GemmParams p, int epi, hipStream_t stream) {
   p.splits = 1;
   const dim3 grid{unsigned(persistent_blocks(ntm * ntn, MINB))};
   switch (epi) {
-    case EPI_I32: gemm_pipe_kernel<BM, BN, NS, EPI_I32, AP, MINB><<<grid, 256, 0, stream>>>(p); break;
-    case EPI_BF16: gemm_pipe_kernel<BM, BN, NS, EPI_BF16, AP, MINB><<<grid, 256, 0, stream>>>(p); break;
-    case EPI_GELU: gemm_pipe_kernel<BM, BN, NS, EPI_GELU, AP, MINB><<<grid, 256, 0, stream>>>(p); break;
-    case EPI_RESID: gemm_pipe_kernel<BM, BN, NS, EPI_RESID, AP, MINB><<<grid, 256, 0, stream>>>(p); break;
+    case EPI_I32: gemm_pipe_kernel<BM, BN, WGM, NS, EPI_I32, AP, MINB><<<grid, 256, 0, stream>>>(p); break;
+    case EPI_BF16: gemm_pipe_kernel<BM, BN, WGM, NS, EPI_BF16, AP, MINB><<<grid, 256, 0, stream>>>(p); break;
+    case EPI_GELU: gemm_pipe_kernel<BM, BN, WGM, NS, EPI_GELU, AP, MINB><<<grid, 256, 0, stream>>>(p); break;
+    case EPI_RESID: gemm_pipe_kernel<BM, BN, WGM, NS, EPI_RESID, AP, MINB><<<grid, 256, 0, stream>>>(p); break;
   }
 }
 
@@ -1206,9 +1238,9 @@ template <int D>
 static void launch_pipe(const GemmParams& p, int epi, bool a_packed, hipStream_t stream) {
   constexpr PipeCfg c = kPipe[D];
   if (a_packed)
-    launch_pipe_epi<c.bm, c.bn, c.ns, c.minb, true>(p, epi, stream);
+    launch_pipe_epi<c.bm, c.bn, c.wgm, c.ns, c.minb, true>(p, epi, stream);
   else
-    launch_pipe_epi<c.bm, c.bn, c.ns, c.minb, false>(p, epi, stream);
+    launch_pipe_epi<c.bm, c.bn, c.wgm, c.ns, c.minb, false>(p, epi, stream);
 }
 
 // Tile choice, from timing every configuration with the bf16 epilogues on the E2B prefill
