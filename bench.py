@@ -16,7 +16,8 @@ roofline of the dominant kernel (the gate_up GEMM, timed live with HIP events on
 stream), the host CPU's torch._int_mm on the same GEMMs (the reference's --backend cpu-int8
 path, pipeline.py:237), and `extra`: the same step captured in one HIP graph and replayed
 (checked bit for bit against the eager run), the full-prefill GEMM sweep at M=3658 / 4096, the M=16384
-stress GEMMs, a decoder layer's whole linear path on the device (the six GEMMs with the fused
+stress GEMMs, the int32 GEMMs of those shapes against hipBLASLt (torch._int_mm on the same GPU, cold
+weights), a decoder layer's whole linear path on the device (the six GEMMs with the fused
 norm / RoPE / GELU / residual / quant kernels between them, one HIP graph), and the decode GEMV
 bandwidth.
 """
@@ -311,6 +312,56 @@ def sweep(M, dev, reps):
     total_ops = sum(workloads.gemm_ops(M, N, K) for _, _, _, K, N in shapes)
     wbytes = sum(K * N for _, _, _, K, N in shapes)
     return ms, total_ops, wbytes, [(K, N) for _, _, _, K, N in shapes], run
+
+
+def vendor_compare(dev, cases=((3658, ("qkv", "o", "gate_up", "down", "ple_proj")),
+                               (16384, ("gate_up", "down")))):
+    """The int32 GEMM (automatic tile) against hipBLASLt through torch._int_mm on the same GPU, the
+    same operands and the same weight temperature: per shape, enough distinct weight copies to pass
+    512 MB (more than the 256 MB MALL) are cycled, so both read their weights cold; each side is
+    timed twice, alternating, and the faster run kept.  hipBLASLt has no fused epilogues, so the
+    comparison is int8 -> int32 on both sides; outputs are compared bit for bit."""
+    import torch
+    from w8a8 import lib, ops, workloads
+    shapes = dict(workloads.LAYER_GROUPS, ple_proj=workloads.PLE_PROJ)
+    out = {}
+    for M, names in cases:
+        for name in names:
+            K, N, _ = shapes[name]
+            copies = max(2, -(-512 * 2 ** 20 // (K * N)))
+            g = torch.Generator(device=dev).manual_seed(77)
+            a = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8, device=dev)
+            ap = ops.pack_act(a)
+            ws = [torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8, device=dev) for _ in range(copies)]
+            pws = [ops.pack_weight(w, "nk") for w in ws]
+            wts = [w.t() for w in ws]  # [K, N] column-major: hipBLASLt's faster B layout here
+            c = torch.empty((M, N), dtype=torch.int32, device=dev)
+            it = [0]
+
+            def ours():
+                ops.gemm_i32(ap, pws[it[0] % copies], c)
+                it[0] += 1
+
+            def theirs():
+                torch._int_mm(a, wts[it[0] % copies], out=c)
+                it[0] += 1
+
+            n = max(copies, 20)
+            t = {"ours": 1e9, "hipblaslt": 1e9}
+            for _ in range(2):
+                t["ours"] = min(t["ours"], event_time_ms(ours, n, 2))
+                t["hipblaslt"] = min(t["hipblaslt"], event_time_ms(theirs, n, 2))
+            ref = torch._int_mm(a, wts[0])
+            ops.gemm_i32(ap, pws[0], c)
+            same = bool(torch.equal(ref, c))
+            key = f"m{M}_{name}"
+            out[key] = {"K": K, "N": N, "tile": lib().w8a8_gemm_pick_tile_config(M, N, K, -1),
+                        "ours_us": round(t["ours"] * 1e3, 1), "hipblaslt_us": round(t["hipblaslt"] * 1e3, 1),
+                        "speedup": round(t["hipblaslt"] / t["ours"], 3), "bit_exact": same}
+            log(f"bench: vs hipBLASLt {key}: {out[key]}")
+            del a, ap, ws, pws, wts, c, ref
+            torch.cuda.empty_cache()
+    return out
 
 
 def gemv_bench(M, K, N, dev, reps, seed=5):
@@ -922,6 +973,7 @@ def main():
                                               "frac_mfma": round(t / PEAK_INT8_TOPS, 4)}
             log(f"bench: stress {name}: {extra[f'stress_m16384_{name}']}")
             del x, q, w, pw, res, out
+        extra["vs_hipblaslt_int32"] = vendor_compare(dev)
         ms, eager, c = time_chain(M, dev, reps=100)
         extra[f"device_layer_chain_m{M}"] = {
             "us": round(ms * 1e3, 1), "eager_us": round(eager * 1e3, 1), "launches": c["launches"],

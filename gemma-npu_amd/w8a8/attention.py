@@ -201,10 +201,13 @@ def local_sdpa(module, query, key, value, attention_mask, dropout=0.0, scaling=N
     Tk = key.shape[2]
     if Tk < T:
         raise ValueError(f"local_sdpa: {Tk} keys for {T} queries")
+    from . import torch_ops  # the registered operators while torch.compile traces, else the calls above
     scale = float(scaling) if scaling is not None else D ** -0.5
     out = torch.empty((1, T, H, D), dtype=torch.bfloat16, device=query.device)
     if T == 1 and H // key.shape[1] <= 16:
-        decode(query[0, :, 0], key[0], value[0], Tk - 1, int(sliding_window or 0), scale, out=out[0, 0])
+        torch_ops.attention_decode(query[0, :, 0], key[0], value[0], Tk - 1, int(sliding_window or 0), scale,
+                                   out=out[0, 0])
     else:
-        attention(query[0], key[0], value[0], Tk - T, int(sliding_window or 0), scale, out=out[0].transpose(0, 1))
+        torch_ops.attention(query[0], key[0], value[0], Tk - T, int(sliding_window or 0), scale,
+                            out=out[0].transpose(0, 1))
     return out, None

@@ -24,11 +24,13 @@ output is computed once per input:
 Rows < 16 (decode) take the weight-only int8 GEMV with bf16 scales (gemma_npu.py:120-121), more
 rows per-token quant -> int8 GEMM -> dequant (gemma_npu.py:123-152).  Every RMSNorm module becomes
 one launch of the engine's row kernel (GpuRMSNorm).  RoPE, residuals, the KV cache and the decode
-loop stay HF's own torch ops on the GPU.
+loop stay HF's own torch ops on the GPU.  Under torch.compile (the reference compiles each layer's
+forward, gemma_npu.py:255-265) these modules call the engine through its registered torch operators
+(w8a8.torch_ops), which the compiler traces instead of breaking the graph.
 """
 import torch
 
-from . import attention, ops
+from . import attention, ops, torch_ops
 
 DECODE_ROWS = 16  # rows below this go to the GEMV (gemma_npu.py:120)
 
@@ -75,13 +77,13 @@ class QuantizedWeight:
         x2d = x2d.to(torch.bfloat16).contiguous()
         rows = x2d.shape[0]
         if rows < DECODE_ROWS:
-            y = ops.gemv_bf16(x2d, self.gemv_w, self.sw_bf16)
+            y = torch_ops.gemv(x2d, self.gemv_w, self.sw_bf16)
         elif self.has_gemm:
-            y = ops.linear_bf16(x2d, self.packed)
+            y = torch_ops.linear(x2d, self.packed)
         else:
             y = torch.empty((rows, self.N), dtype=torch.bfloat16, device=x2d.device)
             for r in range(0, rows, DECODE_ROWS):
-                ops.gemv_bf16(x2d[r:r + DECODE_ROWS], self.gemv_w, self.sw_bf16, y[r:r + DECODE_ROWS])
+                torch_ops.gemv(x2d[r:r + DECODE_ROWS], self.gemv_w, self.sw_bf16, y[r:r + DECODE_ROWS])
         return y.to(self.dtype)
 
 
@@ -161,9 +163,11 @@ class GpuRMSNorm(torch.nn.Module):
                 or (w is not None and (w.dtype != torch.bfloat16 or w.device != x.device))):
             return self.orig(x)
         x2 = x.reshape(-1, N)
+        if torch_ops.tracing():
+            return torch_ops.rms_norm(x2, w, self.eps).reshape(x.shape)
         if not x2.is_contiguous() or x2.data_ptr() % 16:
             x2 = x2.clone(memory_format=torch.contiguous_format)
-        return ops.rms_residual(x2, None, w, self.eps).reshape(x.shape)
+        return torch_ops.rms_norm(x2, w, self.eps).reshape(x.shape)
 
 
 class GpuMLP(torch.nn.Module):
@@ -185,7 +189,7 @@ class GpuMLP(torch.nn.Module):
         x2 = x.reshape(-1, x.shape[-1])
         I = self.gate_up.N // 2
         if self.fused and x2.shape[0] >= DECODE_ROWS:
-            a = ops.linear_bf16(x2.to(torch.bfloat16).contiguous(), self.gate_up.packed_gelu, epilogue="gelu")
+            a = torch_ops.linear(x2.to(torch.bfloat16).contiguous(), self.gate_up.packed_gelu, epilogue="gelu")
             a = a.to(self.gate_up.dtype)
         else:
             y = self.gate_up.apply(x2)
