@@ -52,14 +52,14 @@ __device__ __forceinline__ v8bf widen8(uint32_t lo, uint32_t hi) {
 // LM head (K=1536, N=262144), 6.2 TB/s against 5.0 TB/s for the row-major weight, where each load
 // takes 64-byte pieces of 16 rows.  Row-major weights keep the default policy (a streamed half
 // line would be fetched twice).
-template <int TPW, int U, bool PACKED>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
-  __shared__ v4f red[4][TPW][64];
+template <int TPW, int U, bool PACKED, int NWB>
+__global__ __launch_bounds__(NWB * 64) void gemv_kernel(GemvParams p) {
+  __shared__ v4f red[NWB][TPW][64];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int group_in_block = wave / p.split;
   const int ks = wave % p.split;
-  const int groups_per_block = 4 / p.split;
+  const int groups_per_block = NWB / p.split;
   const int group = blockIdx.x * groups_per_block + group_in_block;
   const int tile0 = group * TPW;
   const int ntiles = (p.N + 15) >> 4;
@@ -180,19 +180,28 @@ static void gemv_launch(const GemvParams& p0, hipStream_t stream) {
     p.split = 1;
     if (p.M <= 8) {
       const int64_t groups = (ntiles + 1) / 2;
-      gemv_kernel<2, 4, PACKED><<<unsigned((groups + 3) / 4), 256, 0, stream>>>(p);
+      gemv_kernel<2, 4, PACKED, 4><<<unsigned((groups + 3) / 4), 256, 0, stream>>>(p);
     } else {
       const int64_t groups = (ntiles + 3) / 4;
-      gemv_kernel<4, 2, PACKED><<<unsigned((groups + 3) / 4), 256, 0, stream>>>(p);
+      gemv_kernel<4, 2, PACKED, 4><<<unsigned((groups + 3) / 4), 256, 0, stream>>>(p);
     }
   } else {
-    // Few n-tiles (per-layer decode shapes): one tile per wave and K split over up to four
-    // waves, aiming for ~16 waves per CU over 256 CUs.
+    // Few n-tiles (the per-layer decode shapes: 96-768 tiles): one tile per group of `split`
+    // waves that share its K range, up to 16 waves of one workgroup, aiming for ~4096 waves over
+    // the chip's 1024 SIMDs, each with at least two k-blocks.  The weights here are 3-19 MB, so
+    // what bounds them is how many bytes are in flight: with at most four waves per tile the
+    // down projection (96 tiles) ran 384 waves and reached ~1 TB/s.
     int split = 1;
-    while (split < 4 && ntiles * split < 4096 && split * 2 <= p.KB) split *= 2;
+    while (split < 16 && ntiles * split < 4096 && split * 2 <= p.KB) split *= 2;
     p.split = split;
-    const int gpb = 4 / split;
-    gemv_kernel<1, 4, PACKED><<<unsigned((ntiles + gpb - 1) / gpb), 256, 0, stream>>>(p);
+    if (split <= 4) {
+      const int gpb = 4 / split;
+      gemv_kernel<1, 4, PACKED, 4><<<unsigned((ntiles + gpb - 1) / gpb), 256, 0, stream>>>(p);
+    } else if (split == 8) {
+      gemv_kernel<1, 4, PACKED, 8><<<unsigned(ntiles), 512, 0, stream>>>(p);
+    } else {
+      gemv_kernel<1, 4, PACKED, 16><<<unsigned(ntiles), 1024, 0, stream>>>(p);
+    }
   }
 }
 
