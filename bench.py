@@ -759,8 +759,8 @@ def main():
     M = 512
     if args.profile_sweep:
         for Ms in (3658,):
-            sweep(Ms, dev, reps=args.steps)
-        log(f"bench: ran the 141-GEMM int32 prefill sweep at M=3658 {args.steps} + 2 times")
+            ms = sweep(Ms, dev, reps=args.steps)[0]
+        log(f"bench: ran the 141-GEMM int32 prefill sweep at M=3658 {args.steps} + 2 times, {ms:.3f} ms per timed sweep")
         return 0
     if args.profile_gemv:
         K, N = workloads.LM_HEAD
