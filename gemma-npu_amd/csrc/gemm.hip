@@ -1208,16 +1208,19 @@ static void launch_dw(const GemmParams& p, int epi, bool a_packed, hipStream_t s
     launch_dw_epi<c.bm, c.nwn, c.wtn, c.ks, c.pw, c.minb, false>(p, epi, stream);
 }
 
-// Blocks of the persistent kernels: one per CU per block the registers allow, at most one per tile.
-static int persistent_blocks(int tiles, int per_cu) {
+// Compute units of the current device (256 on MI355X), read once.
+static int cu_count() {
   static int cus = [] {
     int dev = 0, n = 0;
     if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
       n = 256;
     return n;
   }();
-  return min(tiles, cus * per_cu);
+  return cus;
 }
+
+// Blocks of the persistent kernels: one per CU per block the registers allow, at most one per tile.
+static int persistent_blocks(int tiles, int per_cu) { return min(tiles, cu_count() * per_cu); }
 
 template <int BM, int BN, int WGM, int NS, int MINB, bool AP>
 static void launch_pipe_epi(GemmParams p, int epi, hipStream_t stream) {
@@ -1276,6 +1279,16 @@ static void launch_pipe(const GemmParams& p, int epi, bool a_packed, hipStream_t
 // software-pipelined persistent 256x256 kernel (26): gate/up at M = 16384 393 against 440 us, the
 // 141-GEMM sweep 6.92 -> 6.78 ms at M = 3658 and 7.64 -> 7.31 ms at M = 4096.  It is tried for
 // int32 only: its bf16 epilogues run on one wave per SIMD and lose to the two-blocks-per-CU tiles.
+// Where its 256x256 tiles leave a nearly empty last round (0 < tiles mod CUs <= CUs / 4), the
+// direct-W 128x256 tile with two blocks per CU (25) fills it: the PLE projection (N = 8960) at
+// M = 3658 (525 tiles on 256 CUs) 66.9 against 85.9 us, at M = 4096 (560 tiles) 80.7 against 92.0 us;
+// with fuller last rounds 26 keeps the lead (gate/up at M = 4096, 768 tiles: 94.3 against 101.7 us).
+static bool pipe_tail_is_short(int M, int NP) {
+  const int cus = cu_count();
+  const int tail = ((M + 255) / 256) * ((NP + 255) / 256) % cus;
+  return tail > 0 && 4 * tail <= cus;
+}
+
 int gemm_pick_config(int M, int NP, int K, int epi) {
   if (M <= 1024) {
     if (K >= 2048 && NP <= 4096) return 22;  // few 64x64 tiles, long K: four waves split the k-steps
@@ -1285,10 +1298,10 @@ int gemm_pick_config(int M, int NP, int K, int epi) {
   if (epi == EPI_GELU) return 25;  // direct-W 128x256, two blocks per CU
   if (M <= 8192) {
     if (K >= 4096 && NP <= 2048) return 24;  // long-K narrow (down): direct-W 128x256
-    if (NP >= 8192) return epi == EPI_I32 ? 26 : 0;  // wide: pipelined persistent 256x256
+    if (NP >= 8192) return epi == EPI_I32 ? (pipe_tail_is_short(M, NP) ? 25 : 26) : 0;  // wide
     return 12;
   }
-  return NP >= 8192 && epi == EPI_I32 ? 26 : 25;
+  return NP >= 8192 && epi == EPI_I32 && !pipe_tail_is_short(M, NP) ? 26 : 25;
 }
 
 int gemm_launch(const GemmParams& p, int epi, int cfg, bool a_packed, void* ws, int64_t ws_bytes,
