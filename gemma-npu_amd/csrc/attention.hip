@@ -35,6 +35,14 @@
 // distinct banks.  V blocks are loaded into registers one block ahead and written transposed
 // (V^T [D][BN + 8], 8-byte stores of 4 keys) into a 2-slot ring.  Loads past the end of K / V
 // read zero and are masked.  One barrier per block.
+#include <algorithm>
+#include <map>
+#include <mutex>
+#include <queue>
+#include <tuple>
+#include <type_traits>
+#include <vector>
+
 #include "w8a8_common.h"
 
 namespace w8a8 {
@@ -42,7 +50,9 @@ namespace w8a8 {
 typedef short v4s __attribute__((ext_vector_type(4)));
 typedef short v8s __attribute__((ext_vector_type(8)));
 
-constexpr int ATTN_NW = 8;  // waves per workgroup, 16 query rows each
+constexpr int ATTN_NW = 8;        // waves per workgroup, 16 query rows each
+constexpr int ATTN_MAX_SEG = 16;     // segments of the causal work list (= most parts of one tile)
+constexpr int ATTN_MAX_ORDER = 1536;  // items of a launch-order table (kernel arguments < 4 KiB)
 
 struct AttnParams {
   const uint16_t* q; int64_t qhs, qrs;  // bf16 [H, Tq, D] (element strides, last dim contiguous)
@@ -53,13 +63,22 @@ struct AttnParams {
   uint32_t k_bytes, v_bytes;            // extent of one KV group's K / V rows, bytes
   int H, KV, G, PB, Tq, Tk, q_start, window;
   int ntiles;                           // ceil(Tq / PB) query tiles per KV group
-  // Key splitting of the longest causal tiles: tiles >= split_from are each computed by `split`
-  // workgroups over consecutive parts of their key blocks, the last to finish merging the parts.
-  int split, split_from;
-  float* part;                          // [KV][ntiles - split_from][split] partial tiles (lane-native)
-  int* counters;                        // [KV][ntiles - split_from] arrival counts, zero between calls
+  // Work items of a KV group, in launch order (causal calls): the tiles from the longest down;
+  // segment s holds tiles seg_tile[s], seg_tile[s] - 1, .. , each computed by seg_k[s] workgroups
+  // over consecutive ranges of its key blocks (the last part to finish merges them), starting at
+  // item seg_item[s].  Split tiles come first: they are the group's nsplit_tiles longest tiles and
+  // its first nsplit_items items.  Sliding windows: one item per tile, nseg = 1.
+  int per_group, nseg, nsplit_tiles, nsplit_items;
+  int seg_tile[ATTN_MAX_SEG], seg_k[ATTN_MAX_SEG], seg_item[ATTN_MAX_SEG + 1];
+  // Launch order of the items: workgroup j * KV + g runs item order[j] of group g (item j when
+  // `ordered` is 0).
+  int ordered;
+  uint16_t order[ATTN_MAX_ORDER];
+  float* part;                          // [KV][nsplit_items] parked partial tiles, slot-major
+  int* counters;                        // [KV][nsplit_tiles] arrival counts, zero between calls
   float scale, c;                       // c = scale * log2(e)
 };
+static_assert(sizeof(AttnParams) <= 4096, "kernel arguments");
 
 template <int N>
 __device__ __forceinline__ void attn_wait_vmcnt() {
@@ -102,23 +121,25 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(AttnParams p) {
   const int qi = lane & 15, qq = lane >> 4;  // query column, lane group
 
   // ---- which KV group and query rows -------------------------------------------------------
-  // Workgroups per KV group: split * (ntiles - split_from) parts of split tiles, then one per
-  // remaining tile.  Sliding windows: neighbouring tiles (sharing their keys) on one XCD.  Causal:
-  // the longest tiles first, consecutive workgroups (other XCDs) a mix of lengths.
-  const int nsplit_tiles = p.ntiles - p.split_from;
-  const int per_group = p.split * nsplit_tiles + p.split_from;
-  const int lb = p.window > 0 ? attn_xcd_remap(blockIdx.x, p.KV * per_group) : int(blockIdx.x);
-  const int g = lb / per_group, b = lb % per_group;
-  int tile, part = 0;
+  // Sliding windows: one workgroup per tile, neighbouring tiles (sharing their keys) on one XCD.
+  // Causal: item b of every KV group in turn, so the longest items of all groups start first.
+  int g, b, tile, part = 0, nparts = 1;
   if (p.window > 0) {
-    tile = b;
-  } else if (b < p.split * nsplit_tiles) {
-    tile = p.ntiles - 1 - b / p.split;
-    part = b % p.split;
+    const int lb = attn_xcd_remap(blockIdx.x, p.KV * p.per_group);
+    g = lb / p.per_group;
+    b = tile = lb % p.per_group;
   } else {
-    tile = p.split_from - 1 - (b - p.split * nsplit_tiles);
+    g = int(blockIdx.x) % p.KV;
+    b = int(blockIdx.x) / p.KV;
+    if (p.ordered) b = p.order[b];
+    int s = 0;
+    while (s + 1 < p.nseg && b >= p.seg_item[s + 1]) ++s;
+    nparts = p.seg_k[s];
+    const int off = b - p.seg_item[s];
+    tile = p.seg_tile[s] - off / nparts;
+    part = off % nparts;
   }
-  const bool split_tile = p.split > 1 && tile >= p.split_from;
+  const bool split_tile = nparts > 1;
   const int i0 = tile * p.PB;
   const int r = wave * 16 + qi;
   const int hl = r % p.G, pl = r / p.G;
@@ -133,27 +154,14 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(AttnParams p) {
   const int klo = p.window > 0 ? max(0, pmin - p.window + 1) : 0;
   const int kb_first = (klo / BN) * BN;
   const int nblk_tile = khi >= kb_first ? (khi - kb_first) / BN + 1 : 0;
-  // this workgroup's key blocks: part `part` of `split` consecutive parts when the tile is split
-  const int n_lo = split_tile ? part * nblk_tile / p.split : 0;
-  const int n_hi = split_tile ? (part + 1) * nblk_tile / p.split : nblk_tile;
+  // this workgroup's key blocks: part `part` of `nparts` consecutive ranges
+  const int n_lo = part * nblk_tile / nparts;
+  const int n_hi = (part + 1) * nblk_tile / nparts;
   const int kb0 = kb_first + n_lo * BN;
   const int nblk = n_hi - n_lo;
 
   const __amdgpu_buffer_rsrc_t rk = make_rsrc(p.k + int64_t(g) * p.khs, p.k_bytes);
   const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.v + int64_t(g) * p.vhs, p.v_bytes);
-
-  // ---- Q fragments: B operand of v_mfma_f32_16x16x32_bf16, lane (qi, qq) holds
-  // q[row qi][32 kk + 8 qq .. + 7] ---------------------------------------------------------------
-  v8bf qf[NKK];
-  {
-    const uint16_t* qp = p.q + int64_t(h) * p.qhs + int64_t(qrow) * p.qrs + 8 * qq;
-#pragma unroll
-    for (int kk = 0; kk < NKK; ++kk) {
-      v4i t = v4i{0, 0, 0, 0};
-      if (valid) t = *reinterpret_cast<const v4i*>(qp + 32 * kk);
-      qf[kk] = __builtin_bit_cast(v8bf, t);
-    }
-  }
 
   // ---- staging ------------------------------------------------------------------------------
   // K chunk x = (u * NW + wave) * 64 + lane of a block: key row x / KCH, stored chunk x % KCH,
@@ -233,11 +241,25 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(AttnParams p) {
   const int win = p.window;
   const int Tk = p.Tk;
 
+  // the first block's K and V loads go out before the Q loads, so their latencies overlap
   if (nblk > 0) {
     issue_k(kb0, 0);
     load_v(kb0);
-    store_vt(0);
   }
+  // ---- Q fragments: B operand of v_mfma_f32_16x16x32_bf16, lane (qi, qq) holds
+  // q[row qi][32 kk + 8 qq .. + 7] ---------------------------------------------------------------
+  v8bf qf[NKK];
+  {
+    const uint16_t* qp = p.q + int64_t(h) * p.qhs + int64_t(qrow) * p.qrs + 8 * qq;
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk) {
+      v4i t = v4i{0, 0, 0, 0};
+      if (valid) t = *reinterpret_cast<const v4i*>(qp + 32 * kk);
+      qf[kk] = __builtin_bit_cast(v8bf, t);
+    }
+  }
+
+  if (nblk > 0) store_vt(0);
   for (int n = 0; n < nblk; ++n) {
     const int kb = kb0 + n * BN;
     const int slot = n & 1;
@@ -315,74 +337,121 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(AttnParams p) {
     if (n + 1 < nblk) store_vt(slot ^ 1);
   }
 
+  // ---- output: o / l per row (bf16), and the logsumexp ms ln 2 + ln l -----------------------------
+  auto row_sum = [&](float x) {  // the row's total over its four lane groups
+    x += __shfl_xor(x, 16, 64);
+    return x + __shfl_xor(x, 32, 64);
+  };
+  uint16_t* const op = p.o + int64_t(h) * p.ohs + int64_t(qrow) * p.ors + 4 * qq;
+  auto store_o = [&](int dt, v4f x, float inv) {
+    if (!valid) return;
+    v2u w;
+    w[0] = pack_bf16x2(x[0] * inv, x[1] * inv);
+    w[1] = pack_bf16x2(x[2] * inv, x[3] * inv);
+    *reinterpret_cast<v2u*>(op + 16 * dt) = w;
+  };
+  auto store_lse = [&](float m, float lt) {
+    if (valid && p.lse && qq == 0)
+      p.lse[int64_t(h) * p.Tq + qrow] = lt > 0.0f ? m * 0.69314718055994531f + __logf(lt) : -__builtin_inff();
+  };
+
   // ---- split tiles: park this part; the last part to arrive merges them in part order ---------
   // The XCDs' L2 caches are not coherent with each other, so the parts go through system-scope
   // (sc0 sc1) buffer stores and loads and the arrival count is a system-scope atomic; each
-  // thread's stores are complete (vmcnt 0) before the barrier that precedes the count.
+  // thread's stores are complete (vmcnt 0) before the barrier that precedes the count.  A parked
+  // part is slot-major (slot dt of every thread, then the next slot), so each store and load of a
+  // wave covers 1 KiB of whole cache lines: these accesses bypass the caches, and a lane-major
+  // layout (each lane's slots contiguous) made every one of them a partial-line write.
   if (split_tile) {
-    constexpr uint32_t LANE_BYTES = (NDT + 1) * 16;  // o[NDT] and (m, l) per lane
-    constexpr uint32_t PART_BYTES = NW * 64 * LANE_BYTES;
-    const int slot_tile = g * nsplit_tiles + (tile - p.split_from);
+    constexpr uint32_t SLOT_BYTES = NT * 16;              // one 16-byte slot of every thread
+    constexpr uint32_t PART_BYTES = (NDT + 1) * SLOT_BYTES;  // o[NDT] and (m, l)
+    const int first_item = g * p.nsplit_items + (b - part);
     const __amdgpu_buffer_rsrc_t rp =
-        make_rsrc(p.part + size_t(slot_tile) * p.split * (PART_BYTES / 4), uint32_t(p.split) * PART_BYTES);
-    const uint32_t lane_off = uint32_t(tid) * LANE_BYTES;
+        make_rsrc(p.part + size_t(first_item) * (PART_BYTES / 4), uint32_t(nparts) * PART_BYTES);
+    const uint32_t lane_off = uint32_t(tid) * 16u;
     {
       const uint32_t base = uint32_t(part) * PART_BYTES + lane_off;
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt)
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, o[dt]), rp, base + dt * 16, 0, 0x11);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, o[dt]), rp, base + dt * SLOT_BYTES, 0, 0x11);
       const v4f ml = v4f{ms, l, 0.0f, 0.0f};
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, ml), rp, base + NDT * 16, 0, 0x11);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, ml), rp, base + NDT * SLOT_BYTES, 0, 0x11);
     }
     __builtin_amdgcn_s_waitcnt(0);
     int* arrived = reinterpret_cast<int*>(lds);
+    const int counter = g * p.nsplit_tiles + (p.ntiles - 1 - tile);
     __syncthreads();
     if (tid == 0)
-      *arrived = __hip_atomic_fetch_add(p.counters + slot_tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      *arrived = __hip_atomic_fetch_add(p.counters + counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     __syncthreads();
-    if (*arrived != p.split - 1) return;
-    // merge: M = max of the parts' references, w_s = exp2(ms_s - M), o = sum_s w_s o_s, l likewise
-    float M = -__builtin_inff();
-    for (int sp = 0; sp < p.split; ++sp) {
-      const v4f ml = __builtin_bit_cast(
-          v4f, __builtin_amdgcn_raw_buffer_load_b128(rp, uint32_t(sp) * PART_BYTES + lane_off + NDT * 16, 0, 0x11));
-      M = fmaxf(M, ml[0]);
-    }
-    const float Ms = M == -__builtin_inff() ? 0.0f : M;
+    if (*arrived != nparts - 1) return;
+    // merge: M = max of the parts' references, w_s = exp2(ms_s - M), o = sum_s w_s o_s, l likewise,
+    // each sum in part order.  NP (4, 8 or 16) >= nparts slots per sum are loaded unconditionally
+    // -- those past the last part lie outside the buffer resource and read zero, and take weight
+    // 0, so they add +0 to sums that are never -0 -- in batches of 16 loads per thread (DG d tiles
+    // at a time), each summed and stored as soon as it arrives.
+    auto merge = [&](auto np_tag) {
+      constexpr int NP = decltype(np_tag)::value;
+      constexpr int DG = 16 / NP;
+      static_assert(NDT % DG == 0, "d tiles per batch");
+      float wsp[NP], lsp[NP];
+      float M = -__builtin_inff();
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) o[dt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    l = 0.0f;
-    for (int sp = 0; sp < p.split; ++sp) {
-      const uint32_t base = uint32_t(sp) * PART_BYTES + lane_off;
-      const v4f ml = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rp, base + NDT * 16, 0, 0x11));
-      const float w = __builtin_amdgcn_exp2f(ml[0] - Ms);
-      l = __builtin_fmaf(w, ml[1], l);
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) {
-        const v4f od = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rp, base + dt * 16, 0, 0x11));
-#pragma unroll
-        for (int i = 0; i < 4; ++i) o[dt][i] = __builtin_fmaf(w, od[i], o[dt][i]);
+      for (int sp = 0; sp < NP; ++sp) {
+        const v4f ml = __builtin_bit_cast(
+            v4f, __builtin_amdgcn_raw_buffer_load_b128(rp, uint32_t(sp) * PART_BYTES + lane_off + NDT * SLOT_BYTES,
+                                                       0, 0x11));
+        wsp[sp] = sp < nparts ? ml[0] : -__builtin_inff();
+        lsp[sp] = ml[1];
+        M = fmaxf(M, wsp[sp]);
       }
-    }
-    ms = M;
-    if (tid == 0) __hip_atomic_store(p.counters + slot_tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      const float Ms = M == -__builtin_inff() ? 0.0f : M;
+      float lm = 0.0f;
+#pragma unroll
+      for (int sp = 0; sp < NP; ++sp) {
+        wsp[sp] = sp < nparts ? __builtin_amdgcn_exp2f(wsp[sp] - Ms) : 0.0f;
+        lm = __builtin_fmaf(wsp[sp], lsp[sp], lm);
+      }
+      const float lt = row_sum(lm);
+      const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+#pragma unroll
+      for (int d0 = 0; d0 < NDT; d0 += DG) {
+        v4f od[DG][NP];
+#pragma unroll
+        for (int j = 0; j < DG; ++j)
+#pragma unroll
+          for (int sp = 0; sp < NP; ++sp)
+            od[j][sp] = __builtin_bit_cast(
+                v4f, __builtin_amdgcn_raw_buffer_load_b128(
+                         rp, uint32_t(sp) * PART_BYTES + lane_off + uint32_t(d0 + j) * SLOT_BYTES, 0, 0x11));
+#pragma unroll
+        for (int j = 0; j < DG; ++j) {
+          v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int sp = 0; sp < NP; ++sp)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(wsp[sp], od[j][sp][i], acc[i]);
+          store_o(d0 + j, acc, inv);
+        }
+      }
+      store_lse(M, lt);
+    };
+    if (tid == 0) __hip_atomic_store(p.counters + counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    if (nparts <= 4)
+      merge(std::integral_constant<int, 4>{});
+    else if (nparts <= 8)
+      merge(std::integral_constant<int, 8>{});
+    else
+      merge(std::integral_constant<int, 16>{});
+    return;
   }
 
   // ---- normalise and store --------------------------------------------------------------------
-  float lt = l + __shfl_xor(l, 16, 64);
-  lt += __shfl_xor(lt, 32, 64);
-  if (!valid) return;
+  const float lt = row_sum(l);
   const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-  uint16_t* op = p.o + int64_t(h) * p.ohs + int64_t(qrow) * p.ors + 4 * qq;
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt) {
-    v2u w;
-    w[0] = pack_bf16x2(o[dt][0] * inv, o[dt][1] * inv);
-    w[1] = pack_bf16x2(o[dt][2] * inv, o[dt][3] * inv);
-    *reinterpret_cast<v2u*>(op + 16 * dt) = w;
-  }
-  if (p.lse && qq == 0)
-    p.lse[int64_t(h) * p.Tq + qrow] = lt > 0.0f ? ms * 0.69314718055994531f + __logf(lt) : -__builtin_inff();
+  for (int dt = 0; dt < NDT; ++dt) store_o(dt, o[dt], inv);
+  store_lse(ms, lt);
 }
 
 // ---- decode: one query per head, keys split into chunks --------------------------------------
@@ -648,39 +717,195 @@ static int attn_cu_count() {
   return cus;
 }
 
-// Key splitting for causal calls whose longest query tile has far more key blocks than the chip's
-// fair share (total blocks / CUs): the tiles past that share are split into `split` parts.
-static void attn_plan(int64_t H, int64_t KV, int64_t Tq, int64_t Tk, int64_t D, int64_t q_start, int64_t window,
-                      int& ntiles, int& split, int& split_from) {
-  const int G = int(H / KV), PB = ATTN_NW * 16 / G, BN = attn_bn(D);
-  ntiles = int((Tq + PB - 1) / PB);
-  split = 1;
-  split_from = ntiles;
-  if (window > 0 || Tq == 0) return;
-  auto nblk = [&](int t) {
-    const int64_t i0 = int64_t(t) * PB;
-    const int64_t pmax = q_start + (i0 + PB < Tq ? i0 + PB : Tq) - 1;
-    const int64_t khi = pmax < Tk - 1 ? pmax : Tk - 1;
-    return int(khi / BN + 1);
-  };
-  int64_t total = 0;
-  int mx = 0;
-  for (int t = 0; t < ntiles; ++t) {
-    const int n = nblk(t);
-    total += n;
-    mx = n > mx ? n : mx;
+// ---- the causal work list ---------------------------------------------------------------------
+//
+// A causal call's query tiles differ in length (tile t sees the keys up to its last position), and
+// a workgroup holds its CU alone (the kernel's LDS), so the split of long tiles and the launch
+// order set the time.  The hardware hands workgroup i to XCD i % 8, there to the XCD's four
+// shader engines (8 CUs each) in a fixed rotation, and there to the first CU that frees, in launch
+// order: workgroup i waits in the queue of one of 32 engines (i % 32 on a 256-CU part) however
+// idle the others are.  The plan splits each tile of n key blocks into k = ceil(n / L) parts (at
+// most ATTN_MAX_SEG) for a target part length L and launches the items longest first (each
+// engine's queue then runs longest-first too); it takes the L whose list finishes first on a
+// model of that dispatch, in units of one key block: an item costs its blocks plus a fixed start
+// and output cost, a split part the time to park its result, and a merge a fixed cost plus the
+// time to read each part.  Measured per-block costs on the chip: ~3.3 us at head_dim 512 (32
+// keys) and 256 (64 keys) with every CU busy.
+
+struct AttnPlan {
+  int ntiles = 0, per_group = 0, nseg = 1, nsplit_tiles = 0, nsplit_items = 0;
+  int seg_tile[ATTN_MAX_SEG] = {}, seg_k[ATTN_MAX_SEG] = {}, seg_item[ATTN_MAX_SEG + 1] = {};
+  std::vector<uint16_t> order;  // launch order of the items (empty: item order)
+};
+
+// Model constants fitted to per-workgroup timings of the full-attention layer (head_dim 512) at
+// T = 3658 over seven part lengths, and of 256 queries at position 3402 over five.
+constexpr double ATTN_ITEM_COST = 2.0;        // start (Q, first block in flight) and output, in blocks
+constexpr double ATTN_PARK_COST = 1.5;        // parking a split part
+constexpr double ATTN_MERGE_COST = 2.0;       // a merge: fixed part ...
+constexpr double ATTN_MERGE_PART_COST = 0.5;  // ... and per part read
+
+// Key blocks tile t of a causal call sees (keys 0 .. its last position).
+static int attn_causal_blocks(int t, int PB, int BN, int64_t Tq, int64_t q_start) {
+  const int64_t end = (int64_t(t) + 1) * PB < Tq ? (int64_t(t) + 1) * PB : Tq;
+  return int((q_start + end - 1) / BN + 1);
+}
+
+// One-tile-per-workgroup list, longest tile first (sliding windows, calls without a workspace,
+// calls the split does not speed up).
+static void attn_plan_unsplit(AttnPlan& pl) {
+  pl.per_group = pl.ntiles;
+  pl.nseg = 1;
+  pl.seg_tile[0] = pl.ntiles - 1;
+  pl.seg_k[0] = 1;
+  pl.seg_item[0] = 0;
+  pl.seg_item[1] = pl.ntiles;
+  pl.nsplit_tiles = pl.nsplit_items = 0;
+  pl.order.clear();
+}
+
+// Segments of the list for target part length L (tiles from the longest down, k parts each).
+static void attn_plan_segments(const std::vector<int>& nb, int L, AttnPlan& pl) {
+  pl.nseg = 0;
+  pl.nsplit_tiles = pl.nsplit_items = 0;
+  int items = 0;
+  for (int t = pl.ntiles - 1; t >= 0; --t) {
+    int k = (nb[t] + L - 1) / L;
+    k = k < 1 ? 1 : (k > ATTN_MAX_SEG ? ATTN_MAX_SEG : k);
+    if (pl.nseg == 0 || pl.seg_k[pl.nseg - 1] != k) {
+      pl.seg_tile[pl.nseg] = t;
+      pl.seg_k[pl.nseg] = k;
+      pl.seg_item[pl.nseg] = items;
+      ++pl.nseg;
+    }
+    items += k;
+    if (k > 1) {
+      ++pl.nsplit_tiles;
+      pl.nsplit_items += k;
+    }
   }
-  const int64_t cus = attn_cu_count();
-  const int64_t fair = (total * KV + cus - 1) / cus;
-  if (mx < 8 || 4 * int64_t(mx) <= 5 * fair) return;
-  const int64_t want = (mx + fair - 1) / fair;
-  split = int(want < 8 ? want : 8);
-  int from = ntiles;
-  while (from > 0 && nblk(from - 1) > fair) --from;
-  const int max_counters = 1024;
-  if (KV * (ntiles - from) > max_counters) from = int(ntiles - max_counters / KV);
-  split_from = from;
-  if (split_from >= ntiles) split = 1;
+  pl.seg_item[pl.nseg] = items;
+  pl.per_group = items;
+  pl.order.clear();
+}
+
+// Key blocks and modelled cost of every item, in item order.
+static void attn_plan_items(const AttnPlan& pl, const std::vector<int>& nb, std::vector<int>& blocks,
+                            std::vector<double>& cost) {
+  blocks.resize(pl.per_group);
+  cost.resize(pl.per_group);
+  for (int s = 0; s < pl.nseg; ++s) {
+    const int k = pl.seg_k[s];
+    for (int item = pl.seg_item[s]; item < pl.seg_item[s + 1]; ++item) {
+      const int off = item - pl.seg_item[s], t = pl.seg_tile[s] - off / k, part = off % k;
+      blocks[item] = (part + 1) * nb[t] / k - part * nb[t] / k;
+      double c = ATTN_ITEM_COST + blocks[item];
+      if (k > 1) c += ATTN_PARK_COST + (part == k - 1 ? ATTN_MERGE_COST + ATTN_MERGE_PART_COST * k : 0.0);
+      cost[item] = c;
+    }
+  }
+}
+
+// Launch the items longest first (ties in item order), when the table fits the kernel arguments.
+static void attn_plan_order(AttnPlan& pl, const std::vector<int>& blocks) {
+  pl.order.clear();
+  if (pl.per_group > ATTN_MAX_ORDER) return;
+  pl.order.resize(pl.per_group);
+  for (int i = 0; i < pl.per_group; ++i) pl.order[i] = uint16_t(i);
+  std::stable_sort(pl.order.begin(), pl.order.end(), [&](uint16_t x, uint16_t y) { return blocks[x] > blocks[y]; });
+}
+
+// Modelled finishing time: workgroup w = j * KV + g (item order[j] of group g) joins the queue of
+// engine w % (CUs / 8), whose 8 CUs take their queue's items in turn as they free.
+static double attn_plan_makespan(const AttnPlan& pl, const std::vector<double>& cost, int KV, int cus) {
+  const int ne = cus % 8 == 0 ? cus / 8 : 1, per_e = cus / ne;
+  std::vector<std::priority_queue<double, std::vector<double>, std::greater<double>>> free_at(ne);
+  for (auto& q : free_at)
+    for (int c = 0; c < per_e; ++c) q.push(0.0);
+  double end = 0.0;
+  int64_t wg = 0;
+  for (int j = 0; j < pl.per_group; ++j) {
+    const double c = cost[pl.order.empty() ? j : pl.order[j]];
+    for (int g = 0; g < KV; ++g, ++wg) {
+      auto& q = free_at[wg % ne];
+      const double t0 = q.top();
+      q.pop();
+      q.push(t0 + c);
+      end = t0 + c > end ? t0 + c : end;
+    }
+  }
+  return end;
+}
+
+static AttnPlan attn_plan_compute(int64_t H, int64_t KV, int64_t Tq, int64_t Tk, int64_t D, int64_t q_start,
+                                  int64_t window) {
+  (void)Tk;
+  AttnPlan pl;
+  const int PB = int(ATTN_NW * 16 / (H / KV)), BN = attn_bn(D);
+  pl.ntiles = int((Tq + PB - 1) / PB);
+  attn_plan_unsplit(pl);
+  if (window > 0 || pl.ntiles == 0) return pl;
+  std::vector<int> nb(pl.ntiles);
+  int mx = 0;
+  for (int t = 0; t < pl.ntiles; ++t) {
+    nb[t] = attn_causal_blocks(t, PB, BN, Tq, q_start);
+    mx = nb[t] > mx ? nb[t] : mx;
+  }
+  const int cus = attn_cu_count();
+  // the list would not fit the model's budget of simulated items: keep one item per tile
+  if (mx < 8 || int64_t(pl.ntiles) * KV * ATTN_MAX_SEG > (int64_t(1) << 22)) return pl;
+  std::vector<int> blocks;
+  std::vector<double> cost;
+  attn_plan_items(pl, nb, blocks, cost);
+  const double unsplit = attn_plan_makespan(pl, cost, int(KV), cus);
+  // part lengths from 4 blocks up to the longest tile, ~12% apart; a split list is taken only
+  // when it beats one workgroup per tile by 2% on the model
+  double best = 0.0;
+  AttnPlan split;
+  int prev = 0;
+  for (double Lf = 4.0; Lf < mx; Lf *= 1.125) {
+    const int L = int(Lf);
+    if (L == prev) continue;
+    prev = L;
+    AttnPlan c;
+    c.ntiles = pl.ntiles;
+    attn_plan_segments(nb, L, c);
+    attn_plan_items(c, nb, blocks, cost);
+    attn_plan_order(c, blocks);
+    const double ms = attn_plan_makespan(c, cost, int(KV), cus);
+    if (split.ntiles == 0 || ms < best) {
+      best = ms;
+      split = c;
+    }
+  }
+  if (split.ntiles > 0 && best < 0.98 * unsplit) pl = split;
+  return pl;
+}
+
+// Plans are cached per call shape: the model runs once per (shape, position).
+static AttnPlan attn_plan(int64_t H, int64_t KV, int64_t Tq, int64_t Tk, int64_t D, int64_t q_start, int64_t window) {
+  static std::mutex mu;
+  static std::map<std::tuple<int64_t, int64_t, int64_t, int64_t, int64_t, int64_t>, AttnPlan> cache;
+  const auto key = std::make_tuple(H, KV, Tq, D, q_start, window);
+  {
+    std::lock_guard<std::mutex> g(mu);
+    auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+  }
+  const AttnPlan pl = attn_plan_compute(H, KV, Tq, Tk, D, q_start, window);
+  std::lock_guard<std::mutex> g(mu);
+  if (cache.size() >= 1024) cache.clear();
+  cache.emplace(key, pl);
+  return pl;
+}
+
+static int64_t attn_counter_bytes(const AttnPlan& pl, int64_t KV) {
+  return (KV * pl.nsplit_tiles * 4 + 255) / 256 * 256;
+}
+
+static int64_t attn_split_workspace(const AttnPlan& pl, int64_t KV, int64_t D) {
+  if (pl.nsplit_tiles == 0) return 0;
+  return attn_counter_bytes(pl, KV) + KV * int64_t(pl.nsplit_items) * attn_part_bytes(D);
 }
 
 extern "C" int64_t w8a8_attention_workspace_bytes(int64_t H, int64_t KV, int64_t Tq, int64_t Tk, int64_t D,
@@ -688,10 +913,7 @@ extern "C" int64_t w8a8_attention_workspace_bytes(int64_t H, int64_t KV, int64_t
   if (H < 1 || KV < 1 || H % KV != 0 || H / KV > 128 || (D != 128 && D != 256 && D != 512) || Tq < 0 ||
       q_start < 0 || window < 0 || Tk < q_start + Tq)
     return -1;
-  int ntiles, split, split_from;
-  attn_plan(H, KV, Tq, Tk, D, q_start, window, ntiles, split, split_from);
-  if (split <= 1) return 0;
-  return 4096 + KV * int64_t(ntiles - split_from) * split * attn_part_bytes(D);
+  return attn_split_workspace(attn_plan(H, KV, Tq, Tk, D, q_start, window), KV, D);
 }
 
 static int attention_launch(const uint16_t* q, int64_t q_head_stride, int64_t q_row_stride, const uint16_t* k,
@@ -730,14 +952,13 @@ static int attention_launch(const uint16_t* q, int64_t q_head_stride, int64_t q_
   p.k_bytes = uint32_t(kb); p.v_bytes = uint32_t(vb);
   p.H = int(H); p.KV = int(KV); p.G = int(H / KV); p.PB = ATTN_NW * 16 / p.G;
   p.Tq = int(Tq); p.Tk = int(Tk); p.q_start = int(q_start); p.window = int(window);
-  attn_plan(H, KV, Tq, Tk, D, q_start, window, p.ntiles, p.split, p.split_from);
+  AttnPlan pl = attn_plan(H, KV, Tq, Tk, D, q_start, window);
   p.part = nullptr;
   p.counters = nullptr;
-  if (p.split > 1) {
-    const int64_t need = 4096 + KV * int64_t(p.ntiles - p.split_from) * p.split * attn_part_bytes(D);
+  if (pl.nsplit_tiles > 0) {
+    const int64_t need = attn_split_workspace(pl, KV, D);
     if (!workspace) {
-      p.split = 1;
-      p.split_from = p.ntiles;
+      attn_plan_unsplit(pl);
     } else if (workspace_bytes < need) {
       return fail(W8A8_EINVAL, "attention: workspace of %lld bytes, %lld needed", (long long)workspace_bytes,
                   (long long)need);
@@ -745,11 +966,23 @@ static int attention_launch(const uint16_t* q, int64_t q_head_stride, int64_t q_
       return fail(W8A8_EALIGN, "attention: the workspace must be 16-byte aligned");
     } else {
       p.counters = static_cast<int*>(workspace);
-      p.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + 4096);
+      p.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + attn_counter_bytes(pl, KV));
     }
   }
+  p.ntiles = pl.ntiles;
+  p.per_group = pl.per_group;
+  p.nseg = pl.nseg;
+  p.nsplit_tiles = pl.nsplit_tiles;
+  p.nsplit_items = pl.nsplit_items;
+  for (int i = 0; i < ATTN_MAX_SEG; ++i) {
+    p.seg_tile[i] = pl.seg_tile[i];
+    p.seg_k[i] = pl.seg_k[i];
+  }
+  for (int i = 0; i <= ATTN_MAX_SEG; ++i) p.seg_item[i] = pl.seg_item[i];
+  p.ordered = pl.order.empty() ? 0 : 1;
+  for (size_t i = 0; i < pl.order.size(); ++i) p.order[i] = pl.order[i];
   p.scale = scale; p.c = scale * 1.4426950408889634f;
-  const int64_t nwg = KV * (int64_t(p.split) * (p.ntiles - p.split_from) + p.split_from);
+  const int64_t nwg = KV * int64_t(p.per_group);
   if (nwg > INT32_MAX) return fail(W8A8_ENOTSUP, "attention: too many query tiles");
   const dim3 grid{unsigned(nwg), 1, 1};
   if (D == 128)
