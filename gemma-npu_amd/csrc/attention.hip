@@ -52,6 +52,7 @@ typedef short v8s __attribute__((ext_vector_type(8)));
 
 constexpr int ATTN_NW = 8;        // waves per workgroup, 16 query rows each
 constexpr int ATTN_MAX_SEG = 16;     // segments of the causal work list (= most parts of one tile)
+constexpr int ATTN_FWD2_NW = 8;      // waves of attn_fwd2_kernel (4, one per SIMD, measured slower)
 constexpr int ATTN_MAX_ORDER = 1536;  // items of a launch-order table (kernel arguments < 4 KiB)
 
 struct AttnParams {
@@ -454,6 +455,450 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(AttnParams p) {
   store_lse(ms, lt);
 }
 
+// ---- prefill, head_dim split over the waves for P V -------------------------------------------
+//
+// attn_fwd2_kernel computes the same function as attn_fwd_kernel with the same work list and
+// moves less data through LDS per key block.  NW waves (4 or 8) own the tile's 128 rows for the S
+// phase, RT = 8 / NW row tiles of 16 each (Q of those rows in registers, K from LDS as the A
+// operand: each K fragment feeds RT MFMAs).  The softmax writes the rows' P (bf16) and rescale
+// factors to LDS, and the P V product is split over head_dim instead of rows: wave w computes O^T
+// for columns [w D/NW, (w+1) D/NW) of all 128 rows, its V^T operand read from the row-major V rows
+// (DMA'd like K, chunk x of row r stored at x ^ 2 (r & 3)) with ds_read_b64_tr_b16, its P^T operand
+// from the P rows.  Per block the workgroup reads K NW times from LDS but V and P once each, and V
+// needs no transposing pass through registers.  With 4 waves (one per SIMD, 512 registers each)
+// the waves hold Q of 32 rows and a quarter of O^T and still have registers to keep several LDS
+// reads in flight; with 8 (two per SIMD, 256 registers) head_dim 512 leaves room for one.
+//
+// Pipeline, one barrier per key block: iteration n computes P V of block n and the S phase and
+// softmax of block n + 1, while the DMAs of K(n + 2) and V(n + 1) are in flight; K, V and P each
+// have two slots (block n in slot n % 2).  Key masking is branch-free so the two phases share one
+// basic block.  The O rescale for a grown row maximum (rare: the reference exponent trails the
+// maximum lazily) is skipped unless some row of the workgroup grew past a finite maximum.
+//
+// Split tiles park O^T slot-major (slot (dt, rt) of every thread, then the next slot) followed by
+// each row's (m, l, 0, 0); the merging workgroup first turns the parts' (m, l) into per-row
+// weights in LDS, then sums each O^T slot over the parts in part order.
+template <int D, int BN, int NW>
+struct AttnFwd2Shape {
+  static constexpr int NT = NW * 64;
+  static constexpr int RT = 8 / NW;                  // 16-row tiles per wave in the S phase
+  static constexpr int KCH = D / 8;                  // 16-byte chunks per K / V row
+  static constexpr int ROW = D * 2;                  // bytes per K / V row
+  static constexpr int KV_SLOT = BN * ROW;           // one K or V block
+  static constexpr int PLD = BN + 8;                 // padded P row, elements
+  static constexpr int P_SLOT = 128 * PLD * 2;       // the 128 rows' P of one block
+  static constexpr int V_OFF = 2 * KV_SLOT, P_OFF = 4 * KV_SLOT, A_OFF = P_OFF + 2 * P_SLOT;
+  static constexpr int A_BYTES = 2 * 128 * 4 + 2 * 16 * 4 + 128 * 4;  // alpha [2][128], flags [2][16], inv [128]
+  static constexpr int LDS = A_OFF + A_BYTES;
+  static constexpr int NDW = D / NW / 16;            // 16-wide d tiles of O^T per wave
+  static constexpr int SLOTS = NDW * 8;              // O^T registers (v4f) per thread
+  static constexpr uint32_t PART_O = uint32_t(SLOTS) * NT * 16;
+  static constexpr uint32_t PART_BYTES = PART_O + 128 * 16;  // + each row's (m, l, 0, 0)
+};
+
+template <int D, int BN, int NW>
+__global__ __launch_bounds__(NW * 64, 1) void attn_fwd2_kernel(AttnParams p) {
+  using S = AttnFwd2Shape<D, BN, NW>;
+  constexpr int NT = S::NT, RT = S::RT, KCH = S::KCH, ROW = S::ROW, PLD = S::PLD, NDW = S::NDW;
+  constexpr int NKC = BN / 32;                       // 32-key chunks per block
+  constexpr int KU = BN * KCH / NT;                  // DMA instructions per thread per K or V block
+  constexpr int NKK = D / 32;                        // k-steps of S^T
+  static_assert((NW == 4 || NW == 8) && KU * NT == BN * KCH && NDW >= 1, "tiling");
+  static_assert(S::LDS <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(1024))) char lds[S::LDS];
+  float* const alpha_s = reinterpret_cast<float*>(lds + S::A_OFF);       // [2][128]
+  int* const flag_s = reinterpret_cast<int*>(lds + S::A_OFF + 1024);     // [2][16]
+  float* const inv_s = reinterpret_cast<float*>(lds + S::A_OFF + 1152);  // [128]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int qi = lane & 15, qq = lane >> 4;
+
+  // ---- which KV group and query rows (as attn_fwd_kernel) ----------------------------------
+  int g, b, tile, part = 0, nparts = 1;
+  if (p.window > 0) {
+    const int lb = attn_xcd_remap(blockIdx.x, p.KV * p.per_group);
+    g = lb / p.per_group;
+    b = tile = lb % p.per_group;
+  } else {
+    g = int(blockIdx.x) % p.KV;
+    b = int(blockIdx.x) / p.KV;
+    if (p.ordered) b = p.order[b];
+    int s = 0;
+    while (s + 1 < p.nseg && b >= p.seg_item[s + 1]) ++s;
+    nparts = p.seg_k[s];
+    const int off = b - p.seg_item[s];
+    tile = p.seg_tile[s] - off / nparts;
+    part = off % nparts;
+  }
+  const bool split_tile = nparts > 1;
+  // the lambdas below read these copies, never p itself: a reference to the kernel arguments
+  // would make the compiler copy the whole argument block (launch-order table included) to scratch
+  const int G = p.G, PB = p.PB, Tq = p.Tq;
+  const uint32_t krs2 = uint32_t(p.krs) * 2u, vrs2 = uint32_t(p.vrs) * 2u;
+  uint16_t* const out = p.o;
+  const int64_t ohs = p.ohs, ors = p.ors;
+  float* const lse = p.lse;
+  const int i0 = tile * PB;
+  // row r of the tile is (head r % G, position r / G); this lane's S-phase rows are
+  // srow[j] = 16 (RT wave + j) + qi
+  auto row_valid = [&](int r) __attribute__((always_inline)) { return r / G < PB && i0 + r / G < Tq; };
+  int srow[RT], pos[RT];
+  bool valid[RT];
+#pragma unroll
+  for (int j = 0; j < RT; ++j) {
+    srow[j] = 16 * (RT * wave + j) + qi;
+    valid[j] = row_valid(srow[j]);
+    pos[j] = p.q_start + i0 + srow[j] / G;
+  }
+
+  const int pmin = p.q_start + i0;
+  const int pmax = p.q_start + min(i0 + PB, Tq) - 1;
+  const int khi = min(pmax, p.Tk - 1);
+  const int klo = p.window > 0 ? max(0, pmin - p.window + 1) : 0;
+  const int kb_first = (klo / BN) * BN;
+  const int nblk_tile = khi >= kb_first ? (khi - kb_first) / BN + 1 : 0;
+  const int n_lo = part * nblk_tile / nparts;
+  const int n_hi = (part + 1) * nblk_tile / nparts;
+  const int kb0 = kb_first + n_lo * BN;
+  const int nblk = n_hi - n_lo;
+
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(p.k + int64_t(g) * p.khs, p.k_bytes);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.v + int64_t(g) * p.vhs, p.v_bytes);
+
+  // ---- DMA offsets: chunk x = (u NW + wave) 64 + lane of a block is key row x / KCH, stored
+  // chunk x % KCH; K holds source chunk (x % KCH) ^ swz(row), swz(row) = (row & 3) | ((row >> 1)
+  // & 12), V holds source chunk (x % KCH) ^ 2 (row & 3).
+  uint32_t koff[KU], voff[KU];
+#pragma unroll
+  for (int u = 0; u < KU; ++u) {
+    const int x = (u * NW + wave) * 64 + lane;
+    const int row = x / KCH, cs = x % KCH;
+    koff[u] = uint32_t(row) * krs2 + uint32_t(cs ^ ((row & 3) | ((row >> 1) & 12))) * 16u;
+    voff[u] = uint32_t(row) * vrs2 + uint32_t(cs ^ (2 * (row & 3))) * 16u;
+  }
+  auto issue_k = [&](int kb, int slot) __attribute__((always_inline)) {
+    char* base = lds + slot * S::KV_SLOT;
+    const uint32_t rowoff = uint32_t(kb) * krs2;
+#pragma unroll
+    for (int u = 0; u < KU; ++u) attn_dma16(rk, base + (u * NW + wave) * 1024, rowoff + koff[u]);
+  };
+  auto issue_v = [&](int kb, int slot) __attribute__((always_inline)) {
+    char* base = lds + S::V_OFF + slot * S::KV_SLOT;
+    const uint32_t rowoff = uint32_t(kb) * vrs2;
+#pragma unroll
+    for (int u = 0; u < KU; ++u) attn_dma16(rv, base + (u * NW + wave) * 1024, rowoff + voff[u]);
+  };
+
+  // ---- first blocks' loads, then Q (B operand: lane (qi, qq) of row tile j holds
+  // q[srow[j]][32 kk + 8 qq .. + 7]) ------------------------------------------------------------
+  if (nblk > 0) {
+    issue_k(kb0, 0);
+    issue_v(kb0, 0);
+  }
+  v8bf qf[RT][NKK];
+#pragma unroll
+  for (int j = 0; j < RT; ++j) {
+    const uint16_t* qp = p.q + int64_t(g * G + srow[j] % G) * p.qhs + int64_t(i0 + srow[j] / G) * p.qrs + 8 * qq;
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk) {
+      v4i t = v4i{0, 0, 0, 0};
+      if (valid[j]) t = *reinterpret_cast<const v4i*>(qp + 32 * kk);
+      qf[j][kk] = __builtin_bit_cast(v8bf, t);
+    }
+  }
+  if (nblk > 1) issue_k(kb0 + BN, 1);
+
+  // ---- S phase operand offsets (K rows of S^T tile 2c + hh, as attn_fwd_kernel) ------------
+  const int krow = 8 * (qi >> 2) + (qi & 3);
+  uint32_t kofs[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) kofs[j] = uint32_t(krow * KCH * 16 + (((4 * j + qq) ^ qi) * 16));
+
+  // running softmax state of rows srow[j]: reference exponent ms (log2 units, trailing the maximum
+  // by at most 8) and this lane group's share l of sum exp2(s c - ms)
+  float ms[RT], l[RT];
+#pragma unroll
+  for (int j = 0; j < RT; ++j) {
+    ms[j] = -__builtin_inff();
+    l[j] = 0.0f;
+  }
+  const float c = p.c;
+  const int win = p.window;
+  const int Tk = p.Tk;
+
+  // S^T of block n (K slot n % 2), softmax, P rows and rescale factors into slot n % 2
+  auto s_phase = [&](int n) __attribute__((always_inline)) {
+    const int kb = kb0 + n * BN;
+    const int slot = n & 1;
+    v4f s[RT][2 * NKC];
+    const char* kbase = lds + slot * S::KV_SLOT;
+#pragma unroll
+    for (int j = 0; j < RT; ++j)
+#pragma unroll
+      for (int t = 0; t < 2 * NKC; ++t) s[j][t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk)
+#pragma unroll
+      for (int t = 0; t < 2 * NKC; ++t) {
+        const int row0 = 32 * (t >> 1) + 4 * (t & 1);
+        const v8bf a = *reinterpret_cast<const v8bf*>(kbase + kofs[kk % 4] + row0 * (KCH * 16) + (kk / 4) * 256);
+#pragma unroll
+        for (int j = 0; j < RT; ++j) s[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[j][kk], s[j][t], 0, 0, 0);
+      }
+    bool any = false;
+#pragma unroll
+    for (int j = 0; j < RT; ++j) {
+      float bm = -__builtin_inff();
+#pragma unroll
+      for (int t = 0; t < 2 * NKC; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = kb + 32 * (t >> 1) + 8 * qq + 4 * (t & 1) + i;
+          const bool vis = valid[j] && key <= pos[j] && key < Tk && (win == 0 || pos[j] - key < win);
+          s[j][t][i] = vis ? s[j][t][i] : -__builtin_inff();
+          bm = fmaxf(bm, s[j][t][i]);
+        }
+      bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
+      bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+      const float bmc = bm * c;
+      const bool grow = bmc > ms[j] + 8.0f;  // false while every key so far is masked (bmc = -inf)
+      const bool had = ms[j] != -__builtin_inff();
+      const float alpha = !grow ? 1.0f : (had ? __builtin_amdgcn_exp2f(ms[j] - bmc) : 0.0f);
+      ms[j] = grow ? bmc : ms[j];
+      const float mref = ms[j] == -__builtin_inff() ? 0.0f : ms[j];
+      float bs = 0.0f;
+      uint16_t* prow = reinterpret_cast<uint16_t*>(lds + S::P_OFF + slot * S::P_SLOT) + srow[j] * PLD + 8 * qq;
+#pragma unroll
+      for (int ch = 0; ch < NKC; ++ch) {
+        v8bf pb;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float pe = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j][2 * ch + (e >> 2)][e & 3], c, -mref));
+          bs += pe;
+          pb[e] = (__bf16)pe;
+        }
+        *reinterpret_cast<v8bf*>(prow + 32 * ch) = pb;
+      }
+      l[j] = l[j] * alpha + bs;
+      if (qq == 0) alpha_s[slot * 128 + srow[j]] = alpha;
+      any = any || (grow && had);
+    }
+    // a row whose maximum grew past a finite one needs its O rescaled (a row that had none has O = 0)
+    const bool wave_any = __builtin_amdgcn_ballot_w64(any) != 0;
+    if (lane == 0) flag_s[slot * 16 + wave] = wave_any ? 1 : 0;
+  };
+
+  // ---- O^T for columns [wave D/NW, (wave+1) D/NW) of all rows: o[dt][rt] register i of lane
+  // (qi, qq) is d = wave D/NW + 16 dt + 4 qq + i, row 16 rt + qi -------------------------------
+  v4f o[NDW][8];
+#pragma unroll
+  for (int dt = 0; dt < NDW; ++dt)
+#pragma unroll
+    for (int rt = 0; rt < 8; ++rt) o[dt][rt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  const int vsrc = qq * 8 + (qi >> 2);  // this lane's V source row within a 32-key chunk (+4)
+  auto pv_phase = [&](int n) __attribute__((always_inline)) {
+    const int slot = n & 1;
+    const int* fl = flag_s + slot * 16;
+    int f = 0;
+#pragma unroll
+    for (int w4 = 0; w4 < NW; w4 += 4) {
+      const v4i fv = *reinterpret_cast<const v4i*>(fl + w4);
+      f |= fv[0] | fv[1] | fv[2] | fv[3];
+    }
+    if (f != 0) {
+#pragma unroll
+      for (int rt = 0; rt < 8; ++rt) {
+        const float a = alpha_s[slot * 128 + rt * 16 + qi];
+#pragma unroll
+        for (int dt = 0; dt < NDW; ++dt) o[dt][rt] *= a;
+      }
+    }
+    const char* vl = lds + S::V_OFF + slot * S::KV_SLOT;
+    const uint16_t* pl = reinterpret_cast<const uint16_t*>(lds + S::P_OFF + slot * S::P_SLOT);
+#pragma unroll
+    for (int ch = 0; ch < NKC; ++ch) {
+      v8bf va[NDW];
+#pragma unroll
+      for (int dt = 0; dt < NDW; ++dt) {
+        const int d = wave * (D / NW) + 16 * dt + 4 * (qi & 3);  // this lane's 4 source columns
+        const int r0 = 32 * ch + vsrc, r1 = r0 + 4;
+        const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(
+            vl + r0 * ROW + (((d >> 3) ^ (2 * (r0 & 3))) * 16) + (d & 7) * 2));
+        const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(
+            vl + r1 * ROW + (((d >> 3) ^ (2 * (r1 & 3))) * 16) + (d & 7) * 2));
+        va[dt] = __builtin_bit_cast(v8bf, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      }
+#pragma unroll
+      for (int rt = 0; rt < 8; ++rt) {
+        const v8bf pb = *reinterpret_cast<const v8bf*>(pl + (rt * 16 + qi) * PLD + 32 * ch + 8 * qq);
+#pragma unroll
+        for (int dt = 0; dt < NDW; ++dt) o[dt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt], pb, o[dt][rt], 0, 0, 0);
+      }
+    }
+  };
+
+  // ---- main loop --------------------------------------------------------------------------
+  // iteration n: P V of block n and the S phase of block n + 1 (one basic block, so their MFMAs
+  // and LDS reads interleave), with K(n + 2) and V(n + 1) loading into the slots freed by
+  // iteration n - 1
+  if (nblk > 0) {
+    if (nblk > 1)
+      attn_wait_vmcnt<KU>();  // K(0), V(0) and Q have landed; K(1) may be in flight
+    else
+      attn_wait_vmcnt<0>();
+    __syncthreads();
+    s_phase(0);
+  }
+  for (int n = 0; n + 1 < nblk; ++n) {
+    attn_wait_vmcnt<0>();
+    __syncthreads();  // P(n) of every row; K(n + 1) and V(n) in LDS; the other slots free
+    if (n + 2 < nblk) issue_k(kb0 + (n + 2) * BN, n & 1);
+    issue_v(kb0 + (n + 1) * BN, (n + 1) & 1);
+    pv_phase(n);
+    s_phase(n + 1);
+  }
+  if (nblk > 0) {
+    attn_wait_vmcnt<0>();
+    __syncthreads();
+    pv_phase(nblk - 1);
+  }
+
+  // ---- output ---------------------------------------------------------------------------------
+  const int d_lane = wave * (D / NW) + 4 * qq;  // + 16 dt + i
+  auto out_row = [&](int r) __attribute__((always_inline)) {  // output row pointer of tile row r
+    const int hl = r % G, pr = r / G;
+    return out + int64_t(g * G + hl) * ohs + int64_t(i0 + pr) * ors;
+  };
+  auto store_slot = [&](int dt, int rt, v4f x, float inv) __attribute__((always_inline)) {
+    const int r = rt * 16 + qi;
+    if (!row_valid(r)) return;
+    v2u w;
+    w[0] = pack_bf16x2(x[0] * inv, x[1] * inv);
+    w[1] = pack_bf16x2(x[2] * inv, x[3] * inv);
+    *reinterpret_cast<v2u*>(out_row(r) + d_lane + 16 * dt) = w;
+  };
+  auto store_lse = [&](int r, float m, float lt) __attribute__((always_inline)) {
+    if (row_valid(r) && lse)
+      lse[int64_t(g * G + r % G) * Tq + i0 + r / G] = lt > 0.0f ? m * 0.69314718055994531f + __logf(lt) : -__builtin_inff();
+  };
+  float lt[RT];
+#pragma unroll
+  for (int j = 0; j < RT; ++j) {
+    lt[j] = l[j] + __shfl_xor(l[j], 16, 64);
+    lt[j] += __shfl_xor(lt[j], 32, 64);
+  }
+
+  if (split_tile) {
+    // park O^T slot-major and each row's (ms, l); the last part to arrive merges in part order
+    const int first_item = g * p.nsplit_items + (b - part);
+    const __amdgpu_buffer_rsrc_t rp =
+        make_rsrc(p.part + size_t(first_item) * (S::PART_BYTES / 4), uint32_t(nparts) * S::PART_BYTES);
+    const uint32_t lane_off = uint32_t(tid) * 16u;
+    {
+      const uint32_t base = uint32_t(part) * S::PART_BYTES;
+#pragma unroll
+      for (int dt = 0; dt < NDW; ++dt)
+#pragma unroll
+        for (int rt = 0; rt < 8; ++rt)
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, o[dt][rt]), rp,
+                                                 base + uint32_t(dt * 8 + rt) * (NT * 16) + lane_off, 0, 0x11);
+      if (qq == 0) {
+#pragma unroll
+        for (int j = 0; j < RT; ++j) {
+          const v4f ml = v4f{ms[j], lt[j], 0.0f, 0.0f};
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, ml), rp,
+                                                 base + S::PART_O + uint32_t(srow[j]) * 16u, 0, 0x11);
+        }
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    int* arrived = reinterpret_cast<int*>(lds);
+    const int counter = g * p.nsplit_tiles + (p.ntiles - 1 - tile);
+    __syncthreads();
+    if (tid == 0)
+      *arrived = __hip_atomic_fetch_add(p.counters + counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __syncthreads();
+    if (*arrived != nparts - 1) return;
+    if (tid == 0) __hip_atomic_store(p.counters + counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    // per-row weights w_s = exp2(m_s - M) (0 past the last part) into LDS, 1 / sum_s w_s l_s too
+    float* const wts = reinterpret_cast<float*>(lds + 1024);  // [ATTN_MAX_SEG][128], over the K slots
+    if (tid < 128) {
+      float M = -__builtin_inff();
+      float mv[ATTN_MAX_SEG], lv[ATTN_MAX_SEG];
+#pragma unroll
+      for (int sp = 0; sp < ATTN_MAX_SEG; ++sp) {
+        // (16-byte records: this compiler lowers __builtin_amdgcn_raw_buffer_load_b64 to a one-dword load)
+        const v4f ml = sp < nparts ? __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(
+                                         rp, uint32_t(sp) * S::PART_BYTES + S::PART_O + uint32_t(tid) * 16u, 0, 0x11))
+                                   : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        mv[sp] = sp < nparts ? ml[0] : -__builtin_inff();
+        lv[sp] = ml[1];
+        M = fmaxf(M, mv[sp]);
+      }
+      const float Ms = M == -__builtin_inff() ? 0.0f : M;
+      float L = 0.0f;
+#pragma unroll
+      for (int sp = 0; sp < ATTN_MAX_SEG; ++sp) {
+        const float w = sp < nparts ? __builtin_amdgcn_exp2f(mv[sp] - Ms) : 0.0f;
+        wts[sp * 128 + tid] = w;
+        L = __builtin_fmaf(w, lv[sp], L);
+      }
+      inv_s[tid] = L > 0.0f ? 1.0f / L : 0.0f;
+      store_lse(tid, M, L);
+    }
+    __syncthreads();
+    auto merge = [&](auto np_tag) __attribute__((always_inline)) {
+      constexpr int NP = decltype(np_tag)::value;
+      constexpr int DG = 16 / NP;  // O^T slots per batch of 16 loads
+      static_assert((NDW * 8) % DG == 0, "slots per batch");
+#pragma unroll
+      for (int s0 = 0; s0 < NDW * 8; s0 += DG) {
+        v4f od[DG][NP];
+#pragma unroll
+        for (int j = 0; j < DG; ++j)
+#pragma unroll
+          for (int sp = 0; sp < NP; ++sp)
+            od[j][sp] = __builtin_bit_cast(
+                v4f, __builtin_amdgcn_raw_buffer_load_b128(
+                         rp, uint32_t(sp) * S::PART_BYTES + uint32_t(s0 + j) * (NT * 16) + lane_off, 0, 0x11));
+#pragma unroll
+        for (int j = 0; j < DG; ++j) {
+          const int dt = (s0 + j) / 8, rt = (s0 + j) % 8;
+          v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int sp = 0; sp < NP; ++sp) {
+            const float w = wts[sp * 128 + rt * 16 + qi];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(w, od[j][sp][i], acc[i]);
+          }
+          store_slot(dt, rt, acc, inv_s[rt * 16 + qi]);
+        }
+      }
+    };
+    if (nparts <= 4)
+      merge(std::integral_constant<int, 4>{});
+    else if (nparts <= 8)
+      merge(std::integral_constant<int, 8>{});
+    else
+      merge(std::integral_constant<int, 16>{});
+    return;
+  }
+
+  // ---- normalise and store ------------------------------------------------------------------
+#pragma unroll
+  for (int j = 0; j < RT; ++j) {
+    if (qq == 0) {
+      inv_s[srow[j]] = lt[j] > 0.0f ? 1.0f / lt[j] : 0.0f;
+      store_lse(srow[j], ms[j], lt[j]);
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int dt = 0; dt < NDW; ++dt)
+#pragma unroll
+    for (int rt = 0; rt < 8; ++rt) store_slot(dt, rt, o[dt][rt], inv_s[rt * 16 + qi]);
+}
+
 // ---- decode: one query per head, keys split into chunks --------------------------------------
 //
 // The reference's decode step (local_attn.py:44-68, _split_kv_decode; local_sdpa's decode branch,
@@ -702,7 +1147,11 @@ using namespace w8a8;
 
 static int attn_bn(int64_t D) { return D == 128 ? 128 : (D == 256 ? 64 : 32); }
 
-static int64_t attn_part_bytes(int64_t D) { return int64_t(ATTN_NW) * 64 * (D / 16 + 1) * 16; }
+// Bytes of one parked split part: attn_fwd2_kernel's (head_dim 512) or attn_fwd_kernel's.
+static int64_t attn_part_bytes(int64_t D) {
+  if (D == 512) return AttnFwd2Shape<512, 32, ATTN_FWD2_NW>::PART_BYTES;
+  return int64_t(ATTN_NW) * 64 * (D / 16 + 1) * 16;
+}
 
 static int attn_cu_count() {
   static int cus = 0;
@@ -990,7 +1439,7 @@ static int attention_launch(const uint16_t* q, int64_t q_head_stride, int64_t q_
   else if (D == 256)
     attn_fwd_kernel<256, 64, ATTN_NW><<<grid, dim3{ATTN_NW * 64, 1, 1}, 0, stream>>>(p);
   else
-    attn_fwd_kernel<512, 32, ATTN_NW><<<grid, dim3{ATTN_NW * 64, 1, 1}, 0, stream>>>(p);
+    attn_fwd2_kernel<512, 32, ATTN_FWD2_NW><<<grid, dim3{ATTN_FWD2_NW * 64, 1, 1}, 0, stream>>>(p);
   return check_launch("attention_bf16");
 }
 
