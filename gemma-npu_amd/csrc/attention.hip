@@ -636,15 +636,24 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd2_kernel(AttnParams p) {
     for (int j = 0; j < RT; ++j)
 #pragma unroll
       for (int t = 0; t < 2 * NKC; ++t) s[j][t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    // K fragments through a ring of KR registers: fragment i + KR is read once fragment i has fed
+    // its MFMAs, so KR reads are in flight while the MFMAs run
+    constexpr int NR = NKK * 2 * NKC, KR = 3;
+    auto kfrag = [&](int i) __attribute__((always_inline)) {
+      const int kk = i / (2 * NKC), t = i % (2 * NKC);
+      const int row0 = 32 * (t >> 1) + 4 * (t & 1);
+      return *reinterpret_cast<const v8bf*>(kbase + kofs[kk % 4] + row0 * (KCH * 16) + (kk / 4) * 256);
+    };
+    v8bf kf[KR];
 #pragma unroll
-    for (int kk = 0; kk < NKK; ++kk)
+    for (int i = 0; i < KR; ++i) kf[i] = kfrag(i);
 #pragma unroll
-      for (int t = 0; t < 2 * NKC; ++t) {
-        const int row0 = 32 * (t >> 1) + 4 * (t & 1);
-        const v8bf a = *reinterpret_cast<const v8bf*>(kbase + kofs[kk % 4] + row0 * (KCH * 16) + (kk / 4) * 256);
+    for (int i = 0; i < NR; ++i) {
+      const int kk = i / (2 * NKC), t = i % (2 * NKC);
 #pragma unroll
-        for (int j = 0; j < RT; ++j) s[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[j][kk], s[j][t], 0, 0, 0);
-      }
+      for (int j = 0; j < RT; ++j) s[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[i % KR], qf[j][kk], s[j][t], 0, 0, 0);
+      if (i + KR < NR) kf[i % KR] = kfrag(i + KR);
+    }
     bool any = false;
 #pragma unroll
     for (int j = 0; j < RT; ++j) {
