@@ -844,6 +844,12 @@ def main():
                 attn.attention(q, k, v, 0, W, out=out)
             torch.cuda.synchronize()
             log(f"bench: ran {name} attention (T={ATTN_T}, head_dim {D}, window {W}) {args.steps} times")
+            # the reference pipeline's last micro-batch of this layer kind (as attention_bench)
+            qs = ATTN_T - (512 if W else 256)
+            for _ in range(args.steps):
+                attn.attention(q[:, qs:], k, v, qs, W, out=out[:, qs:])
+            torch.cuda.synchronize()
+            log(f"bench: ran {name} attention for {ATTN_T - qs} queries at position {qs} {args.steps} times")
         return 0
     if args.profile_chain:
         c = build_chain(M, dev)

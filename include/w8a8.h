@@ -328,16 +328,19 @@ int w8a8_attention_bf16(const uint16_t *q, int64_t q_head_stride, int64_t q_row_
                         int64_t o_row_stride, float *lse, hipStream_t stream);
 
 /* Bytes of the workspace w8a8_attention_ws_bf16 uses for these arguments (0: it splits no query
- * tile and needs none; -1: invalid arguments).  Causal calls whose longest query tiles hold far more
- * key blocks than the chip's fair share (at T = 3658, head_dim 512: 115 blocks of 32 keys against
- * ~52) split those tiles' keys over several workgroups, the last to finish merging the parts by
- * their logsumexp. */
+ * tile and needs none; -1: invalid arguments).  For causal calls the host plans the work list: long
+ * query tiles' keys are split over several workgroups (the last to finish merging the parts by their
+ * logsumexp) when a model of the chip's workgroup dispatch says the split finishes sooner (at
+ * T = 3658, head_dim 512: 229 tiles of 1 to 115 blocks of 32 keys become 520 items of at most 33
+ * blocks), and the items are launched longest first.  The plan depends on the arguments and the
+ * device's CU count only, so this size is stable for a shape. */
 int64_t w8a8_attention_workspace_bytes(int64_t H, int64_t KV, int64_t Tq, int64_t Tk, int64_t D, int64_t q_start,
                                        int64_t window);
 
 /* w8a8_attention_bf16 with a workspace for splitting long causal tiles: device memory of at least
- * w8a8_attention_workspace_bytes(...) bytes, 16-byte aligned, ZERO-FILLED BEFORE ITS FIRST USE (its
- * first 4 KiB are arrival counters that every call leaves zero; the rest is scratch).  Calls that
+ * w8a8_attention_workspace_bytes(...) bytes, 16-byte aligned, ZERO-FILLED BEFORE ITS FIRST USE (it
+ * starts with one arrival counter per split tile, rounded up to 256 bytes, that every call leaves
+ * zero; the rest is scratch for the parked parts).  Calls that
  * share a workspace must be ordered (one stream).  NULL behaves as w8a8_attention_bf16.  The parts
  * are merged in a fixed order, so results are deterministic; they may differ from the unsplit
  * call's in the last bits. */
