@@ -15,7 +15,8 @@ TOP/s over the step's 2*M*N*K ops with inputs resident in HBM.  The JSON line al
 roofline of the dominant kernel (the gate_up GEMM, timed live with HIP events on the launch
 stream), the host CPU's torch._int_mm on the same GEMMs (the reference's --backend cpu-int8
 path, pipeline.py:237), and `extra`: the same step captured in one HIP graph and replayed
-(checked bit for bit against the eager run), the full-prefill GEMM sweep at M=3658 / 4096, the M=16384
+(checked bit for bit against the eager run; also 50 steps per graph, which spreads a replay's fixed
+launch cost), the full-prefill GEMM sweep at M=3658 / 4096, the M=16384
 stress GEMMs, the int32 GEMMs of those shapes against hipBLASLt (torch._int_mm on the same GPU, cold
 weights), a decoder layer's whole linear path on the device (the six GEMMs with the fused
 norm / RoPE / GELU / residual / quant kernels between them, one HIP graph), and the decode GEMV
@@ -901,6 +902,9 @@ def main():
             raise RuntimeError(f"timed layer step output differs from the first run for {g['name']}")
     graph_ms = event_time_ms(graph.replay, args.steps, args.warmup)
     log(f"bench: graph-replayed layer step {graph_ms * 1e3:.1f} us")
+    # the same step 50 times in one graph: a replay's fixed launch cost spread over 50 steps
+    graph50_ms = graph_time_ms(lambda: layer_step(groups, ws), dev, launches=50, reps=4)
+    log(f"bench: layer step from a 50-step graph {graph50_ms * 1e3:.1f} us")
 
     # ---- dominant kernel: the gate_up GEMM with fused GELU epilogue ----------------------
     gu = next(g for g in groups if g["name"] == "gate_up")
@@ -939,6 +943,7 @@ def main():
         log(f"bench: cpu _int_mm layer {cpu_ms:.1f} ms")
 
     extra = {"graph_layer_step_us": round(graph_ms * 1e3, 1),
+             "graph_layer_step_us_50_per_replay": round(graph50_ms * 1e3, 1),
              "gemm_us_m512": {k: round(v * 1e3, 2) for k, v in per_ms.items()}}
     if not args.no_extra:
         for Ms in (3658, 4096):

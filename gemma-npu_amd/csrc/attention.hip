@@ -71,13 +71,13 @@ struct AttnParams {
   // its first nsplit_items items.  Sliding windows: one item per tile, nseg = 1.
   int per_group, nseg, nsplit_tiles, nsplit_items;
   int seg_tile[ATTN_MAX_SEG], seg_k[ATTN_MAX_SEG], seg_item[ATTN_MAX_SEG + 1];
-  // Launch order of the items: workgroup j * KV + g runs item order[j] of group g (item j when
-  // `ordered` is 0).
-  int ordered;
-  uint16_t order[ATTN_MAX_ORDER];
   float* part;                          // [KV][nsplit_items] parked partial tiles, slot-major
   int* counters;                        // [KV][nsplit_tiles] arrival counts, zero between calls
   float scale, c;                       // c = scale * log2(e)
+  // Launch order of the items: workgroup j * KV + g runs item order[j] of group g (item j when
+  // `ordered` is 0).  Last, after every pointer and scalar.
+  int ordered;
+  uint16_t order[ATTN_MAX_ORDER];
 };
 static_assert(sizeof(AttnParams) <= 4096, "kernel arguments");
 
@@ -133,12 +133,14 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(AttnParams p) {
     g = int(blockIdx.x) % p.KV;
     b = int(blockIdx.x) / p.KV;
     if (p.ordered) b = p.order[b];
+    if (b >= p.per_group) return;  // (never: the order table is a permutation of the items)
     int s = 0;
     while (s + 1 < p.nseg && b >= p.seg_item[s + 1]) ++s;
     nparts = p.seg_k[s];
     const int off = b - p.seg_item[s];
     tile = p.seg_tile[s] - off / nparts;
     part = off % nparts;
+    if (tile < 0 || (nparts > 1 && b >= p.nsplit_items)) return;  // (never, as above)
   }
   const bool split_tile = nparts > 1;
   const int i0 = tile * p.PB;
@@ -523,12 +525,14 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd2_kernel(AttnParams p) {
     g = int(blockIdx.x) % p.KV;
     b = int(blockIdx.x) / p.KV;
     if (p.ordered) b = p.order[b];
+    if (b >= p.per_group) return;  // (never: the order table is a permutation of the items)
     int s = 0;
     while (s + 1 < p.nseg && b >= p.seg_item[s + 1]) ++s;
     nparts = p.seg_k[s];
     const int off = b - p.seg_item[s];
     tile = p.seg_tile[s] - off / nparts;
     part = off % nparts;
+    if (tile < 0 || (nparts > 1 && b >= p.nsplit_items)) return;  // (never, as above)
   }
   const bool split_tile = nparts > 1;
   // the lambdas below read these copies, never p itself: a reference to the kernel arguments
@@ -1190,6 +1194,11 @@ static int attn_cu_count() {
 // time to read each part.  Measured per-block costs on the chip: ~3.3 us at head_dim 512 (32
 // keys) and 256 (64 keys) with every CU busy.
 
+// A split workspace starts with ATTN_COUNTER_BYTES of arrival counters at fixed offsets, whatever
+// the plan: every call leaves its counters zero, and calls of different shapes share a workspace
+// (one per stream), so no call's parked parts may overlap another plan's counters.
+constexpr int64_t ATTN_COUNTER_BYTES = 65536;
+
 struct AttnPlan {
   int ntiles = 0, per_group = 0, nseg = 1, nsplit_tiles = 0, nsplit_items = 0;
   int seg_tile[ATTN_MAX_SEG] = {}, seg_k[ATTN_MAX_SEG] = {}, seg_item[ATTN_MAX_SEG + 1] = {};
@@ -1328,6 +1337,7 @@ static AttnPlan attn_plan_compute(int64_t H, int64_t KV, int64_t Tq, int64_t Tk,
     AttnPlan c;
     c.ntiles = pl.ntiles;
     attn_plan_segments(nb, L, c);
+    if (KV * c.nsplit_tiles * 4 > ATTN_COUNTER_BYTES) continue;  // one counter per split tile
     attn_plan_items(c, nb, blocks, cost);
     attn_plan_order(c, blocks);
     const double ms = attn_plan_makespan(c, cost, int(KV), cus);
@@ -1357,13 +1367,9 @@ static AttnPlan attn_plan(int64_t H, int64_t KV, int64_t Tq, int64_t Tk, int64_t
   return pl;
 }
 
-static int64_t attn_counter_bytes(const AttnPlan& pl, int64_t KV) {
-  return (KV * pl.nsplit_tiles * 4 + 255) / 256 * 256;
-}
-
 static int64_t attn_split_workspace(const AttnPlan& pl, int64_t KV, int64_t D) {
   if (pl.nsplit_tiles == 0) return 0;
-  return attn_counter_bytes(pl, KV) + KV * int64_t(pl.nsplit_items) * attn_part_bytes(D);
+  return ATTN_COUNTER_BYTES + KV * int64_t(pl.nsplit_items) * attn_part_bytes(D);
 }
 
 extern "C" int64_t w8a8_attention_workspace_bytes(int64_t H, int64_t KV, int64_t Tq, int64_t Tk, int64_t D,
@@ -1424,7 +1430,7 @@ static int attention_launch(const uint16_t* q, int64_t q_head_stride, int64_t q_
       return fail(W8A8_EALIGN, "attention: the workspace must be 16-byte aligned");
     } else {
       p.counters = static_cast<int*>(workspace);
-      p.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + attn_counter_bytes(pl, KV));
+      p.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + ATTN_COUNTER_BYTES);
     }
   }
   p.ntiles = pl.ntiles;

@@ -338,9 +338,9 @@ int64_t w8a8_attention_workspace_bytes(int64_t H, int64_t KV, int64_t Tq, int64_
                                        int64_t window);
 
 /* w8a8_attention_bf16 with a workspace for splitting long causal tiles: device memory of at least
- * w8a8_attention_workspace_bytes(...) bytes, 16-byte aligned, ZERO-FILLED BEFORE ITS FIRST USE (it
- * starts with one arrival counter per split tile, rounded up to 256 bytes, that every call leaves
- * zero; the rest is scratch for the parked parts).  Calls that
+ * w8a8_attention_workspace_bytes(...) bytes, 16-byte aligned, ZERO-FILLED BEFORE ITS FIRST USE (its
+ * first 64 KiB are arrival counters that every call leaves zero, at the same offsets for every
+ * shape, so one workspace serves calls of any shapes; the rest is scratch for the parked parts).  Calls that
  * share a workspace must be ordered (one stream).  NULL behaves as w8a8_attention_bf16.  The parts
  * are merged in a fixed order, so results are deterministic; they may differ from the unsplit
  * call's in the last bits. */

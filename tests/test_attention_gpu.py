@@ -166,6 +166,27 @@ def test_split_tiles_and_the_unsplit_entry():
     assert np.allclose(lse_u[:, T - 200:].cpu().numpy(), lse_ref, rtol=1e-5, atol=1e-4)
 
 
+def test_split_workspace_shared_across_shapes():
+    """Split calls of different shapes share the stream's workspace.  A whole-prompt causal call at
+    head_dim 512 (T = 3658: ~190 split tiles), then 256 queries at the end of the prompt (16 split
+    tiles), then the first call again: the second plan parks its parts past the same fixed counter
+    region, so the first call's counters are still zero and its repeat is bit-identical, finite and
+    within the tolerance of the unsplit entry on the last rows (checked against the oracle there)."""
+    T, D = 3658, 512
+    q, k, v = make(8, 1, T, T, D, seed=31, qscale=0.3)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    first = attn.attention(qd, kd, vd, 0, 0)
+    qs = T - 256
+    mb = attn.attention(qd[:, qs:], kd, vd, qs, 0)
+    again = attn.attention(qd, kd, vd, 0, 0)
+    assert torch.isfinite(again).all()
+    assert torch.equal(again, first)
+    assert torch.equal(attn.attention(qd[:, qs:], kd, vd, qs, 0), mb)
+    ref, bud, _ = reference(q[:, qs:], k, v, qs, 0)
+    check(again[:, qs:], ref, bud, "whole prompt after a micro-batch, last rows")
+    check(mb, ref, bud, "micro-batch")
+
+
 def test_deterministic():
     q, k, v = make(8, 1, 600, 600, 512, seed=3, qscale=0.3)
     qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
