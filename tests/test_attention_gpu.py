@@ -166,6 +166,33 @@ def test_split_tiles_and_the_unsplit_entry():
     assert np.allclose(lse_u[:, T - 200:].cpu().numpy(), lse_ref, rtol=1e-5, atol=1e-4)
 
 
+SPLIT_CASES = [
+    # H, KV, Tq, Tk, D, q_start: causal calls whose plans split their longest tiles
+    (8, 1, 1300, 1300, 256, 0),     # head_dim 256 (attn_fwd_kernel's park and merge)
+    (8, 2, 1300, 1300, 256, 0),     # two KV groups interleaved in the launch order
+    (4, 2, 1300, 1300, 128, 0),     # head_dim 128, 2 heads per group
+    (8, 2, 1300, 1300, 512, 0),     # head_dim 512 (attn_fwd2_kernel), two KV groups
+    (8, 1, 256, 1300, 256, 1044),   # a micro-batch at the end of the prompt: every tile split
+]
+
+
+@pytest.mark.parametrize("H,KV,Tq,Tk,D,q_start", SPLIT_CASES)
+def test_split_plans_match_oracle(H, KV, Tq, Tk, D, q_start):
+    """Split causal calls at head_dims 128 / 256 / 512, with one and two KV groups: the first 40 and
+    the last 200 rows against the oracle, the logsumexp of the last rows, and two calls equal."""
+    from w8a8 import lib
+    assert lib().w8a8_attention_workspace_bytes(H, KV, Tq, Tk, D, q_start, 0) > 0
+    q, k, v = make(H, KV, Tq, Tk, D, seed=41 + D + KV, qscale=0.3)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    a, lse = attn.attention(qd, kd, vd, q_start, 0, return_lse=True)
+    assert torch.equal(a, attn.attention(qd, kd, vd, q_start, 0))
+    ref, bud, _ = reference(q[:, :40], k[:, :q_start + 40], v[:, :q_start + 40], q_start, 0)
+    check(a[:, :40], ref, bud, "first rows")
+    ref, bud, lse_ref = reference(q[:, Tq - 200:], k, v, q_start + Tq - 200, 0)
+    check(a[:, Tq - 200:], ref, bud, "last rows")
+    assert np.allclose(lse[:, Tq - 200:].cpu().numpy(), lse_ref, rtol=1e-5, atol=1e-4)
+
+
 def test_split_workspace_shared_across_shapes():
     """Split calls of different shapes share the stream's workspace.  A whole-prompt causal call at
     head_dim 512 (T = 3658: ~190 split tiles), then 256 queries at the end of the prompt (16 split
