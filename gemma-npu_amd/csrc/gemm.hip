@@ -1250,6 +1250,11 @@ static void launch_pipe(const GemmParams& p, int epi, bool a_packed, hipStream_t
 // shapes (M = 512, 3658, 16384).  At one 512-row micro-batch the GEMMs are bound by how fast
 // each CU streams its operands, so small tiles that spread the work over more CUs win: 64x128
 // three blocks per CU (12) for the wide and short-K GEMMs, 64x64 (14) for narrow short-K ones.
+// Where the wide GEMM's 64x128 tiles fit in one round on the CUs (qkv, N = 2560, at M <= 768; the
+// PLE projection, N = 8960, at M <= 128), one block per CU with two waves per sub-tile splitting its
+// k-steps (20) beats 12 by 1-3% at K = 1536 (qkv at M = 512: 8.42 against 8.64 us, the whole
+// layer step 61.3-61.8 against 62.5-64.0 us); with more tiles than CUs it loses by half (10.6
+// against 15.7 us at M = 1024), and at K = 1024 the two are even.
 // The narrow long-K GEMMs (the output projection, K = 2048, and the down projection, K = 6144,
 // both N = 1536) have only 192 such tiles, one block per CU, whose two waves cannot hide their
 // LDS reads behind two MFMAs per k-step: four waves that each own the whole 64x64 tile and take
@@ -1293,7 +1298,10 @@ int gemm_pick_config(int M, int NP, int K, int epi) {
   if (M <= 1024) {
     if (K >= 2048 && NP <= 4096) return 22;  // few 64x64 tiles, long K: four waves split the k-steps
     if (epi == EPI_GELU) return 23;          // direct-W 64x256, two blocks per CU
-    return NP <= 2048 ? 14 : 12;
+    if (NP <= 2048) return 14;
+    // wide, short K: 64x128 tiles with two waves per 32-row sub-tile splitting its k-steps (20) while
+    // the tiles fit one round on the CUs, three blocks per CU (12) past that
+    return ((M + 63) / 64) * ((NP + 127) / 128) <= cu_count() ? 20 : 12;
   }
   if (epi == EPI_GELU) return 25;  // direct-W 128x256, two blocks per CU
   if (M <= 8192) {
