@@ -197,7 +197,8 @@ TILE_NAMES = {
     23: "gemm_dw_kernel (direct-W) 64x256 tiles, two blocks per CU",
     24: "gemm_dw_kernel (direct-W) 128x256 tiles, W 8 k-steps ahead",
     25: "gemm_dw_kernel (direct-W) 128x256 tiles, two blocks per CU",
-    26: "gemm_pipe_kernel (software-pipelined, persistent) 256x256 tiles",
+    26: "gemm_dw_kernel (direct-W) 96x256 tiles, W 8 k-steps ahead",
+    27: "gemm_pipe_kernel (software-pipelined, persistent) 256x256 tiles",
 }
 
 

@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
     missing = [n for n in declared_functions() if not hasattr(L, n)]
     assert not missing, f"not exported: {missing}"
     assert L.w8a8_abi_version() == 1
-    assert L.w8a8_gemm_tile_configs() == 27
+    assert L.w8a8_gemm_tile_configs() == 28
 
 
 def test_pick_tile_config_is_a_valid_configuration():
@@ -45,6 +45,14 @@ def test_pick_tile_config_is_a_valid_configuration():
                 cfg = L.w8a8_gemm_pick_tile_config(M, N, K, epi)
                 assert 0 <= cfg < n, (M, N, K, epi, cfg)
     assert L.w8a8_gemm_pick_tile_config(512, 12288, 1536, 1) != L.w8a8_gemm_pick_tile_config(3658, 12288, 1536, 1)
+    # narrow long-K GEMMs past one micro-batch (256 CUs): 96x256 direct-W tiles while one round of them
+    # fits, then 128x256, then 128x256 with two blocks per CU; the wide int32 gate/up on the pipelined kernel
+    assert L.w8a8_gemm_pick_tile_config(3658, 1536, 6144, -1) == 26
+    assert L.w8a8_gemm_pick_tile_config(3658, 1536, 2048, -1) == 26
+    assert L.w8a8_gemm_pick_tile_config(4096, 1536, 6144, -1) == 24
+    assert L.w8a8_gemm_pick_tile_config(8192, 1536, 6144, -1) == 25
+    assert L.w8a8_gemm_pick_tile_config(16384, 1536, 6144, 2) == 25
+    assert L.w8a8_gemm_pick_tile_config(3658, 12288, 1536, -1) == 27
     assert L.w8a8_gemm_pick_tile_config(0, 64, 64, 0) == -1
     assert L.w8a8_gemm_pick_tile_config(64, 64, 64, 3) == -1
     assert L.w8a8_gemm_pick_tile_config(64, 64, 64, -2) == -1
@@ -78,8 +86,9 @@ def test_linear_workspace_bytes():
     assert L.w8a8_gemm_workspace_bytes(512, 1536, 6144, 19, 4) == 0
     assert L.w8a8_gemm_workspace_bytes(512, 1536, 6144, 22, 4) == 0
     assert L.w8a8_gemm_workspace_bytes(3658, 1536, 6144, 24, 4) == 0       # direct-W: never split
-    assert L.w8a8_gemm_workspace_bytes(3658, 12288, 1536, 26, 4) == 0      # pipelined: never split
-    assert L.w8a8_gemm_workspace_bytes(3658, 1536, 6144, 27, 0) == -1      # past the last configuration
+    assert L.w8a8_gemm_workspace_bytes(3658, 1536, 6144, 26, 4) == 0       # direct-W 96x256: never split
+    assert L.w8a8_gemm_workspace_bytes(3658, 12288, 1536, 27, 4) == 0      # pipelined: never split
+    assert L.w8a8_gemm_workspace_bytes(3658, 1536, 6144, 28, 0) == -1      # past the last configuration
     assert L.w8a8_linear_workspace_bytes(512, 1536, 6144) == 4096 + 512 * 6144 + 512 * 4
     assert L.w8a8_linear_workspace_bytes(512, 1536, 2048) == 4096 + 512 * 2048 + 512 * 4
     assert L.w8a8_linear_workspace_bytes(3, 64, 64) == 4096 + 32 * 64 + 256  # counters kept; rows to 32
