@@ -198,7 +198,9 @@ TILE_NAMES = {
     24: "gemm_dw_kernel (direct-W) 128x256 tiles, W 8 k-steps ahead",
     25: "gemm_dw_kernel (direct-W) 128x256 tiles, two blocks per CU",
     26: "gemm_dw_kernel (direct-W) 96x256 tiles, W 8 k-steps ahead",
-    27: "gemm_pipe_kernel (software-pipelined, persistent) 256x256 tiles",
+    27: "gemm_dw_kernel (direct-W) 160x256 tiles, W 8 k-steps ahead",
+    28: "gemm_dw_kernel (direct-W) 192x256 tiles, W 8 k-steps ahead",
+    29: "gemm_pipe_kernel (software-pipelined, persistent) 256x256 tiles",
 }
 
 

@@ -1066,6 +1066,8 @@ static constexpr DwCfg kDw[] = {
     {128, 4, 2, 8, 8},     // 24: 128x256, k-tile 256, W 8 k-steps ahead, one block per CU
     {128, 4, 2, 8, 4, 2},  // 25: 128x256, k-tile 256, W 4 k-steps ahead, two blocks per CU
     {96, 4, 2, 8, 8},      // 26: 96x256, k-tile 256, W 8 k-steps ahead, one block per CU
+    {160, 4, 2, 8, 8},     // 27: 160x256, the same
+    {192, 4, 2, 8, 8},     // 28: 192x256, the same
 };
 static constexpr int kNumDw = int(sizeof(kDw) / sizeof(kDw[0]));
 
@@ -1076,10 +1078,10 @@ struct PipeCfg {
   int bm, bn, wgm, ns, minb;
 };
 static constexpr PipeCfg kPipe[] = {
-    {256, 256, 2, 4, 1},  // 27: 128x128 per wave, 32 KiB slots, 128 KiB ring
+    {256, 256, 2, 4, 1},  // 29: 128x128 per wave, 32 KiB slots, 128 KiB ring
 };
 static constexpr int kNumPipe = int(sizeof(kPipe) / sizeof(kPipe[0]));
-static_assert(kNumCfg == 23 && kNumDw == 4 && kNumPipe == 1, "every configuration needs its case in gemm_launch");
+static_assert(kNumCfg == 23 && kNumDw == 6 && kNumPipe == 1, "every configuration needs its case in gemm_launch");
 static constexpr int64_t kCounterBytes = 4096;
 
 int gemm_config_count() { return kNumCfg + kNumDw + kNumPipe; }
@@ -1282,22 +1284,24 @@ static void launch_pipe(const GemmParams& p, int epi, bool a_packed, hipStream_t
 // (gate/up 92 us in the sequence against 98 us on 128x256), while one GEMM repeated on a
 // cache-resident weight favours 128x256 (92 against 108 us); the direct-W tiles change the sweep
 // by less than 1% there.  The wide int32 GEMMs (N >= 8192) past one micro-batch take the
-// software-pipelined persistent 256x256 kernel (27): gate/up at M = 16384 393 against 440 us, the
+// software-pipelined persistent 256x256 kernel (29): gate/up at M = 16384 393 against 440 us, the
 // 141-GEMM sweep 6.92 -> 6.78 ms at M = 3658 and 7.64 -> 7.31 ms at M = 4096.  It is tried for
 // int32 only: its bf16 epilogues run on one wave per SIMD and lose to the two-blocks-per-CU tiles.
 // Where its 256x256 tiles leave a nearly empty last round (0 < tiles mod CUs <= CUs / 4), the
 // direct-W 128x256 tile with two blocks per CU (25) fills it: the PLE projection (N = 8960) at
 // M = 3658 (525 tiles on 256 CUs) 66.9 against 85.9 us, at M = 4096 (560 tiles) 80.7 against 92.0 us;
-// with fuller last rounds 27 keeps the lead (gate/up at M = 4096, 768 tiles: 94.3 against 101.7 us).
-// The narrow long-K GEMMs (N <= 2048, K >= 2048: the output and down projections) stream
-// (BM + BN) * K bytes per tile at the per-CU L2 delivery rate, one tile per CU, so their time is
-// rounds x (BM + BN): the 128x256 tile gives 29 x 6 = 174 tiles at M = 3658, leaving 82 CUs idle.
-// Where 96x256 tiles (26) still fit one round (M up to ~4000 at N = 1536) they move 352 instead of
-// 384 bytes per row of K per tile over 234 CUs: at M = 3658 down 38.9 against 42.7 us (K = 6144),
-// 69.2 against 77.4 us (K = 12288), the output projection (K = 2048) 17.2 against 19.3 us on 12;
-// all bit-identical.  At M = 4096 they need 258 tiles, two rounds (55.0 against 44.2 us), and
-// 128x256 takes over; past one round of those (M = 8192, 384 tiles) two blocks per CU (25) win,
-// 79.2 against 84.5 us.
+// with fuller last rounds 29 keeps the lead (gate/up at M = 4096, 768 tiles: 94.3 against 101.7 us).
+// Past one micro-batch the GEMMs up to N = 4096 (qkv, the output and down projections) stream
+// (BM + BN) * K bytes per tile at the per-CU L2 delivery rate, so their time follows the bytes the
+// busiest CU moves: rounds x (BM + BN).  One round of direct-W BMx256 tiles, one block per CU,
+// with the smallest BM in 96, 128, 160, 192 that fits, is taken where it moves fewer bytes per CU
+// than the 64x128 three-per-CU tiles (12), i.e. ceil(tiles / CUs) x 192.  At M = 3658: down
+// 38.9 against 42.7 us on 128x256 (K = 6144; 69.2 against 77.4 us at K = 12288) and the output
+// projection 17.2 against 19.3 us on 12, on 96x256 (26, 234 tiles); qkv 22.3 against 25.6 us on
+// 12, on 160x256 (27, 230 tiles).  At M = 4096: qkv 25.5 against 27.6 us on 192x256 (28, 220
+// tiles; 160x256 needs 260 tiles, two rounds: 37.5 us); down on 128x256 (24), 44.2 against 55.0 us
+// for 96x256's two rounds.  All bit-identical.  Past one round of every such tile (down at M =
+// 8192, 384 128x256 tiles) two blocks per CU (25) win, 79.2 against 84.5 us.
 static bool pipe_tail_is_short(int M, int NP) {
   const int cus = cu_count();
   const int tail = ((M + 255) / 256) * ((NP + 255) / 256) % cus;
@@ -1316,13 +1320,23 @@ int gemm_pick_config(int M, int NP, int K, int epi) {
   if (epi == EPI_GELU) return 25;  // direct-W 128x256, two blocks per CU
   const int cus = cu_count();
   auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((NP + bn - 1) / bn); };
-  if (K >= 2048 && NP <= 2048 && tiles(96, 256) <= cus) return 26;  // narrow long-K, one round of 96x256
+  if (K >= 1024 && NP <= 4096) {
+    // one round of direct-W BMx256 tiles, smallest BM first, where the busiest CU moves fewer bytes
+    // than on the 64x128 three-per-CU tiles
+    const int cost12 = (tiles(64, 128) + cus - 1) / cus * (64 + 128);
+    constexpr int kBm[4] = {96, 128, 160, 192}, kCfgOf[4] = {26, 24, 27, 28};
+    for (int i = 0; i < 4; ++i)
+      if (tiles(kBm[i], 256) <= cus) {
+        if (kBm[i] + 256 < cost12) return kCfgOf[i];
+        break;
+      }
+  }
   if (M <= 8192) {
-    if (K >= 4096 && NP <= 2048) return tiles(128, 256) <= cus ? 24 : 25;  // long-K narrow (down)
-    if (NP >= 8192) return epi == EPI_I32 ? (pipe_tail_is_short(M, NP) ? 25 : 27) : 0;  // wide
+    if (K >= 4096 && NP <= 2048) return 25;  // long-K narrow past one round of 128x256: two blocks per CU
+    if (NP >= 8192) return epi == EPI_I32 ? (pipe_tail_is_short(M, NP) ? 25 : 29) : 0;  // wide
     return 12;
   }
-  return NP >= 8192 && epi == EPI_I32 && !pipe_tail_is_short(M, NP) ? 27 : 25;
+  return NP >= 8192 && epi == EPI_I32 && !pipe_tail_is_short(M, NP) ? 29 : 25;
 }
 
 int gemm_launch(const GemmParams& p, int epi, int cfg, bool a_packed, void* ws, int64_t ws_bytes,
@@ -1356,7 +1370,9 @@ int gemm_launch(const GemmParams& p, int epi, int cfg, bool a_packed, void* ws, 
     case 24: launch_dw<1>(p, epi, a_packed, stream); break;
     case 25: launch_dw<2>(p, epi, a_packed, stream); break;
     case 26: launch_dw<3>(p, epi, a_packed, stream); break;
-    case 27: launch_pipe<0>(p, epi, a_packed, stream); break;
+    case 27: launch_dw<4>(p, epi, a_packed, stream); break;
+    case 28: launch_dw<5>(p, epi, a_packed, stream); break;
+    case 29: launch_pipe<0>(p, epi, a_packed, stream); break;
     default: return fail(W8A8_EINVAL, "gemm: unknown tile config %d", cfg);
   }
   return check_launch("gemm");

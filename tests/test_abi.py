@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
     missing = [n for n in declared_functions() if not hasattr(L, n)]
     assert not missing, f"not exported: {missing}"
     assert L.w8a8_abi_version() == 1
-    assert L.w8a8_gemm_tile_configs() == 28
+    assert L.w8a8_gemm_tile_configs() == 30
 
 
 def test_pick_tile_config_is_a_valid_configuration():
@@ -45,14 +45,19 @@ def test_pick_tile_config_is_a_valid_configuration():
                 cfg = L.w8a8_gemm_pick_tile_config(M, N, K, epi)
                 assert 0 <= cfg < n, (M, N, K, epi, cfg)
     assert L.w8a8_gemm_pick_tile_config(512, 12288, 1536, 1) != L.w8a8_gemm_pick_tile_config(3658, 12288, 1536, 1)
-    # narrow long-K GEMMs past one micro-batch (256 CUs): 96x256 direct-W tiles while one round of them
-    # fits, then 128x256, then 128x256 with two blocks per CU; the wide int32 gate/up on the pipelined kernel
+    # past one micro-batch (256 CUs), N <= 4096: one round of direct-W BMx256 tiles with the smallest BM
+    # that fits (96: 26, 128: 24, 160: 27, 192: 28) where it moves fewer bytes per CU than the 64x128
+    # tiles (12); then 128x256 with two blocks per CU for the long-K narrow ones; the wide int32
+    # gate/up on the pipelined kernel (29)
     assert L.w8a8_gemm_pick_tile_config(3658, 1536, 6144, -1) == 26
     assert L.w8a8_gemm_pick_tile_config(3658, 1536, 2048, -1) == 26
+    assert L.w8a8_gemm_pick_tile_config(3658, 2560, 1536, -1) == 27
+    assert L.w8a8_gemm_pick_tile_config(4096, 2560, 1536, -1) == 28
     assert L.w8a8_gemm_pick_tile_config(4096, 1536, 6144, -1) == 24
     assert L.w8a8_gemm_pick_tile_config(8192, 1536, 6144, -1) == 25
     assert L.w8a8_gemm_pick_tile_config(16384, 1536, 6144, 2) == 25
-    assert L.w8a8_gemm_pick_tile_config(3658, 12288, 1536, -1) == 27
+    assert L.w8a8_gemm_pick_tile_config(3658, 256, 1536, -1) == 12      # one column tile: 64x128 moves less
+    assert L.w8a8_gemm_pick_tile_config(3658, 12288, 1536, -1) == 29
     assert L.w8a8_gemm_pick_tile_config(0, 64, 64, 0) == -1
     assert L.w8a8_gemm_pick_tile_config(64, 64, 64, 3) == -1
     assert L.w8a8_gemm_pick_tile_config(64, 64, 64, -2) == -1
@@ -86,9 +91,10 @@ def test_linear_workspace_bytes():
     assert L.w8a8_gemm_workspace_bytes(512, 1536, 6144, 19, 4) == 0
     assert L.w8a8_gemm_workspace_bytes(512, 1536, 6144, 22, 4) == 0
     assert L.w8a8_gemm_workspace_bytes(3658, 1536, 6144, 24, 4) == 0       # direct-W: never split
-    assert L.w8a8_gemm_workspace_bytes(3658, 1536, 6144, 26, 4) == 0       # direct-W 96x256: never split
-    assert L.w8a8_gemm_workspace_bytes(3658, 12288, 1536, 27, 4) == 0      # pipelined: never split
-    assert L.w8a8_gemm_workspace_bytes(3658, 1536, 6144, 28, 0) == -1      # past the last configuration
+    for cfg in (26, 27, 28):                                                # direct-W 96/160/192 x 256
+        assert L.w8a8_gemm_workspace_bytes(3658, 1536, 6144, cfg, 4) == 0  # never split
+    assert L.w8a8_gemm_workspace_bytes(3658, 12288, 1536, 29, 4) == 0      # pipelined: never split
+    assert L.w8a8_gemm_workspace_bytes(3658, 1536, 6144, 30, 0) == -1      # past the last configuration
     assert L.w8a8_linear_workspace_bytes(512, 1536, 6144) == 4096 + 512 * 6144 + 512 * 4
     assert L.w8a8_linear_workspace_bytes(512, 1536, 2048) == 4096 + 512 * 2048 + 512 * 4
     assert L.w8a8_linear_workspace_bytes(3, 64, 64) == 4096 + 32 * 64 + 256  # counters kept; rows to 32
