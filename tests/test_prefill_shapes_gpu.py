@@ -184,3 +184,38 @@ def test_stress_m16384_residual_epilogue(stress_inputs):
     ref_y, _, _ = orc.linear_bf16(to_bits(x[rows]), w.numpy(), sw.numpy())
     assert np.array_equal(to_bits(y[rows.to(DEV)]), ref_y)
     print(f"stress down+residual: tile config {cfg}, bit-exact")
+
+
+# Past one micro-batch, GEMMs up to N = 4096 take one round of the smallest direct-W BMx256 tile
+# (BM = 96, 128, 160, 192) that fits the CUs; the choice changes where ceil(M / BM) * ceil(N / 256)
+# crosses the CU count (256 on MI355X), and each side of every such edge is a different tile.
+ONE_ROUND_EDGES = [
+    (2048, 1536, (1025, 4032, 4033)),             # output projection: 64x128, 96x256, 128x256
+    (6144, 1536, (4032, 4033, 5376, 5377)),       # down: 96x256, 128x256, then 160x256
+    (1536, 2560, (2400, 2401, 3200, 3201, 4000, 4001, 4800, 4801)),  # qkv: 96/128/160/192 rows, then 64x128
+]
+
+
+@pytest.mark.parametrize("K,N,Ms", ONE_ROUND_EDGES, ids=["o", "down", "qkv"])
+def test_one_round_tile_edges(K, N, Ms):
+    """int32 C bit-exact against torch._int_mm on both sides of every edge of the one-round tile
+    choice, and the bf16 residual epilogue on the chosen tile bit-identical to the 64x128 tile's."""
+    g = torch.Generator(device=DEV).manual_seed(K + N)
+    w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8, device=DEV)
+    _, sw = workloads.weights(N, K, seed=K)
+    pw = ops.pack_weight(w, "nk", sw=sw.to(DEV))
+    picked = set()
+    for M in Ms:
+        x = workloads.activations(M, K, seed=M).to(DEV)
+        pa, sx = ops.quant_rows_packed(x)
+        q, _ = ops.quant_rows(x)
+        cfg = lib().w8a8_gemm_pick_tile_config(M, N, K, -1)
+        picked.add(cfg)
+        c = ops.gemm_i32(pa, pw)
+        ref = torch._int_mm(q, w.t())
+        assert torch.equal(c, ref), f"K={K} N={N} M={M} tile {cfg}: {(c != ref).sum().item()} mismatches"
+        res = workloads.activations(M, N, seed=M + 1, outliers=False).to(DEV)
+        y = ops.gemm_bf16(pa, sx, pw, epilogue="residual", residual=res)
+        y12 = ops.gemm_bf16(pa, sx, pw, epilogue="residual", residual=res, tile_cfg=12)
+        assert torch.equal(y, y12), f"K={K} N={N} M={M}: residual epilogue differs between tiles"
+    assert len(picked) >= 2, f"K={K} N={N}: the edges {Ms} gave one tile {picked}"
