@@ -50,6 +50,25 @@ namespace w8a8 {
 typedef short v4s __attribute__((ext_vector_type(4)));
 typedef short v8s __attribute__((ext_vector_type(8)));
 
+// v combined over the four lanes l, l ^ 16, l ^ 32, l ^ 48 (the same row of an MFMA tile in the four
+// 16-lane groups) by the gfx950 lane swaps, in VALU instead of two ds_bpermute round trips through
+// LDS: v_permlane16_swap exchanges 16-lane groups 0 <-> 1 and 2 <-> 3, v_permlane32_swap the two
+// halves, and of the two results one holds the lane's own value and the other its partner's.  The
+// pairs are those of a xor-16 then xor-32 butterfly and both combines are commutative, so the result
+// is bit-identical to that butterfly on every lane.
+__device__ __forceinline__ float lanes4_max(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float lanes4_sum(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 constexpr int ATTN_NW = 8;        // waves per workgroup, 16 query rows each
 constexpr int ATTN_MAX_SEG = 16;     // segments of the causal work list (= most parts of one tile)
 constexpr int ATTN_FWD2_NW = 8;      // waves of attn_fwd2_kernel (4, one per SIMD, measured slower)
@@ -304,8 +323,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(AttnParams p) {
     for (int t = 0; t < 2 * NKC; ++t)
 #pragma unroll
       for (int i = 0; i < 4; ++i) bm = fmaxf(bm, s[t][i]);
-    bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
-    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+    bm = lanes4_max(bm);
     const float bmc = bm * c;
     const bool grow = bmc > ms + 8.0f;  // false while every key so far is masked (bmc = -inf)
     const float alpha = !grow ? 1.0f : (ms == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(ms - bmc));
@@ -342,8 +360,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(AttnParams p) {
 
   // ---- output: o / l per row (bf16), and the logsumexp ms ln 2 + ln l -----------------------------
   auto row_sum = [&](float x) {  // the row's total over its four lane groups
-    x += __shfl_xor(x, 16, 64);
-    return x + __shfl_xor(x, 32, 64);
+    return lanes4_sum(x);
   };
   uint16_t* const op = p.o + int64_t(h) * p.ohs + int64_t(qrow) * p.ors + 4 * qq;
   auto store_o = [&](int dt, v4f x, float inv) {
@@ -671,8 +688,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd2_kernel(AttnParams p) {
           s[j][t][i] = vis ? s[j][t][i] : -__builtin_inff();
           bm = fmaxf(bm, s[j][t][i]);
         }
-      bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
-      bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+      bm = lanes4_max(bm);
       const float bmc = bm * c;
       const bool grow = bmc > ms[j] + 8.0f;  // false while every key so far is masked (bmc = -inf)
       const bool had = ms[j] != -__builtin_inff();
@@ -797,8 +813,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd2_kernel(AttnParams p) {
   float lt[RT];
 #pragma unroll
   for (int j = 0; j < RT; ++j) {
-    lt[j] = l[j] + __shfl_xor(l[j], 16, 64);
-    lt[j] += __shfl_xor(lt[j], 32, 64);
+    lt[j] = lanes4_sum(l[j]);
   }
 
   if (split_tile) {
@@ -1014,8 +1029,7 @@ __global__ __launch_bounds__(256, 2) void attn_decode_split_kernel(DecodeParams 
     sc[i] = (has_tile && key <= p.pos && key < p.Tk) ? s0[i] + s1[i] : -__builtin_inff();
     bm = fmaxf(bm, sc[i]);
   }
-  bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
-  bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+  bm = lanes4_max(bm);
   if (qq == 0) smax[wave * 16 + qi] = bm;
   __syncthreads();
   float M = fmaxf(fmaxf(smax[qi], smax[16 + qi]), fmaxf(smax[32 + qi], smax[48 + qi]));
@@ -1029,8 +1043,7 @@ __global__ __launch_bounds__(256, 2) void attn_decode_split_kernel(DecodeParams 
     reinterpret_cast<uint16_t*>(&pw)[i] = f32_to_bf16(pe);
   }
   if (has_tile) *reinterpret_cast<v2u*>(pl + qi * PLD + 16 * wave + 4 * qq) = v2u{pw[0], pw[1]};
-  ls += __shfl_xor(ls, 16, 64);
-  ls += __shfl_xor(ls, 32, 64);
+  ls = lanes4_sum(ls);
   if (qq == 0) ssum[wave * 16 + qi] = ls;
   __syncthreads();
 
