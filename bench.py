@@ -77,6 +77,27 @@ def build_layer(M, dev, seed0=0):
     return groups
 
 
+def single_gemm(dev, M=512, K=1536, N=6144):
+    """The single prefill micro-batch GEMM (M=512 K=1536 N=6144, seed 0: int8 A from the quantized
+    activations, int32 out) on the automatic tile: average launch from a 50-launch graph, with the
+    output checked bit for bit against the eager launch."""
+    import torch
+    from w8a8 import lib, ops, workloads
+    a, _ = ops.quant_rows_packed(workloads.activations(M, K, seed=0).to(dev))
+    w, _ = workloads.weights(N, K, seed=1)
+    pw = ops.pack_weight(w.to(dev), "nk")
+    c = torch.empty((M, N), dtype=torch.int32, device=dev)
+    ops.gemm_i32(a, pw, c)
+    first = c.clone()
+    ms = graph_time_ms(lambda: ops.gemm_i32(a, pw, c), dev)
+    if not torch.equal(c, first):
+        raise RuntimeError("graph-replayed single GEMM differs from its eager launch")
+    t = workloads.gemm_ops(M, N, K) / (ms * 1e-3) / 1e12
+    return {"us": round(ms * 1e3, 2), "tops": round(t, 1), "frac_mfma": round(t / PEAK_INT8_TOPS, 4),
+            "tile": tile_name(lib().w8a8_gemm_pick_tile_config(M, N, K, -1)),
+            "shape": f"M={M} K={K} N={N}, packed int8 A, int32 out, weights hot"}
+
+
 def layer_step(groups, ws=None):
     from w8a8 import ops
     for g in groups:
@@ -947,7 +968,9 @@ def main():
 
     extra = {"graph_layer_step_us": round(graph_ms * 1e3, 1),
              "graph_layer_step_us_50_per_replay": round(graph50_ms * 1e3, 1),
-             "gemm_us_m512": {k: round(v * 1e3, 2) for k, v in per_ms.items()}}
+             "gemm_us_m512": {k: round(v * 1e3, 2) for k, v in per_ms.items()},
+             "single_gemm_m512_int32": single_gemm(dev)}
+    log(f"bench: single micro-batch GEMM: {extra['single_gemm_m512_int32']}")
     if not args.no_extra:
         for Ms in (3658, 4096):
             ms, tops_ops, wbytes, shp, run = sweep(Ms, dev, reps=5)

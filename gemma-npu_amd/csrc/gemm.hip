@@ -1269,6 +1269,13 @@ static void launch_pipe(const GemmParams& p, int epi, bool a_packed, hipStream_t
 // 16.1-18.0 us on 12 for N = 12288, 26.5 against 32.5 us for the double-wide N = 24576.  A 128x192
 // tile, one per CU (256 tiles), measured slower than 12 (17.2 against 15.9 us): its one wave per
 // SIMD leaves the LDS reads exposed.
+// The same direct-W 64x256 tile takes the other epilogues where 64x128 tiles would need more than
+// one round on the CUs but 64x256 tiles fit in one: at M = 512, N = 4608-8192 (the single
+// micro-batch GEMM, N = 6144: 10.2-10.6 against 11.3-11.7 us int32, 9.7 against 11.3 us with the
+// dequant epilogue; N = 4608 9.7 against 10.7, N = 8192 12.2 against 13.0; K = 2048 / 6144 / 12288
+// 12.2 / 27.3 / 48.6 against 13.5 / 29.6 / 52.8 us), and M = 384 / 640 at N = 6144 (9.6 / 11.9
+// against 10.6 / 12.6 us).  Past one round (M = 512 at N = 8960 / 12288, M = 768 / 1024 at
+// N = 6144) it loses to 12 by 5-12%, and where 64x128 tiles fit one round 20 stays ahead.
 // At a few thousand rows the long-K narrow down projections (K = 6144 / 12288, N = 1536) take the
 // direct-W 128x256 tile with W 8 k-steps ahead (24): 43 against 49 us at K = 6144 (the int32
 // sweep 7.02 -> 6.83 ms at M = 3658, 7.89 -> 7.61 ms at M = 4096), 78 against 89 us at K = 12288.
@@ -1313,9 +1320,12 @@ int gemm_pick_config(int M, int NP, int K, int epi) {
     if (K >= 2048 && NP <= 4096) return 22;  // few 64x64 tiles, long K: four waves split the k-steps
     if (epi == EPI_GELU) return 23;          // direct-W 64x256, two blocks per CU
     if (NP <= 2048) return 14;
-    // wide, short K: 64x128 tiles with two waves per 32-row sub-tile splitting its k-steps (20) while
-    // the tiles fit one round on the CUs, three blocks per CU (12) past that
-    return ((M + 63) / 64) * ((NP + 127) / 128) <= cu_count() ? 20 : 12;
+    // wide: 64x128 tiles with two waves per 32-row sub-tile splitting its k-steps (20) while the
+    // tiles fit one round on the CUs, then one round of direct-W 64x256 tiles (23), three blocks
+    // per CU on 64x128 tiles (12) past that
+    const int cus = cu_count(), mt = (M + 63) / 64;
+    if (mt * ((NP + 127) / 128) <= cus) return 20;
+    return mt * ((NP + 255) / 256) <= cus ? 23 : 12;
   }
   if (epi == EPI_GELU) return 25;  // direct-W 128x256, two blocks per CU
   const int cus = cu_count();

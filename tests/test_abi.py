@@ -58,6 +58,11 @@ def test_pick_tile_config_is_a_valid_configuration():
     assert L.w8a8_gemm_pick_tile_config(16384, 1536, 6144, 2) == 25
     assert L.w8a8_gemm_pick_tile_config(3658, 256, 1536, -1) == 12      # one column tile: 64x128 moves less
     assert L.w8a8_gemm_pick_tile_config(3658, 12288, 1536, -1) == 29
+    assert L.w8a8_gemm_pick_tile_config(512, 6144, 1536, -1) == 23      # one round of 64x256 tiles
+    assert L.w8a8_gemm_pick_tile_config(512, 8192, 1536, 0) == 23
+    assert L.w8a8_gemm_pick_tile_config(512, 4096, 1536, -1) == 20      # 64x128 tiles fit one round
+    assert L.w8a8_gemm_pick_tile_config(512, 8960, 1536, -1) == 12      # 64x256 tiles past one round
+    assert L.w8a8_gemm_pick_tile_config(768, 6144, 1536, 2) == 12
     assert L.w8a8_gemm_pick_tile_config(0, 64, 64, 0) == -1
     assert L.w8a8_gemm_pick_tile_config(64, 64, 64, 3) == -1
     assert L.w8a8_gemm_pick_tile_config(64, 64, 64, -2) == -1
