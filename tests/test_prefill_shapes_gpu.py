@@ -193,10 +193,13 @@ ONE_ROUND_EDGES = [
     (2048, 1536, (1025, 4032, 4033)),             # output projection: 64x128, 96x256, 128x256
     (6144, 1536, (4032, 4033, 5376, 5377)),       # down: 96x256, 128x256, then 160x256
     (1536, 2560, (2400, 2401, 3200, 3201, 4000, 4001, 4800, 4801)),  # qkv: 96/128/160/192 rows, then 64x128
+    # one micro-batch: 64x128 one per CU, then one round of direct-W 64x256, then 64x128 three per CU
+    (1536, 6144, (256, 384, 640, 704)),
+    (1536, 8192, (448, 512, 513)),
 ]
 
 
-@pytest.mark.parametrize("K,N,Ms", ONE_ROUND_EDGES, ids=["o", "down", "qkv"])
+@pytest.mark.parametrize("K,N,Ms", ONE_ROUND_EDGES, ids=["o", "down", "qkv", "micro_n6144", "micro_n8192"])
 def test_one_round_tile_edges(K, N, Ms):
     """int32 C bit-exact against torch._int_mm on both sides of every edge of the one-round tile
     choice, and the bf16 residual epilogue on the chosen tile bit-identical to the 64x128 tile's."""
