@@ -1284,16 +1284,23 @@ static void launch_pipe(const GemmParams& p, int epi, bool a_packed, hipStream_t
 // at M = 3658 (N = 12288), 142 against 164 us for N = 24576, 308 against 352 us at M = 16384; down
 // + residual at M = 16384 141 against 167 us.  64x256 with three or four blocks per CU, and
 // 128x256 with W only 2 k-steps ahead, measured slower on all of these.
-// The other int32 GEMMs at a few thousand rows (M = 3658, 4096) keep 256x256 tiles (0) for the
-// wide gate/up and PLE projections and 64x128 tiles with their accumulators staged through LDS
-// for row-contiguous stores (12) for the rest.  This is timed on the 141-GEMM int32 prefill sweep
-// itself, with a distinct weight per layer: there the 256-row tiles' halved weight reads decide
-// (gate/up 92 us in the sequence against 98 us on 128x256), while one GEMM repeated on a
-// cache-resident weight favours 128x256 (92 against 108 us); the direct-W tiles change the sweep
-// by less than 1% there.  The wide int32 GEMMs (N >= 8192) past one micro-batch take the
-// software-pipelined persistent 256x256 kernel (29): gate/up at M = 16384 393 against 440 us, the
-// 141-GEMM sweep 6.92 -> 6.78 ms at M = 3658 and 7.64 -> 7.31 ms at M = 4096.  It is tried for
-// int32 only: its bf16 epilogues run on one wave per SIMD and lose to the two-blocks-per-CU tiles.
+// Between one micro-batch and 8192 rows the GEMMs that no rule above takes (N between 4096 and
+// 8192, and narrower ones too tall for one round of direct-W tiles) run on that 128x256
+// two-per-CU tile (25) rather than 64x128 tiles with their accumulators staged through LDS (12),
+// unless its tiles are fewer than the CUs or leave a last round of at most a quarter of them.
+// Timed with distinct cold weights per call: M = 3658, N = 4096 / 5120 30.3 / 43.5 against
+// 37.7 / 47.5 us, K = 2048 N = 4096 35.9 against 46.7 us, M = 8192 N = 6144 98.5 against 122.1 us;
+// with the short last rounds (576 or 320 tiles) 12 is even or up to 7% ahead.  The wide GEMMs
+// (N >= 8192) with bf16 epilogues take 25 too, where the 256x256 8-wave tile (0) ran before:
+// the PLE projection at M = 3658 58.8 against 86.2 us, N = 12288 83.6 against 91.7 us (cold),
+// the residual epilogue 68.8 against 106.1 us.  The 256-row tiles read the weight half as often,
+// which decides only on the int32 gate/up of the 141-GEMM sweep, timed with a distinct weight per
+// layer (92 us in the sequence against 98 us on 128x256, while one GEMM repeated on a
+// cache-resident weight favours 128x256, 92 against 108 us).  The wide int32 GEMMs (N >= 8192)
+// past one micro-batch take the software-pipelined persistent 256x256 kernel (29): gate/up at
+// M = 16384 393 against 440 us, the 141-GEMM sweep 6.92 -> 6.78 ms at M = 3658 and 7.64 -> 7.31 ms
+// at M = 4096.  It is tried for int32 only: its bf16 epilogues run on one wave per SIMD and lose to
+// the two-blocks-per-CU tiles.
 // Where its 256x256 tiles leave a nearly empty last round (0 < tiles mod CUs <= CUs / 4), the
 // direct-W 128x256 tile with two blocks per CU (25) fills it: the PLE projection (N = 8960) at
 // M = 3658 (525 tiles on 256 CUs) 66.9 against 85.9 us, at M = 4096 (560 tiles) 80.7 against 92.0 us;
@@ -1343,8 +1350,11 @@ int gemm_pick_config(int M, int NP, int K, int epi) {
   }
   if (M <= 8192) {
     if (K >= 4096 && NP <= 2048) return 25;  // long-K narrow past one round of 128x256: two blocks per CU
-    if (NP >= 8192) return epi == EPI_I32 ? (pipe_tail_is_short(M, NP) ? 25 : 29) : 0;  // wide
-    return 12;
+    if (NP >= 8192) return epi != EPI_I32 || pipe_tail_is_short(M, NP) ? 25 : 29;  // wide
+    // the rest on 128x256 tiles, two blocks per CU, unless they are fewer than the CUs or leave a
+    // nearly empty last round
+    const int t25 = tiles(128, 256), tail = t25 % cus;
+    return t25 >= cus && !(tail > 0 && 4 * tail <= cus) ? 25 : 12;
   }
   return NP >= 8192 && epi == EPI_I32 && !pipe_tail_is_short(M, NP) ? 29 : 25;
 }

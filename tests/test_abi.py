@@ -63,6 +63,11 @@ def test_pick_tile_config_is_a_valid_configuration():
     assert L.w8a8_gemm_pick_tile_config(512, 4096, 1536, -1) == 20      # 64x128 tiles fit one round
     assert L.w8a8_gemm_pick_tile_config(512, 8960, 1536, -1) == 12      # 64x256 tiles past one round
     assert L.w8a8_gemm_pick_tile_config(768, 6144, 1536, 2) == 12
+    assert L.w8a8_gemm_pick_tile_config(3658, 8960, 1536, 0) == 25      # wide, bf16 epilogue
+    assert L.w8a8_gemm_pick_tile_config(3658, 5120, 1536, -1) == 25     # 580 128x256 tiles, a full last round
+    assert L.w8a8_gemm_pick_tile_config(3072, 6144, 1536, -1) == 12     # 576 tiles: a short last round
+    assert L.w8a8_gemm_pick_tile_config(2048, 5120, 1536, 2) == 12      # 320 tiles: likewise
+    assert L.w8a8_gemm_pick_tile_config(3658, 256, 256, -1) == 12       # fewer 128x256 tiles than CUs
     assert L.w8a8_gemm_pick_tile_config(0, 64, 64, 0) == -1
     assert L.w8a8_gemm_pick_tile_config(64, 64, 64, 3) == -1
     assert L.w8a8_gemm_pick_tile_config(64, 64, 64, -2) == -1
