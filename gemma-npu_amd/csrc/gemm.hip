@@ -1273,8 +1273,9 @@ static void launch_pipe(const GemmParams& p, int epi, bool a_packed, hipStream_t
 // one round on the CUs but 64x256 tiles fit in one: at M = 512, N = 4608-8192 (the single
 // micro-batch GEMM, N = 6144: 10.2-10.6 against 11.3-11.7 us int32, 9.7 against 11.3 us with the
 // dequant epilogue; N = 4608 9.7 against 10.7, N = 8192 12.2 against 13.0; K = 2048 / 6144 / 12288
-// 12.2 / 27.3 / 48.6 against 13.5 / 29.6 / 52.8 us), and M = 384 / 640 at N = 6144 (9.6 / 11.9
-// against 10.6 / 12.6 us).  Past one round (M = 512 at N = 8960 / 12288, M = 768 / 1024 at
+// 12.2 / 27.3 / 48.6 against 13.5 / 29.6 / 52.8 us), M = 384 / 640 at N = 6144 (9.6 / 11.9
+// against 10.6 / 12.6 us), and from 77 to 1024 rows at N = 2560-24576 (M = 1024, N = 2560: 10.3
+// against 11.4 us; M = 256, N = 8960 with the dequant epilogue: 9.6 against 11.0).  Past one round (M = 512 at N = 8960 / 12288, M = 768 / 1024 at
 // N = 6144) it loses to 12 by 5-12%, and where 64x128 tiles fit one round 20 stays ahead.
 // At a few thousand rows the long-K narrow down projections (K = 6144 / 12288, N = 1536) take the
 // direct-W 128x256 tile with W 8 k-steps ahead (24): 43 against 49 us at K = 6144 (the int32
