@@ -44,7 +44,8 @@ class QuantizedWeight:
     gemma_npu.py:81-82) for decode rows, and for a [gate; up] pair `packed_gelu`, packed for the GEMM's
     fused GELU epilogue.  With gemm=False only the GEMV form exists (the LM head) and every row goes
     through it, 16 rows per launch.  The plain GEMM packing of a [gate; up] pair is made on first
-    use: the fused path does not need it."""
+    use, by permuting the tiles of `packed_gelu`: the fused path does not need it, and no int8
+    copy is kept for it."""
 
     def __init__(self, weights, gemm=True, gelu_pair=False):
         w = torch.cat([t.detach() for t in weights], 0)
@@ -58,7 +59,6 @@ class QuantizedWeight:
         self.sw, self.sw_bf16 = sw, sw.to(torch.bfloat16)
         self.gemv_w = ops.pack_gemv_weight(q)
         self.has_gemm = bool(gemm)
-        self._q = q if (gemm and gelu_pair) else None  # kept until the plain packing is asked for
         self._packed = ops.pack_weight(q, "nk", sw=sw) if (gemm and not gelu_pair) else None
         self.packed_gelu = ops.pack_weight(q, "nk", self.N // 2, sw=sw) if (gemm and gelu_pair) else None
         self.name = ""
@@ -68,8 +68,7 @@ class QuantizedWeight:
         if self._packed is None:
             if not self.has_gemm:
                 raise AttributeError("this weight is kept for the GEMV only")
-            self._packed = ops.pack_weight(self._q, "nk", sw=self.sw)
-            self._q = None
+            self._packed = ops.unpair_packed(self.packed_gelu)
         return self._packed
 
     def apply(self, x2d):

@@ -123,6 +123,19 @@ def pack_weight(w, layout="nk", interleave=0, sw=None):
     return PackedWeight(data, N, K, interleave, sw)
 
 
+def unpair_packed(pw):
+    """The plain packing of a [gate; up] PackedWeight packed for the GELU epilogue, without the
+    int8 source.  Both layouts store whole 32-channel tiles as contiguous blocks of KF KiB; the
+    paired one orders them gate 0, up 0, gate 1, up 1, ..., the plain one gate 0 .. I/32-1 then
+    up 0 .. I/32-1, so the plain weight is a permutation of the paired one's blocks."""
+    if not isinstance(pw, PackedWeight) or pw.interleave <= 0:
+        raise ValueError("unpair_packed: expects a PackedWeight packed with interleave > 0")
+    nt = pw.N // 32
+    blocks = pw.data.view(nt, -1)
+    perm = torch.cat([torch.arange(0, nt, 2), torch.arange(1, nt, 2)]).to(blocks.device)
+    return PackedWeight(blocks.index_select(0, perm).reshape(-1), pw.N, pw.K, 0, pw.sw)
+
+
 def quant_rows(x, q=None, scale=None):
     """Per-row int8 quant of bf16 or fp32 rows (pipeline.py:49-52) -> (q int8 [M,K], scale fp32 [M])."""
     if x.dtype not in (torch.bfloat16, torch.float32):

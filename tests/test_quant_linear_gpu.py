@@ -199,3 +199,25 @@ def test_selfcheck_quant_step():
     bad, pairs = counts.cpu().tolist()
     assert pairs == 1065402240
     assert bad == 0
+
+
+@pytest.mark.parametrize("I,K", [(32, 64), (96, 208), (6144, 1536)])
+def test_unpair_packed_equals_the_plain_packing(I, K):
+    """The plain packing derived from a GELU-paired one by permuting its tiles is the packing of
+    the same weight made directly, byte for byte, and multiplies to torch._int_mm's result."""
+    g = torch.Generator().manual_seed(I + K)
+    w = torch.randint(-127, 128, (2 * I, K), generator=g, dtype=torch.int8).to(DEV)
+    sw = torch.rand(2 * I, generator=g).to(DEV)
+    plain = ops.pack_weight(w, "nk", sw=sw)
+    derived = ops.unpair_packed(ops.pack_weight(w, "nk", I, sw=sw))
+    assert derived.interleave == 0 and derived.sw is sw
+    assert torch.equal(derived.data, plain.data)
+    a = torch.randint(-127, 128, (40, K), generator=g, dtype=torch.int8).to(DEV)
+    ref = torch._int_mm(a.cpu(), w.cpu().t().contiguous())
+    assert torch.equal(ops.gemm_i32(a, derived).cpu(), ref)
+
+
+def test_unpair_packed_refuses_a_plain_weight():
+    w = torch.zeros((64, 64), dtype=torch.int8, device=DEV)
+    with pytest.raises(ValueError):
+        ops.unpair_packed(ops.pack_weight(w, "nk"))
