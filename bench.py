@@ -83,8 +83,8 @@ def single_gemm(dev, M=512, K=1536, N=6144):
     output checked bit for bit against the eager launch."""
     import torch
     from w8a8 import lib, ops, workloads
-    a, _ = ops.quant_rows_packed(workloads.activations(M, K, seed=0).to(dev))
-    w, _ = workloads.weights(N, K, seed=1)
+    x, w, _ = workloads.single_gemm_inputs(M, K, N, seed=0)
+    a, _ = ops.quant_rows_packed(x.to(dev))
     pw = ops.pack_weight(w.to(dev), "nk")
     c = torch.empty((M, N), dtype=torch.int32, device=dev)
     ops.gemm_i32(a, pw, c)
@@ -211,17 +211,17 @@ def cpu_int_mm_ms(shapes, M, warm=3, reps=5, budget_s=None):
 
 
 TILE_NAMES = {
-    12: "gemm_kernel 64x128 tiles, three blocks per CU",
-    14: "gemm_kernel 64x64 tiles, two waves",
-    22: "gemm_kernel 64x64 tiles with 4-wave split-K, 512-deep k-tiles",
-    0: "gemm_kernel 256x256 tiles, 8 waves",
-    23: "gemm_dw_kernel (direct-W) 64x256 tiles, two blocks per CU",
-    24: "gemm_dw_kernel (direct-W) 128x256 tiles, W 8 k-steps ahead",
-    25: "gemm_dw_kernel (direct-W) 128x256 tiles, two blocks per CU",
-    26: "gemm_dw_kernel (direct-W) 96x256 tiles, W 8 k-steps ahead",
-    27: "gemm_dw_kernel (direct-W) 160x256 tiles, W 8 k-steps ahead",
-    28: "gemm_dw_kernel (direct-W) 192x256 tiles, W 8 k-steps ahead",
-    29: "gemm_pipe_kernel (software-pipelined, persistent) 256x256 tiles",
+    0: "gemm_kernel 64x128 tiles, three blocks per CU",
+    1: "gemm_kernel 64x64 tiles, two waves",
+    2: "gemm_kernel 64x128 tiles, two waves per 32-row sub-tile splitting its k-steps",
+    3: "gemm_kernel 64x64 tiles with 4-wave split-K, 512-deep k-tiles",
+    4: "gemm_dw_kernel (direct-W) 64x256 tiles, two blocks per CU",
+    5: "gemm_dw_kernel (direct-W) 128x256 tiles, W 8 k-steps ahead",
+    6: "gemm_dw_kernel (direct-W) 128x256 tiles, two blocks per CU",
+    7: "gemm_dw_kernel (direct-W) 96x256 tiles, W 8 k-steps ahead",
+    8: "gemm_dw_kernel (direct-W) 160x256 tiles, W 8 k-steps ahead",
+    9: "gemm_dw_kernel (direct-W) 192x256 tiles, W 8 k-steps ahead",
+    10: "gemm_pipe_kernel (software-pipelined, persistent) 256x256 tiles",
 }
 
 

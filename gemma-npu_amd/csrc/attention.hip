@@ -1179,16 +1179,16 @@ static int64_t attn_part_bytes(int64_t D) {
   return int64_t(ATTN_NW) * 64 * (D / 16 + 1) * 16;
 }
 
+// Compute units of the current device (256 on MI355X), read once; the initialisation of a
+// function-local static is thread-safe, so concurrent first calls from several host threads agree.
 static int attn_cu_count() {
-  static int cus = 0;
-  if (cus == 0) {
+  static const int cus = [] {
     int dev = 0, n = 0;
-    if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) ==
-                                                 hipSuccess && n > 0)
-      cus = n;
-    else
-      cus = 256;
-  }
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                                hipSuccess || n <= 0)
+      n = 256;
+    return n;
+  }();
   return cus;
 }
 
@@ -1391,6 +1391,14 @@ extern "C" int64_t w8a8_attention_workspace_bytes(int64_t H, int64_t KV, int64_t
       q_start < 0 || window < 0 || Tk < q_start + Tq)
     return -1;
   return attn_split_workspace(attn_plan(H, KV, Tq, Tk, D, q_start, window), KV, D);
+}
+
+extern "C" int64_t w8a8_attention_plan_items(int64_t H, int64_t KV, int64_t Tq, int64_t Tk, int64_t D,
+                                             int64_t q_start, int64_t window, int* launch_order) {
+  if (w8a8_attention_workspace_bytes(H, KV, Tq, Tk, D, q_start, window) < 0) return -1;
+  const AttnPlan pl = attn_plan(H, KV, Tq, Tk, D, q_start, window);
+  if (launch_order) *launch_order = pl.order.empty() ? 0 : 1;
+  return pl.per_group;
 }
 
 static int attention_launch(const uint16_t* q, int64_t q_head_stride, int64_t q_row_stride, const uint16_t* k,

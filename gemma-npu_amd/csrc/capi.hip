@@ -132,11 +132,9 @@ int w8a8_gemm_pick_tile_config(int64_t M, int64_t N, int64_t K, int epilogue) {
 }
 
 int64_t w8a8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int tile_cfg, int split_k) {
-  if (M <= 0 || N <= 0 || K <= 0 || M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) return 0;
-  if (tile_cfg >= gemm_config_count()) return -1;
-  const int np = int((N + 31) / 32 * 32), kf = int(2 * ((K + 63) / 64));
-  const int cfg = tile_cfg < 0 ? gemm_pick_config(int(M), np, kf * 32, EPI_BF16) : tile_cfg;
-  return gemm_workspace_bytes(int(M), np, kf, cfg, split_k < 0 ? 0 : split_k);
+  if (tile_cfg >= gemm_config_count() || split_k > 1) return -1;
+  (void)M, (void)N, (void)K;
+  return 0;  // no configuration splits K across blocks: the GEMMs need no workspace
 }
 
 int w8a8_gemm_i32_ex(const int8_t* a, int64_t lda, int a_packed, const int8_t* w_packed, int64_t M, int64_t N,
@@ -149,13 +147,13 @@ int w8a8_gemm_i32_ex(const int8_t* a, int64_t lda, int a_packed, const int8_t* w
   if (ldc < N) return fail(W8A8_EINVAL, "gemm_i32: ldc=%lld < N=%lld", (long long)ldc, (long long)N);
   if ((uintptr_t)c % 4 != 0) return fail(W8A8_EALIGN, "gemm_i32: C must be 4-byte aligned");
   if (tile_cfg >= gemm_config_count()) return fail(W8A8_EINVAL, "gemm_i32: tile config %d out of range", tile_cfg);
+  if (split_k > 1) return fail(W8A8_ENOTSUP, "gemm_i32: split_k=%d: K is never split across blocks", split_k);
+  (void)workspace, (void)workspace_bytes;
   if (M == 0) return W8A8_OK;
   p.c = c;
   p.ldc = ldc;
   p.vec_store = (ldc % 4 == 0) && ((uintptr_t)c % 16 == 0);
-  p.split_req = split_k < 0 ? 0 : split_k;
-  if (workspace && (uintptr_t)workspace % 256 != 0) return fail(W8A8_EALIGN, "gemm_i32: workspace not 256-byte aligned");
-  return gemm_launch(p, EPI_I32, tile_cfg, a_packed != 0, workspace, workspace_bytes, stream);
+  return gemm_launch(p, EPI_I32, tile_cfg, a_packed != 0, stream);
 }
 
 int w8a8_gemm_i32(const int8_t* a, int64_t lda, const int8_t* w_packed, int64_t M, int64_t N, int64_t K, int32_t* c,
@@ -194,6 +192,8 @@ int w8a8_gemm_bf16_ex(const int8_t* a, int64_t lda, int a_packed, const float* s
   if (ldo < out_cols) return fail(W8A8_EINVAL, "gemm_bf16: ldo=%lld too small", (long long)ldo);
   if ((uintptr_t)out % 2 != 0) return fail(W8A8_EALIGN, "gemm_bf16: output must be 2-byte aligned");
   if (tile_cfg >= gemm_config_count()) return fail(W8A8_EINVAL, "gemm_bf16: tile config %d out of range", tile_cfg);
+  if (split_k > 1) return fail(W8A8_ENOTSUP, "gemm_bf16: split_k=%d: K is never split across blocks", split_k);
+  (void)workspace, (void)workspace_bytes;
   if (M == 0) return W8A8_OK;
   p.sx = sx;
   p.sw = sw;
@@ -203,9 +203,7 @@ int w8a8_gemm_bf16_ex(const int8_t* a, int64_t lda, int a_packed, const float* s
   p.res = res;
   p.ldr = ldr;
   p.res_vec = res && (ldr % 4 == 0) && ((uintptr_t)res % 8 == 0);
-  p.split_req = split_k < 0 ? 0 : split_k;
-  if (workspace && (uintptr_t)workspace % 256 != 0) return fail(W8A8_EALIGN, "gemm_bf16: workspace not 256-byte aligned");
-  return gemm_launch(p, epi, tile_cfg, a_packed != 0, workspace, workspace_bytes, stream);
+  return gemm_launch(p, epi, tile_cfg, a_packed != 0, stream);
 }
 
 int w8a8_gemm_bf16(const int8_t* a, int64_t lda, const float* sx, const int8_t* w_packed, const float* sw, int64_t M,
@@ -215,19 +213,13 @@ int w8a8_gemm_bf16(const int8_t* a, int64_t lda, const float* sx, const int8_t* 
                            nullptr, 0, stream);
 }
 
-// Workspace of w8a8_linear_bf16: [GEMM split-K workspace | packed int8 rows | per-row scales],
-// each part 256-byte aligned.  The split-K part starts with its counters at offset 0.
+// Workspace of w8a8_linear_bf16: [packed int8 rows | per-row scales], each part 256-byte aligned.
 static int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
-// The GEMM part always spans the 4 KiB counter block, so the scratch behind it never lands on
-// counters another call on the same workspace relies on.
-static int64_t linear_gemm_part(int64_t g) { return align256(g > 4096 ? g : 4096); }
 
 int64_t w8a8_linear_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   const int64_t a = w8a8_packed_act_bytes(M, K);
   if (a < 0 || N <= 0) return -1;
-  const int64_t g = w8a8_gemm_workspace_bytes(M, N, K, -1, 0);
-  if (g < 0) return -1;
-  return linear_gemm_part(g) + align256(a) + align256(M * 4);
+  return align256(a) + align256(M * 4);
 }
 
 }  // extern "C"
@@ -252,24 +244,22 @@ static int check_linear(const char* fn, const uint16_t* x, int64_t M, int64_t N,
   return W8A8_OK;
 }
 
-// quant_rows(x) into the packed rows q and scales sx, then the GEMM with its epilogue.  gws: the
-// GEMM's split-K workspace, or null (the automatic tile choice never splits K, so both give the
-// same kernels and the same bits).
+// quant_rows(x) into the packed rows q and scales sx, then the GEMM with its epilogue.
 static int run_linear(const uint16_t* x, int64_t ldx, const int8_t* w_packed, const float* sw, int64_t M, int64_t N,
                       int64_t K, int epilogue, int64_t interleave, const uint16_t* res, int64_t ldr,
-                      const uint16_t* rms_w, float eps, uint16_t* out, int64_t ldo, int8_t* q, float* sx, void* gws,
-                      int64_t gbytes, hipStream_t stream) {
+                      const uint16_t* rms_w, float eps, uint16_t* out, int64_t ldo, int8_t* q, float* sx,
+                      hipStream_t stream) {
   int rc = w8a8_quant_rows_packed_bf16(x, ldx, M, K, q, sx, stream);
   if (rc) return rc;
   if (epilogue == 3) {
     // Reference order (pipeline.py:113): y = dequant (bf16) first, then res + rms(y) * w.
-    rc = w8a8_gemm_bf16_ex(q, 0, 1, sx, w_packed, sw, M, N, K, 0, 0, nullptr, 0, out, ldo, -1, 0, gws, gbytes,
+    rc = w8a8_gemm_bf16_ex(q, 0, 1, sx, w_packed, sw, M, N, K, 0, 0, nullptr, 0, out, ldo, -1, 0, nullptr, 0,
                            stream);
     if (rc) return rc;
     return w8a8_rms_residual_bf16(out, ldo, res, ldr, rms_w, eps, M, N, out, ldo, nullptr, 0, nullptr, stream);
   }
-  return w8a8_gemm_bf16_ex(q, 0, 1, sx, w_packed, sw, M, N, K, epilogue, interleave, res, ldr, out, ldo, -1, 0, gws,
-                           gbytes, stream);
+  return w8a8_gemm_bf16_ex(q, 0, 1, sx, w_packed, sw, M, N, K, epilogue, interleave, res, ldr, out, ldo, -1, 0,
+                           nullptr, 0, stream);
 }
 
 // ---- scratch of the linear that allocates nothing -----------------------------------------------
@@ -319,11 +309,10 @@ int w8a8_linear_bf16(const uint16_t* x, int64_t ldx, const int8_t* w_packed, con
   if (!workspace || workspace_bytes < need || (uintptr_t)workspace % 256 != 0)
     return fail(W8A8_EINVAL, "linear_bf16: workspace needs %lld bytes, 256-byte aligned", (long long)need);
   char* base = static_cast<char*>(workspace);
-  const int64_t gbytes = linear_gemm_part(w8a8_gemm_workspace_bytes(M, N, K, -1, 0));
-  int8_t* q = reinterpret_cast<int8_t*>(base + gbytes);
-  float* sx = reinterpret_cast<float*>(base + gbytes + align256(w8a8_packed_act_bytes(M, K)));
-  return run_linear(x, ldx, w_packed, sw, M, N, K, epilogue, interleave, res, ldr, rms_w, eps, out, ldo, q, sx, base,
-                    gbytes, stream);
+  int8_t* q = reinterpret_cast<int8_t*>(base);
+  float* sx = reinterpret_cast<float*>(base + align256(w8a8_packed_act_bytes(M, K)));
+  return run_linear(x, ldx, w_packed, sw, M, N, K, epilogue, interleave, res, ldr, rms_w, eps, out, ldo, q, sx,
+                    stream);
 }
 
 int w8a8_linear_bf16_noalloc(const uint16_t* x, int64_t ldx, const int8_t* w_packed, const float* sw, int64_t M,
@@ -346,7 +335,7 @@ int w8a8_linear_bf16_noalloc(const uint16_t* x, int64_t ldx, const int8_t* w_pac
   int8_t* q = static_cast<int8_t*>(base);
   float* sx = reinterpret_cast<float*>(static_cast<char*>(base) + abytes);
   return run_linear(x, ldx, w_packed, sw, M, N, K, epilogue, interleave, res, ldr, rms_w, eps, out, ldo, q, sx,
-                    nullptr, 0, stream);
+                    stream);
 }
 
 }  // extern "C"

@@ -20,11 +20,6 @@ struct GemmParams {
   int vec_store;        // output rows allow 4-wide vector stores (alignment checked on the host)
   int res_vec;          // residual rows allow 4-wide (8-byte) vector loads
   int gm;               // row tiles per group in the block -> tile order (set by the launcher)
-  int split_req;        // requested split-K: 0 = automatic, n = at most n splits
-  int splits;           // blocks per output tile along K (1 = no split)
-  int kt_per_split;     // k-tiles of 64 per split
-  int32_t* ws;          // split-K partial sums (splits > 1)
-  int* counters;        // split-K arrival counters, one per output tile, zero between calls
   int32_t* c; int64_t ldc;          // EPI_I32
   const float* sx; const float* sw; // per-row / per-channel scales
   uint16_t* out; int64_t ldo;       // bf16 epilogues
@@ -32,11 +27,8 @@ struct GemmParams {
 };
 
 int gemm_config_count();
-// Automatic tile configuration for [M, NP, K] with epilogue epi (split-K needs never depend on epi).
+// Automatic tile configuration for [M, NP, K] with epilogue epi.
 int gemm_pick_config(int M, int NP, int K, int epi);
-// ws: split-K workspace (zero-filled before first use; the kernels leave it zeroed), may be null.
-int gemm_launch(const GemmParams& p, int epi, int cfg, bool a_packed, void* ws, int64_t ws_bytes,
-                hipStream_t stream);
-int64_t gemm_workspace_bytes(int M, int NP, int KF, int cfg, int split_k);
+int gemm_launch(const GemmParams& p, int epi, int cfg, bool a_packed, hipStream_t stream);
 
 }  // namespace w8a8

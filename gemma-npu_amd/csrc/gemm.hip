@@ -37,9 +37,6 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
-// Buffer cache policy sc0 | sc1: system scope, coherent across the XCDs' caches.
-static constexpr int kSysCoherent = 0x11;
-
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
 }
@@ -134,8 +131,8 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, const v16i& acc,
   }
 }
 
-// Epilogue of the wave split-K kernels.  `red` holds the KW waves' partial tiles as row-major
-// int32 [KW][BM][LDR].  Thread q of a row (TPR = BN/16 threads per row) adds the partials of 4
+// Epilogue of gemm_kernel, from the accumulators staged in LDS.  `red` holds the KW waves'
+// partial tiles (KW = 1: the one tile) as row-major int32 [KW][BM][LDR].  Thread q of a row (TPR = BN/16 threads per row) adds the partials of 4
 // columns in each quarter of the tile, columns 4q + (BN/4)*st (st = 0..3), so in each step the
 // TPR threads of a row read and store one contiguous run.  For GELU (BN of 64 or 128) the gate
 // column c of a [gate | up] pair of 32-channel tiles sits in quarter st and its up column c + 32
@@ -248,7 +245,7 @@ __device__ __forceinline__ void tile_coords(int t, int ntm, int ntn, int gm, int
   tn = r / gsz;
 }
 
-template <int BM, int BN, int WGM, int WGN, int KW, int KS, int NS, int EPI, bool A_PACKED, bool SPLIT, int MINB>
+template <int BM, int BN, int WGM, int WGN, int KW, int KS, int NS, int EPI, bool A_PACKED, int MINB>
 __global__ __launch_bounds__(WGM * WGN * KW * 64, MINB) void gemm_kernel(GemmParams p) {
   constexpr int NW = WGM * WGN * KW;  // KW waves share each output sub-tile, splitting its k-steps
   constexpr int MT = BM / 32;         // A row-tiles per block
@@ -262,7 +259,6 @@ __global__ __launch_bounds__(WGM * WGN * KW * 64, MINB) void gemm_kernel(GemmPar
   static_assert(WTM * WGM == MT && WTN * WGN == NTB, "wave grid must divide the block tile");
   static_assert(EPI != EPI_GELU || (WTN % 2 == 0), "GELU pairs need an even tile count per wave");
   static_assert(KS % (2 * KW) == 0, "each wave's k-steps alternate between two register sets");
-  static_assert(KW == 1 || !SPLIT, "wave split-K and block split-K do not combine");
   constexpr int SW = KS / KW;  // k-steps per wave per k-tile
   static_assert(NS >= 2, "the ring needs one slot being read and one landing");
   static_assert(FW * (NS - 1) < 64, "outstanding loads must fit the 6-bit vmcnt");
@@ -289,20 +285,13 @@ __global__ __launch_bounds__(WGM * WGN * KW * 64, MINB) void gemm_kernel(GemmPar
 
   const int ntm = (p.M + BM - 1) / BM;
   const int ntn = (p.NT + NTB - 1) / NTB;
-  // With split-K, the p.splits blocks of one output tile are consecutive logical blocks and
-  // each multiplies k-tiles [k_lo, k_hi).
-  const int lb = xcd_remap(blockIdx.x, ntm * ntn * p.splits);
-  const int tile = lb / p.splits;
-  const int split = lb % p.splits;
   int tm, tn;
-  tile_coords(tile, ntm, ntn, p.gm, tm, tn);
+  tile_coords(xcd_remap(blockIdx.x, ntm * ntn), ntm, ntn, p.gm, tm, tn);
   const int m0 = tm * BM;
   const int t0 = tn * NTB;
-  const int KTT = (p.KF + KS - 1) / KS;  // k-tiles over the whole K
-  const int k_lo = split * p.kt_per_split;
-  const int k_hi = min(KTT, k_lo + p.kt_per_split);
-  // k-steps (of 32) in this block's last k-tile: K is padded to 64, not to 32 * KS.
-  const int last_steps = min(p.KF, k_hi * KS) - (k_hi - 1) * KS;
+  const int KT = (p.KF + KS - 1) / KS;  // k-tiles over the whole K
+  // k-steps (of 32) in the last k-tile: K is padded to 64, not to 32 * KS.
+  const int last_steps = p.KF - (KT - 1) * KS;
 
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a, p.a_bytes);
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.wp, p.w_bytes);
@@ -393,10 +382,9 @@ __global__ __launch_bounds__(WGM * WGN * KW * 64, MINB) void gemm_kernel(GemmPar
   // wait on MFMAs still reading the set they overwrite; sched_barrier keeps the compiler from
   // reordering the phases.  One barrier per k-tile publishes the next k-tile and frees the
   // current slot.
-  const int KT = k_hi - k_lo;  // k-tiles this block multiplies
 #pragma unroll
   for (int s = 0; s < NS; ++s)
-    if (s < KT) issue(k_lo + s);
+    if (s < KT) issue(s);
   if (NS <= KT)
     wait_vmcnt<FW * (NS - 1)>();
   else
@@ -411,7 +399,7 @@ __global__ __launch_bounds__(WGM * WGN * KW * 64, MINB) void gemm_kernel(GemmPar
   }
 
   v4i a0[WTM], b0[WTN], a1[WTM], b1[WTN];
-  if (KT > 0) read(k_lo, kw, a0, b0);
+  if (KT > 0) read(0, kw, a0, b0);
   for (int kt = 0; kt < KT; ++kt) {
     const bool more = kt + 1 < KT;
 #pragma unroll
@@ -425,7 +413,7 @@ __global__ __launch_bounds__(WGM * WGN * KW * 64, MINB) void gemm_kernel(GemmPar
       if (live) mma(ca, cb, 0, EARLY);
       __builtin_amdgcn_sched_barrier(0);
       if (j + 1 < SW) {
-        read(k_lo + kt, s + KW, na, nb);
+        read(kt, s + KW, na, nb);
       } else if (more) {
         // Every read of this k-tile has completed (lgkmcnt 0) and, after the barrier, on every
         // wave: its slot takes k-tile kt+NS.  k-tile kt+1 has landed once at most the NS-2
@@ -436,112 +424,39 @@ __global__ __launch_bounds__(WGM * WGN * KW * 64, MINB) void gemm_kernel(GemmPar
         else
           wait_vmcnt<0>();
         __builtin_amdgcn_s_barrier();
-        if (kt + NS < KT) issue(k_lo + kt + NS);
-        read(k_lo + kt + 1, kw, na, nb);
+        if (kt + NS < KT) issue(kt + NS);
+        read(kt + 1, kw, na, nb);
       }
       __builtin_amdgcn_sched_barrier(0);
       if (live) mma(ca, cb, EARLY, NQ);
     }
   }
 
-  // ---- row-major epilogue through LDS: wave split-K tiles add their KW partials there; other
-  // tiles whose ring can hold the whole accumulator tile stage it there too, so that every
-  // store instruction writes whole row segments instead of 16 or 32 bytes of 32 rows --------
+  // ---- row-major epilogue through LDS: wave split-K tiles add their KW partials there, and every
+  // tile stages its accumulators there, so that each store instruction writes whole row segments
+  // instead of 16 or 32 bytes of 32 rows -------------------------------------------------------
   constexpr int LDR = BN + 4;  // padded row (int32) of the staged tiles
-  constexpr bool STAGED = KW > 1 || (!SPLIT && BM * LDR * 4 <= RING && (NW * 64) % (BN / 16) == 0 &&
-                                     (EPI != EPI_GELU || BN == 64 || BN == 128));
-  if constexpr (STAGED) {
-    static_assert(KW * BM * LDR * 4 <= RING, "the staged partial tiles must fit in the ring");
-    int32_t* red = reinterpret_cast<int32_t*>(lds);
-    // Every DMA has landed (the last k-tiles waited for vmcnt 0) and, after this barrier, every
-    // wave has finished reading the ring.
-    __syncthreads();
-    const int lrow = lane & 31, lcol = 4 * (lane >> 5);
+  static_assert(KW * BM * LDR * 4 <= RING, "the staged partial tiles must fit in the ring");
+  static_assert((NW * 64) % (BN / 16) == 0, "whole threads per staged row");
+  static_assert(EPI != EPI_GELU || BN == 64 || BN == 128, "GELU pairing in the staged epilogue");
+  int32_t* red = reinterpret_cast<int32_t*>(lds);
+  // Every DMA has landed (the last k-tiles waited for vmcnt 0) and, after this barrier, every
+  // wave has finished reading the ring.
+  __syncthreads();
+  const int lrow = lane & 31, lcol = 4 * (lane >> 5);
 #pragma unroll
-    for (int i = 0; i < WTM; ++i)
+  for (int i = 0; i < WTM; ++i)
 #pragma unroll
-      for (int j = 0; j < WTN; ++j)
+    for (int j = 0; j < WTN; ++j)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int row = (wm * WTM + i) * 32 + lrow;
-          const int col = (wn * WTN + j) * 32 + 8 * g + lcol;
-          *reinterpret_cast<v4i*>(red + (kw * BM + row) * LDR + col) =
-              v4i{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
-        }
-    __syncthreads();
-    ksplit_epilogue<EPI, BM, BN, KW, NW, LDR>(p, red, s_scale, m0, t0);
-    return;
-  }
-
-  // ---- split-K: park partial sums; the last block of the tile adds them up -------------------
-  // The XCDs' L2 caches are not coherent with each other, so the partials go through with
-  // system-scope (sc0 sc1) buffer stores and loads, which are coherent by themselves, and the
-  // arrival count is a system-scope atomic.  Each thread's stores are complete (vmcnt 0)
-  // before the barrier that precedes the count, so a block that sees itself last reads every
-  // other block's finished partials.  No cache-wide writeback or invalidate is needed.
-  if constexpr (SPLIT) {
-    constexpr uint32_t kPartialBytes = uint32_t(NW) * NQ * 64 * 64;  // one split's tile, lane-native
-    const __amdgpu_buffer_rsrc_t rp = make_rsrc(p.ws + size_t(tile) * p.splits * (kPartialBytes / 4),
-                                                uint32_t(p.splits) * kPartialBytes);
-#pragma unroll
-    for (int i = 0; i < WTM; ++i)
-#pragma unroll
-      for (int j = 0; j < WTN; ++j)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const uint32_t off =
-              uint32_t(split) * kPartialBytes + ((wave * NQ + i * WTN + j) * 64 + lane) * 64 + g * 16;
-          const v4u v = {uint32_t(acc[i][j][4 * g]), uint32_t(acc[i][j][4 * g + 1]), uint32_t(acc[i][j][4 * g + 2]),
-                         uint32_t(acc[i][j][4 * g + 3])};
-          __builtin_amdgcn_raw_buffer_store_b128(v, rp, off, 0, kSysCoherent);
-        }
-    __builtin_amdgcn_s_waitcnt(0);
-    // The ring is idle now (every wave's reads completed before its last MFMAs), so its first
-    // word carries the arrival count to the whole block.
-    int* arrived = reinterpret_cast<int*>(lds);
-    __syncthreads();
-    if (threadIdx.x == 0)
-      *arrived = __hip_atomic_fetch_add(p.counters + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    __syncthreads();
-    if (*arrived != p.splits - 1) return;
-    for (int o = 0; o < p.splits; ++o) {
-      if (o == split) continue;
-#pragma unroll
-      for (int i = 0; i < WTM; ++i)
-#pragma unroll
-        for (int j = 0; j < WTN; ++j)
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const uint32_t off = uint32_t(o) * kPartialBytes + ((wave * NQ + i * WTN + j) * 64 + lane) * 64 + g * 16;
-            const v4i v = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rp, off, 0, kSysCoherent));
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[i][j][4 * g + r] += v[r];
-          }
-    }
-    if (threadIdx.x == 0) __hip_atomic_store(p.counters + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-  }
-
-  // ---- epilogue ---------------------------------------------------------------------------
-  if constexpr (EPI != EPI_I32) __syncthreads();  // s_scale is visible to every wave
-  const int lrow = lane & 31;
-  const int lcol = 4 * (lane >> 5);
-#pragma unroll
-  for (int i = 0; i < WTM; ++i) {
-    const int ml = (wm * WTM + i) * 32 + lrow;  // row within the tile
-    const int m = m0 + ml;
-    if (m >= p.M) continue;
-    const float sxm = EPI == EPI_I32 ? 0.0f : s_scale[ml];
-    const float* swt = s_scale + (EPI == EPI_I32 ? 0 : BM) + wn * WTN * 32 + lcol;
-    if constexpr (EPI == EPI_GELU) {
-#pragma unroll
-      for (int j = 0; j < WTN; j += 2)
-        store_tile<EPI>(p, acc[i][j], &acc[i][j + 1], m, t0 + wn * WTN + j, lcol, sxm, swt + j * 32);
-    } else {
-#pragma unroll
-      for (int j = 0; j < WTN; ++j)
-        store_tile<EPI>(p, acc[i][j], nullptr, m, t0 + wn * WTN + j, lcol, sxm, swt + j * 32);
-    }
-  }
+      for (int g = 0; g < 4; ++g) {
+        const int row = (wm * WTM + i) * 32 + lrow;
+        const int col = (wn * WTN + j) * 32 + 8 * g + lcol;
+        *reinterpret_cast<v4i*>(red + (kw * BM + row) * LDR + col) =
+            v4i{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+      }
+  __syncthreads();
+  ksplit_epilogue<EPI, BM, BN, KW, NW, LDR>(p, red, s_scale, m0, t0);
 }
 
 
@@ -1021,102 +936,54 @@ __global__ __launch_bounds__(256, MINB) void gemm_pipe_kernel(GemmParams p) {
 
 // ---- host-side launch ----------------------------------------------------------------------
 
-// Tile configurations: block tile BM x BN, waves (WGM x WGN, one wave per 32-multiple sub-tile),
-// k-tile depth 32*KS, LDS ring of NS k-tiles.
+// Tile configurations, numbered 0 .. 10 as the C ABI's tile_cfg: the ones the automatic choice
+// (gemm_pick_config) takes for some shape, and no others.
+//
+// gemm_kernel (0 - 3): block tile BM x BN, waves (WGM x WGN sub-tiles, kw waves per sub-tile taking
+// alternate k-steps, their partials added in LDS), k-tile depth 32*KS, LDS ring of NS k-tiles.
 struct TileCfg {
   int bm, bn, waves, ks, ns;
-  int kw = 1;  // waves sharing each output sub-tile, splitting its k-steps (partials added in LDS)
+  int kw = 1;
 };
 static constexpr TileCfg kCfg[] = {
-    {256, 256, 8, 4, 2},  // 0: 64 KiB slots, 128 KiB ring
-    {128, 256, 8, 4, 3},  // 1: 48 KiB slots, 144 KiB ring
-    {256, 128, 8, 4, 3},  // 2: 48 KiB slots, 144 KiB ring
-    {128, 256, 8, 2, 4},  // 3: 24 KiB slots, 96 KiB ring
-    {256, 128, 8, 2, 4},  // 4: 24 KiB slots, 96 KiB ring
-    {128, 256, 8, 2, 3},  // 5: 24 KiB slots, 72 KiB ring (two blocks per CU, 16 waves)
-    {256, 128, 8, 2, 3},  // 6: 24 KiB slots, 72 KiB ring (two blocks per CU, 16 waves)
-    {128, 128, 8, 4, 2},  // 7: 32 KiB slots, 64 KiB ring (two blocks per CU, 16 waves)
-    {128, 128, 4, 4, 4},  // 8: 32 KiB slots, 128 KiB ring
-    {128, 128, 4, 4, 2},  // 9: 32 KiB slots, 64 KiB ring (two blocks per CU)
-    {128, 128, 4, 2, 4},  // 10: 16 KiB slots, 64 KiB ring (two blocks per CU)
-    {128, 256, 4, 2, 3},  // 11: 24 KiB slots, 72 KiB ring (two blocks per CU)
-    {64, 128, 4, 4, 2},   // 12: 24 KiB slots, 48 KiB ring (three blocks per CU)
-    {64, 128, 4, 4, 3},   // 13: 24 KiB slots, 72 KiB ring (two blocks per CU)
-    {64, 64, 2, 4, 2},    // 14: 16 KiB slots, 32 KiB ring, 2 waves (four blocks per CU)
-    {64, 64, 2, 4, 6},    // 15: 16 KiB slots, 96 KiB ring: five k-tiles in flight
-    {64, 128, 4, 4, 5},   // 16: 24 KiB slots, 120 KiB ring: four k-tiles in flight
-    {64, 64, 2, 8, 3},    // 17: 32 KiB slots (k-tile 256), 96 KiB ring
-    {64, 128, 4, 8, 3},   // 18: 48 KiB slots (k-tile 256), 144 KiB ring
-    // wave split-K: each 64x64 sub-tile is computed by kw waves taking alternate k-steps
-    {64, 64, 4, 8, 3, 4},   // 19: one sub-tile, 4 waves; 96 KiB ring
-    {64, 128, 4, 8, 3, 2},  // 20: two sub-tiles side by side, 2 waves each; 144 KiB ring
-    {128, 64, 4, 8, 3, 2},  // 21: two sub-tiles stacked, 2 waves each; 144 KiB ring
-    {64, 64, 4, 16, 2, 4},  // 22: one sub-tile, 4 waves; k-tile 512, 128 KiB ring
+    {64, 128, 4, 4, 2},     // 0: 24 KiB slots, 48 KiB ring (three blocks per CU)
+    {64, 64, 2, 4, 2},      // 1: 16 KiB slots, 32 KiB ring, 2 waves (four blocks per CU)
+    {64, 128, 4, 8, 3, 2},  // 2: two 64x64 sub-tiles side by side, 2 waves each; 144 KiB ring
+    {64, 64, 4, 16, 2, 4},  // 3: one 64x64 sub-tile, 4 waves; k-tile 512, 128 KiB ring
 };
 static constexpr int kNumCfg = int(sizeof(kCfg) / sizeof(kCfg[0]));
 
-// Direct-W configurations (gemm_dw_kernel), numbered after kCfg: block tile BM x (NWN*WTN*32),
-// A k-tiles of 32*KS, W register ring of PW k-steps.
+// gemm_dw_kernel (4 - 9): block tile BM x (NWN*WTN*32), A k-tiles of 32*KS, W register ring of PW
+// k-steps.
 struct DwCfg {
   int bm, nwn, wtn, ks, pw;
   int minb = 1;  // blocks per CU the registers are budgeted for
 };
 static constexpr DwCfg kDw[] = {
-    {64, 4, 2, 8, 4, 2},   // 23: 64x256, k-tile 256, W 4 k-steps ahead, two blocks per CU
-    {128, 4, 2, 8, 8},     // 24: 128x256, k-tile 256, W 8 k-steps ahead, one block per CU
-    {128, 4, 2, 8, 4, 2},  // 25: 128x256, k-tile 256, W 4 k-steps ahead, two blocks per CU
-    {96, 4, 2, 8, 8},      // 26: 96x256, k-tile 256, W 8 k-steps ahead, one block per CU
-    {160, 4, 2, 8, 8},     // 27: 160x256, the same
-    {192, 4, 2, 8, 8},     // 28: 192x256, the same
+    {64, 4, 2, 8, 4, 2},   // 4: 64x256, k-tile 256, W 4 k-steps ahead, two blocks per CU
+    {128, 4, 2, 8, 8},     // 5: 128x256, k-tile 256, W 8 k-steps ahead, one block per CU
+    {128, 4, 2, 8, 4, 2},  // 6: 128x256, k-tile 256, W 4 k-steps ahead, two blocks per CU
+    {96, 4, 2, 8, 8},      // 7: 96x256, k-tile 256, W 8 k-steps ahead, one block per CU
+    {160, 4, 2, 8, 8},     // 8: 160x256, the same
+    {192, 4, 2, 8, 8},     // 9: 192x256, the same
 };
 static constexpr int kNumDw = int(sizeof(kDw) / sizeof(kDw[0]));
 
-// Software-pipelined configurations (gemm_pipe_kernel), numbered after kDw: block tile BM x BN,
-// waves along M (the other 4 / wgm along N), NS-slot ring of 64-deep k-tiles, blocks per CU the
-// registers are budgeted for.
+// gemm_pipe_kernel (10): block tile BM x BN, waves along M (the other 4 / wgm along N), NS-slot
+// ring of 64-deep k-tiles, blocks per CU the registers are budgeted for.
 struct PipeCfg {
   int bm, bn, wgm, ns, minb;
 };
 static constexpr PipeCfg kPipe[] = {
-    {256, 256, 2, 4, 1},  // 29: 128x128 per wave, 32 KiB slots, 128 KiB ring
+    {256, 256, 2, 4, 1},  // 10: 128x128 per wave, 32 KiB slots, 128 KiB ring
 };
 static constexpr int kNumPipe = int(sizeof(kPipe) / sizeof(kPipe[0]));
-static_assert(kNumCfg == 23 && kNumDw == 6 && kNumPipe == 1, "every configuration needs its case in gemm_launch");
-static constexpr int64_t kCounterBytes = 4096;
+static_assert(kNumCfg == 4 && kNumDw == 6 && kNumPipe == 1, "every configuration needs its case in gemm_launch");
+enum { CFG_64x128 = 0, CFG_64x64 = 1, CFG_64x128_KW2 = 2, CFG_64x64_KW4 = 3, CFG_DW_64x256 = 4,
+       CFG_DW_128x256_PW8 = 5, CFG_DW_128x256 = 6, CFG_DW_96x256 = 7, CFG_DW_160x256 = 8, CFG_DW_192x256 = 9,
+       CFG_PIPE_256x256 = 10 };
 
 int gemm_config_count() { return kNumCfg + kNumDw + kNumPipe; }
-
-// Split-K: blocks per output tile along K.  Explicit requests (req = n >= 1) split into at most
-// n parts, only when there are few output tiles.  Automatic selection (req = 0) splits the
-// few-tile, long-K shapes (the down projection at one 512-row micro-batch: 96 tiles of
-// 64x128 over K = 6144), where measured on MI355X two halves of K beat one block per tile;
-// shorter K loses more to the partial-sum exchange than it gains.  Every split keeps at least
-// 256 of K; `kps` is the number of k-tiles per split.
-static int pick_splits(int tiles, int KT, int ks, int req, int& kps, int kw = 1) {
-  int s = 1;
-  if (kw > 1) {  // wave split-K kernels do not split across blocks
-    kps = KT;
-    return 1;
-  }
-  if (req > 1 && tiles < 200) s = min(req, 256 / tiles);  // and so tiles < kCounterBytes / 4
-  if (req == 0 && tiles <= 128 && KT * ks * 32 >= 4096) s = 2;
-  const int min_kt = max(1, 8 / ks);
-  s = max(1, min(s, min(8, KT / min_kt)));
-  kps = (KT + s - 1) / s;
-  return (KT + kps - 1) / kps;
-}
-
-// Split-K workspace: kCounterBytes of arrival counters (one int per output tile; zero before
-// and after every call) followed by the partial sums (scratch).
-int64_t gemm_workspace_bytes(int M, int NP, int KF, int cfg, int split_k) {
-  if (cfg >= kNumCfg) return 0;  // direct-W and pipelined kernels never split K across blocks
-  const TileCfg& c = kCfg[cfg];
-  const int ntm = (M + c.bm - 1) / c.bm, ntn = (NP + c.bn - 1) / c.bn;
-  int kps;
-  const int s = pick_splits(ntm * ntn, (KF + c.ks - 1) / c.ks, c.ks, split_k, kps, c.kw);
-  if (s <= 1) return 0;
-  return kCounterBytes + int64_t(ntm) * ntn * s * c.bm * c.bn * 4;
-}
 
 // Blocks per CU the tile is built for: as many rings as fit in the 160 KiB of LDS, at most four.
 template <int BM, int BN, int KS, int NS>
@@ -1125,65 +992,36 @@ constexpr int blocks_per_cu() {
   return 4 * ring <= 160 * 1024 ? 4 : (3 * ring <= 160 * 1024 ? 3 : (2 * ring <= 160 * 1024 ? 2 : 1));
 }
 
-template <int BM, int BN, int WGM, int WGN, int KW, int KS, int NS, bool AP, bool SPLIT>
-static void launch_kernel(const GemmParams& p, int epi, dim3 grid, hipStream_t stream) {
-  const int threads = WGM * WGN * KW * 64;
-  constexpr int B = blocks_per_cu<BM, BN, KS, NS>();
-  switch (epi) {
-    case EPI_I32: gemm_kernel<BM, BN, WGM, WGN, KW, KS, NS, EPI_I32, AP, SPLIT, B><<<grid, threads, 0, stream>>>(p); break;
-    case EPI_BF16: gemm_kernel<BM, BN, WGM, WGN, KW, KS, NS, EPI_BF16, AP, SPLIT, B><<<grid, threads, 0, stream>>>(p); break;
-    case EPI_GELU: gemm_kernel<BM, BN, WGM, WGN, KW, KS, NS, EPI_GELU, AP, SPLIT, B><<<grid, threads, 0, stream>>>(p); break;
-    case EPI_RESID: gemm_kernel<BM, BN, WGM, WGN, KW, KS, NS, EPI_RESID, AP, SPLIT, B><<<grid, threads, 0, stream>>>(p); break;
-  }
-}
-
 template <int BM, int BN, int WGM, int WGN, int KW, int KS, int NS, bool AP>
-static void launch_epi(GemmParams p, int epi, void* ws, int64_t ws_bytes, hipStream_t stream) {
+static void launch_epi(GemmParams p, int epi, hipStream_t stream) {
   const int ntm = (p.M + BM - 1) / BM;
   const int ntn = (p.NT * 32 + BN - 1) / BN;
   p.gm = min(ntm, BM >= BN ? 4 : 8);
-  const int KT = (p.KF + KS - 1) / KS;
-  p.splits = 1;
-  p.kt_per_split = KT;
-  if (ws && KW == 1) {
-    int kps;
-    const int s = pick_splits(ntm * ntn, KT, KS, p.split_req, kps);
-    const int64_t need = kCounterBytes + int64_t(ntm) * ntn * s * BM * BN * 4;
-    if (s > 1 && ws_bytes >= need && ntm * ntn * 4 <= kCounterBytes) {
-      p.splits = s;
-      p.kt_per_split = kps;
-      p.counters = static_cast<int*>(ws);
-      p.ws = reinterpret_cast<int32_t*>(static_cast<char*>(ws) + kCounterBytes);
-    }
+  const dim3 grid(unsigned(ntm * ntn));
+  const int threads = WGM * WGN * KW * 64;
+  constexpr int B = blocks_per_cu<BM, BN, KS, NS>();
+  switch (epi) {
+    case EPI_I32: gemm_kernel<BM, BN, WGM, WGN, KW, KS, NS, EPI_I32, AP, B><<<grid, threads, 0, stream>>>(p); break;
+    case EPI_BF16: gemm_kernel<BM, BN, WGM, WGN, KW, KS, NS, EPI_BF16, AP, B><<<grid, threads, 0, stream>>>(p); break;
+    case EPI_GELU: gemm_kernel<BM, BN, WGM, WGN, KW, KS, NS, EPI_GELU, AP, B><<<grid, threads, 0, stream>>>(p); break;
+    case EPI_RESID: gemm_kernel<BM, BN, WGM, WGN, KW, KS, NS, EPI_RESID, AP, B><<<grid, threads, 0, stream>>>(p); break;
   }
-  dim3 grid(unsigned(ntm * ntn * p.splits));
-  if constexpr (KW == 1) {
-    if (p.splits > 1) {
-      launch_kernel<BM, BN, WGM, WGN, KW, KS, NS, AP, true>(p, epi, grid, stream);
-      return;
-    }
-  }
-  launch_kernel<BM, BN, WGM, WGN, KW, KS, NS, AP, false>(p, epi, grid, stream);
 }
 
 template <int CFG>
-static void launch(const GemmParams& p, int epi, bool a_packed, void* ws, int64_t ws_bytes, hipStream_t stream) {
+static void launch(const GemmParams& p, int epi, bool a_packed, hipStream_t stream) {
   constexpr TileCfg c = kCfg[CFG];
-  // The waves / kw wave groups laid out along the longer side of the block tile: 8 as 4x2
-  // (BM >= BN) or 2x4, 4 as 2x2, 2 as 2x1 (BM >= BN) or 1x2, 1 as 1x1.
+  // The waves / kw wave groups laid out along the longer side of the block tile: 4 as 2x2, 2 as
+  // 2x1 (BM >= BN) or 1x2, 1 as 1x1.
   constexpr int WG = c.waves / c.kw;
-  constexpr int WGM = WG == 1 ? 1
-                    : WG == 2 ? (c.bm >= c.bn ? 2 : 1)
-                    : WG == 4 ? 2
-                    : WG == 8 ? (c.bm >= c.bn ? 4 : 2)
-                              : (c.bm >= c.bn ? 8 : 2);
+  constexpr int WGM = WG == 1 ? 1 : WG == 2 ? (c.bm >= c.bn ? 2 : 1) : 2;
   constexpr int WGN = WG / WGM;
+  static_assert(WGM * WGN == WG, "wave grid");
   if (a_packed)
-    launch_epi<c.bm, c.bn, WGM, WGN, c.kw, c.ks, c.ns, true>(p, epi, ws, ws_bytes, stream);
+    launch_epi<c.bm, c.bn, WGM, WGN, c.kw, c.ks, c.ns, true>(p, epi, stream);
   else
-    launch_epi<c.bm, c.bn, WGM, WGN, c.kw, c.ks, c.ns, false>(p, epi, ws, ws_bytes, stream);
+    launch_epi<c.bm, c.bn, WGM, WGN, c.kw, c.ks, c.ns, false>(p, epi, stream);
 }
-
 
 template <int BM, int NWN, int WTN, int KS, int PW, int MINB, bool AP>
 static void launch_dw_epi(GemmParams p, int epi, hipStream_t stream) {
@@ -1191,7 +1029,6 @@ static void launch_dw_epi(GemmParams p, int epi, hipStream_t stream) {
   const int ntm = (p.M + BM - 1) / BM;
   const int ntn = (p.NT * 32 + BN - 1) / BN;
   p.gm = min(ntm, BM >= BN ? 4 : 8);
-  p.splits = 1;
   const dim3 grid{unsigned(ntm * ntn)};
   const int threads = NWN * 64;
   switch (epi) {
@@ -1230,7 +1067,6 @@ static void launch_pipe_epi(GemmParams p, int epi, hipStream_t stream) {
   const int ntm = (p.M + BM - 1) / BM;
   const int ntn = (p.NT * 32 + BN - 1) / BN;
   p.gm = min(ntm, BM >= BN ? 4 : 8);
-  p.splits = 1;
   const dim3 grid{unsigned(persistent_blocks(ntm * ntn, MINB))};
   switch (epi) {
     case EPI_I32: gemm_pipe_kernel<BM, BN, WGM, NS, EPI_I32, AP, MINB><<<grid, 256, 0, stream>>>(p); break;
@@ -1249,151 +1085,76 @@ static void launch_pipe(const GemmParams& p, int epi, bool a_packed, hipStream_t
     launch_pipe_epi<c.bm, c.bn, c.wgm, c.ns, c.minb, false>(p, epi, stream);
 }
 
-// Tile choice, from timing every configuration with the bf16 epilogues on the E2B prefill
-// shapes (M = 512, 3658, 16384).  At one 512-row micro-batch the GEMMs are bound by how fast
-// each CU streams its operands, so small tiles that spread the work over more CUs win: 64x128
-// three blocks per CU (12) for the wide and short-K GEMMs, 64x64 (14) for narrow short-K ones.
-// Where the wide GEMM's 64x128 tiles fit in one round on the CUs (qkv, N = 2560, at M <= 768; the
-// PLE projection, N = 8960, at M <= 128), one block per CU with two waves per sub-tile splitting its
-// k-steps (20) beats 12 by 1-3% at K = 1536 (qkv at M = 512: 8.42 against 8.64 us, the whole
-// layer step 61.3-61.8 against 62.5-64.0 us); with more tiles than CUs it loses by half (10.6
-// against 15.7 us at M = 1024), and at K = 1024 the two are even.
-// The narrow long-K GEMMs (the output projection, K = 2048, and the down projection, K = 6144,
-// both N = 1536) have only 192 such tiles, one block per CU, whose two waves cannot hide their
-// LDS reads behind two MFMAs per k-step: four waves that each own the whole 64x64 tile and take
-// every fourth k-step keep all four SIMDs issuing (output projection 7.3 us against 9.5 us on
-// 64x64 with two waves, down 16.1 us against 21.6 us or more, with 256-deep k-tiles in a 3-slot
-// ring (19)); 512-deep k-tiles in a 2-slot ring (22) keep more bytes in flight per CU: 6.7 and
-// 14.9 us.  The gate/up GEMM with its GELU
-// epilogue runs best on the direct-W 64x256 tile, two blocks per CU (23): 14.8 us against
-// 16.1-18.0 us on 12 for N = 12288, 26.5 against 32.5 us for the double-wide N = 24576.  A 128x192
-// tile, one per CU (256 tiles), measured slower than 12 (17.2 against 15.9 us): its one wave per
-// SIMD leaves the LDS reads exposed.
-// The same direct-W 64x256 tile takes the other epilogues where 64x128 tiles would need more than
-// one round on the CUs but 64x256 tiles fit in one: at M = 512, N = 4608-8192 (the single
-// micro-batch GEMM, N = 6144: 10.2-10.6 against 11.3-11.7 us int32, 9.7 against 11.3 us with the
-// dequant epilogue; N = 4608 9.7 against 10.7, N = 8192 12.2 against 13.0; K = 2048 / 6144 / 12288
-// 12.2 / 27.3 / 48.6 against 13.5 / 29.6 / 52.8 us), M = 384 / 640 at N = 6144 (9.6 / 11.9
-// against 10.6 / 12.6 us), and from 77 to 1024 rows at N = 2560-24576 (M = 1024, N = 2560: 10.3
-// against 11.4 us; M = 256, N = 8960 with the dequant epilogue: 9.6 against 11.0).  Past one round (M = 512 at N = 8960 / 12288, M = 768 / 1024 at
-// N = 6144) it loses to 12 by 5-12%, and where 64x128 tiles fit one round 20 stays ahead.
-// At a few thousand rows the long-K narrow down projections (K = 6144 / 12288, N = 1536) take the
-// direct-W 128x256 tile with W 8 k-steps ahead (24): 43 against 49 us at K = 6144 (the int32
-// sweep 7.02 -> 6.83 ms at M = 3658, 7.89 -> 7.61 ms at M = 4096), 78 against 89 us at K = 12288.
-// Past 1024 rows the GELU epilogue, and everything past 8192 rows, take the direct-W 128x256 tile
-// with two blocks per CU (25): gate/up + GELU 76-78 against 90 us on the 8-wave 128x256 tile (5)
-// at M = 3658 (N = 12288), 142 against 164 us for N = 24576, 308 against 352 us at M = 16384; down
-// + residual at M = 16384 141 against 167 us.  64x256 with three or four blocks per CU, and
-// 128x256 with W only 2 k-steps ahead, measured slower on all of these.
-// Between one micro-batch and 8192 rows the GEMMs that no rule above takes (N between 4096 and
-// 8192, and narrower ones too tall for one round of direct-W tiles) run on that 128x256
-// two-per-CU tile (25) rather than 64x128 tiles with their accumulators staged through LDS (12),
-// unless its tiles are fewer than the CUs or leave a last round of at most a quarter of them.
-// Timed with distinct cold weights per call: M = 3658, N = 4096 / 5120 30.3 / 43.5 against
-// 37.7 / 47.5 us, K = 2048 N = 4096 35.9 against 46.7 us, M = 8192 N = 6144 98.5 against 122.1 us;
-// with the short last rounds (576 or 320 tiles) 12 is even or up to 7% ahead.  The wide GEMMs
-// (N >= 8192) with bf16 epilogues take 25 too, where the 256x256 8-wave tile (0) ran before:
-// the PLE projection at M = 3658 58.8 against 86.2 us, N = 12288 83.6 against 91.7 us (cold),
-// the residual epilogue 68.8 against 106.1 us.  The 256-row tiles read the weight half as often,
-// which decides only on the int32 gate/up of the 141-GEMM sweep, timed with a distinct weight per
-// layer (92 us in the sequence against 98 us on 128x256, while one GEMM repeated on a
-// cache-resident weight favours 128x256, 92 against 108 us).  The wide int32 GEMMs (N >= 8192)
-// past one micro-batch take the software-pipelined persistent 256x256 kernel (29): gate/up at
-// M = 16384 393 against 440 us, the 141-GEMM sweep 6.92 -> 6.78 ms at M = 3658 and 7.64 -> 7.31 ms
-// at M = 4096.  It is tried for int32 only: its bf16 epilogues run on one wave per SIMD and lose to
-// the two-blocks-per-CU tiles.
-// Where its 256x256 tiles leave a nearly empty last round (0 < tiles mod CUs <= CUs / 4), the
-// direct-W 128x256 tile with two blocks per CU (25) fills it: the PLE projection (N = 8960) at
-// M = 3658 (525 tiles on 256 CUs) 66.9 against 85.9 us, at M = 4096 (560 tiles) 80.7 against 92.0 us;
-// with fuller last rounds 29 keeps the lead (gate/up at M = 4096, 768 tiles: 94.3 against 101.7 us).
-// Past one micro-batch the GEMMs up to N = 4096 (qkv, the output and down projections) stream
-// (BM + BN) * K bytes per tile at the per-CU L2 delivery rate, so their time follows the bytes the
-// busiest CU moves: rounds x (BM + BN).  One round of direct-W BMx256 tiles, one block per CU,
-// with the smallest BM in 96, 128, 160, 192 that fits, is taken where it moves fewer bytes per CU
-// than the 64x128 three-per-CU tiles (12), i.e. ceil(tiles / CUs) x 192.  At M = 3658: down
-// 38.9 against 42.7 us on 128x256 (K = 6144; 69.2 against 77.4 us at K = 12288) and the output
-// projection 17.2 against 19.3 us on 12, on 96x256 (26, 234 tiles); qkv 22.3 against 25.6 us on
-// 12, on 160x256 (27, 230 tiles).  At M = 4096: qkv 25.5 against 27.6 us on 192x256 (28, 220
-// tiles; 160x256 needs 260 tiles, two rounds: 37.5 us); down on 128x256 (24), 44.2 against 55.0 us
-// for 96x256's two rounds.  All bit-identical.  Past one round of every such tile (down at M =
-// 8192, 384 128x256 tiles) two blocks per CU (25) win, 79.2 against 84.5 us.
+// The pipelined kernel's 256x256 tiles leave a nearly empty last round on the CUs.
 static bool pipe_tail_is_short(int M, int NP) {
   const int cus = cu_count();
   const int tail = ((M + 255) / 256) * ((NP + 255) / 256) % cus;
   return tail > 0 && 4 * tail <= cus;
 }
 
+// Tile choice.  Every rule was set by timing the configurations on MI355X (the measured times are
+// tabulated with the design notes); the reasons, briefly:
+//  * One 512-row micro-batch (M <= 1024): the GEMMs are bound by how fast each CU streams its
+//    operands, so small tiles spread over many CUs.  Narrow long-K GEMMs (the output and down
+//    projections) have only ~192 64x64 tiles, one per CU, so four waves split each tile's k-steps
+//    with 512-deep k-tiles (3).  The gate/up GEMM with its GELU epilogue runs on the direct-W 64x256
+//    tile, two blocks per CU (4).  Narrow short-K GEMMs take 64x64 (1).  Wide ones take 64x128 with
+//    two waves per sub-tile while those tiles fit one round on the CUs (2), then one round of
+//    direct-W 64x256 tiles (4), else 64x128 three blocks per CU (0).
+//  * Past one micro-batch: the GELU epilogue on the direct-W 128x256 tile, two blocks per CU (6).
+//    GEMMs up to N = 4096 stream (BM + BN) * K bytes per tile at the per-CU L2 delivery rate, so
+//    one round of the smallest direct-W BMx256 tile that fits the CUs (BM = 96, 128, 160, 192:
+//    7, 5, 8, 9) wins where its bytes per CU undercut the 64x128 three-per-CU tiles'.  The wide
+//    int32 GEMMs (N >= 8192) take the software-pipelined persistent 256x256 kernel (10), which
+//    reads each weight half as often, unless its last round would be nearly empty; everything
+//    else the 128x256 two-per-CU tile (6), or 64x128 (0) where 6's tiles are fewer than the CUs or
+//    leave a nearly empty last round.
 int gemm_pick_config(int M, int NP, int K, int epi) {
-  if (M <= 1024) {
-    if (K >= 2048 && NP <= 4096) return 22;  // few 64x64 tiles, long K: four waves split the k-steps
-    if (epi == EPI_GELU) return 23;          // direct-W 64x256, two blocks per CU
-    if (NP <= 2048) return 14;
-    // wide: 64x128 tiles with two waves per 32-row sub-tile splitting its k-steps (20) while the
-    // tiles fit one round on the CUs, then one round of direct-W 64x256 tiles (23), three blocks
-    // per CU on 64x128 tiles (12) past that
-    const int cus = cu_count(), mt = (M + 63) / 64;
-    if (mt * ((NP + 127) / 128) <= cus) return 20;
-    return mt * ((NP + 255) / 256) <= cus ? 23 : 12;
-  }
-  if (epi == EPI_GELU) return 25;  // direct-W 128x256, two blocks per CU
   const int cus = cu_count();
+  if (M <= 1024) {
+    if (K >= 2048 && NP <= 4096) return CFG_64x64_KW4;
+    if (epi == EPI_GELU) return CFG_DW_64x256;
+    if (NP <= 2048) return CFG_64x64;
+    const int mt = (M + 63) / 64;
+    if (mt * ((NP + 127) / 128) <= cus) return CFG_64x128_KW2;
+    return mt * ((NP + 255) / 256) <= cus ? CFG_DW_64x256 : CFG_64x128;
+  }
+  if (epi == EPI_GELU) return CFG_DW_128x256;
   auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((NP + bn - 1) / bn); };
   if (K >= 1024 && NP <= 4096) {
     // one round of direct-W BMx256 tiles, smallest BM first, where the busiest CU moves fewer bytes
     // than on the 64x128 three-per-CU tiles
-    const int cost12 = (tiles(64, 128) + cus - 1) / cus * (64 + 128);
-    constexpr int kBm[4] = {96, 128, 160, 192}, kCfgOf[4] = {26, 24, 27, 28};
+    const int cost0 = (tiles(64, 128) + cus - 1) / cus * (64 + 128);
+    constexpr int kBm[4] = {96, 128, 160, 192};
+    constexpr int kCfgOf[4] = {CFG_DW_96x256, CFG_DW_128x256_PW8, CFG_DW_160x256, CFG_DW_192x256};
     for (int i = 0; i < 4; ++i)
       if (tiles(kBm[i], 256) <= cus) {
-        if (kBm[i] + 256 < cost12) return kCfgOf[i];
+        if (kBm[i] + 256 < cost0) return kCfgOf[i];
         break;
       }
   }
-  if (M <= 8192) {
-    if (K >= 4096 && NP <= 2048) return 25;  // long-K narrow past one round of 128x256: two blocks per CU
-    if (NP >= 8192) return epi != EPI_I32 || pipe_tail_is_short(M, NP) ? 25 : 29;  // wide
-    // the rest on 128x256 tiles, two blocks per CU, unless they are fewer than the CUs or leave a
-    // nearly empty last round
-    const int t25 = tiles(128, 256), tail = t25 % cus;
-    return t25 >= cus && !(tail > 0 && 4 * tail <= cus) ? 25 : 12;
-  }
-  return NP >= 8192 && epi == EPI_I32 && !pipe_tail_is_short(M, NP) ? 29 : 25;
+  const bool pipe = NP >= 8192 && epi == EPI_I32 && !pipe_tail_is_short(M, NP);
+  if (M > 8192) return pipe ? CFG_PIPE_256x256 : CFG_DW_128x256;
+  if (K >= 4096 && NP <= 2048) return CFG_DW_128x256;  // long-K narrow past one round of 128x256
+  if (NP >= 8192) return pipe ? CFG_PIPE_256x256 : CFG_DW_128x256;
+  const int t6 = tiles(128, 256), tail = t6 % cus;
+  return t6 >= cus && !(tail > 0 && 4 * tail <= cus) ? CFG_DW_128x256 : CFG_64x128;
 }
 
-int gemm_launch(const GemmParams& p, int epi, int cfg, bool a_packed, void* ws, int64_t ws_bytes,
-                hipStream_t stream) {
+int gemm_launch(const GemmParams& p, int epi, int cfg, bool a_packed, hipStream_t stream) {
   if (cfg < 0) cfg = gemm_pick_config(p.M, p.NT * 32, p.KF * 32, epi);
   switch (cfg) {
-    case 0: launch<0>(p, epi, a_packed, ws, ws_bytes, stream); break;
-    case 1: launch<1>(p, epi, a_packed, ws, ws_bytes, stream); break;
-    case 2: launch<2>(p, epi, a_packed, ws, ws_bytes, stream); break;
-    case 3: launch<3>(p, epi, a_packed, ws, ws_bytes, stream); break;
-    case 4: launch<4>(p, epi, a_packed, ws, ws_bytes, stream); break;
-    case 5: launch<5>(p, epi, a_packed, ws, ws_bytes, stream); break;
-    case 6: launch<6>(p, epi, a_packed, ws, ws_bytes, stream); break;
-    case 7: launch<7>(p, epi, a_packed, ws, ws_bytes, stream); break;
-    case 8: launch<8>(p, epi, a_packed, ws, ws_bytes, stream); break;
-    case 9: launch<9>(p, epi, a_packed, ws, ws_bytes, stream); break;
-    case 10: launch<10>(p, epi, a_packed, ws, ws_bytes, stream); break;
-    case 11: launch<11>(p, epi, a_packed, ws, ws_bytes, stream); break;
-    case 12: launch<12>(p, epi, a_packed, ws, ws_bytes, stream); break;
-    case 13: launch<13>(p, epi, a_packed, ws, ws_bytes, stream); break;
-    case 14: launch<14>(p, epi, a_packed, ws, ws_bytes, stream); break;
-    case 15: launch<15>(p, epi, a_packed, ws, ws_bytes, stream); break;
-    case 16: launch<16>(p, epi, a_packed, ws, ws_bytes, stream); break;
-    case 17: launch<17>(p, epi, a_packed, ws, ws_bytes, stream); break;
-    case 18: launch<18>(p, epi, a_packed, ws, ws_bytes, stream); break;
-    case 19: launch<19>(p, epi, a_packed, ws, ws_bytes, stream); break;
-    case 20: launch<20>(p, epi, a_packed, ws, ws_bytes, stream); break;
-    case 21: launch<21>(p, epi, a_packed, ws, ws_bytes, stream); break;
-    case 22: launch<22>(p, epi, a_packed, ws, ws_bytes, stream); break;
-    case 23: launch_dw<0>(p, epi, a_packed, stream); break;
-    case 24: launch_dw<1>(p, epi, a_packed, stream); break;
-    case 25: launch_dw<2>(p, epi, a_packed, stream); break;
-    case 26: launch_dw<3>(p, epi, a_packed, stream); break;
-    case 27: launch_dw<4>(p, epi, a_packed, stream); break;
-    case 28: launch_dw<5>(p, epi, a_packed, stream); break;
-    case 29: launch_pipe<0>(p, epi, a_packed, stream); break;
+    case 0: launch<0>(p, epi, a_packed, stream); break;
+    case 1: launch<1>(p, epi, a_packed, stream); break;
+    case 2: launch<2>(p, epi, a_packed, stream); break;
+    case 3: launch<3>(p, epi, a_packed, stream); break;
+    case 4: launch_dw<0>(p, epi, a_packed, stream); break;
+    case 5: launch_dw<1>(p, epi, a_packed, stream); break;
+    case 6: launch_dw<2>(p, epi, a_packed, stream); break;
+    case 7: launch_dw<3>(p, epi, a_packed, stream); break;
+    case 8: launch_dw<4>(p, epi, a_packed, stream); break;
+    case 9: launch_dw<5>(p, epi, a_packed, stream); break;
+    case 10: launch_pipe<0>(p, epi, a_packed, stream); break;
     default: return fail(W8A8_EINVAL, "gemm: unknown tile config %d", cfg);
   }
   return check_launch("gemm");

@@ -49,20 +49,12 @@ def _ld(t):
     return t.stride(0) if t.shape[0] > 1 else max(t.shape[1], 1)
 
 
-_WORKSPACES = {}
-
-
 def workspace(device, nbytes):
-    """The zero-initialised split-K / linear workspace of (device, current stream), grown to at
-    least nbytes.  Calls on one stream are ordered, so they can share it; its first 4 KiB of
-    counters are zero between calls by the kernels' own contract."""
-    device = torch.device(device)
-    key = (device.index, current_stream_handle(device))
-    ws = _WORKSPACES.get(key)
-    if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(int(nbytes), 1 << 20), dtype=torch.uint8, device=device)
-        _WORKSPACES[key] = ws
-    return ws
+    """Scratch of at least nbytes on device for one call on the current stream (the linear's packed
+    int8 rows and row scales: nothing is kept between calls).  It comes from torch's caching
+    allocator, which ties the block to the current stream, so no buffer outlives its stream and no
+    stream reuses another's while that one may still be running."""
+    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=torch.device(device))
 
 
 def _same_device(*ts):
@@ -244,10 +236,8 @@ def gemm_i32(a, w, c=None, tile_cfg=-1, split_k=0):
     if tuple(c.shape) != (M, w.N):
         raise ValueError(f"gemm_i32: C has shape {tuple(c.shape)}, expected {(M, w.N)}")
     _same_device(at, w.data, c)
-    need = lib().w8a8_gemm_workspace_bytes(M, w.N, K, tile_cfg, split_k) if M else 0
-    ws = workspace(at.device, need) if need > 0 else None
     call("w8a8_gemm_i32_ex", ap, lda, a_packed, w.data.data_ptr(), M, w.N, K, c.data_ptr(), _ld(c), tile_cfg,
-         split_k, ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0, _stream(at))
+         split_k, None, 0, _stream(at))
     return c
 
 
@@ -281,11 +271,8 @@ def gemm_bf16(a, sx, w, sw=None, epilogue="none", residual=None, out=None, tile_
             raise ValueError("gemm_bf16: residual shape does not match")
         rp, ldr = residual.data_ptr(), _ld(residual)
     _same_device(at, sx, sw, w.data, out, residual)
-    need = lib().w8a8_gemm_workspace_bytes(M, w.N, K, tile_cfg, split_k) if M else 0
-    ws = workspace(at.device, need) if need > 0 else None
     call("w8a8_gemm_bf16_ex", ap, lda, a_packed, sx.data_ptr(), w.data.data_ptr(), sw.data_ptr(), M, w.N, K,
-         epi, w.interleave, rp, ldr, out.data_ptr(), _ld(out), tile_cfg, split_k,
-         ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0, _stream(at))
+         epi, w.interleave, rp, ldr, out.data_ptr(), _ld(out), tile_cfg, split_k, None, 0, _stream(at))
     return out
 
 
@@ -338,7 +325,8 @@ def linear_workspace_bytes(M, N, K):
 
 def linear_bf16(x, w, sw=None, epilogue="none", residual=None, rms_w=None, eps=1e-6, out=None, ws_arg=None):
     """bf16 x -> per-token quant -> W8A8 GEMM -> dequant epilogue -> bf16 (gemma_npu.py:117-152).
-    ws_arg: a zero-initialised uint8 workspace to use instead of the per-stream one."""
+    ws_arg: a uint8 device tensor of at least linear_workspace_bytes(M, N, K) bytes to use as the call's
+    scratch instead of a fresh one from torch's caching allocator."""
     w = _packed(w)
     sw = w.sw if sw is None else sw
     if sw is None:

@@ -67,7 +67,8 @@ def rms_norm_op(x: Tensor, w: Optional[Tensor], eps: float) -> Tensor:
 
 @rms_norm_op.register_fake
 def _rms_norm_fake(x, w, eps):
-    return torch.empty_like(x)
+    # the real op works on (and returns) a contiguous copy of a strided x
+    return x.new_empty(x.shape)
 
 
 @torch.library.custom_op("w8a8::attention", mutates_args=(), device_types="cuda")

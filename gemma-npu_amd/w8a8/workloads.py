@@ -50,6 +50,14 @@ def weights(N, K, seed):
     return w, sw
 
 
+def single_gemm_inputs(M=512, K=1536, N=6144, seed=0):
+    """The single prefill micro-batch GEMM (M=512, K=1536, N=6144): bf16 activations (with outliers)
+    and int8 weights with their scales, both drawn from one seed (0 by default)."""
+    x = activations(M, K, seed)
+    w, sw = weights(N, K, seed)
+    return x, w, sw
+
+
 def layer_seed(layer, group):
     """Seed of one layer's weight group in the full-prefill sweep (distinct per layer)."""
     return 1000 + 16 * layer + group

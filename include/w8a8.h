@@ -136,21 +136,16 @@ int w8a8_gemm_tile_configs(void);
  * for tests and benchmarks that report which kernel ran. */
 int w8a8_gemm_pick_tile_config(int64_t M, int64_t N, int64_t K, int epilogue);
 
-/* Split-K workspace the _ex GEMMs use for [M, N, K] with tile_cfg (-1 = automatic) and split_k
- * (n >= 1 = at most n blocks per output tile along K, only when there are fewer than 200 output
- * tiles; 0 = automatic: two blocks per output tile when a block-split tile configuration has at
- * most 128 output tiles and K >= 4096, otherwise none -- the automatic tile choice currently
- * takes no such configuration, so with tile_cfg = -1 this is 0).  0 when no split will happen.
- * Its first 4 KiB hold arrival counters that must be zero before a call and are zero again after
- * it (zero-fill a new workspace once); the rest is scratch, so one workspace serves any shapes.
- * Calls that overlap in time need separate workspaces. */
+/* Workspace bytes the _ex GEMMs need for [M, N, K] with tile_cfg (-1 = automatic) and split_k:
+ * always 0, since no tile configuration splits K across blocks (the long-K configurations split
+ * a tile's k-steps among the waves of one block and add the partials in LDS); -1 for a tile_cfg out
+ * of range or split_k > 1.  Kept so that callers written against a split-K workspace still work. */
 int64_t w8a8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int tile_cfg, int split_k);
 
 /* As w8a8_gemm_i32 with A given either row-major (a_packed = 0, lda used) or packed
- * (a_packed = 1, lda ignored), an explicit tile configuration (0 .. w8a8_gemm_tile_configs()-1, -1 = automatic), a split-K
- * request (as w8a8_gemm_workspace_bytes) and its workspace (NULL or too small: no split;
- * 256-byte aligned).  Split-K keeps the result bit-exact: int32 partial sums are added in a
- * fixed order by the last block of each output tile. */
+ * (a_packed = 1, lda ignored) and an explicit tile configuration (0 .. w8a8_gemm_tile_configs()-1,
+ * -1 = automatic).  split_k must be 0 (automatic) or 1; larger values fail with W8A8_ENOTSUP.
+ * workspace / workspace_bytes are not used (may be NULL / 0). */
 int w8a8_gemm_i32_ex(const int8_t *a, int64_t lda, int a_packed, const int8_t *w_packed, int64_t M, int64_t N,
                      int64_t K, int32_t *c, int64_t ldc, int tile_cfg, int split_k, void *workspace,
                      int64_t workspace_bytes, hipStream_t stream);
@@ -166,8 +161,8 @@ int w8a8_gemm_bf16(const int8_t *a, int64_t lda, const float *sx, const int8_t *
                    int64_t M, int64_t N, int64_t K, int epilogue, int64_t interleave, const uint16_t *res,
                    int64_t ldr, uint16_t *out, int64_t ldo, hipStream_t stream);
 
-/* As w8a8_gemm_bf16 with packed or row-major A, an explicit tile configuration and an
- * optional split-K workspace (as w8a8_gemm_i32_ex). */
+/* As w8a8_gemm_bf16 with packed or row-major A and an explicit tile configuration; split_k and
+ * the workspace as w8a8_gemm_i32_ex. */
 int w8a8_gemm_bf16_ex(const int8_t *a, int64_t lda, int a_packed, const float *sx, const int8_t *w_packed,
                       const float *sw, int64_t M, int64_t N, int64_t K, int epilogue, int64_t interleave,
                       const uint16_t *res, int64_t ldr, uint16_t *out, int64_t ldo, int tile_cfg, int split_k,
@@ -255,9 +250,9 @@ int w8a8_k_ple_out(const int32_t *acc, int64_t ldacc, const float *sx, const flo
 
 /* ---- whole linear: bf16 in -> bf16 out (NPUGemm.matmul, gemma_npu.py:117-152) ------------ */
 
-/* Workspace for w8a8_linear_bf16: the GEMM's split-K workspace (counters first, as
- * w8a8_gemm_workspace_bytes), packed int8 rows and per-row scales.  Same rules: zero-fill it
- * once; calls that overlap in time need separate workspaces. */
+/* Workspace for w8a8_linear_bf16: the packed int8 rows and the per-row scales, 256-byte aligned
+ * parts (scratch: nothing is kept between calls, no clearing is needed).  Calls that overlap in
+ * time need separate workspaces. */
 int64_t w8a8_linear_workspace_bytes(int64_t M, int64_t N, int64_t K);
 
 /* quant_rows(x) -> GEMM -> epilogue.  epilogue 0-2 as w8a8_gemm_bf16; 3: residual with RMSNorm,
@@ -336,6 +331,14 @@ int w8a8_attention_bf16(const uint16_t *q, int64_t q_head_stride, int64_t q_row_
  * device's CU count only, so this size is stable for a shape. */
 int64_t w8a8_attention_workspace_bytes(int64_t H, int64_t KV, int64_t Tq, int64_t Tk, int64_t D, int64_t q_start,
                                        int64_t window);
+
+/* Diagnostic, no counterpart in the reference (for tests that must reach every form of the work
+ * list): the items per KV group w8a8_attention_ws_bf16 plans for these arguments (query tiles,
+ * each counted once per part its keys are split into), with *launch_order (if not NULL) set to 1
+ * when the items launch through the longest-first order table and 0 when they run in plain item
+ * order (plans of more than 1536 items per group, or one item per tile); -1 if invalid. */
+int64_t w8a8_attention_plan_items(int64_t H, int64_t KV, int64_t Tq, int64_t Tk, int64_t D, int64_t q_start,
+                                  int64_t window, int *launch_order);
 
 /* w8a8_attention_bf16 with a workspace for splitting long causal tiles: device memory of at least
  * w8a8_attention_workspace_bytes(...) bytes, 16-byte aligned, ZERO-FILLED BEFORE ITS FIRST USE (its

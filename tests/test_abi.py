@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
     missing = [n for n in declared_functions() if not hasattr(L, n)]
     assert not missing, f"not exported: {missing}"
     assert L.w8a8_abi_version() == 1
-    assert L.w8a8_gemm_tile_configs() == 30
+    assert L.w8a8_gemm_tile_configs() == 11
 
 
 def test_pick_tile_config_is_a_valid_configuration():
@@ -46,31 +46,44 @@ def test_pick_tile_config_is_a_valid_configuration():
                 assert 0 <= cfg < n, (M, N, K, epi, cfg)
     assert L.w8a8_gemm_pick_tile_config(512, 12288, 1536, 1) != L.w8a8_gemm_pick_tile_config(3658, 12288, 1536, 1)
     # past one micro-batch (256 CUs), N <= 4096: one round of direct-W BMx256 tiles with the smallest BM
-    # that fits (96: 26, 128: 24, 160: 27, 192: 28) where it moves fewer bytes per CU than the 64x128
-    # tiles (12); then 128x256 with two blocks per CU for the long-K narrow ones; the wide int32
-    # gate/up on the pipelined kernel (29)
-    assert L.w8a8_gemm_pick_tile_config(3658, 1536, 6144, -1) == 26
-    assert L.w8a8_gemm_pick_tile_config(3658, 1536, 2048, -1) == 26
-    assert L.w8a8_gemm_pick_tile_config(3658, 2560, 1536, -1) == 27
-    assert L.w8a8_gemm_pick_tile_config(4096, 2560, 1536, -1) == 28
-    assert L.w8a8_gemm_pick_tile_config(4096, 1536, 6144, -1) == 24
-    assert L.w8a8_gemm_pick_tile_config(8192, 1536, 6144, -1) == 25
-    assert L.w8a8_gemm_pick_tile_config(16384, 1536, 6144, 2) == 25
-    assert L.w8a8_gemm_pick_tile_config(3658, 256, 1536, -1) == 12      # one column tile: 64x128 moves less
-    assert L.w8a8_gemm_pick_tile_config(3658, 12288, 1536, -1) == 29
-    assert L.w8a8_gemm_pick_tile_config(512, 6144, 1536, -1) == 23      # one round of 64x256 tiles
-    assert L.w8a8_gemm_pick_tile_config(512, 8192, 1536, 0) == 23
-    assert L.w8a8_gemm_pick_tile_config(512, 4096, 1536, -1) == 20      # 64x128 tiles fit one round
-    assert L.w8a8_gemm_pick_tile_config(512, 8960, 1536, -1) == 12      # 64x256 tiles past one round
-    assert L.w8a8_gemm_pick_tile_config(768, 6144, 1536, 2) == 12
-    assert L.w8a8_gemm_pick_tile_config(3658, 8960, 1536, 0) == 25      # wide, bf16 epilogue
-    assert L.w8a8_gemm_pick_tile_config(3658, 5120, 1536, -1) == 25     # 580 128x256 tiles, a full last round
-    assert L.w8a8_gemm_pick_tile_config(3072, 6144, 1536, -1) == 12     # 576 tiles: a short last round
-    assert L.w8a8_gemm_pick_tile_config(2048, 5120, 1536, 2) == 12      # 320 tiles: likewise
-    assert L.w8a8_gemm_pick_tile_config(3658, 256, 256, -1) == 12       # fewer 128x256 tiles than CUs
+    # that fits (96: 7, 128: 5, 160: 8, 192: 9) where it moves fewer bytes per CU than the 64x128
+    # tiles (0); then 128x256 with two blocks per CU (6) for the long-K narrow ones; the wide int32
+    # gate/up on the pipelined kernel (10)
+    assert L.w8a8_gemm_pick_tile_config(3658, 1536, 6144, -1) == 7
+    assert L.w8a8_gemm_pick_tile_config(3658, 1536, 2048, -1) == 7
+    assert L.w8a8_gemm_pick_tile_config(3658, 2560, 1536, -1) == 8
+    assert L.w8a8_gemm_pick_tile_config(4096, 2560, 1536, -1) == 9
+    assert L.w8a8_gemm_pick_tile_config(4096, 1536, 6144, -1) == 5
+    assert L.w8a8_gemm_pick_tile_config(8192, 1536, 6144, -1) == 6
+    assert L.w8a8_gemm_pick_tile_config(16384, 1536, 6144, 2) == 6
+    assert L.w8a8_gemm_pick_tile_config(3658, 256, 1536, -1) == 0      # one column tile: 64x128 moves less
+    assert L.w8a8_gemm_pick_tile_config(3658, 12288, 1536, -1) == 10
+    assert L.w8a8_gemm_pick_tile_config(512, 6144, 1536, -1) == 4      # one round of 64x256 tiles
+    assert L.w8a8_gemm_pick_tile_config(512, 8192, 1536, 0) == 4
+    assert L.w8a8_gemm_pick_tile_config(512, 4096, 1536, -1) == 2      # 64x128 tiles fit one round
+    assert L.w8a8_gemm_pick_tile_config(512, 8960, 1536, -1) == 0      # 64x256 tiles past one round
+    assert L.w8a8_gemm_pick_tile_config(768, 6144, 1536, 2) == 0
+    assert L.w8a8_gemm_pick_tile_config(3658, 8960, 1536, 0) == 6      # wide, bf16 epilogue
+    assert L.w8a8_gemm_pick_tile_config(3658, 5120, 1536, -1) == 6     # 580 128x256 tiles, a full last round
+    assert L.w8a8_gemm_pick_tile_config(3072, 6144, 1536, -1) == 0     # 576 tiles: a short last round
+    assert L.w8a8_gemm_pick_tile_config(2048, 5120, 1536, 2) == 0      # 320 tiles: likewise
+    assert L.w8a8_gemm_pick_tile_config(3658, 256, 256, -1) == 0       # fewer 128x256 tiles than CUs
     assert L.w8a8_gemm_pick_tile_config(0, 64, 64, 0) == -1
     assert L.w8a8_gemm_pick_tile_config(64, 64, 64, 3) == -1
     assert L.w8a8_gemm_pick_tile_config(64, 64, 64, -2) == -1
+
+
+def test_every_tile_configuration_is_reachable():
+    """The library builds exactly the configurations the automatic choice takes: each of them is the
+    choice for one of these E2B prefill shapes (M, N, K, epilogue)."""
+    L = _lib.lib()
+    cases = {0: (3658, 256, 1536, -1), 1: (512, 1536, 1536, 0), 2: (512, 4096, 1536, -1),
+             3: (512, 1536, 6144, 2), 4: (512, 12288, 1536, 1), 5: (4096, 1536, 6144, -1),
+             6: (8192, 1536, 6144, -1), 7: (3658, 1536, 6144, -1), 8: (3658, 2560, 1536, -1),
+             9: (4096, 2560, 1536, -1), 10: (3658, 12288, 1536, -1)}
+    assert sorted(cases) == list(range(L.w8a8_gemm_tile_configs()))
+    for cfg, (M, N, K, epi) in cases.items():
+        assert L.w8a8_gemm_pick_tile_config(M, N, K, epi) == cfg, (cfg, M, N, K, epi)
 
 
 def test_packed_weight_bytes():
@@ -90,24 +103,16 @@ def test_linear_workspace_bytes():
     assert L.w8a8_packed_act_bytes(512, 1536) == 512 * 1536
     assert L.w8a8_packed_act_bytes(33, 40) == 64 * 64       # rows to 32, k to 64
     assert L.w8a8_packed_act_bytes(0, 64) == 0
-    assert L.w8a8_gemm_workspace_bytes(16384, 12288, 1536, -1, 8) == 0       # enough tiles: no split
-    assert L.w8a8_gemm_workspace_bytes(512, 1536, 2048, 10, 0) == 0           # automatic: short K kept whole
-    auto = L.w8a8_gemm_workspace_bytes(512, 1536, 6144, 10, 0)             # automatic: few tiles, long K
-    assert auto == 4096 + 48 * 2 * 128 * 128 * 4
-    g = L.w8a8_gemm_workspace_bytes(512, 1536, 6144, 10, 8)                  # 48 tiles, asked to split
-    assert g == 4096 + 48 * 5 * 128 * 128 * 4
-    # automatic tile for the long-K down projection at M=512: wave split-K, never split across blocks
-    assert L.w8a8_gemm_workspace_bytes(512, 1536, 6144, -1, 0) == 0
-    assert L.w8a8_gemm_workspace_bytes(512, 1536, 6144, 19, 4) == 0
-    assert L.w8a8_gemm_workspace_bytes(512, 1536, 6144, 22, 4) == 0
-    assert L.w8a8_gemm_workspace_bytes(3658, 1536, 6144, 24, 4) == 0       # direct-W: never split
-    for cfg in (26, 27, 28):                                                # direct-W 96/160/192 x 256
-        assert L.w8a8_gemm_workspace_bytes(3658, 1536, 6144, cfg, 4) == 0  # never split
-    assert L.w8a8_gemm_workspace_bytes(3658, 12288, 1536, 29, 4) == 0      # pipelined: never split
-    assert L.w8a8_gemm_workspace_bytes(3658, 1536, 6144, 30, 0) == -1      # past the last configuration
-    assert L.w8a8_linear_workspace_bytes(512, 1536, 6144) == 4096 + 512 * 6144 + 512 * 4
-    assert L.w8a8_linear_workspace_bytes(512, 1536, 2048) == 4096 + 512 * 2048 + 512 * 4
-    assert L.w8a8_linear_workspace_bytes(3, 64, 64) == 4096 + 32 * 64 + 256  # counters kept; rows to 32
+    # no configuration splits K across blocks: the GEMMs need no workspace, and split_k > 1 is refused
+    for cfg in range(-1, 11):
+        assert L.w8a8_gemm_workspace_bytes(512, 1536, 6144, cfg, 0) == 0
+        assert L.w8a8_gemm_workspace_bytes(3658, 12288, 1536, cfg, 1) == 0
+    assert L.w8a8_gemm_workspace_bytes(512, 1536, 6144, 3, 4) == -1
+    assert L.w8a8_gemm_workspace_bytes(3658, 1536, 6144, 11, 0) == -1      # past the last configuration
+    # the linear's scratch: packed int8 rows (to 32 rows, k to 64), then the row scales, 256-aligned
+    assert L.w8a8_linear_workspace_bytes(512, 1536, 6144) == 512 * 6144 + 512 * 4
+    assert L.w8a8_linear_workspace_bytes(512, 1536, 2048) == 512 * 2048 + 512 * 4
+    assert L.w8a8_linear_workspace_bytes(3, 64, 64) == 32 * 64 + 256
 
 
 def _status(name, *args):

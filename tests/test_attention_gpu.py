@@ -193,6 +193,34 @@ def test_split_plans_match_oracle(H, KV, Tq, Tk, D, q_start):
     assert np.allclose(lse[:, Tq - 200:].cpu().numpy(), lse_ref, rtol=1e-5, atol=1e-4)
 
 
+def test_split_plan_past_the_order_table():
+    """A causal call whose split plan holds more items per KV group than the launch-order table
+    (1536): a 20000-token prompt at head_dim 512, 1250 query tiles of which the longest are split.
+    Its items then run in plain item order.  The first and last 40 rows against the oracle, and
+    two calls equal."""
+    import ctypes
+    from w8a8 import lib
+    H, KV, D = 8, 1, 512
+    order = ctypes.c_int(-1)
+    T = next((t for t in (20000, 20500, 21000, 19500, 21500, 22000)
+              if lib().w8a8_attention_plan_items(H, KV, t, t, D, 0, 0, ctypes.byref(order)) > 1536
+              and lib().w8a8_attention_workspace_bytes(H, KV, t, t, D, 0, 0) > 0), None)
+    assert T is not None, "no prompt length in the list plans past the order table"
+    lib().w8a8_attention_plan_items(H, KV, T, T, D, 0, 0, ctypes.byref(order))
+    assert order.value == 0
+    print(f"attention T={T} D={D}: {lib().w8a8_attention_plan_items(H, KV, T, T, D, 0, 0, None)} items, "
+          "item order", flush=True)
+    q, k, v = make(H, KV, T, T, D, seed=57, qscale=0.3)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    a, lse = attn.attention(qd, kd, vd, 0, 0, return_lse=True)
+    assert torch.equal(a, attn.attention(qd, kd, vd, 0, 0))
+    ref, bud, _ = reference(q[:, :40], k[:, :40], v[:, :40], 0, 0)
+    check(a[:, :40], ref, bud, "first rows")
+    ref, bud, lse_ref = reference(q[:, T - 40:], k, v, T - 40, 0)
+    check(a[:, T - 40:], ref, bud, "last rows")
+    assert np.allclose(lse[:, T - 40:].cpu().numpy(), lse_ref, rtol=1e-5, atol=1e-4)
+
+
 def test_split_workspace_shared_across_shapes():
     """Split calls of different shapes share the stream's workspace.  A whole-prompt causal call at
     head_dim 512 (T = 3658: ~190 split tiles), then 256 queries at the end of the prompt (16 split

@@ -89,9 +89,8 @@ def test_gemm_i32_strided_views():
 def test_gemm_i32_single_prefill_microbatch():
     """One prefill micro-batch GEMM, M=512 K=1536 N=6144, seed 0: bit-exact vs torch._int_mm."""
     M, K, N = 512, 1536, 6144
-    x = workloads.activations(M, K, seed=0)
+    x, w, _ = workloads.single_gemm_inputs(M, K, N, seed=0)
     a, _ = ops.quant_rows(x.to(DEV))
-    w, _ = workloads.weights(N, K, seed=1)
     c = ops.gemm_i32(a, packed_from_nk(w))
     ref = torch._int_mm(a.cpu(), w.t().contiguous())
     assert torch.equal(c.cpu(), ref)
@@ -228,51 +227,20 @@ def test_gemm_bf16_packed_a_epilogues(cfg):
     assert_bf16_close(f32(to_bits(g)), f32(orc.gelu_mul(y)), what="gelu packed A")
 
 
-# ---- split-K ----------------------------------------------------------------------------------
+# ---- long K ---------------------------------------------------------------------------------
 
-@pytest.mark.parametrize("cfg", [10, 8, 1])
-@pytest.mark.parametrize("packed_a", [False, True])
-@pytest.mark.parametrize("M,N,K", [(64, 256, 6144), (512, 1536, 6144), (512, 2560, 1536), (100, 96, 2048),
-                                   (96, 128, 2112)])
-def test_gemm_i32_split_k(cfg, packed_a, M, N, K):
-    """Few output tiles: the GEMM splits K over blocks and the last block adds the int32
-    partials, so the result stays bit-exact.  Run twice (the arrival counters must reset)."""
-    from w8a8 import lib
-    assert lib().w8a8_gemm_workspace_bytes(M, N, K, cfg, 8) > 0, "shape should split K"
-    a = rand_i8((M, K), seed=M + 7 * N)
-    w = rand_i8((N, K), seed=K + 3 * N)
-    ref = torch._int_mm(a, w.t().contiguous()) if M > 16 else torch.from_numpy(orc.int_mm_nk(a.numpy(), w.numpy()))
-    pw = packed_from_nk(w)
-    A = ops.pack_act(a.to(DEV)) if packed_a else a.to(DEV)
-    for _ in range(2):
-        c = ops.gemm_i32(A, pw, tile_cfg=cfg, split_k=8)
-        assert torch.equal(c.cpu(), ref)
+def test_split_k_request_is_refused():
+    """No configuration splits K across blocks: a request for it fails before launching."""
+    from w8a8 import W8A8Error
+    a = rand_i8((64, 256), 1).to(DEV)
+    w = packed_from_nk(rand_i8((128, 256), 2))
+    with pytest.raises(W8A8Error, match="never split"):
+        ops.gemm_i32(a, w, split_k=4)
 
 
-def test_split_k_epilogues_and_workspace_reuse():
-    M, K, I = 256, 4096, 256
-    x, w, sw, q, sx = _inputs(M, K, 2 * I, 61)
-    pa, sx_d = ops.quant_rows_packed(x.to(DEV))
-    y = orc.dequant(orc.int_mm_nk(q, w.numpy()), sx, sw.numpy())
-    kw = dict(tile_cfg=10, split_k=8)
-    out = ops.gemm_bf16(pa, sx_d, packed_from_nk(w), sw.to(DEV), **kw)
-    assert np.array_equal(to_bits(out), y)
-    g = ops.gemm_bf16(pa, sx_d, packed_from_nk(w, interleave=I), sw.to(DEV), epilogue="gelu", **kw)
-    assert_bf16_close(f32(to_bits(g)), f32(orc.gelu_mul(y)), what="split-K gelu")
-    res = workloads.activations(M, 2 * I, 62, outliers=False)
-    r = ops.gemm_bf16(pa, sx_d, packed_from_nk(w), sw.to(DEV), epilogue="residual", residual=res.to(DEV), **kw)
-    assert np.array_equal(to_bits(r), orc.add_residual(y, to_bits(res)))
-    # a different shape on the same per-stream workspace, then the first again
-    a2 = rand_i8((40, 2048), 63)
-    w2 = rand_i8((128, 2048), 64)
-    c2 = ops.gemm_i32(a2.to(DEV), packed_from_nk(w2), **kw)
-    assert np.array_equal(c2.cpu().numpy(), orc.int_mm_nk(a2.numpy(), w2.numpy()))
-    out2 = ops.gemm_bf16(pa, sx_d, packed_from_nk(w), sw.to(DEV), **kw)
-    assert np.array_equal(to_bits(out2), y)
-
-
-def test_linear_split_k_layer_shapes():
-    """The M=512 micro-batch groups that split K (o: K=2048 N=1536; down: K=6144 N=1536)."""
+def test_linear_long_k_layer_shapes():
+    """The M=512 micro-batch groups with long K (o: K=2048 N=1536; down: K=6144 N=1536), whose
+    64x64 tiles have four waves split the k-steps and add their partials in LDS."""
     for K, N in ((2048, 1536), (6144, 1536)):
         x = workloads.activations(512, K, seed=K)
         w, sw = workloads.weights(N, K, seed=N + K)
@@ -282,17 +250,19 @@ def test_linear_split_k_layer_shapes():
         assert np.array_equal(to_bits(out), ref)
 
 
-def test_split_k_repeated_launches_fresh_inputs():
-    """Back-to-back split-K launches with different A each time: a stale partial or a counter
-    left non-zero by an earlier launch would show up as a wrong product."""
+def test_long_k_repeated_launches_fresh_inputs():
+    """Back-to-back launches of the wave split-K tile (M=512, K=6144, N=1536) with a different A each
+    time: a partial tile left in LDS or an output written from the wrong launch would show up as a
+    wrong product."""
     M, N, K = 512, 1536, 6144
     w = rand_i8((N, K), 71)
     pw = packed_from_nk(w)
     wt = w.t().contiguous()
+    assert lib().w8a8_gemm_pick_tile_config(M, N, K, -1) == 3
     outs, refs = [], []
     for it in range(12):
         a = rand_i8((M, K), 100 + it)
-        outs.append(ops.gemm_i32(ops.pack_act(a.to(DEV)), pw, tile_cfg=10, split_k=8))
+        outs.append(ops.gemm_i32(ops.pack_act(a.to(DEV)), pw))
         refs.append(torch._int_mm(a, wt))
     for it, (c, r) in enumerate(zip(outs, refs)):
         assert torch.equal(c.cpu(), r), f"launch {it}"

@@ -73,6 +73,36 @@ def test_gemv_lm_head_m1():
     assert_bf16_close(f32(to_bits(y)), f32(to_bits(ref)), what="lm head", extra=extra)
 
 
+def test_gemv_lm_head_m16():
+    """The LM head with 16 decode rows (K=1536, N=262144, M=16; BASELINE's largest GEMV row count)
+    on the packed weight, N(0,1) activations: every element against torch's CPU op with bf16
+    scales (the reference's decode copy, gemma_npu.py:82), and a 4096-column sample against the
+    oracle with fp32 scales."""
+    K, N = workloads.LM_HEAD
+    M = 16
+    x = workloads.activations(M, K, seed=79, outliers=False)
+    w, sw = workloads.weights(N, K, seed=80)
+    s = sw.to(torch.bfloat16)
+    wd = w.to(DEV)
+    pw = ops.pack_gemv_weight(wd)
+    y = ops.gemv_bf16(x.to(DEV), pw, s.to(DEV))
+    ref = torch._weight_int8pack_mm(x, w, s)
+    # the fp32 accumulation allowance of dot_error_bound, from float64 products on the GPU
+    # (|x| w sums are far below 2^53, so the bound itself is exact)
+    extra = ((4.0 * 2.0 ** -24) * (x.to(DEV).double().abs() @ wd.double().abs().t())
+             * s.to(DEV).double().abs()[None, :]).float().cpu().numpy()
+    got = f32(to_bits(y))
+    assert_bf16_close(got, f32(to_bits(ref)), what="lm head M16 vs torch", extra=extra)
+    assert (got == f32(to_bits(ref))).mean() > 0.97
+    cols = torch.randperm(N, generator=torch.Generator().manual_seed(81))[:4096].sort().values
+    yf = ops.gemv_bf16(x.to(DEV), pw, sw.to(DEV))
+    wc = w[cols].contiguous()
+    ref_o = orc.gemv(to_bits(x), wc.numpy(), sw[cols].numpy(), "f32")
+    extra_c = dot_error_bound(x.float().numpy(), wc.numpy(), sw[cols].numpy())
+    assert_bf16_close(f32(to_bits(yf))[:, cols.numpy()], f32(ref_o), what="lm head M16 fp32 scales vs oracle",
+                      extra=extra_c)
+
+
 def test_gemv_deterministic():
     x = workloads.activations(4, 6144, seed=1, outliers=False).to(DEV)
     w, sw = workloads.weights(1536, 6144, seed=2)

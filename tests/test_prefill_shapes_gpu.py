@@ -219,6 +219,6 @@ def test_one_round_tile_edges(K, N, Ms):
         assert torch.equal(c, ref), f"K={K} N={N} M={M} tile {cfg}: {(c != ref).sum().item()} mismatches"
         res = workloads.activations(M, N, seed=M + 1, outliers=False).to(DEV)
         y = ops.gemm_bf16(pa, sx, pw, epilogue="residual", residual=res)
-        y12 = ops.gemm_bf16(pa, sx, pw, epilogue="residual", residual=res, tile_cfg=12)
+        y12 = ops.gemm_bf16(pa, sx, pw, epilogue="residual", residual=res, tile_cfg=0)  # 64x128
         assert torch.equal(y, y12), f"K={K} N={N} M={M}: residual epilogue differs between tiles"
     assert len(picked) >= 2, f"K={K} N={N}: the edges {Ms} gave one tile {picked}"
