@@ -93,6 +93,9 @@ struct AttnParams {
   float* part;                          // [KV][nsplit_items] parked partial tiles, slot-major
   int* counters;                        // [KV][nsplit_tiles] arrival counts, zero between calls
   float scale, c;                       // c = scale * log2(e)
+  // 0: the last part of a split tile to arrive merges the parts; 1: the parts are only parked and
+  // attn_merge_kernel, launched next on the stream, merges every split tile.
+  int merge_mode;
   // Launch order of the items: workgroup j * KV + g runs item order[j] of group g (item j when
   // `ordered` is 0).  Last, after every pointer and scalar.
   int ordered;
@@ -141,10 +144,11 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(AttnParams p) {
   const int qi = lane & 15, qq = lane >> 4;  // query column, lane group
 
   // ---- which KV group and query rows -------------------------------------------------------
-  // Sliding windows: one workgroup per tile, neighbouring tiles (sharing their keys) on one XCD.
-  // Causal: item b of every KV group in turn, so the longest items of all groups start first.
+  // Unsplit sliding windows: one workgroup per tile, neighbouring tiles (sharing their keys) on one
+  // XCD.  Otherwise item b of every KV group in turn, so the longest items of all groups start
+  // first (split sliding windows: every tile in the same number of parts).
   int g, b, tile, part = 0, nparts = 1;
-  if (p.window > 0) {
+  if (p.window > 0 && p.nsplit_tiles == 0) {
     const int lb = attn_xcd_remap(blockIdx.x, p.KV * p.per_group);
     g = lb / p.per_group;
     b = tile = lb % p.per_group;
@@ -389,14 +393,21 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(AttnParams p) {
     const __amdgpu_buffer_rsrc_t rp =
         make_rsrc(p.part + size_t(first_item) * (PART_BYTES / 4), uint32_t(nparts) * PART_BYTES);
     const uint32_t lane_off = uint32_t(tid) * 16u;
-    {
-      const uint32_t base = uint32_t(part) * PART_BYTES + lane_off;
+    const uint32_t base = uint32_t(part) * PART_BYTES + lane_off;
+    const v4f ml = v4f{ms, l, 0.0f, 0.0f};
+    if (p.merge_mode) {
+      // attn_merge_kernel merges the parts after this kernel, whose end writes the L2s back: plain
+      // (write-back) stores suffice
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt)
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, o[dt]), rp, base + dt * SLOT_BYTES, 0, 0x11);
-      const v4f ml = v4f{ms, l, 0.0f, 0.0f};
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, ml), rp, base + NDT * SLOT_BYTES, 0, 0x11);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, o[dt]), rp, base + dt * SLOT_BYTES, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, ml), rp, base + NDT * SLOT_BYTES, 0, 0);
+      return;
     }
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, o[dt]), rp, base + dt * SLOT_BYTES, 0, 0x11);
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, ml), rp, base + NDT * SLOT_BYTES, 0, 0x11);
     __builtin_amdgcn_s_waitcnt(0);
     int* arrived = reinterpret_cast<int*>(lds);
     const int counter = g * p.nsplit_tiles + (p.ntiles - 1 - tile);
@@ -534,7 +545,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd2_kernel(AttnParams p) {
 
   // ---- which KV group and query rows (as attn_fwd_kernel) ----------------------------------
   int g, b, tile, part = 0, nparts = 1;
-  if (p.window > 0) {
+  if (p.window > 0 && p.nsplit_tiles == 0) {
     const int lb = attn_xcd_remap(blockIdx.x, p.KV * p.per_group);
     g = lb / p.per_group;
     b = tile = lb % p.per_group;
@@ -822,23 +833,31 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd2_kernel(AttnParams p) {
     const __amdgpu_buffer_rsrc_t rp =
         make_rsrc(p.part + size_t(first_item) * (S::PART_BYTES / 4), uint32_t(nparts) * S::PART_BYTES);
     const uint32_t lane_off = uint32_t(tid) * 16u;
-    {
+    // write-through (system-scope) stores when the last part merges in this kernel on another XCD;
+    // plain stores when attn_merge_kernel merges after this kernel, whose end writes the L2s back
+    auto park = [&](auto policy) __attribute__((always_inline)) {
+      constexpr int POL = decltype(policy)::value;
       const uint32_t base = uint32_t(part) * S::PART_BYTES;
 #pragma unroll
       for (int dt = 0; dt < NDW; ++dt)
 #pragma unroll
         for (int rt = 0; rt < 8; ++rt)
           __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, o[dt][rt]), rp,
-                                                 base + uint32_t(dt * 8 + rt) * (NT * 16) + lane_off, 0, 0x11);
+                                                 base + uint32_t(dt * 8 + rt) * (NT * 16) + lane_off, 0, POL);
       if (qq == 0) {
 #pragma unroll
         for (int j = 0; j < RT; ++j) {
           const v4f ml = v4f{ms[j], lt[j], 0.0f, 0.0f};
           __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, ml), rp,
-                                                 base + S::PART_O + uint32_t(srow[j]) * 16u, 0, 0x11);
+                                                 base + S::PART_O + uint32_t(srow[j]) * 16u, 0, POL);
         }
       }
+    };
+    if (p.merge_mode) {
+      park(std::integral_constant<int, 0>{});
+      return;
     }
+    park(std::integral_constant<int, 0x11>{});
     __builtin_amdgcn_s_waitcnt(0);
     int* arrived = reinterpret_cast<int*>(lds);
     const int counter = g * p.nsplit_tiles + (p.ntiles - 1 - tile);
@@ -925,6 +944,105 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd2_kernel(AttnParams p) {
   for (int dt = 0; dt < NDW; ++dt)
 #pragma unroll
     for (int rt = 0; rt < 8; ++rt) store_slot(dt, rt, o[dt][rt], inv_s[rt * 16 + qi]);
+}
+
+// ---- merge of parked parts (merge_mode 1) ------------------------------------------------------
+//
+// Where every part of a call would run in one round on the CUs, the last part of a tile to arrive
+// would merge its tile's parts on one CU at the end (one tile at head_dim 512 parks ~256 KiB per
+// part), so instead the parts are only parked and this kernel merges them, spread over one
+// workgroup per (KV group, split tile, 16-byte slot of the parked O^T): 16 (head_dim 256) or 32
+// (head_dim 512) workgroups per tile.  Thread t merges what thread t of the attention workgroup
+// parked in that slot -- 4 output columns of one row -- with the arithmetic of the in-kernel merge
+// (weights exp2(m_s - M) in part order, the row's l summed the same way), so both modes give the
+// same bits.
+//   FWD2 = false (attn_fwd_kernel): slot dt of thread t = (wave, qq, qi) holds row 16 wave + qi,
+//     columns 16 dt + 4 qq ..; slot D/16 holds that thread's (m, lane-group share of l).
+//   FWD2 = true (attn_fwd2_kernel): slot 8 dt + rt holds row 16 rt + qi, columns
+//     wave D/8 + 4 qq + 16 dt ..; each row's (m, l) sits after the slots.
+template <int D, bool FWD2>
+__global__ __launch_bounds__(512) void attn_merge_kernel(AttnParams p) {
+  using S2 = AttnFwd2Shape<D, 32, ATTN_FWD2_NW>;
+  constexpr int NT = 512;
+  constexpr uint32_t SLOT_BYTES = NT * 16;
+  constexpr int NSLOT = FWD2 ? S2::SLOTS : D / 16;
+  constexpr uint32_t PART_BYTES = FWD2 ? S2::PART_BYTES : uint32_t(D / 16 + 1) * SLOT_BYTES;
+  static_assert(!FWD2 || (ATTN_FWD2_NW * 64 == NT && S2::NDW * 8 == NSLOT), "head_dim 512 layout");
+  static_assert(FWD2 || ATTN_NW * 64 == NT, "attn_fwd_kernel layout");
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, qi = lane & 15, qq = lane >> 4;
+  const int slot = int(blockIdx.x) % NSLOT;
+  const int st = (int(blockIdx.x) / NSLOT) % p.nsplit_tiles;
+  const int g = int(blockIdx.x) / (NSLOT * p.nsplit_tiles);
+  // split tile st is tile ntiles - 1 - st; its parts are consecutive items of its segment
+  const int tile = p.ntiles - 1 - st;
+  int s = 0;
+  while (s + 1 < p.nseg && tile <= p.seg_tile[s + 1]) ++s;
+  const int nparts = p.seg_k[s];
+  const int first_item = g * p.nsplit_items + p.seg_item[s] + (p.seg_tile[s] - tile) * nparts;
+  const __amdgpu_buffer_rsrc_t rp =
+      make_rsrc(p.part + size_t(first_item) * (PART_BYTES / 4), uint32_t(nparts) * PART_BYTES);
+  int r, d;
+  uint32_t ml_off;
+  if constexpr (FWD2) {
+    r = (slot % 8) * 16 + qi;
+    d = wave * (D / ATTN_FWD2_NW) + 4 * qq + 16 * (slot / 8);
+    ml_off = S2::PART_O + uint32_t(r) * 16u;
+  } else {
+    r = wave * 16 + qi;
+    d = 16 * slot + 4 * qq;
+    ml_off = uint32_t(NSLOT) * SLOT_BYTES + uint32_t(tid) * 16u;
+  }
+  // NP >= nparts records per sum are loaded unconditionally, all before any is used: those past the
+  // last part lie outside the buffer resource, read zero and take weight 0
+  auto merge = [&](auto np_tag, float& M, float& lt, v4f& acc) __attribute__((always_inline)) {
+    constexpr int NP = decltype(np_tag)::value;
+    v4f mlv[NP], od[NP];
+#pragma unroll
+    for (int sp = 0; sp < NP; ++sp) {
+      mlv[sp] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rp, uint32_t(sp) * PART_BYTES + ml_off, 0, 0));
+      od[sp] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(
+                                             rp, uint32_t(sp) * PART_BYTES + uint32_t(slot) * SLOT_BYTES +
+                                                     uint32_t(tid) * 16u, 0, 0));
+    }
+    float w[NP];
+    M = -__builtin_inff();
+#pragma unroll
+    for (int sp = 0; sp < NP; ++sp) {
+      w[sp] = sp < nparts ? mlv[sp][0] : -__builtin_inff();
+      M = fmaxf(M, w[sp]);
+    }
+    const float Ms = M == -__builtin_inff() ? 0.0f : M;
+    float lm = 0.0f;
+#pragma unroll
+    for (int sp = 0; sp < NP; ++sp) {
+      w[sp] = sp < nparts ? __builtin_amdgcn_exp2f(w[sp] - Ms) : 0.0f;
+      lm = __builtin_fmaf(w[sp], mlv[sp][1], lm);
+    }
+    lt = FWD2 ? lm : lanes4_sum(lm);
+    acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int sp = 0; sp < NP; ++sp)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(w[sp], od[sp][i], acc[i]);
+  };
+  float M, lt;
+  v4f acc;
+  if (nparts <= 4)
+    merge(std::integral_constant<int, 4>{}, M, lt, acc);
+  else if (nparts <= 8)
+    merge(std::integral_constant<int, 8>{}, M, lt, acc);
+  else
+    merge(std::integral_constant<int, 16>{}, M, lt, acc);
+  const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+  const int i0 = tile * p.PB, pr = r / p.G, hl = r % p.G;
+  if (pr >= p.PB || i0 + pr >= p.Tq) return;
+  const int h = g * p.G + hl;
+  v2u w;
+  w[0] = pack_bf16x2(acc[0] * inv, acc[1] * inv);
+  w[1] = pack_bf16x2(acc[2] * inv, acc[3] * inv);
+  *reinterpret_cast<v2u*>(p.o + int64_t(h) * p.ohs + int64_t(i0 + pr) * p.ors + d) = w;
+  if (d == 0 && p.lse)
+    p.lse[int64_t(h) * p.Tq + i0 + pr] = lt > 0.0f ? M * 0.69314718055994531f + __logf(lt) : -__builtin_inff();
 }
 
 // ---- decode: one query per head, keys split into chunks --------------------------------------
@@ -1215,6 +1333,7 @@ constexpr int64_t ATTN_COUNTER_BYTES = 65536;
 struct AttnPlan {
   int ntiles = 0, per_group = 0, nseg = 1, nsplit_tiles = 0, nsplit_items = 0;
   int seg_tile[ATTN_MAX_SEG] = {}, seg_k[ATTN_MAX_SEG] = {}, seg_item[ATTN_MAX_SEG + 1] = {};
+  int merge_mode = 0;           // 0: the last part merges in the kernel; 1: attn_merge_kernel after it
   std::vector<uint16_t> order;  // launch order of the items (empty: item order)
 };
 
@@ -1241,6 +1360,7 @@ static void attn_plan_unsplit(AttnPlan& pl) {
   pl.seg_item[0] = 0;
   pl.seg_item[1] = pl.ntiles;
   pl.nsplit_tiles = pl.nsplit_items = 0;
+  pl.merge_mode = 0;
   pl.order.clear();
 }
 
@@ -1280,10 +1400,21 @@ static void attn_plan_items(const AttnPlan& pl, const std::vector<int>& nb, std:
       const int off = item - pl.seg_item[s], t = pl.seg_tile[s] - off / k, part = off % k;
       blocks[item] = (part + 1) * nb[t] / k - part * nb[t] / k;
       double c = ATTN_ITEM_COST + blocks[item];
-      if (k > 1) c += ATTN_PARK_COST + (part == k - 1 ? ATTN_MERGE_COST + ATTN_MERGE_PART_COST * k : 0.0);
+      if (k > 1) {
+        c += ATTN_PARK_COST;
+        if (pl.merge_mode == 0 && part == k - 1) c += ATTN_MERGE_COST + ATTN_MERGE_PART_COST * k;
+      }
       cost[item] = c;
     }
   }
+}
+
+// The merge kernel of merge_mode 1, in block units: its launch, then the parked parts read once at
+// the rate many CUs reach together (~5 TB/s, 16.5 MB per 3.3 us block).
+constexpr double ATTN_MERGE_KERNEL_COST = 1.0;
+constexpr double ATTN_MERGE_BYTES_PER_BLOCK = 16.5e6;
+static double attn_merge_kernel_cost(const AttnPlan& pl, int64_t KV, int64_t D) {
+  return ATTN_MERGE_KERNEL_COST + double(KV) * pl.nsplit_items * double(attn_part_bytes(D)) / ATTN_MERGE_BYTES_PER_BLOCK;
 }
 
 // Launch the items longest first (ties in item order), when the table fits the kernel arguments.
@@ -1319,47 +1450,81 @@ static double attn_plan_makespan(const AttnPlan& pl, const std::vector<double>& 
 
 static AttnPlan attn_plan_compute(int64_t H, int64_t KV, int64_t Tq, int64_t Tk, int64_t D, int64_t q_start,
                                   int64_t window) {
-  (void)Tk;
   AttnPlan pl;
   const int PB = int(ATTN_NW * 16 / (H / KV)), BN = attn_bn(D);
   pl.ntiles = int((Tq + PB - 1) / PB);
   attn_plan_unsplit(pl);
-  if (window > 0 || pl.ntiles == 0) return pl;
+  if (pl.ntiles == 0) return pl;
+  const int cus = attn_cu_count();
   std::vector<int> nb(pl.ntiles);
   int mx = 0;
   for (int t = 0; t < pl.ntiles; ++t) {
-    nb[t] = attn_causal_blocks(t, PB, BN, Tq, q_start);
+    if (window > 0) {  // the kernels' key range of a sliding-window tile
+      const int64_t pmin = q_start + int64_t(t) * PB, pmax = q_start + std::min<int64_t>((int64_t(t) + 1) * PB, Tq) - 1;
+      const int64_t khi = std::min<int64_t>(pmax, Tk - 1), klo = std::max<int64_t>(0, pmin - window + 1);
+      const int64_t kb_first = klo / BN * BN;
+      nb[t] = khi >= kb_first ? int((khi - kb_first) / BN + 1) : 0;
+    } else {
+      nb[t] = attn_causal_blocks(t, PB, BN, Tq, q_start);
+    }
     mx = nb[t] > mx ? nb[t] : mx;
   }
-  const int cus = attn_cu_count();
   // the list would not fit the model's budget of simulated items: keep one item per tile
-  if (mx < 8 || int64_t(pl.ntiles) * KV * ATTN_MAX_SEG > (int64_t(1) << 22)) return pl;
+  if (mx < 2 || int64_t(pl.ntiles) * KV * ATTN_MAX_SEG > (int64_t(1) << 22)) return pl;
   std::vector<int> blocks;
   std::vector<double> cost;
   attn_plan_items(pl, nb, blocks, cost);
   const double unsplit = attn_plan_makespan(pl, cost, int(KV), cus);
-  // part lengths from 4 blocks up to the longest tile, ~12% apart; a split list is taken only
-  // when it beats one workgroup per tile by 2% on the model
   double best = 0.0;
   AttnPlan split;
-  int prev = 0;
-  for (double Lf = 4.0; Lf < mx; Lf *= 1.125) {
-    const int L = int(Lf);
-    if (L == prev) continue;
-    prev = L;
-    AttnPlan c;
-    c.ntiles = pl.ntiles;
-    attn_plan_segments(nb, L, c);
-    if (KV * c.nsplit_tiles * 4 > ATTN_COUNTER_BYTES) continue;  // one counter per split tile
+  auto consider = [&](AttnPlan& c) {
     attn_plan_items(c, nb, blocks, cost);
     attn_plan_order(c, blocks);
-    const double ms = attn_plan_makespan(c, cost, int(KV), cus);
+    double ms = attn_plan_makespan(c, cost, int(KV), cus);
+    if (c.merge_mode == 1) ms += attn_merge_kernel_cost(c, KV, D);
     if (split.ntiles == 0 || ms < best) {
       best = ms;
       split = c;
     }
+  };
+  if (window > 0) {
+    // every tile's keys in the same number of parts k (a tile with fewer blocks parks empty parts),
+    // merged by the merge kernel: taken where the tiles alone would leave most CUs idle
+    if (KV * int64_t(pl.ntiles) < cus) {
+      for (int k = 2; k <= ATTN_MAX_SEG && k <= mx; ++k) {
+        AttnPlan c;
+        c.ntiles = pl.ntiles;
+        c.nseg = 1;
+        c.seg_tile[0] = pl.ntiles - 1;
+        c.seg_k[0] = k;
+        c.seg_item[0] = 0;
+        c.seg_item[1] = pl.ntiles * k;
+        c.per_group = pl.ntiles * k;
+        c.nsplit_tiles = pl.ntiles;
+        c.nsplit_items = pl.ntiles * k;
+        c.merge_mode = 1;
+        consider(c);
+      }
+    }
+  } else if (mx >= 8) {
+    // part lengths from 4 blocks up to the longest tile, ~12% apart, with either merge
+    int prev = 0;
+    for (double Lf = 4.0; Lf < mx; Lf *= 1.125) {
+      const int L = int(Lf);
+      if (L == prev) continue;
+      prev = L;
+      for (int mode = 0; mode < 2; ++mode) {
+        AttnPlan c;
+        c.ntiles = pl.ntiles;
+        attn_plan_segments(nb, L, c);
+        if (mode == 0 && KV * c.nsplit_tiles * 4 > ATTN_COUNTER_BYTES) continue;  // one counter per split tile
+        c.merge_mode = mode;
+        consider(c);
+      }
+    }
   }
-  if (split.ntiles > 0 && best < 0.98 * unsplit) pl = split;
+  // a split list is taken only when it beats one workgroup per tile by 2% on the model
+  if (split.ntiles > 0 && split.nsplit_tiles > 0 && best < 0.98 * unsplit) pl = split;
   return pl;
 }
 
@@ -1394,10 +1559,11 @@ extern "C" int64_t w8a8_attention_workspace_bytes(int64_t H, int64_t KV, int64_t
 }
 
 extern "C" int64_t w8a8_attention_plan_items(int64_t H, int64_t KV, int64_t Tq, int64_t Tk, int64_t D,
-                                             int64_t q_start, int64_t window, int* launch_order) {
+                                             int64_t q_start, int64_t window, int* launch_order, int* merge_kernel) {
   if (w8a8_attention_workspace_bytes(H, KV, Tq, Tk, D, q_start, window) < 0) return -1;
   const AttnPlan pl = attn_plan(H, KV, Tq, Tk, D, q_start, window);
   if (launch_order) *launch_order = pl.order.empty() ? 0 : 1;
+  if (merge_kernel) *merge_kernel = pl.nsplit_tiles > 0 ? pl.merge_mode : 0;
   return pl.per_group;
 }
 
@@ -1464,6 +1630,7 @@ static int attention_launch(const uint16_t* q, int64_t q_head_stride, int64_t q_
     p.seg_k[i] = pl.seg_k[i];
   }
   for (int i = 0; i <= ATTN_MAX_SEG; ++i) p.seg_item[i] = pl.seg_item[i];
+  p.merge_mode = pl.nsplit_tiles > 0 ? pl.merge_mode : 0;
   p.ordered = pl.order.empty() ? 0 : 1;
   for (size_t i = 0; i < pl.order.size(); ++i) p.order[i] = pl.order[i];
   p.scale = scale; p.c = scale * 1.4426950408889634f;
@@ -1476,7 +1643,18 @@ static int attention_launch(const uint16_t* q, int64_t q_head_stride, int64_t q_
     attn_fwd_kernel<256, 64, ATTN_NW><<<grid, dim3{ATTN_NW * 64, 1, 1}, 0, stream>>>(p);
   else
     attn_fwd2_kernel<512, 32, ATTN_FWD2_NW><<<grid, dim3{ATTN_FWD2_NW * 64, 1, 1}, 0, stream>>>(p);
-  return check_launch("attention_bf16");
+  int rc = check_launch("attention_bf16");
+  if (rc || !p.merge_mode) return rc;
+  // one workgroup per (KV group, split tile, parked O^T slot)
+  const int nslot = D == 512 ? AttnFwd2Shape<512, 32, ATTN_FWD2_NW>::SLOTS : int(D / 16);
+  const dim3 mgrid{unsigned(KV * int64_t(p.nsplit_tiles) * nslot), 1, 1};
+  if (D == 128)
+    attn_merge_kernel<128, false><<<mgrid, dim3{512, 1, 1}, 0, stream>>>(p);
+  else if (D == 256)
+    attn_merge_kernel<256, false><<<mgrid, dim3{512, 1, 1}, 0, stream>>>(p);
+  else
+    attn_merge_kernel<512, true><<<mgrid, dim3{512, 1, 1}, 0, stream>>>(p);
+  return check_launch("attention_merge");
 }
 
 extern "C" int w8a8_attention_bf16(const uint16_t* q, int64_t q_head_stride, int64_t q_row_stride, const uint16_t* k,

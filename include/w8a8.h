@@ -336,9 +336,11 @@ int64_t w8a8_attention_workspace_bytes(int64_t H, int64_t KV, int64_t Tq, int64_
  * list): the items per KV group w8a8_attention_ws_bf16 plans for these arguments (query tiles,
  * each counted once per part its keys are split into), with *launch_order (if not NULL) set to 1
  * when the items launch through the longest-first order table and 0 when they run in plain item
- * order (plans of more than 1536 items per group, or one item per tile); -1 if invalid. */
+ * order (plans of more than 1536 items per group, or one item per tile), and *merge_kernel (if not
+ * NULL) set to 1 when split tiles are merged by a second kernel after the parts, 0 when the last
+ * part of each tile merges them (or nothing is split); -1 if invalid. */
 int64_t w8a8_attention_plan_items(int64_t H, int64_t KV, int64_t Tq, int64_t Tk, int64_t D, int64_t q_start,
-                                  int64_t window, int *launch_order);
+                                  int64_t window, int *launch_order, int *merge_kernel);
 
 /* w8a8_attention_bf16 with a workspace for splitting long causal tiles: device memory of at least
  * w8a8_attention_workspace_bytes(...) bytes, 16-byte aligned, ZERO-FILLED BEFORE ITS FIRST USE (its

@@ -182,17 +182,32 @@ def test_attention_workspace_and_errors():
     """Attention workspace sizing (closed forms) and argument errors, all decided on the host."""
     L = _lib.lib()
     part512 = 32 * 512 * 16 + 128 * 16          # one split part of a 128-row tile at head_dim 512: O^T, (m, l)
-    # sliding windows and short causal calls need no workspace
+    part256 = 8 * 64 * (256 // 16 + 1) * 16     # one at head_dim 256: O^T and each thread's (m, l)
+    counters = 65536
+    # a whole-prompt sliding-window call (229 tiles) and short causal calls need no workspace
     assert L.w8a8_attention_workspace_bytes(8, 1, 3658, 3658, 256, 0, 512) == 0
     assert L.w8a8_attention_workspace_bytes(8, 1, 200, 200, 128, 0, 0) == 0
+    # a 512-query sliding-window micro-batch (32 tiles of ~9 key blocks on 256 CUs) splits every tile
+    # into the same number of parts, merged by the second kernel
+    ws = L.w8a8_attention_workspace_bytes(8, 1, 512, 3658, 256, 3146, 512)
+    order, merge = ctypes.c_int(-1), ctypes.c_int(-1)
+    items = L.w8a8_attention_plan_items(8, 1, 512, 3658, 256, 3146, 512, ctypes.byref(order), ctypes.byref(merge))
+    assert items % 32 == 0 and 2 <= items // 32 <= 16 and merge.value == 1
+    assert ws == counters + items * part256
     # 256 queries at the end of the 3658-token prompt, head_dim 512: 16 tiles of ~110 key blocks
     # against a fair share of 7 blocks per CU -> every tile split, into 8 to 16 (the cap) parts,
-    # parked after the 64 KiB of arrival counters (at the same offsets for every shape)
-    counters = 65536
+    # parked after the 64 KiB of arrival counters (at the same offsets for every shape); one round of
+    # workgroups, so the merge kernel merges them
     ws = L.w8a8_attention_workspace_bytes(8, 1, 256, 3658, 512, 3402, 0)
     assert (ws - counters) % part512 == 0 and 16 * 8 <= (ws - counters) // part512 <= 16 * 16
+    L.w8a8_attention_plan_items(8, 1, 256, 3658, 512, 3402, 0, None, ctypes.byref(merge))
+    assert merge.value == 1
+    # the whole prompt: more items than CUs, so the last part of each split tile merges it in the
+    # kernel while other tiles still run
     ws = L.w8a8_attention_workspace_bytes(8, 1, 3658, 3658, 512, 0, 0)
     assert ws > counters and (ws - counters) % part512 == 0
+    L.w8a8_attention_plan_items(8, 1, 3658, 3658, 512, 0, 0, None, ctypes.byref(merge))
+    assert merge.value == 0
     assert L.w8a8_attention_workspace_bytes(8, 3, 16, 16, 256, 0, 0) == -1     # H % KV
     assert L.w8a8_attention_workspace_bytes(8, 1, 16, 8, 256, 0, 0) == -1      # Tk < Tq
     assert L.w8a8_attention_workspace_bytes(8, 1, 16, 16, 64, 0, 0) == -1      # head_dim

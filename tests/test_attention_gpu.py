@@ -81,8 +81,15 @@ def test_attention_matches_oracle(H, KV, Tq, Tk, D, q_start, window, scale, qsca
 
 def test_micro_batches_like_the_reference_pipeline():
     """pipeline.py:281-295: each 512-row micro-batch of a sliding layer attends to keys 0..e, each
-    256-row chunk of a full layer to keys 0..s+r1; the chunks are the pipeline's calls."""
+    256-row chunk of a full layer to keys 0..s+r1; the chunks are the pipeline's calls.  These calls
+    are too few tiles for the CUs, so their keys are split and the parts merged by the second kernel
+    (the planner's choice is checked, so the test keeps covering that path)."""
+    import ctypes
+    from w8a8 import lib
     T = 1300
+    merge = ctypes.c_int(-1)
+    for args in ((8, 1, 512, 1024, 256, 512, 512), (8, 1, 256, 768, 512, 512, 0)):
+        assert lib().w8a8_attention_plan_items(*args, None, ctypes.byref(merge)) > 0 and merge.value == 1, args
     q, k, v = make(8, 1, T, T, 256, seed=1, qscale=0.3)
     qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
     ref, bud, _ = reference(q, k, v, 0, 512)
@@ -203,12 +210,12 @@ def test_split_plan_past_the_order_table():
     H, KV, D = 8, 1, 512
     order = ctypes.c_int(-1)
     T = next((t for t in (20000, 20500, 21000, 19500, 21500, 22000)
-              if lib().w8a8_attention_plan_items(H, KV, t, t, D, 0, 0, ctypes.byref(order)) > 1536
+              if lib().w8a8_attention_plan_items(H, KV, t, t, D, 0, 0, ctypes.byref(order), None) > 1536
               and lib().w8a8_attention_workspace_bytes(H, KV, t, t, D, 0, 0) > 0), None)
     assert T is not None, "no prompt length in the list plans past the order table"
-    lib().w8a8_attention_plan_items(H, KV, T, T, D, 0, 0, ctypes.byref(order))
+    lib().w8a8_attention_plan_items(H, KV, T, T, D, 0, 0, ctypes.byref(order), None)
     assert order.value == 0
-    print(f"attention T={T} D={D}: {lib().w8a8_attention_plan_items(H, KV, T, T, D, 0, 0, None)} items, "
+    print(f"attention T={T} D={D}: {lib().w8a8_attention_plan_items(H, KV, T, T, D, 0, 0, None, None)} items, "
           "item order", flush=True)
     q, k, v = make(H, KV, T, T, D, seed=57, qscale=0.3)
     qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
