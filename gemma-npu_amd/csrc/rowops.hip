@@ -16,6 +16,11 @@
 // qkv             k_qkv (pipeline.py:72-85): per (token, head) dequant, RMSNorm over the head,
 //                 rotary embedding, written head-major [heads, T, D].
 //
+// Every entry point that takes an int32 GEMM result with its scales has a `_y` twin that takes the
+// dequantised bf16 rows instead -- what the GEMM's dequant epilogue writes, bf16((acc * sx) * sw),
+// the same values the int32 entry computes first -- so a GEMM feeding these kernels can write half
+// the bytes and the results are bit-identical.
+//
 // rms(x) = x * (mean(x^2) + eps)^-0.5 * w in fp32 (_rms, pipeline.py:43-46).  Every bf16 rounding
 // the eager torch ops perform is performed here too; the row sums of squares are added in a
 // different order than torch's, so normalised values agree to fp32 rounding, not bit for bit.
@@ -268,8 +273,9 @@ __global__ __launch_bounds__(256) void row_chain_kernel(RowChain p) {
 
 // ---- k_qkv ------------------------------------------------------------------------------------
 struct QkvParams {
-  const int32_t* acc; int64_t ldacc;
+  const int32_t* acc; int64_t ldacc;      // int32 GEMM result with its scales, or
   const float* sx; const float* sw;
+  const uint16_t* y; int64_t ldy;         // the dequantised bf16 rows (then acc, sx, sw are unused)
   const uint16_t* cs; const uint16_t* sn; int64_t ldcs;  // cos / sin bf16 [T, D]
   const uint16_t* qw; const uint16_t* kw;                // q_norm / k_norm weights bf16 [D]
   uint16_t* q; uint16_t* k; uint16_t* v;                 // [H, T, D], [KV, T, D], [KV, T, D]
@@ -326,7 +332,7 @@ __device__ __forceinline__ void store_bf16(uint16_t* p, const float (&o)[E]) {
 // value heads, at columns slot * D of the GEMM result (pipeline.py:76-82).  A lane holds E = D/128
 // elements of each half of the head at positions p0 .. p0+E-1 and p0+D/2 .. : the rotation pairs
 // element d with d + D/2, so RoPE needs no lane exchange.
-template <int E>
+template <int E, bool IN_BF16>
 __global__ __launch_bounds__(256) void qkv_kernel(QkvParams p) {
   constexpr int D = 128 * E, HALF = 64 * E;
   const int lane = threadIdx.x & 63;
@@ -335,9 +341,13 @@ __global__ __launch_bounds__(256) void qkv_kernel(QkvParams p) {
   const int t = item / p.slots, slot = item % p.slots;
   const int p0 = lane * E;
   const int col = slot * D + p0;
-  const float sxm = p.sx[t];
   float y1[E], y2[E];
-  {
+  if constexpr (IN_BF16) {
+    const uint16_t* yr = p.y + int64_t(t) * p.ldy;
+    load_bf16<E>(yr + col, y1);
+    load_bf16<E>(yr + col + HALF, y2);
+  } else {
+    const float sxm = p.sx[t];
     int a1[E], a2[E];
     float s1[E], s2[E];
     const int32_t* ar = p.acc + int64_t(t) * p.ldacc;
@@ -426,6 +436,7 @@ static int launch_row_chain(const RowChain& p, bool in_i32, hipStream_t stream, 
     if (in_i32 && p.op == RC_NORM_RES) row_chain_kernel<C, true, RC_NORM_RES><<<grid, threads, 0, stream>>>(p); \
     else if (in_i32 && p.op == RC_GELU_MUL) row_chain_kernel<C, true, RC_GELU_MUL><<<grid, threads, 0, stream>>>(p); \
     else if (!in_i32 && p.op == RC_NORM_RES) row_chain_kernel<C, false, RC_NORM_RES><<<grid, threads, 0, stream>>>(p); \
+    else if (!in_i32 && p.op == RC_GELU_MUL) row_chain_kernel<C, false, RC_GELU_MUL><<<grid, threads, 0, stream>>>(p); \
     else if (!in_i32 && p.op == RC_NONE) row_chain_kernel<C, false, RC_NONE><<<grid, threads, 0, stream>>>(p); \
     else return fail(W8A8_EINVAL, "%s: unsupported row-chain combination", what);         \
   } while (0)
@@ -566,12 +577,35 @@ int w8a8_k_attn_out(const uint16_t* o, int64_t head_stride, int64_t row_stride, 
   return launch_row_chain(p, false, stream, what);
 }
 
-int w8a8_k_post_attn(const int32_t* acc, int64_t ldacc, const float* sx, const float* sw, const uint16_t* res,
-                     int64_t ldr, const uint16_t* w_post, const uint16_t* w_pre_ff, float eps, int64_t M, int64_t N,
-                     uint16_t* h, int64_t ldh, int8_t* q, int64_t ldq, int q_packed, float* sq, hipStream_t stream) {
+}  // extern "C"
+
+namespace w8a8 {
+
+// The input of a row-chain entry: an int32 GEMM result with its scales, or dequantised bf16 rows.
+struct RowInput {
+  const void* p; int64_t ld; const float* sx; const float* sw; bool i32;
+};
+
+static int check_input(const char* what, const RowInput& in, int64_t N) {
+  if (in.i32) return check_acc(what, static_cast<const int32_t*>(in.p), in.ld, in.sx, in.sw, N);
+  return check_bf16_rows(what, "y", static_cast<const uint16_t*>(in.p), in.ld, N);
+}
+
+static void set_input(RowChain& p, const RowInput& in, int64_t N) {
+  p.in = in.p; p.ld_in = in.ld;
+  if (in.i32) {
+    p.sx = in.sx; p.sw = in.sw;
+  } else {
+    p.head_stride = N; p.head_len = int(N);
+  }
+}
+
+static int k_post_attn(const RowInput& in, const uint16_t* res, int64_t ldr, const uint16_t* w_post,
+                       const uint16_t* w_pre_ff, float eps, int64_t M, int64_t N, uint16_t* h, int64_t ldh, int8_t* q,
+                       int64_t ldq, int q_packed, float* sq, hipStream_t stream) {
   const char* what = "k_post_attn";
   W8A8_TRY(check_rows(what, M, N));
-  W8A8_TRY(check_acc(what, acc, ldacc, sx, sw, N));
+  W8A8_TRY(check_input(what, in, N));
   W8A8_TRY(check_bf16_rows(what, "res", res, ldr, N));
   W8A8_TRY(check_bf16_rows(what, "h", h, ldh, N));
   W8A8_TRY(check_vec16(what, "w_post", w_post));
@@ -579,11 +613,122 @@ int w8a8_k_post_attn(const int32_t* acc, int64_t ldacc, const float* sx, const f
   RowChain p{};
   W8A8_TRY(set_q(what, p, q, ldq, q_packed, sq, N));
   if (M == 0) return W8A8_OK;
-  p.in = acc; p.ld_in = ldacc; p.sx = sx; p.sw = sw;
+  set_input(p, in, N);
   p.op = RC_NORM_RES; p.aux = res; p.ld_aux = ldr; p.w1 = w_post;
   p.h = h; p.ldh = ldh; p.norm2 = 1; p.w2 = w_pre_ff;
   p.eps = eps; p.M = int(M); p.N = int(N);
-  return launch_row_chain(p, true, stream, what);
+  return launch_row_chain(p, in.i32, stream, what);
+}
+
+static int k_post_ff(const RowInput& in, const uint16_t* res, int64_t ldr, const uint16_t* w_post_ff, float eps,
+                     int64_t M, int64_t N, uint16_t* h, int64_t ldh, int8_t* q, int64_t ldq, int q_packed, float* sq,
+                     hipStream_t stream) {
+  const char* what = "k_post_ff";
+  W8A8_TRY(check_rows(what, M, N));
+  W8A8_TRY(check_input(what, in, N));
+  W8A8_TRY(check_bf16_rows(what, "res", res, ldr, N));
+  W8A8_TRY(check_bf16_rows(what, "h", h, ldh, N));
+  W8A8_TRY(check_vec16(what, "w_post_ff", w_post_ff));
+  RowChain p{};
+  W8A8_TRY(set_q(what, p, q, ldq, q_packed, sq, N));
+  if (M == 0) return W8A8_OK;
+  set_input(p, in, N);
+  p.op = RC_NORM_RES; p.aux = res; p.ld_aux = ldr; p.w1 = w_post_ff;
+  p.h = h; p.ldh = ldh;
+  p.eps = eps; p.M = int(M); p.N = int(N);
+  return launch_row_chain(p, in.i32, stream, what);
+}
+
+static int k_ple_gate(const RowInput& in, const uint16_t* ple, int64_t ldp, int64_t M, int64_t N, int8_t* q,
+                      int64_t ldq, int q_packed, float* sq, hipStream_t stream) {
+  const char* what = "k_ple_gate";
+  W8A8_TRY(check_rows(what, M, N));
+  W8A8_TRY(check_input(what, in, N));
+  W8A8_TRY(check_bf16_rows(what, "ple", ple, ldp, N));
+  RowChain p{};
+  W8A8_TRY(set_q(what, p, q, ldq, q_packed, sq, N));
+  if (M == 0) return W8A8_OK;
+  set_input(p, in, N);
+  p.op = RC_GELU_MUL; p.aux = ple; p.ld_aux = ldp;
+  p.M = int(M); p.N = int(N);
+  return launch_row_chain(p, in.i32, stream, what);
+}
+
+static int k_ple_out(const RowInput& in, const uint16_t* h, int64_t ldh, const uint16_t* w_post_ple,
+                     const uint16_t* scalar, float eps, int64_t M, int64_t N, uint16_t* out, int64_t ldo,
+                     hipStream_t stream) {
+  const char* what = "k_ple_out";
+  W8A8_TRY(check_rows(what, M, N));
+  W8A8_TRY(check_input(what, in, N));
+  W8A8_TRY(check_bf16_rows(what, "h", h, ldh, N));
+  W8A8_TRY(check_bf16_rows(what, "out", out, ldo, N));
+  W8A8_TRY(check_vec16(what, "w_post_ple", w_post_ple));
+  if (!scalar) return fail(W8A8_EINVAL, "k_ple_out: scalar is null");
+  if (M == 0) return W8A8_OK;
+  RowChain p{};
+  set_input(p, in, N);
+  p.op = RC_NORM_RES; p.aux = h; p.ld_aux = ldh; p.w1 = w_post_ple; p.scalar = scalar;
+  p.h = out; p.ldh = ldo;
+  p.eps = eps; p.M = int(M); p.N = int(N);
+  return launch_row_chain(p, in.i32, stream, what);
+}
+
+static int k_qkv(const RowInput& in, const uint16_t* cos_, const uint16_t* sin_, int64_t ldcs, const uint16_t* qw,
+                 const uint16_t* kw, float eps, int64_t T, int64_t H, int64_t KV, int64_t D, int shared, uint16_t* q,
+                 uint16_t* k, uint16_t* v, hipStream_t stream) {
+  const char* what = "k_qkv";
+  if (T < 0 || H <= 0 || KV < 0 || (!shared && KV <= 0))
+    return fail(W8A8_EINVAL, "k_qkv: bad shape T=%lld H=%lld KV=%lld", (long long)T, (long long)H, (long long)KV);
+  if (D != 128 && D != 256 && D != 512)
+    return fail(W8A8_ENOTSUP, "k_qkv: head_dim D=%lld (supported: 128, 256, 512)", (long long)D);
+  const int64_t slots = shared ? H : H + 2 * KV;
+  W8A8_TRY(check_input(what, in, slots * D));
+  if (!cos_ || !sin_ || !q || (!shared && (!k || !v))) return fail(W8A8_EINVAL, "k_qkv: null pointer");
+  if (ldcs < D) return fail(W8A8_EINVAL, "k_qkv: ldcs below D");
+  if (!al16(cos_) || !al16(sin_) || ldcs % 8 != 0 || !al16(q) || (!shared && (!al16(k) || !al16(v))))
+    return fail(W8A8_EALIGN, "k_qkv: cos / sin rows and q / k / v must be 16-byte aligned");
+  W8A8_TRY(check_vec16(what, "qw", qw));
+  W8A8_TRY(check_vec16(what, "kw", kw));
+  if (T * slots > INT32_MAX - 4) return fail(W8A8_ENOTSUP, "k_qkv: too large");
+  if (T == 0) return W8A8_OK;
+  QkvParams p{};
+  if (in.i32) {
+    p.acc = static_cast<const int32_t*>(in.p); p.ldacc = in.ld; p.sx = in.sx; p.sw = in.sw;
+  } else {
+    p.y = static_cast<const uint16_t*>(in.p); p.ldy = in.ld;
+  }
+  p.cs = cos_; p.sn = sin_; p.ldcs = ldcs; p.qw = qw; p.kw = shared ? nullptr : kw;
+  p.q = q; p.k = k; p.v = v;
+  p.eps = eps; p.T = int(T); p.H = int(H); p.KV = shared ? 0 : int(KV); p.slots = int(slots);
+  const dim3 grid{static_cast<unsigned>((T * slots + 3) / 4)};
+#define W8A8_QKV(E)                                                                  \
+  do {                                                                               \
+    if (in.i32) qkv_kernel<E, false><<<grid, 256, 0, stream>>>(p);                   \
+    else qkv_kernel<E, true><<<grid, 256, 0, stream>>>(p);                           \
+  } while (0)
+  if (D == 128) W8A8_QKV(1);
+  else if (D == 256) W8A8_QKV(2);
+  else W8A8_QKV(4);
+#undef W8A8_QKV
+  return check_launch(what);
+}
+
+}  // namespace w8a8
+
+extern "C" {
+
+int w8a8_k_post_attn(const int32_t* acc, int64_t ldacc, const float* sx, const float* sw, const uint16_t* res,
+                     int64_t ldr, const uint16_t* w_post, const uint16_t* w_pre_ff, float eps, int64_t M, int64_t N,
+                     uint16_t* h, int64_t ldh, int8_t* q, int64_t ldq, int q_packed, float* sq, hipStream_t stream) {
+  return w8a8::k_post_attn(RowInput{acc, ldacc, sx, sw, true}, res, ldr, w_post, w_pre_ff, eps, M, N, h, ldh, q, ldq,
+                           q_packed, sq, stream);
+}
+
+int w8a8_k_post_attn_y(const uint16_t* y, int64_t ldy, const uint16_t* res, int64_t ldr, const uint16_t* w_post,
+                       const uint16_t* w_pre_ff, float eps, int64_t M, int64_t N, uint16_t* h, int64_t ldh, int8_t* q,
+                       int64_t ldq, int q_packed, float* sq, hipStream_t stream) {
+  return w8a8::k_post_attn(RowInput{y, ldy, nullptr, nullptr, false}, res, ldr, w_post, w_pre_ff, eps, M, N, h, ldh,
+                           q, ldq, q_packed, sq, stream);
 }
 
 int w8a8_k_gelu(const int32_t* acc, int64_t ldacc, const float* sx, const float* sw, int64_t M, int64_t I, int8_t* q,
@@ -603,86 +748,54 @@ int w8a8_k_gelu(const int32_t* acc, int64_t ldacc, const float* sx, const float*
 int w8a8_k_post_ff(const int32_t* acc, int64_t ldacc, const float* sx, const float* sw, const uint16_t* res,
                    int64_t ldr, const uint16_t* w_post_ff, float eps, int64_t M, int64_t N, uint16_t* h, int64_t ldh,
                    int8_t* q, int64_t ldq, int q_packed, float* sq, hipStream_t stream) {
-  const char* what = "k_post_ff";
-  W8A8_TRY(check_rows(what, M, N));
-  W8A8_TRY(check_acc(what, acc, ldacc, sx, sw, N));
-  W8A8_TRY(check_bf16_rows(what, "res", res, ldr, N));
-  W8A8_TRY(check_bf16_rows(what, "h", h, ldh, N));
-  W8A8_TRY(check_vec16(what, "w_post_ff", w_post_ff));
-  RowChain p{};
-  W8A8_TRY(set_q(what, p, q, ldq, q_packed, sq, N));
-  if (M == 0) return W8A8_OK;
-  p.in = acc; p.ld_in = ldacc; p.sx = sx; p.sw = sw;
-  p.op = RC_NORM_RES; p.aux = res; p.ld_aux = ldr; p.w1 = w_post_ff;
-  p.h = h; p.ldh = ldh;
-  p.eps = eps; p.M = int(M); p.N = int(N);
-  return launch_row_chain(p, true, stream, what);
+  return w8a8::k_post_ff(RowInput{acc, ldacc, sx, sw, true}, res, ldr, w_post_ff, eps, M, N, h, ldh, q, ldq, q_packed,
+                         sq, stream);
+}
+
+int w8a8_k_post_ff_y(const uint16_t* y, int64_t ldy, const uint16_t* res, int64_t ldr, const uint16_t* w_post_ff,
+                     float eps, int64_t M, int64_t N, uint16_t* h, int64_t ldh, int8_t* q, int64_t ldq, int q_packed,
+                     float* sq, hipStream_t stream) {
+  return w8a8::k_post_ff(RowInput{y, ldy, nullptr, nullptr, false}, res, ldr, w_post_ff, eps, M, N, h, ldh, q, ldq,
+                         q_packed, sq, stream);
 }
 
 int w8a8_k_ple_gate(const int32_t* acc, int64_t ldacc, const float* sx, const float* sw, const uint16_t* ple,
                     int64_t ldp, int64_t M, int64_t N, int8_t* q, int64_t ldq, int q_packed, float* sq,
                     hipStream_t stream) {
-  const char* what = "k_ple_gate";
-  W8A8_TRY(check_rows(what, M, N));
-  W8A8_TRY(check_acc(what, acc, ldacc, sx, sw, N));
-  W8A8_TRY(check_bf16_rows(what, "ple", ple, ldp, N));
-  RowChain p{};
-  W8A8_TRY(set_q(what, p, q, ldq, q_packed, sq, N));
-  if (M == 0) return W8A8_OK;
-  p.in = acc; p.ld_in = ldacc; p.sx = sx; p.sw = sw;
-  p.op = RC_GELU_MUL; p.aux = ple; p.ld_aux = ldp;
-  p.M = int(M); p.N = int(N);
-  return launch_row_chain(p, true, stream, what);
+  return w8a8::k_ple_gate(RowInput{acc, ldacc, sx, sw, true}, ple, ldp, M, N, q, ldq, q_packed, sq, stream);
+}
+
+int w8a8_k_ple_gate_y(const uint16_t* y, int64_t ldy, const uint16_t* ple, int64_t ldp, int64_t M, int64_t N,
+                      int8_t* q, int64_t ldq, int q_packed, float* sq, hipStream_t stream) {
+  return w8a8::k_ple_gate(RowInput{y, ldy, nullptr, nullptr, false}, ple, ldp, M, N, q, ldq, q_packed, sq, stream);
 }
 
 int w8a8_k_ple_out(const int32_t* acc, int64_t ldacc, const float* sx, const float* sw, const uint16_t* h,
                    int64_t ldh, const uint16_t* w_post_ple, const uint16_t* scalar, float eps, int64_t M, int64_t N,
                    uint16_t* out, int64_t ldo, hipStream_t stream) {
-  const char* what = "k_ple_out";
-  W8A8_TRY(check_rows(what, M, N));
-  W8A8_TRY(check_acc(what, acc, ldacc, sx, sw, N));
-  W8A8_TRY(check_bf16_rows(what, "h", h, ldh, N));
-  W8A8_TRY(check_bf16_rows(what, "out", out, ldo, N));
-  W8A8_TRY(check_vec16(what, "w_post_ple", w_post_ple));
-  if (!scalar) return fail(W8A8_EINVAL, "k_ple_out: scalar is null");
-  if (M == 0) return W8A8_OK;
-  RowChain p{};
-  p.in = acc; p.ld_in = ldacc; p.sx = sx; p.sw = sw;
-  p.op = RC_NORM_RES; p.aux = h; p.ld_aux = ldh; p.w1 = w_post_ple; p.scalar = scalar;
-  p.h = out; p.ldh = ldo;
-  p.eps = eps; p.M = int(M); p.N = int(N);
-  return launch_row_chain(p, true, stream, what);
+  return w8a8::k_ple_out(RowInput{acc, ldacc, sx, sw, true}, h, ldh, w_post_ple, scalar, eps, M, N, out, ldo, stream);
+}
+
+int w8a8_k_ple_out_y(const uint16_t* y, int64_t ldy, const uint16_t* h, int64_t ldh, const uint16_t* w_post_ple,
+                     const uint16_t* scalar, float eps, int64_t M, int64_t N, uint16_t* out, int64_t ldo,
+                     hipStream_t stream) {
+  return w8a8::k_ple_out(RowInput{y, ldy, nullptr, nullptr, false}, h, ldh, w_post_ple, scalar, eps, M, N, out, ldo,
+                         stream);
 }
 
 int w8a8_k_qkv(const int32_t* acc, int64_t ldacc, const float* sx, const float* sw, const uint16_t* cos_,
                const uint16_t* sin_, int64_t ldcs, const uint16_t* qw, const uint16_t* kw, float eps, int64_t T,
                int64_t H, int64_t KV, int64_t D, int shared, uint16_t* q, uint16_t* k, uint16_t* v,
                hipStream_t stream) {
-  const char* what = "k_qkv";
-  if (T < 0 || H <= 0 || KV < 0 || (!shared && KV <= 0))
-    return fail(W8A8_EINVAL, "k_qkv: bad shape T=%lld H=%lld KV=%lld", (long long)T, (long long)H, (long long)KV);
-  if (D != 128 && D != 256 && D != 512)
-    return fail(W8A8_ENOTSUP, "k_qkv: head_dim D=%lld (supported: 128, 256, 512)", (long long)D);
-  const int64_t slots = shared ? H : H + 2 * KV;
-  W8A8_TRY(check_acc(what, acc, ldacc, sx, sw, slots * D));
-  if (!cos_ || !sin_ || !q || (!shared && (!k || !v))) return fail(W8A8_EINVAL, "k_qkv: null pointer");
-  if (ldcs < D) return fail(W8A8_EINVAL, "k_qkv: ldcs below D");
-  if (!al16(cos_) || !al16(sin_) || ldcs % 8 != 0 || !al16(q) || (!shared && (!al16(k) || !al16(v))))
-    return fail(W8A8_EALIGN, "k_qkv: cos / sin rows and q / k / v must be 16-byte aligned");
-  W8A8_TRY(check_vec16(what, "qw", qw));
-  W8A8_TRY(check_vec16(what, "kw", kw));
-  if (T * slots > INT32_MAX - 4) return fail(W8A8_ENOTSUP, "k_qkv: too large");
-  if (T == 0) return W8A8_OK;
-  QkvParams p;
-  p.acc = acc; p.ldacc = ldacc; p.sx = sx; p.sw = sw;
-  p.cs = cos_; p.sn = sin_; p.ldcs = ldcs; p.qw = qw; p.kw = shared ? nullptr : kw;
-  p.q = q; p.k = k; p.v = v;
-  p.eps = eps; p.T = int(T); p.H = int(H); p.KV = shared ? 0 : int(KV); p.slots = int(slots);
-  const dim3 grid{static_cast<unsigned>((T * slots + 3) / 4)};
-  if (D == 128) qkv_kernel<1><<<grid, 256, 0, stream>>>(p);
-  else if (D == 256) qkv_kernel<2><<<grid, 256, 0, stream>>>(p);
-  else qkv_kernel<4><<<grid, 256, 0, stream>>>(p);
-  return check_launch(what);
+  return w8a8::k_qkv(RowInput{acc, ldacc, sx, sw, true}, cos_, sin_, ldcs, qw, kw, eps, T, H, KV, D, shared, q, k, v,
+                     stream);
+}
+
+int w8a8_k_qkv_y(const uint16_t* y, int64_t ldy, const uint16_t* cos_, const uint16_t* sin_, int64_t ldcs,
+                 const uint16_t* qw, const uint16_t* kw, float eps, int64_t T, int64_t H, int64_t KV, int64_t D,
+                 int shared, uint16_t* q, uint16_t* k, uint16_t* v, hipStream_t stream) {
+  return w8a8::k_qkv(RowInput{y, ldy, nullptr, nullptr, false}, cos_, sin_, ldcs, qw, kw, eps, T, H, KV, D, shared,
+                     q, k, v, stream);
 }
 
 }  // extern "C"

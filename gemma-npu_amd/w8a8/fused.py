@@ -14,7 +14,10 @@ pipeline, so a caller swaps the module and keeps its code:
 
 acc is the int32 GEMM result [T, N] (rows contiguous, any row stride, as the reference's
 strided view of its result buffer), sx fp32 [T] and sw fp32 [N] its scales; activations and
-norm weights are bf16.  xq is int8 [T, K] row-major, or, with packed=True, a PackedActivation
+norm weights are bf16.  k_qkv, k_post_attn, k_post_ff, k_ple_gate and k_ple_out also take, as acc,
+the dequantised bf16 rows bf16((acc * sx) * sw) that the GEMM's dequant epilogue writes (sx and sw
+are then not read and may be None): the kernels' first step is that dequant, so the results are
+bit-identical and the GEMM writes half the bytes.  xq is int8 [T, K] row-major, or, with packed=True, a PackedActivation
 that the GEMM reads fastest.  q / k / v of k_qkv are contiguous [heads, T, D] tensors holding
 the values of the reference's transposed views.  Everything runs on torch's current stream of
 the tensors' device; there is no CPU fallback.
@@ -35,13 +38,20 @@ def _vec(t, name, n):
     return t.data_ptr()
 
 
-def _acc(acc, sx, sw, ncols):
+def _acc(acc, sx, sw, ncols, dequantised_ok=False):
+    """Checks acc (int32 with its scales, or with dequantised_ok the bf16 rows); True if it is bf16."""
+    if dequantised_ok and isinstance(acc, torch.Tensor) and acc.dtype == torch.bfloat16:
+        _check(acc, "acc", torch.bfloat16)
+        if acc.shape[1] < ncols:
+            raise ValueError(f"acc {tuple(acc.shape)} does not cover {ncols} columns")
+        return True
     _check(acc, "acc", torch.int32)
     _check(sx, "sx", torch.float32, 1)
     _check(sw, "sw", torch.float32, 1)
     if acc.shape[1] < ncols or sx.shape[0] != acc.shape[0] or sw.shape[0] < ncols:
         raise ValueError(f"acc {tuple(acc.shape)} / sx {tuple(sx.shape)} / sw {tuple(sw.shape)} do not cover "
                          f"{ncols} columns")
+    return False
 
 
 def _q_out(M, N, device, packed):
@@ -76,7 +86,7 @@ def k_qkv(acc, sx, sw, cos, sin, qw, kw, eps, H, KV, D, shared):
     """q/k/v GEMM out -> normed, rotated q [H, T, D], k, v [KV, T, D] (bf16)."""
     H, KV, D = int(H), int(KV), int(D)
     slots = H if shared else H + 2 * KV
-    _acc(acc, sx, sw, slots * D)
+    y = _acc(acc, sx, sw, slots * D, dequantised_ok=True)
     T = acc.shape[0]
     for t, name in ((cos, "cos"), (sin, "sin")):
         _check(t, name, torch.bfloat16)
@@ -92,10 +102,16 @@ def k_qkv(acc, sx, sw, cos, sin, qw, kw, eps, H, KV, D, shared):
     if not shared:
         k = torch.empty((KV, T, D), dtype=torch.bfloat16, device=dev)
         v = torch.empty((KV, T, D), dtype=torch.bfloat16, device=dev)
-    _same_device(acc, sx, sw, cos, sin, qw, kw)
-    call("w8a8_k_qkv", acc.data_ptr(), _ld(acc), sx.data_ptr(), sw.data_ptr(), cos.data_ptr(), sin.data_ptr(),
-         _ld(cos), qwp, kwp, float(eps), T, H, KV, D, 1 if shared else 0, q.data_ptr(),
-         None if shared else k.data_ptr(), None if shared else v.data_ptr(), _stream(acc))
+    if y:
+        _same_device(acc, cos, sin, qw, kw)
+        call("w8a8_k_qkv_y", acc.data_ptr(), _ld(acc), cos.data_ptr(), sin.data_ptr(), _ld(cos), qwp, kwp,
+             float(eps), T, H, KV, D, 1 if shared else 0, q.data_ptr(), None if shared else k.data_ptr(),
+             None if shared else v.data_ptr(), _stream(acc))
+    else:
+        _same_device(acc, sx, sw, cos, sin, qw, kw)
+        call("w8a8_k_qkv", acc.data_ptr(), _ld(acc), sx.data_ptr(), sw.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+             _ld(cos), qwp, kwp, float(eps), T, H, KV, D, 1 if shared else 0, q.data_ptr(),
+             None if shared else k.data_ptr(), None if shared else v.data_ptr(), _stream(acc))
     if shared:
         return q, q, q
     return q, k, v
@@ -117,15 +133,19 @@ def k_attn_out(o, packed=False):
 def k_post_attn(acc, sx, sw, res, w_post, w_pre_ff, eps, packed=False):
     """o_proj out -> residual add -> pre-FFN norm -> int8 rows for gate/up: (h, xq, sx)."""
     M, N = res.shape
-    _acc(acc, sx, sw, N)
+    y = _acc(acc, sx, sw, N, dequantised_ok=True)
     rp, ldr = _rows(res, "res", M, N)
     h = torch.empty((M, N), dtype=torch.bfloat16, device=res.device)
     q, ldq, qp, xq = _q_out(M, N, res.device, packed)
     sq = torch.empty((M,), dtype=torch.float32, device=res.device)
-    _same_device(acc, sx, sw, res, w_post, w_pre_ff)
-    call("w8a8_k_post_attn", acc.data_ptr(), _ld(acc), sx.data_ptr(), sw.data_ptr(), rp, ldr,
-         _vec(w_post, "w_post", N), _vec(w_pre_ff, "w_pre_ff", N), float(eps), M, N, h.data_ptr(), N, q.data_ptr(),
-         ldq, qp, sq.data_ptr(), _stream(acc))
+    tail = (rp, ldr, _vec(w_post, "w_post", N), _vec(w_pre_ff, "w_pre_ff", N), float(eps), M, N, h.data_ptr(), N,
+            q.data_ptr(), ldq, qp, sq.data_ptr(), _stream(acc))
+    if y:
+        _same_device(acc, res, w_post, w_pre_ff)
+        call("w8a8_k_post_attn_y", acc.data_ptr(), _ld(acc), *tail)
+    else:
+        _same_device(acc, sx, sw, res, w_post, w_pre_ff)
+        call("w8a8_k_post_attn", acc.data_ptr(), _ld(acc), sx.data_ptr(), sw.data_ptr(), *tail)
     return h, xq, sq
 
 
@@ -145,28 +165,36 @@ def k_gelu(acc, sx, sw, I, packed=False):
 def k_post_ff(acc, sx, sw, res, w_post_ff, eps, packed=False):
     """down_proj out -> residual add -> int8 rows for the PLE gate: (h, xq, sx)."""
     M, N = res.shape
-    _acc(acc, sx, sw, N)
+    y = _acc(acc, sx, sw, N, dequantised_ok=True)
     rp, ldr = _rows(res, "res", M, N)
     h = torch.empty((M, N), dtype=torch.bfloat16, device=res.device)
     q, ldq, qp, xq = _q_out(M, N, res.device, packed)
     sq = torch.empty((M,), dtype=torch.float32, device=res.device)
-    _same_device(acc, sx, sw, res, w_post_ff)
-    call("w8a8_k_post_ff", acc.data_ptr(), _ld(acc), sx.data_ptr(), sw.data_ptr(), rp, ldr,
-         _vec(w_post_ff, "w_post_ff", N), float(eps), M, N, h.data_ptr(), N, q.data_ptr(), ldq, qp, sq.data_ptr(),
-         _stream(acc))
+    tail = (rp, ldr, _vec(w_post_ff, "w_post_ff", N), float(eps), M, N, h.data_ptr(), N, q.data_ptr(), ldq, qp,
+            sq.data_ptr(), _stream(acc))
+    if y:
+        _same_device(acc, res, w_post_ff)
+        call("w8a8_k_post_ff_y", acc.data_ptr(), _ld(acc), *tail)
+    else:
+        _same_device(acc, sx, sw, res, w_post_ff)
+        call("w8a8_k_post_ff", acc.data_ptr(), _ld(acc), sx.data_ptr(), sw.data_ptr(), *tail)
     return h, xq, sq
 
 
 def k_ple_gate(acc, sx, sw, ple, packed=False):
     """PLE gate out -> gelu * this layer's per-layer input -> int8 rows."""
     M, N = ple.shape
-    _acc(acc, sx, sw, N)
+    y = _acc(acc, sx, sw, N, dequantised_ok=True)
     pp, ldp = _rows(ple, "ple", M, N)
     q, ldq, qp, xq = _q_out(M, N, ple.device, packed)
     sq = torch.empty((M,), dtype=torch.float32, device=ple.device)
-    _same_device(acc, sx, sw, ple)
-    call("w8a8_k_ple_gate", acc.data_ptr(), _ld(acc), sx.data_ptr(), sw.data_ptr(), pp, ldp, M, N, q.data_ptr(),
-         ldq, qp, sq.data_ptr(), _stream(acc))
+    tail = (pp, ldp, M, N, q.data_ptr(), ldq, qp, sq.data_ptr(), _stream(acc))
+    if y:
+        _same_device(acc, ple)
+        call("w8a8_k_ple_gate_y", acc.data_ptr(), _ld(acc), *tail)
+    else:
+        _same_device(acc, sx, sw, ple)
+        call("w8a8_k_ple_gate", acc.data_ptr(), _ld(acc), sx.data_ptr(), sw.data_ptr(), *tail)
     return xq, sq
 
 
@@ -176,7 +204,7 @@ def k_ple_out(acc, sx, sw, h, w_post_ple, scalar, eps):
     scalar: a one-element bf16 tensor on the device (the layer scalar), or a Python number,
     which is rounded to bf16 first."""
     M, N = h.shape
-    _acc(acc, sx, sw, N)
+    y = _acc(acc, sx, sw, N, dequantised_ok=True)
     hp, ldh = _rows(h, "h", M, N)
     if not isinstance(scalar, torch.Tensor):
         scalar = torch.tensor([float(scalar)], dtype=torch.bfloat16, device=h.device)
@@ -184,7 +212,12 @@ def k_ple_out(acc, sx, sw, h, w_post_ple, scalar, eps):
         raise ValueError("k_ple_out: scalar must be one bf16 value on the tensors' device")
     scalar = scalar.reshape(1).contiguous()
     out = torch.empty((M, N), dtype=torch.bfloat16, device=h.device)
-    _same_device(acc, sx, sw, h, w_post_ple)
-    call("w8a8_k_ple_out", acc.data_ptr(), _ld(acc), sx.data_ptr(), sw.data_ptr(), hp, ldh,
-         _vec(w_post_ple, "w_post_ple", N), scalar.data_ptr(), float(eps), M, N, out.data_ptr(), N, _stream(acc))
+    tail = (hp, ldh, _vec(w_post_ple, "w_post_ple", N), scalar.data_ptr(), float(eps), M, N, out.data_ptr(), N,
+            _stream(acc))
+    if y:
+        _same_device(acc, h, w_post_ple)
+        call("w8a8_k_ple_out_y", acc.data_ptr(), _ld(acc), *tail)
+    else:
+        _same_device(acc, sx, sw, h, w_post_ple)
+        call("w8a8_k_ple_out", acc.data_ptr(), _ld(acc), sx.data_ptr(), sw.data_ptr(), *tail)
     return out

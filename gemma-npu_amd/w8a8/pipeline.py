@@ -31,7 +31,10 @@ How it is organised here:
 
 The gate/up step takes the GEMM's fused GELU epilogue followed by the quant kernel by default
 (fuse_gelu): the same int8 rows and scales as k_gelu on the int32 result, without writing the
-[T, 2I] int32 result.  The embedding, per-layer-input tables, RoPE tables, final norm and logit
+[T, 2I] int32 result.  The other GEMMs write their dequantised bf16 result by default
+(dequant_in_gemm), which the fused kernels after them read in place of the int32 result and its
+scales: their first step is that dequant, so every value is the same and the hand-over moves half
+the bytes.  The embedding, per-layer-input tables, RoPE tables, final norm and logit
 softcap are the model's own modules (pipeline.py:318-338); inside them the per-layer model
 projection and the LM head run on the engine after hf.to_gpu.
 """
@@ -119,7 +122,7 @@ def prompt_inputs(lm, ids):
 class Prefill:
     """pipeline.py:224-339 on the GPU: Prefill(model)(ids) -> (logits [vocab] fp32, DynamicCache)."""
 
-    def __init__(self, model, layer_gemms=None, row_step=None, fuse_gelu=True):
+    def __init__(self, model, layer_gemms=None, row_step=None, fuse_gelu=True, dequant_in_gemm=True):
         self.model = model
         self.lm = language_model(model)
         self.cfg = cfg = self.lm.config
@@ -130,6 +133,11 @@ class Prefill:
             raise ValueError(f"Prefill: row_step {row_step} must be positive")
         self.row_step = None if row_step is None else int(row_step)
         self.fuse_gelu = bool(fuse_gelu)
+        # The GEMMs that feed k_qkv / k_post_attn / k_post_ff / k_ple_gate / k_ple_out write their
+        # dequantised bf16 result (the dequant epilogue) instead of int32: those kernels dequantise
+        # first, so the results are bit-identical with half the bytes written and read.  False keeps
+        # the reference's int32 hand-over (its NPU GEMM's output, npu_kernels.py:56).
+        self.dequant_in_gemm = bool(dequant_in_gemm)
         if getattr(cfg, "enable_moe_block", False):
             raise NotImplementedError("Prefill: MoE decoder layers are not on the reference's path")
         if not cfg.hidden_size_per_layer_input:
@@ -159,9 +167,15 @@ class Prefill:
         """Rows [start, end) of the prompt through decoder layer p; returns their new hidden rows."""
         eps = self.cfg.rms_norm_eps
         W = p.weights
+
+        def gemm(xq, sx, w):
+            """The result of one GEMM as the fused kernel after it reads it."""
+            if self.dequant_in_gemm:
+                return ops.gemm_bf16(xq, sx, w.packed, w.sw)
+            return ops.gemm_i32(xq, w.packed)
         cos, sin = (t[start:end] for t in rope[p.kind])
         xq, sx = fused.k_in(h, p.norm_in, eps, packed=True)
-        acc = ops.gemm_i32(xq, W["qkv"].packed)
+        acc = gemm(xq, sx, W["qkv"])
         q, k, v = fused.k_qkv(acc, sx, W["qkv"].sw, cos, sin, p.norm_q, p.norm_k, eps, p.heads, p.kv_heads,
                               p.head_dim, p.shares_kv)
         if not p.shares_kv:
@@ -170,7 +184,7 @@ class Prefill:
         o = attention.attention(q, keys, values, start, p.window, 1.0)
 
         xq, sx = fused.k_attn_out(o, packed=True)
-        acc = ops.gemm_i32(xq, W["o"].packed)
+        acc = gemm(xq, sx, W["o"])
         h, xq, sx = fused.k_post_attn(acc, sx, W["o"].sw, h, p.norm_post_attn, p.norm_pre_ff, eps, packed=True)
         gu = W["gate_up"]
         if self.fuse_gelu and getattr(gu, "packed_gelu", None) is not None:
@@ -178,11 +192,11 @@ class Prefill:
             xq, sx = ops.quant_rows_packed(ops.gemm_bf16(xq, sx, gu.packed_gelu, epilogue="gelu"))
         else:
             xq, sx = fused.k_gelu(ops.gemm_i32(xq, gu.packed), sx, gu.sw, gu.N // 2, packed=True)
-        acc = ops.gemm_i32(xq, W["down"].packed)
+        acc = gemm(xq, sx, W["down"])
         h, xq, sx = fused.k_post_ff(acc, sx, W["down"].sw, h, p.norm_post_ff, eps, packed=True)
-        acc = ops.gemm_i32(xq, W["ple_gate"].packed)
+        acc = gemm(xq, sx, W["ple_gate"])
         xq, sx = fused.k_ple_gate(acc, sx, W["ple_gate"].sw, per_layer[start:end, p.index], packed=True)
-        acc = ops.gemm_i32(xq, W["ple_proj"].packed)
+        acc = gemm(xq, sx, W["ple_proj"])
         return fused.k_ple_out(acc, sx, W["ple_proj"].sw, h, p.norm_post_ple, scalar[p.index], eps)
 
     def run_layers(self, h0, per_layer, rope, scalar=None):

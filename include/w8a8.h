@@ -248,6 +248,26 @@ int w8a8_k_ple_out(const int32_t *acc, int64_t ldacc, const float *sx, const flo
                    int64_t ldh, const uint16_t *w_post_ple, const uint16_t *scalar, float eps, int64_t M, int64_t N,
                    uint16_t *out, int64_t ldo, hipStream_t stream);
 
+/* The same five kernels fed the dequantised bf16 rows y [rows, N] (ld = ldy, 16-byte aligned rows)
+ * instead of an int32 result with its scales: y is what the GEMM's dequant epilogue
+ * (w8a8_gemm_bf16 epilogue 0) writes, bf16((acc * sx) * sw), the values the int32 entries compute
+ * first, so the results are bit-identical while the GEMM writes, and the kernel reads, half the
+ * bytes.  Same reference functions as their int32 twins (pipeline.py:72-85, 95-99, 110-127). */
+int w8a8_k_qkv_y(const uint16_t *y, int64_t ldy, const uint16_t *cos_, const uint16_t *sin_, int64_t ldcs,
+                 const uint16_t *qw, const uint16_t *kw, float eps, int64_t T, int64_t H, int64_t KV, int64_t D,
+                 int shared, uint16_t *q, uint16_t *k, uint16_t *v, hipStream_t stream);
+int w8a8_k_post_attn_y(const uint16_t *y, int64_t ldy, const uint16_t *res, int64_t ldr, const uint16_t *w_post,
+                       const uint16_t *w_pre_ff, float eps, int64_t M, int64_t N, uint16_t *h, int64_t ldh, int8_t *q,
+                       int64_t ldq, int q_packed, float *sq, hipStream_t stream);
+int w8a8_k_post_ff_y(const uint16_t *y, int64_t ldy, const uint16_t *res, int64_t ldr, const uint16_t *w_post_ff,
+                     float eps, int64_t M, int64_t N, uint16_t *h, int64_t ldh, int8_t *q, int64_t ldq, int q_packed,
+                     float *sq, hipStream_t stream);
+int w8a8_k_ple_gate_y(const uint16_t *y, int64_t ldy, const uint16_t *ple, int64_t ldp, int64_t M, int64_t N,
+                      int8_t *q, int64_t ldq, int q_packed, float *sq, hipStream_t stream);
+int w8a8_k_ple_out_y(const uint16_t *y, int64_t ldy, const uint16_t *h, int64_t ldh, const uint16_t *w_post_ple,
+                     const uint16_t *scalar, float eps, int64_t M, int64_t N, uint16_t *out, int64_t ldo,
+                     hipStream_t stream);
+
 /* ---- whole linear: bf16 in -> bf16 out (NPUGemm.matmul, gemma_npu.py:117-152) ------------ */
 
 /* Workspace for w8a8_linear_bf16: the packed int8 rows and the per-row scales, 256-byte aligned

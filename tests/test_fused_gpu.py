@@ -235,6 +235,49 @@ def test_k_ple_out(T):
     assert (got == ref).mean() > 0.99
 
 
+# ---- the dequantised bf16 input (the GEMM's dequant epilogue) gives the same bits ----------
+
+@pytest.mark.parametrize("T", [77, 512])
+def test_kernels_on_dequantised_rows_match_int32(T):
+    """k_qkv, k_post_attn, k_post_ff, k_ple_gate and k_ple_out fed y = bf16((acc * sx) * sw) -- the
+    rows the GEMM's dequant epilogue writes, here from the standalone dequant kernel -- give exactly
+    the outputs of the int32 entries on acc, sx, sw, as strided views too."""
+    D, H, KV, N, P = 256, 8, 1, 1536, 256
+
+    def dq(acc, sx, sw, pad=0):
+        a = acc.to(DEV)
+        y = torch.empty((T, a.shape[1] + pad), dtype=torch.bfloat16, device=DEV)[:, :a.shape[1]]
+        return ops.dequant_bf16(a, sx.to(DEV), sw.to(DEV), out=y)
+
+    def same(a, b, what):
+        for x, y in zip(a if isinstance(a, tuple) else (a,), b if isinstance(b, tuple) else (b,)):
+            xs = x.data if hasattr(x, "data") and not isinstance(x, torch.Tensor) else x
+            ys = y.data if hasattr(y, "data") and not isinstance(y, torch.Tensor) else y
+            assert torch.equal(xs, ys), what
+
+    acc, sx, sw = acc_inputs(T, (H + 2 * KV) * D, seed=100 + T)
+    ang = (torch.arange(T).float()[:, None] * 0.01 + torch.arange(D).float()[None, :] * 0.1)
+    cos, sin = ang.cos().to(torch.bfloat16).to(DEV), ang.sin().to(torch.bfloat16).to(DEV)
+    qw, kw = norm_weight(D, 101).to(DEV), norm_weight(D, 102).to(DEV)
+    ref = fused.k_qkv(acc.to(DEV), sx.to(DEV), sw.to(DEV), cos, sin, qw, kw, EPS, H, KV, D, False)
+    same(fused.k_qkv(dq(acc, sx, sw, pad=64), None, None, cos, sin, qw, kw, EPS, H, KV, D, False), ref, "k_qkv")
+    acc, sx, sw = acc_inputs(T, N, seed=110 + T)
+    res, w1, w2 = bf16_rows(T, N, 111).to(DEV), norm_weight(N, 112).to(DEV), norm_weight(N, 113).to(DEV)
+    d = (acc.to(DEV), sx.to(DEV), sw.to(DEV))
+    for packed in (False, True):
+        same(fused.k_post_attn(dq(acc, sx, sw), None, None, res, w1, w2, EPS, packed=packed),
+             fused.k_post_attn(*d, res, w1, w2, EPS, packed=packed), "k_post_attn")
+        same(fused.k_post_ff(dq(acc, sx, sw, pad=8), None, None, res, w1, EPS, packed=packed),
+             fused.k_post_ff(*d, res, w1, EPS, packed=packed), "k_post_ff")
+    scalar = torch.tensor([0.62], dtype=torch.bfloat16, device=DEV)
+    same(fused.k_ple_out(dq(acc, sx, sw), None, None, res, w1, scalar, EPS),
+         fused.k_ple_out(*d, res, w1, scalar, EPS), "k_ple_out")
+    acc, sx, sw = acc_inputs(T, P, seed=120 + T)
+    ple = bf16_rows(T, 4 * P, 121).to(DEV)[:, P:2 * P]
+    same(fused.k_ple_gate(dq(acc, sx, sw), None, None, ple, packed=True),
+         fused.k_ple_gate(acc.to(DEV), sx.to(DEV), sw.to(DEV), ple, packed=True), "k_ple_gate")
+
+
 # ---- a decoder layer's linear path, stage by stage --------------------------------------
 
 def test_layer_chain_stagewise():

@@ -14,6 +14,7 @@ Checks:
   but attention is row-wise, so the final hidden rows agree to bf16 noise;
 - the fused gate/up route (the GEMM's GELU epilogue, then the quant kernel) against k_gelu on the
   int32 result: the same int8 rows and scales, and the same final hidden rows through the model;
+- the GEMMs' dequantised bf16 hand-over to the fused kernels against the int32 one: the same bits;
 - determinism, and its refusals (no layer groups, a bad row_step, ids of the wrong shape).
 """
 import copy
@@ -146,6 +147,25 @@ def test_fused_gelu_route_matches_reference_route():
     a, _ = Prefill(ours)(ids, all_hidden=True)
     b, _ = Prefill(ours, fuse_gelu=False)(ids, all_hidden=True)
     assert torch.equal(a, b)
+
+
+@torch.inference_mode()
+def test_dequant_in_gemm_matches_int32_handover():
+    """Prefill with the GEMMs writing their dequantised bf16 result (the default) and with the
+    reference's int32 hand-over (each fused kernel dequantising first): the same logits, final
+    hidden rows and cache, bit for bit."""
+    from w8a8.pipeline import Prefill
+    ours = engine_model(build(seed=17))
+    ids = torch.randint(0, 512, (1, 45), generator=torch.Generator().manual_seed(18))
+    a, ca = Prefill(ours)(ids)
+    b, cb = Prefill(ours, dequant_in_gemm=False)(ids)
+    assert torch.equal(a, b)
+    for la, lb in zip(ca.layers, cb.layers):
+        if getattr(la, "keys", None) is not None and la.keys.numel():
+            assert torch.equal(la.keys, lb.keys) and torch.equal(la.values, lb.values)
+    ha, _ = Prefill(ours)(ids, all_hidden=True)
+    hb, _ = Prefill(ours, dequant_in_gemm=False)(ids, all_hidden=True)
+    assert torch.equal(ha, hb)
 
 
 @torch.inference_mode()
