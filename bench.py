@@ -443,25 +443,30 @@ def build_chain(M, dev, seed0=500):
     return c
 
 
-def chain_step(c):
+def chain_step(c, dequant_in_gemm=False):
     """k_in -> qkv -> k_qkv -> k_attn_out -> o -> k_post_attn -> gate_up (GELU epilogue) -> quant
-    -> down -> k_post_ff -> ple_gate -> k_ple_gate -> ple_proj -> k_ple_out; returns the new h."""
+    -> down -> k_post_ff -> ple_gate -> k_ple_gate -> ple_proj -> k_ple_out; returns the new h.  The
+    GEMMs before the fused kernels hand over their int32 result (as w8a8.pipeline does at this row
+    count), or with dequant_in_gemm their dequantised bf16 result (the same bits)."""
     from w8a8 import fused, ops
     pw, nw, eps = c["pw"], c["norm"], c["eps"]
+
+    def gemm(xq, sx, w):
+        return ops.gemm_bf16(xq, sx, w) if dequant_in_gemm else ops.gemm_i32(xq, w)
     xq, sx = fused.k_in(c["h0"], nw["in"], eps, packed=True)
-    acc = ops.gemm_i32(xq, pw["qkv"])
+    acc = gemm(xq, sx, pw["qkv"])
     q, k, v = fused.k_qkv(acc, sx, pw["qkv"].sw, c["cos"], c["sin"], nw["qw"], nw["kw"], eps, c["H"], c["KV"],
                           c["D"], False)
     xq, sx = fused.k_attn_out(q, packed=True)
-    acc = ops.gemm_i32(xq, pw["o"])
+    acc = gemm(xq, sx, pw["o"])
     h, xq, sx = fused.k_post_attn(acc, sx, pw["o"].sw, c["h0"], nw["post"], nw["pre_ff"], eps, packed=True)
     a = ops.gemm_bf16(xq, sx, pw["gate_up"], epilogue="gelu")
     xq, sx = ops.quant_rows_packed(a)
-    acc = ops.gemm_i32(xq, pw["down"])
+    acc = gemm(xq, sx, pw["down"])
     h, xq, sx = fused.k_post_ff(acc, sx, pw["down"].sw, h, nw["post_ff"], eps, packed=True)
-    acc = ops.gemm_i32(xq, pw["ple_gate"])
+    acc = gemm(xq, sx, pw["ple_gate"])
     xq, sx = fused.k_ple_gate(acc, sx, pw["ple_gate"].sw, c["ple"], packed=True)
-    acc = ops.gemm_i32(xq, pw["ple_proj"])
+    acc = gemm(xq, sx, pw["ple_proj"])
     c["out"] = fused.k_ple_out(acc, sx, pw["ple_proj"].sw, h, nw["post_ple"], c["scalar"], eps)
     return c["out"]
 
@@ -471,6 +476,8 @@ def time_chain(M, dev, reps):
     import torch
     c = build_chain(M, dev)
     ref = chain_step(c).clone()
+    if not torch.equal(chain_step(c, dequant_in_gemm=True), ref):
+        raise RuntimeError("the bf16 hand-over gives another layer chain result than the int32 one")
     graph = capture(lambda: chain_step(c), dev)
     c["out"].zero_()
     graph.replay()
@@ -479,6 +486,8 @@ def time_chain(M, dev, reps):
         raise RuntimeError("captured layer chain differs from eager")
     ms = event_time_ms(graph.replay, reps, 5)
     eager = event_time_ms(lambda: chain_step(c), reps, 5)
+    graph16 = capture(lambda: chain_step(c, dequant_in_gemm=True), dev)
+    c["bf16_handover_us"] = round(event_time_ms(graph16.replay, reps, 5) * 1e3, 1)
     return ms, eager, c
 
 
@@ -1025,9 +1034,12 @@ def main():
         ms, eager, c = time_chain(M, dev, reps=100)
         extra[f"device_layer_chain_m{M}"] = {
             "us": round(ms * 1e3, 1), "eager_us": round(eager * 1e3, 1), "launches": c["launches"],
+            "bf16_handover_us": c["bf16_handover_us"],
             "gemm_tops": round(c["ops"] / (ms * 1e-3) / 1e12, 1),
             "what": "k_in, qkv GEMM, k_qkv, k_attn_out, o GEMM, k_post_attn, gate_up GEMM+GELU, quant, down GEMM, "
-                    "k_post_ff, PLE gate GEMM, k_ple_gate, PLE proj GEMM, k_ple_out (no attention), one HIP graph"}
+                    "k_post_ff, PLE gate GEMM, k_ple_gate, PLE proj GEMM, k_ple_out (no attention), one HIP graph; "
+                    "the GEMMs hand their int32 result to the fused kernels (bf16_handover_us: their dequantised "
+                    "bf16 result instead, the same bits)"}
         log(f"bench: device layer chain M={M}: {extra[f'device_layer_chain_m{M}']}")
         del c
         for Mg in (1, 4, 16):

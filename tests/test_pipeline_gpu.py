@@ -157,14 +157,14 @@ def test_dequant_in_gemm_matches_int32_handover():
     from w8a8.pipeline import Prefill
     ours = engine_model(build(seed=17))
     ids = torch.randint(0, 512, (1, 45), generator=torch.Generator().manual_seed(18))
-    a, ca = Prefill(ours)(ids)
+    a, ca = Prefill(ours, dequant_in_gemm=True)(ids)
     b, cb = Prefill(ours, dequant_in_gemm=False)(ids)
     assert torch.equal(a, b)
     for la, lb in zip(ca.layers, cb.layers):
         if getattr(la, "keys", None) is not None and la.keys.numel():
             assert torch.equal(la.keys, lb.keys) and torch.equal(la.values, lb.values)
-    ha, _ = Prefill(ours)(ids, all_hidden=True)
-    hb, _ = Prefill(ours, dequant_in_gemm=False)(ids, all_hidden=True)
+    ha, _ = Prefill(ours, dequant_in_gemm=True)(ids, all_hidden=True)
+    hb, _ = Prefill(ours)(ids, all_hidden=True)  # 45 rows: the automatic choice is the int32 hand-over
     assert torch.equal(ha, hb)
 
 
