@@ -964,11 +964,25 @@ def main():
     traffic = read_traffic()
     clock = clock_during(lambda: ops.gemm_bf16(gu["q"], gu["sx"], gu["pw"], epilogue="gelu", out=gu["out"]), dev)
     peak_at_clock = 256 * 8192 * clock / 1e3  # TOP/s: 256 CUs x 8192 int8 op/clk/CU at the measured clock
+    # the step's own roofline: per linear max(t_mfma, t_hbm) over its algorithmic ops and compulsory
+    # bytes (bf16 x in, int8 W, fp32 scales, bf16 out, the residual in), summed over the four
+    step_floor_us = 0.0
+    for g in groups:
+        n_out = g["N"] // 2 if g["epi"] == "gelu" else g["N"]
+        nbytes = 2 * M * g["K"] + g["K"] * g["N"] + 4 * g["N"] + 2 * M * n_out + (2 * M * g["N"] if g["res"] is not None
+                                                                                   else 0)
+        step_floor_us += max(workloads.gemm_ops(M, g["N"], g["K"]) / (PEAK_INT8_TOPS * 1e12),
+                             nbytes / (PEAK_HBM_GBS * 1e9)) * 1e6
     roofline = {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": traffic,
+                "traffic_source": f"{os.path.relpath(PMC_SUMMARY, ROOT)}: rocprofv3 FETCH_SIZE + WRITE_SIZE of this "
+                                  "kernel, each calibrated on a 64 MiB copy (read from the committed summary, not "
+                                  "measured in this run)" if traffic is not None else None,
                 "kernel": f"{tile_name(gu_cfg)} gate_up M=512 K=1536 N=12288 with the GELU epilogue, packed A",
                 "avg_launch_us": round(gu_ms * 1e3, 2), "clock_ghz": round(clock, 3),
-                "frac_at_clock": round(achieved / peak_at_clock, 4)}
+                "frac_at_clock": round(achieved / peak_at_clock, 4),
+                "step_roofline_us": round(step_floor_us, 2),
+                "step_frac": round(step_floor_us / (ms_step * 1e3), 4)}
     log(f"bench: gate_up runs at {clock:.3f} GHz: {achieved:.0f} TOP/s = {achieved / peak_at_clock:.3f} of the "
         f"MFMA peak at that clock ({peak_at_clock:.0f} TOP/s)")
     log(f"bench: per-GEMM us: " + ", ".join(f"{k} {v * 1e3:.1f}" for k, v in per_ms.items()))
