@@ -98,6 +98,38 @@ def single_gemm(dev, M=512, K=1536, N=6144):
             "shape": f"M={M} K={K} N={N}, packed int8 A, int32 out, weights hot"}
 
 
+def host_slot_gemm(dev, M=512, K=1536, N=6144, reps=50):
+    """The same single GEMM through the drop-in `npu_kernels.mm_i8` on the reference's host-side
+    resident buffers (gemma_npu.py:89-115): A staged in pinned host memory, C read back into it,
+    the weight resident in HBM.  Each synchronous call moves A (M*K bytes) to the GPU and the int32
+    C (4*M*N bytes) back over PCIe; this is the boundary's host-buffer rate, not the HBM-resident
+    `value`."""
+    import time
+    import torch
+    import npu_kernels
+    from w8a8 import ops, resident, workloads
+    x, w, _ = workloads.single_gemm_inputs(M, K, N, seed=0)
+    a_dev, _ = ops.quant_rows(x.to(dev))
+    a = resident.empty((M, K), dtype=torch.int8)
+    a.copy_(a_dev.cpu())
+    c = resident.empty((M, N), dtype=torch.int32)
+    b = resident.to_npu(w.t().contiguous(), static=True, device=dev)
+    for _ in range(3):
+        npu_kernels.mm_i8(a, b, c)
+    ref = c.clone()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        npu_kernels.mm_i8(a, b, c)
+    us = (time.perf_counter() - t0) / reps * 1e6
+    if not torch.equal(c, ref):
+        raise RuntimeError("host-slot mm_i8 results differ between calls")
+    nbytes = M * K + 4 * M * N
+    return {"us": round(us, 1), "tops": round(workloads.gemm_ops(M, N, K) / (us * 1e-6) / 1e12, 1),
+            "pcie_bytes": nbytes, "pcie_gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "what": f"npu_kernels.mm_i8 on pinned host A [{M}, {K}] int8 and C [{M}, {N}] int32 "
+                    "(the reference's resident host slots), packed weight in HBM; synchronous calls, wall clock"}
+
+
 def layer_step(groups, ws=None):
     from w8a8 import ops
     for g in groups:
@@ -1006,6 +1038,8 @@ def main():
              "single_gemm_m512_int32": single_gemm(dev)}
     log(f"bench: single micro-batch GEMM: {extra['single_gemm_m512_int32']}")
     if not args.no_extra:
+        extra["mm_i8_host_slots_m512"] = host_slot_gemm(dev)
+        log(f"bench: mm_i8 on host slots: {extra['mm_i8_host_slots_m512']}")
         for Ms in (3658, 4096):
             ms, tops_ops, wbytes, shp, run = sweep(Ms, dev, reps=5)
             tops = tops_ops / (ms * 1e-3) / 1e12
