@@ -131,6 +131,51 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, const v16i& acc,
   }
 }
 
+// int32 store of a wave's WTM x WTN accumulator tiles (rows m0 + 32 i .., packed column tiles
+// t0 + j) through a 4 KiB LDS area private to the wave, so that every store instruction writes
+// eight whole 128-byte lines (8 rows x 32 columns) instead of 32 bytes of each of 32 rows.  Lane l
+// holds row l % 32 of a tile and its 16-byte column chunks 2g + l / 32 (g = 0..3); chunk c of row r
+// sits at chunk position c ^ (r / 2 % 8) of a 128-byte LDS row, which keeps both the writes (16
+// rows of one chunk per 16 lanes) and the reads (two whole rows per 16 lanes) free of bank
+// conflicts.  The wave's LDS operations run in the order it issues them, so the reads see the
+// writes and the next tile's writes follow this tile's reads without a barrier.
+template <int WTM, int WTN>
+__device__ __forceinline__ void store_i32_lines(const GemmParams& p, const v16i (&acc)[WTM][WTN], char* st, int m0,
+                                                int t0, int lane) {
+  const int lrow = lane & 31, half = lane >> 5;
+  const int rr = lane >> 3, c = lane & 7;
+#pragma unroll
+  for (int i = 0; i < WTM; ++i)
+#pragma unroll
+    for (int j = 0; j < WTN; ++j) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int cw = 2 * g + half;
+        *reinterpret_cast<v4i*>(st + lrow * 128 + 16 * (cw ^ ((lrow >> 1) & 7))) =
+            v4i{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+      }
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int r = 8 * k + rr;
+        const v4i v = *reinterpret_cast<const v4i*>(st + r * 128 + 16 * (c ^ ((r >> 1) & 7)));
+        const int m = m0 + 32 * i + r;
+        const int n = (t0 + j) * 32 + 4 * c;
+        if (m < p.M) {
+          int32_t* dst = p.c + int64_t(m) * p.ldc + n;
+          if (p.vec_store && n + 3 < p.N) {
+            *reinterpret_cast<v4i*>(dst) = v;
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (n + e < p.N) dst[e] = v[e];
+          }
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+}
+
 // Epilogue of gemm_kernel, from the accumulators staged in LDS.  `red` holds the KW waves'
 // partial tiles (KW = 1: the one tile) as row-major int32 [KW][BM][LDR].  Thread q of a row (TPR = BN/16 threads per row) adds the partials of 4
 // columns in each quarter of the tile, columns 4q + (BN/4)*st (st = 0..3), so in each step the
@@ -620,7 +665,14 @@ __global__ __launch_bounds__(NWN * 64, MINB) void gemm_dw_kernel(GemmParams p) {
     }
   }
 
-  if constexpr (EPI != EPI_I32) __syncthreads();  // s_scale is visible to every wave
+  if constexpr (EPI == EPI_I32) {
+    // every wave has read its last A fragments: the ring is free to stage the int32 tiles
+    static_assert(2 * SLOT >= NW * 4096, "the ring holds a staging tile per wave");
+    __syncthreads();
+    store_i32_lines<MT, WTN>(p, acc, lds + wave * 4096, m0, t0 + wave * WTN, lane);
+    return;
+  }
+  __syncthreads();  // s_scale is visible to every wave
   const int lrow = lane & 31;
   const int lcol = 4 * (lane >> 5);
 #pragma unroll
@@ -688,7 +740,9 @@ __global__ __launch_bounds__(256, MINB) void gemm_pipe_kernel(GemmParams p) {
   constexpr int SCALE_PER_THREAD = NSCALE ? (NSCALE + 255) / 256 : 1;
   constexpr int SLOT = F * 1024;
   constexpr int RING = NS * SLOT;
-  __shared__ __attribute__((aligned(1024))) char lds[RING + NSCALE * 4];
+  // int32 epilogue: one 32x32 tile per wave staged here, so each store writes whole 128-byte lines
+  constexpr int STAGE = EPI == EPI_I32 ? NW * 4096 : 0;
+  __shared__ __attribute__((aligned(1024))) char lds[RING + NSCALE * 4 + STAGE];
   float* const s_scale = reinterpret_cast<float*>(lds + RING);
 
   const int lane = threadIdx.x & 63;
@@ -910,21 +964,25 @@ __global__ __launch_bounds__(256, MINB) void gemm_pipe_kernel(GemmParams p) {
       }
       __syncthreads();
     }
+    if constexpr (EPI == EPI_I32) {
+      store_i32_lines<WTM, WTN>(p, acc, lds + RING + wave * 4096, m0 + wm * WTM * 32, t0 + wn * WTN, lane);
+    } else {
 #pragma unroll
-    for (int i = 0; i < WTM; ++i) {
-      const int ml = (wm * WTM + i) * 32 + lrow;
-      const int m = m0 + ml;
-      if (m >= p.M) continue;
-      const float sxm = EPI == EPI_I32 ? 0.0f : s_scale[ml];
-      const float* swt = s_scale + (EPI == EPI_I32 ? 0 : BM) + wn * WTN * 32 + lcol;
-      if constexpr (EPI == EPI_GELU) {
+      for (int i = 0; i < WTM; ++i) {
+        const int ml = (wm * WTM + i) * 32 + lrow;
+        const int m = m0 + ml;
+        if (m >= p.M) continue;
+        const float sxm = s_scale[ml];
+        const float* swt = s_scale + BM + wn * WTN * 32 + lcol;
+        if constexpr (EPI == EPI_GELU) {
 #pragma unroll
-        for (int j = 0; j < WTN; j += 2)
-          store_tile<EPI>(p, acc[i][j], &acc[i][j + 1], m, t0 + wn * WTN + j, lcol, sxm, swt + j * 32);
-      } else {
+          for (int j = 0; j < WTN; j += 2)
+            store_tile<EPI>(p, acc[i][j], &acc[i][j + 1], m, t0 + wn * WTN + j, lcol, sxm, swt + j * 32);
+        } else {
 #pragma unroll
-        for (int j = 0; j < WTN; ++j)
-          store_tile<EPI>(p, acc[i][j], nullptr, m, t0 + wn * WTN + j, lcol, sxm, swt + j * 32);
+          for (int j = 0; j < WTN; ++j)
+            store_tile<EPI>(p, acc[i][j], nullptr, m, t0 + wn * WTN + j, lcol, sxm, swt + j * 32);
+        }
       }
     }
     // The epilogue's loads and stores are behind the ring's DMAs in the count of loads in
