@@ -176,6 +176,88 @@ __device__ __forceinline__ void store_i32_lines(const GemmParams& p, const v16i 
     }
 }
 
+// bf16 epilogue values of one 32x32 output tile, as lane l's row l % 32 and columns 8g + 4(l / 32)
+// .. +3 (g = 0..3), packed two per dword: `bf16((acc sx) sw)` (EPI_BF16 and, before its residual,
+// EPI_RESID) or `bf16(bf16(gelu_tanh(gate)) up)` from the gate tile `acc` and the up tile `acc_up`
+// (EPI_GELU).  The same operations, in the same order, as store_tile.
+template <int EPI>
+__device__ __forceinline__ void tile_bf16(const v16i& acc, const v16i* acc_up, float sxm, const float* swt, v2u (&y)[4]) {
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    float o[4];
+    if constexpr (EPI == EPI_GELU) {
+      const v4f swg = *reinterpret_cast<const v4f*>(swt + 8 * g);
+      const v4f swu = *reinterpret_cast<const v4f*>(swt + 32 + 8 * g);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float gate = bf16_to_f32(f32_to_bf16((float(acc[4 * g + r]) * sxm) * swg[r]));
+        const float up = bf16_to_f32(f32_to_bf16((float((*acc_up)[4 * g + r]) * sxm) * swu[r]));
+        const float ge = bf16_to_f32(f32_to_bf16(gelu_tanh_f32(gate)));
+        o[r] = ge * up;
+      }
+    } else {
+      const v4f sw = *reinterpret_cast<const v4f*>(swt + 8 * g);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[r] = (float(acc[4 * g + r]) * sxm) * sw[r];
+    }
+    y[g] = v2u{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+  }
+}
+
+// Store of one 32x32 bf16 output tile (rows m0 .., columns n0 .., n < ncols) through a 2 KiB LDS
+// area private to the wave, so that each store instruction writes 16 rows x 64 contiguous bytes
+// instead of 16 bytes of each of 32 rows.  y is tile_bf16's lane layout; the 16-byte column chunk c
+// of row r sits at chunk position c ^ (r / 4 % 4).  EPI_RESID adds the residual after the
+// exchange, each lane reading the residual elements it then writes (the residual may alias the
+// output).  The wave's LDS operations run in the order it issues them.
+template <int EPI>
+__device__ __forceinline__ void store_bf16_lines(const GemmParams& p, const v2u (&y)[4], char* st, int m0, int n0,
+                                                 int ncols, int lane) {
+  const int lrow = lane & 31, half = lane >> 5;
+#pragma unroll
+  for (int g = 0; g < 4; ++g)
+    *reinterpret_cast<v2u*>(st + lrow * 64 + 16 * (g ^ ((lrow >> 2) & 3)) + 8 * half) = y[g];
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int r = 16 * k + (lane >> 2), c = lane & 3;
+    v4u v = *reinterpret_cast<const v4u*>(st + r * 64 + 16 * (c ^ ((r >> 2) & 3)));
+    const int m = m0 + r, n = n0 + 8 * c;
+    if (m >= p.M) continue;
+    uint16_t* dst = p.out + int64_t(m) * p.ldo + n;
+    const bool whole = n + 7 < ncols;
+    if constexpr (EPI == EPI_RESID) {
+      const uint16_t* rs = p.res + int64_t(m) * p.ldr + n;
+      uint16_t rv[8];
+      if (whole && (reinterpret_cast<uintptr_t>(rs) & 15) == 0) {
+        const v4u t = *reinterpret_cast<const v4u*>(rs);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          rv[2 * e] = uint16_t(t[e]);
+          rv[2 * e + 1] = uint16_t(t[e] >> 16);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) rv[e] = n + e < ncols ? rs[e] : uint16_t(0);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float lo = bf16_to_f32(uint16_t(v[e])) + bf16_to_f32(rv[2 * e]);
+        const float hi = bf16_to_f32(uint16_t(v[e] >> 16)) + bf16_to_f32(rv[2 * e + 1]);
+        v[e] = pack_bf16x2(lo, hi);
+      }
+    }
+    if (whole && (reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
+      *reinterpret_cast<v4u*>(dst) = v;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (n + e < ncols) dst[e] = uint16_t(v[e >> 1] >> (16 * (e & 1)));
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+}
+
 // Epilogue of gemm_kernel, from the accumulators staged in LDS.  `red` holds the KW waves'
 // partial tiles (KW = 1: the one tile) as row-major int32 [KW][BM][LDR].  Thread q of a row (TPR = BN/16 threads per row) adds the partials of 4
 // columns in each quarter of the tile, columns 4q + (BN/4)*st (st = 0..3), so in each step the
@@ -672,24 +754,30 @@ __global__ __launch_bounds__(NWN * 64, MINB) void gemm_dw_kernel(GemmParams p) {
     store_i32_lines<MT, WTN>(p, acc, lds + wave * 4096, m0, t0 + wave * WTN, lane);
     return;
   }
-  __syncthreads();  // s_scale is visible to every wave
+  // s_scale is visible to every wave, and every wave has read its last A fragments: the ring is
+  // free to stage the output tiles
+  static_assert(2 * SLOT >= NW * 2048, "the ring holds a staging tile per wave");
+  __syncthreads();
+  char* const st = lds + wave * 2048;
   const int lrow = lane & 31;
   const int lcol = 4 * (lane >> 5);
 #pragma unroll
   for (int i = 0; i < MT; ++i) {
-    const int ml = i * 32 + lrow;
-    const int m = m0 + ml;
-    if (m >= p.M) continue;
-    const float sxm = EPI == EPI_I32 ? 0.0f : s_scale[ml];
-    const float* swt = s_scale + (EPI == EPI_I32 ? 0 : BM) + wave * WTN * 32 + lcol;
+    const float sxm = s_scale[i * 32 + lrow];
+    const float* swt = s_scale + BM + wave * WTN * 32 + lcol;
+    v2u y[4];
     if constexpr (EPI == EPI_GELU) {
 #pragma unroll
-      for (int j = 0; j < WTN; j += 2)
-        store_tile<EPI>(p, acc[i][j], &acc[i][j + 1], m, t0 + wave * WTN + j, lcol, sxm, swt + j * 32);
+      for (int j = 0; j < WTN; j += 2) {
+        tile_bf16<EPI>(acc[i][j], &acc[i][j + 1], sxm, swt + j * 32, y);
+        store_bf16_lines<EPI>(p, y, st, m0 + i * 32, ((t0 + wave * WTN + j) >> 1) * 32, p.I, lane);
+      }
     } else {
 #pragma unroll
-      for (int j = 0; j < WTN; ++j)
-        store_tile<EPI>(p, acc[i][j], nullptr, m, t0 + wave * WTN + j, lcol, sxm, swt + j * 32);
+      for (int j = 0; j < WTN; ++j) {
+        tile_bf16<EPI>(acc[i][j], nullptr, sxm, swt + j * 32, y);
+        store_bf16_lines<EPI>(p, y, st, m0 + i * 32, (t0 + wave * WTN + j) * 32, p.N, lane);
+      }
     }
   }
 }
