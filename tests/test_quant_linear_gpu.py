@@ -100,6 +100,23 @@ def test_quant_nan_and_inf_rows_follow_torch(K):
         assert np.array_equal(qk.cpu().numpy()[1:], qk_ref[1:]) and not qk_ref[1:4].any()
 
 
+@pytest.mark.parametrize("M,K", [(2048, 1536), (2049, 2048), (3658, 6144), (2056, 12288)])
+def test_quant_rows_packed_long_m(M, K):
+    """Packed quant at the whole-prompt row counts (the GEMM operand of every long-M linear):
+    codes and scales bit-exact against the oracle, NaN / Inf / zero rows among them, row counts
+    that are not multiples of 8 or 32, padding rows and columns zero."""
+    x = workloads.activations(M, K, seed=M + K, row_spread=True)
+    x[:6] = _nan_inf_rows(K)
+    q_ref, s_ref = orc.quant_rows(to_bits(x), "bf16")
+    from test_gemm_gpu import unpack_act
+    pa, s = ops.quant_rows_packed(x.to(DEV))
+    _assert_scales(s[:6], s_ref[:6])
+    assert np.array_equal(s.cpu().numpy()[6:], s_ref[6:])
+    full = unpack_act(pa.data.cpu().numpy(), M, K)
+    assert np.array_equal(full[:M, :K], q_ref)
+    assert not full[M:].any() and not full[:, K:].any(), "padding must be zero"
+
+
 def test_quant_rows_f32_weights():
     """Per-output-channel weight quant (gemma_npu.py:68-69) is the same kernel on fp32 rows."""
     g = torch.Generator().manual_seed(9)
