@@ -152,6 +152,52 @@ def test_gemm_gelu_epilogue(cfg):
     assert (got == ref).mean() > 0.99
 
 
+def _view(rows, cols, dtype, fill):
+    """A [rows, cols] view with an odd row stride and an offset of one element into its buffer (no
+    vector store fits its rows), and the buffer with the elements outside the view."""
+    big = torch.full((rows + 1, cols + 3), fill, dtype=dtype, device=DEV)
+    outside = torch.ones(big.shape, dtype=torch.bool)
+    outside[1:, 1:cols + 1] = False
+    return big[1:, 1:cols + 1], big, outside
+
+
+@pytest.mark.parametrize("cfg", CONFIGS)
+def test_gemm_outputs_in_unaligned_strided_views(cfg):
+    """Every configuration's stores into outputs whose rows allow no vector store (odd row stride,
+    one element of offset), with ragged N: int32, dequant, residual (also aliasing the output) and
+    GELU results exact as above, and nothing written outside the view."""
+    M, K, N, I = 77, 192, 100, 96
+    x, w, sw, q, sx = _inputs(M, K, N, 51)
+    qd, sxd, pw = torch.from_numpy(q).to(DEV), torch.from_numpy(sx).to(DEV), packed_from_nk(w)
+    acc = orc.int_mm_nk(q, w.numpy())
+    c, big, outside = _view(M, N, torch.int32, -7)
+    ops.gemm_i32(qd, pw, c, tile_cfg=cfg)
+    assert np.array_equal(c.cpu().numpy(), acc) and (big.cpu()[outside] == -7).all()
+    y = orc.dequant(acc, sx, sw.numpy())
+    out, big, outside = _view(M, N, torch.bfloat16, 3.0)
+    ops.gemm_bf16(qd, sxd, pw, sw.to(DEV), out=out, tile_cfg=cfg)
+    assert np.array_equal(to_bits(out), y) and (big.cpu()[outside] == 3.0).all()
+    res = workloads.activations(M, N, 52, outliers=False)
+    ref = orc.add_residual(y, to_bits(res))
+    out, big, outside = _view(M, N, torch.bfloat16, 3.0)
+    rv, _, _ = _view(M, N, torch.bfloat16, 0.0)
+    rv.copy_(res.to(DEV))
+    ops.gemm_bf16(qd, sxd, pw, sw.to(DEV), epilogue="residual", residual=rv, out=out, tile_cfg=cfg)
+    assert np.array_equal(to_bits(out), ref) and (big.cpu()[outside] == 3.0).all()
+    out.copy_(res.to(DEV))  # the residual aliasing the output
+    ops.gemm_bf16(qd, sxd, pw, sw.to(DEV), epilogue="residual", residual=out, out=out, tile_cfg=cfg)
+    assert np.array_equal(to_bits(out), ref)
+    wg, swg = workloads.weights(2 * I, K, 53)
+    yg = orc.dequant(orc.int_mm_nk(q, wg.numpy()), sx, swg.numpy())
+    refg = orc.gelu_mul(yg)
+    out, big, outside = _view(M, I, torch.bfloat16, 3.0)
+    ops.gemm_bf16(qd, sxd, packed_from_nk(wg, interleave=I), swg.to(DEV), epilogue="gelu", out=out,
+                  tile_cfg=cfg)
+    got = to_bits(out)
+    assert_bf16_close(f32(got), f32(refg), what="gelu epilogue, strided output")
+    assert (got == refg).mean() > 0.99 and (big.cpu()[outside] == 3.0).all()
+
+
 def test_gemm_gelu_ragged_tiles():
     """I not a multiple of the 128/256-column block: gate/up tiles straddle the block edge."""
     M, K, I = 70, 128, 96
