@@ -970,9 +970,12 @@ __global__ __launch_bounds__(512) void attn_merge_kernel(AttnParams p) {
   static_assert(!FWD2 || (ATTN_FWD2_NW * 64 == NT && S2::NDW * 8 == NSLOT), "head_dim 512 layout");
   static_assert(FWD2 || ATTN_NW * 64 == NT, "attn_fwd_kernel layout");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, qi = lane & 15, qq = lane >> 4;
-  const int slot = int(blockIdx.x) % NSLOT;
-  const int st = (int(blockIdx.x) / NSLOT) % p.nsplit_tiles;
-  const int g = int(blockIdx.x) / (NSLOT * p.nsplit_tiles);
+  // The NSLOT workgroups of a split tile each write a few columns of every row of the tile: dealt
+  // to one XCD (consecutive logical workgroups), so each output line is assembled in one L2.
+  const int lb = attn_xcd_remap(int(blockIdx.x), int(gridDim.x));
+  const int slot = lb % NSLOT;
+  const int st = (lb / NSLOT) % p.nsplit_tiles;
+  const int g = lb / (NSLOT * p.nsplit_tiles);
   // split tile st is tile ntiles - 1 - st; its parts are consecutive items of its segment
   const int tile = p.ntiles - 1 - st;
   int s = 0;
