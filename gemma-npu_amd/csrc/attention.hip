@@ -96,6 +96,10 @@ struct AttnParams {
   // 0: the last part of a split tile to arrive merges the parts; 1: the parts are only parked and
   // attn_merge_kernel, launched next on the stream, merges every split tile.
   int merge_mode;
+  // Quantised output (k_attn_out fused, one KV group): instead of o, the per-token int8 rows of the
+  // [Tq, H*D] output in the packed activation layout (qKF fragments per row, rows zero up to qMp) and
+  // their scales.  Null: o is written.
+  int8_t* qpk; float* qsx; int qKF, qMp;
   // Launch order of the items: workgroup j * KV + g runs item order[j] of group g (item j when
   // `ordered` is 0).  Last, after every pointer and scalar.
   int ordered;
@@ -112,6 +116,23 @@ __device__ __forceinline__ void attn_dma16(__amdgpu_buffer_rsrc_t r, void* lds, 
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
 }
 
+// Key `key` is visible to the query at `pos`: key <= pos, pos - key < the window (wlim = window, or
+// 2^31 for no window) and key < Tk -- one unsigned compare per bound, combined bitwise, so the mask
+// compiles to compares and selects.  A short-circuit chain (key <= pos && ... && (win == 0 || ...))
+// was compiled here to divergent branches, and in one register assignment of attn_fwd_kernel the
+// -inf store of a masked key was hoisted above the branch that then reused its register, leaving
+// keys outside the window unmasked.
+__device__ __forceinline__ bool attn_key_visible(int key, int pos, int Tk, uint32_t wlim) {
+  return (uint32_t(pos - key) < wlim) & (key < Tk);
+}
+__device__ __forceinline__ uint32_t attn_window_limit(int window) {
+  return window > 0 ? uint32_t(window) : 0x80000000u;
+}
+// s where `vis`, else -inf, as a select of the bit patterns
+__device__ __forceinline__ float attn_mask(float s, bool vis) {
+  return __uint_as_float(vis ? __float_as_uint(s) : 0xff800000u);
+}
+
 __device__ __forceinline__ int attn_xcd_remap(int b, int nblocks) {
   const int full = nblocks & ~7;
   if (b >= full) return b;
@@ -119,6 +140,60 @@ __device__ __forceinline__ int attn_xcd_remap(int b, int nblocks) {
   return (b & 7) * per + (b >> 3);
 }
 
+
+// k_attn_out (pipeline.py:88-92) on a tile's normalised bf16 output rows staged in LDS (row r =
+// head r % G of position r / G, orow bytes apart): token t = i0 + r / G is the row [head 0 | head 1 |
+// ...] of G * D values, quantised per token as _quant does and written to the packed activation
+// layout with its scale.  4G consecutive threads (one wave or half of one) take a token: the absmax
+// of their 16-element chunks, xor shuffles over those lanes, then the codes, 16 bytes per store.  The
+// workgroup of the last tile also zero-fills the packed rows from Tq up to the padded row count.
+template <int D, int NT>
+__device__ __forceinline__ void attn_quant_tokens(const AttnParams& p, const char* st, int orow, int i0, int tile,
+                                                  int tid) {
+  const int G = p.G, TPT = NT / p.PB;
+  const int NCH = G * D / 16;
+  const int pl = tid / TPT, j = tid % TPT, t = i0 + pl;
+  const bool live = pl < p.PB && t < p.Tq;
+  auto chunk = [&](int c, v4u& a, v4u& b) __attribute__((always_inline)) {
+    const char* src = st + (pl * G + (16 * c) / D) * orow + ((16 * c) % D) * 2;
+    a = *reinterpret_cast<const v4u*>(src);
+    b = *reinterpret_cast<const v4u*>(src + 16);
+  };
+  float amax = 0.0f;
+  if (live)
+    for (int c = j; c < NCH; c += TPT) {
+      v4u a, b;
+      chunk(c, a, b);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        amax = absmax2(amax, absmax2(fabsf(__uint_as_float(a[e] << 16)), fabsf(__uint_as_float(a[e] & 0xffff0000u))));
+        amax = absmax2(amax, absmax2(fabsf(__uint_as_float(b[e] << 16)), fabsf(__uint_as_float(b[e] & 0xffff0000u))));
+      }
+    }
+  for (int o = 1; o < TPT; o <<= 1) amax = absmax2(amax, __shfl_xor(amax, o, 64));
+  const float s = quant_scale(amax);
+  const float rs = 1.0f / s;
+  if (live) {
+    if (j == 0) p.qsx[t] = s;
+    for (int c = j; c < NCH; c += TPT) {
+      v4u h[2];
+      chunk(c, h[0], h[1]);
+      uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t lo = uint8_t(quant1_bf16(__uint_as_float(h[hh][e] << 16), s, rs));
+          const uint32_t hi = uint8_t(quant1_bf16(__uint_as_float(h[hh][e] & 0xffff0000u), s, rs));
+          w[2 * hh + (e >> 1)] |= (lo | (hi << 8)) << (16 * (e & 1));
+        }
+      *reinterpret_cast<v4u*>(p.qpk + packed_act_offset(t, 16 * c, p.qKF)) = v4u{w[0], w[1], w[2], w[3]};
+    }
+  }
+  if (tile == p.ntiles - 1)
+    for (int x = tid; x < (p.qMp - p.Tq) * NCH; x += NT)
+      *reinterpret_cast<v4u*>(p.qpk + packed_act_offset(p.Tq + x / NCH, 16 * (x % NCH), p.qKF)) = v4u{0u, 0u, 0u, 0u};
+}
 
 template <int D, int BN, int NW>
 __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(AttnParams p) {
@@ -265,6 +340,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(AttnParams p) {
   float l = 0.0f;  // this lane group's share of sum exp2(s * c - ms)
   const float c = p.c;
   const int win = p.window;
+  const uint32_t wlim = attn_window_limit(win);
   const int Tk = p.Tk;
 
   // the first block's K and V loads go out before the Q loads, so their latencies overlap
@@ -318,8 +394,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(AttnParams p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int key = kb + 32 * (t >> 1) + 8 * qq + 4 * (t & 1) + i;
-          const bool vis = valid && key <= pos && key < Tk && (win == 0 || pos - key < win);
-          if (!vis) s[t][i] = -__builtin_inff();
+          s[t][i] = attn_mask(s[t][i], valid & attn_key_visible(key, pos, Tk, wlim));
         }
     }
     float bm = -__builtin_inff();
@@ -367,12 +442,19 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(AttnParams p) {
     return lanes4_sum(x);
   };
   uint16_t* const op = p.o + int64_t(h) * p.ohs + int64_t(qrow) * p.ors + 4 * qq;
+  // quantised output: the bf16 rows are staged in LDS (past the arrival word) for attn_quant_tokens
+  constexpr int QROW = D * 2 + 16;
+  static_assert(1024 + NW * 16 * QROW <= V_OFF + 2 * V_SLOT, "staged rows fit the LDS");
+  char* const qst = lds + 1024;
   auto store_o = [&](int dt, v4f x, float inv) {
     if (!valid) return;
     v2u w;
     w[0] = pack_bf16x2(x[0] * inv, x[1] * inv);
     w[1] = pack_bf16x2(x[2] * inv, x[3] * inv);
-    *reinterpret_cast<v2u*>(op + 16 * dt) = w;
+    if (p.qpk)
+      *reinterpret_cast<v2u*>(qst + r * QROW + (16 * dt + 4 * qq) * 2) = w;
+    else
+      *reinterpret_cast<v2u*>(op + 16 * dt) = w;
   };
   auto store_lse = [&](float m, float lt) {
     if (valid && p.lse && qq == 0)
@@ -474,15 +556,24 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_kernel(AttnParams p) {
       merge(std::integral_constant<int, 8>{});
     else
       merge(std::integral_constant<int, 16>{});
+    if (p.qpk) {
+      __syncthreads();
+      attn_quant_tokens<D, NT>(p, qst, QROW, i0, tile, tid);
+    }
     return;
   }
 
   // ---- normalise and store --------------------------------------------------------------------
   const float lt = row_sum(l);
   const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+  if (p.qpk) __syncthreads();  // every wave is done with the K / V slots the rows are staged over
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) store_o(dt, o[dt], inv);
   store_lse(ms, lt);
+  if (p.qpk) {
+    __syncthreads();
+    attn_quant_tokens<D, NT>(p, qst, QROW, i0, tile, tid);
+  }
 }
 
 // ---- prefill, head_dim split over the waves for P V -------------------------------------------
@@ -656,6 +747,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd2_kernel(AttnParams p) {
   }
   const float c = p.c;
   const int win = p.window;
+  const uint32_t wlim = attn_window_limit(win);
   const int Tk = p.Tk;
 
   // S^T of block n (K slot n % 2), softmax, P rows and rescale factors into slot n % 2
@@ -695,8 +787,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd2_kernel(AttnParams p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int key = kb + 32 * (t >> 1) + 8 * qq + 4 * (t & 1) + i;
-          const bool vis = valid[j] && key <= pos[j] && key < Tk && (win == 0 || pos[j] - key < win);
-          s[j][t][i] = vis ? s[j][t][i] : -__builtin_inff();
+          s[j][t][i] = attn_mask(s[j][t][i], valid[j] & attn_key_visible(key, pos[j], Tk, wlim));
           bm = fmaxf(bm, s[j][t][i]);
         }
       bm = lanes4_max(bm);
@@ -809,13 +900,20 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd2_kernel(AttnParams p) {
     const int hl = r % G, pr = r / G;
     return out + int64_t(g * G + hl) * ohs + int64_t(i0 + pr) * ors;
   };
+  // quantised output: the bf16 rows are staged in LDS past the merge weights and below the row
+  // factors, for attn_quant_tokens
+  constexpr int QOFF = 16 * 1024, QROW = D * 2;
+  static_assert(QOFF + 128 * QROW <= S::A_OFF && ATTN_MAX_SEG * 128 * 4 + 1024 <= QOFF, "staged rows fit");
   auto store_slot = [&](int dt, int rt, v4f x, float inv) __attribute__((always_inline)) {
     const int r = rt * 16 + qi;
     if (!row_valid(r)) return;
     v2u w;
     w[0] = pack_bf16x2(x[0] * inv, x[1] * inv);
     w[1] = pack_bf16x2(x[2] * inv, x[3] * inv);
-    *reinterpret_cast<v2u*>(out_row(r) + d_lane + 16 * dt) = w;
+    if (p.qpk)
+      *reinterpret_cast<v2u*>(lds + QOFF + r * QROW + (d_lane + 16 * dt) * 2) = w;
+    else
+      *reinterpret_cast<v2u*>(out_row(r) + d_lane + 16 * dt) = w;
   };
   auto store_lse = [&](int r, float m, float lt) __attribute__((always_inline)) {
     if (row_valid(r) && lse)
@@ -928,6 +1026,10 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd2_kernel(AttnParams p) {
       merge(std::integral_constant<int, 8>{});
     else
       merge(std::integral_constant<int, 16>{});
+    if (p.qpk) {
+      __syncthreads();
+      attn_quant_tokens<D, NT>(p, lds + QOFF, QROW, i0, tile, tid);
+    }
     return;
   }
 
@@ -944,6 +1046,10 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd2_kernel(AttnParams p) {
   for (int dt = 0; dt < NDW; ++dt)
 #pragma unroll
     for (int rt = 0; rt < 8; ++rt) store_slot(dt, rt, o[dt][rt], inv_s[rt * 16 + qi]);
+  if (p.qpk) {
+    __syncthreads();
+    attn_quant_tokens<D, NT>(p, lds + QOFF, QROW, i0, tile, tid);
+  }
 }
 
 // ---- merge of parked parts (merge_mode 1) ------------------------------------------------------
@@ -1147,7 +1253,7 @@ __global__ __launch_bounds__(256, 2) void attn_decode_split_kernel(DecodeParams 
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int key = kc + 16 * wave + 4 * qq + i;
-    sc[i] = (has_tile && key <= p.pos && key < p.Tk) ? s0[i] + s1[i] : -__builtin_inff();
+    sc[i] = attn_mask(s0[i] + s1[i], has_tile & attn_key_visible(key, p.pos, p.Tk, 0x80000000u));
     bm = fmaxf(bm, sc[i]);
   }
   bm = lanes4_max(bm);
@@ -1575,7 +1681,7 @@ static int attention_launch(const uint16_t* q, int64_t q_head_stride, int64_t q_
                             int64_t v_row_stride, int64_t H, int64_t KV, int64_t Tq, int64_t Tk, int64_t D,
                             int64_t q_start, int64_t window, float scale, uint16_t* o, int64_t o_head_stride,
                             int64_t o_row_stride, float* lse, void* workspace, int64_t workspace_bytes,
-                            hipStream_t stream) {
+                            hipStream_t stream, int8_t* qpk = nullptr, float* qsx = nullptr) {
   if (H < 1 || KV < 1 || H % KV != 0 || H / KV > 128)
     return fail(W8A8_EINVAL, "attention: H=%lld KV=%lld (H must be a multiple of KV, at most 128 heads per KV head)",
                 (long long)H, (long long)KV);
@@ -1586,7 +1692,7 @@ static int attention_launch(const uint16_t* q, int64_t q_head_stride, int64_t q_
                 (long long)Tq, (long long)q_start, (long long)Tk, (long long)window);
   if (!(scale > 0.0f) || scale == __builtin_inff()) return fail(W8A8_EINVAL, "attention: scale must be positive");
   if (Tq == 0) return W8A8_OK;
-  if (!q || !k || !v || !o) return fail(W8A8_EINVAL, "attention: null pointer");
+  if (!q || !k || !v || (!o && !qpk) || (qpk && !qsx)) return fail(W8A8_EINVAL, "attention: null pointer");
   if (q_row_stride < D || k_row_stride < D || v_row_stride < D || o_row_stride < 1 || o_head_stride < 1)
     return fail(W8A8_EINVAL, "attention: row strides smaller than head_dim");
   const int64_t strides[8] = {q_head_stride, q_row_stride, k_head_stride, k_row_stride,
@@ -1637,6 +1743,13 @@ static int attention_launch(const uint16_t* q, int64_t q_head_stride, int64_t q_
   p.ordered = pl.order.empty() ? 0 : 1;
   for (size_t i = 0; i < pl.order.size(); ++i) p.order[i] = pl.order[i];
   p.scale = scale; p.c = scale * 1.4426950408889634f;
+  p.qpk = qpk;
+  p.qsx = qsx;
+  p.qKF = int(2 * ((H * D + 63) / 64));
+  p.qMp = int((Tq + 31) / 32 * 32);
+  if (qpk && p.nsplit_tiles > 0 && p.merge_mode == 1)
+    return fail(W8A8_ENOTSUP, "attention_quant: this call merges its key parts in a second kernel, which does not "
+                              "hold whole token rows");
   const int64_t nwg = KV * int64_t(p.per_group);
   if (nwg > INT32_MAX) return fail(W8A8_ENOTSUP, "attention: too many query tiles");
   const dim3 grid{unsigned(nwg), 1, 1};
@@ -1679,6 +1792,40 @@ extern "C" int w8a8_attention_ws_bf16(const uint16_t* q, int64_t q_head_stride, 
   return attention_launch(q, q_head_stride, q_row_stride, k, k_head_stride, k_row_stride, v, v_head_stride,
                           v_row_stride, H, KV, Tq, Tk, D, q_start, window, scale, o, o_head_stride, o_row_stride, lse,
                           workspace, workspace_bytes, stream);
+}
+
+// The attention output quantised per token in the same launch (k_attn_out, pipeline.py:88-92): one
+// KV group (every head of a token in one workgroup), at most 16 heads, a power of two; and a plan
+// that merges split key parts in the kernel.
+static bool attention_quant_fits(int64_t H, int64_t KV, int64_t Tq, int64_t Tk, int64_t D, int64_t q_start,
+                                 int64_t window) {
+  if (KV != 1 || H < 1 || H > 16 || (H & (H - 1)) != 0) return false;
+  if (w8a8_attention_workspace_bytes(H, KV, Tq, Tk, D, q_start, window) < 0) return false;
+  const AttnPlan pl = attn_plan(H, KV, Tq, Tk, D, q_start, window);
+  return !(pl.nsplit_tiles > 0 && pl.merge_mode == 1);
+}
+
+extern "C" int w8a8_attention_quant_supported(int64_t H, int64_t KV, int64_t Tq, int64_t Tk, int64_t D,
+                                              int64_t q_start, int64_t window) {
+  return attention_quant_fits(H, KV, Tq, Tk, D, q_start, window) ? 1 : 0;
+}
+
+extern "C" int w8a8_attention_quant_bf16(const uint16_t* q, int64_t q_head_stride, int64_t q_row_stride,
+                                         const uint16_t* k, int64_t k_head_stride, int64_t k_row_stride,
+                                         const uint16_t* v, int64_t v_head_stride, int64_t v_row_stride, int64_t H,
+                                         int64_t KV, int64_t Tq, int64_t Tk, int64_t D, int64_t q_start,
+                                         int64_t window, float scale, int8_t* packed, float* sx, void* workspace,
+                                         int64_t workspace_bytes, hipStream_t stream) {
+  if (Tq > 0 && !attention_quant_fits(H, KV, Tq, Tk, D, q_start, window))
+    return fail(W8A8_ENOTSUP, "attention_quant: H=%lld KV=%lld Tq=%lld q_start=%lld window=%lld: needs one KV group of "
+                              "at most 16 heads (a power of two) and a plan without a separate merge",
+                (long long)H, (long long)KV, (long long)Tq, (long long)q_start, (long long)window);
+  if ((uintptr_t)packed % 16) return fail(W8A8_EALIGN, "attention_quant: the packed rows must be 16-byte aligned");
+  if ((Tq + 31) / 32 * 2 * ((H * D + 63) / 64) * 1024 > INT32_MAX)
+    return fail(W8A8_ENOTSUP, "attention_quant: packed output above 2 GiB");
+  return attention_launch(q, q_head_stride, q_row_stride, k, k_head_stride, k_row_stride, v, v_head_stride,
+                          v_row_stride, H, KV, Tq, Tk, D, q_start, window, scale, nullptr, 8, 8, nullptr, workspace,
+                          workspace_bytes, stream, packed, sx);
 }
 
 static void decode_geometry(int64_t D, int64_t q_pos, int64_t window, int& klo, int& nchunk) {

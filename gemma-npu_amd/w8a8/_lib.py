@@ -72,6 +72,9 @@ SIGNATURES = {
     "w8a8_attention_plan_items": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p]),
     "w8a8_attention_ws_bf16": (_i32, [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                       _i64, _i64, _f32, _p, _i64, _i64, _p, _p, _i64, _p]),
+    "w8a8_attention_quant_supported": (_i32, [_i64, _i64, _i64, _i64, _i64, _i64, _i64]),
+    "w8a8_attention_quant_bf16": (_i32, [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64,
+                                         _i64, _i64, _i64, _f32, _p, _p, _p, _i64, _p]),
     "w8a8_attention_decode_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64]),
     "w8a8_attention_decode_bf16": (_i32, [_p, _i64, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                           _i64, _f32, _p, _i64, _p, _p, _i64, _p]),

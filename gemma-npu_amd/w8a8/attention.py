@@ -112,6 +112,39 @@ def attention(q, k, v, q_start=0, window=0, scale=1.0, out=None, return_lse=Fals
     return (out, lse) if return_lse else out
 
 
+def attention_quant(q, k, v, q_start=0, window=0, scale=1.0):
+    """attention(q, k, v, q_start, window, scale) followed by k_attn_out (pipeline.py:88-92): the
+    output's per-token int8 rows [Tq, H*D] in the GEMM's packed activation layout, and their fp32
+    scales -> (PackedActivation, sx).  With one KV group of at most 16 heads (E2B: 8 heads on one)
+    the quantisation runs in the attention launch itself and the bf16 output is never written; other
+    calls (more KV groups, or a plan that merges key parts in a second kernel) run the two steps.
+    Bit-identical either way."""
+    from .fused import k_attn_out
+    from .ops import PackedActivation, packed_act_bytes
+    _check3(q, "q")
+    _check3(k, "k")
+    _check3(v, "v")
+    H, Tq, D = q.shape
+    KV, Tk, Dk = k.shape
+    if tuple(v.shape) != (KV, Tk, Dk) or Dk != D:
+        raise ValueError(f"q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)} do not match")
+    if len({q.device, k.device, v.device}) != 1:
+        raise ValueError("q, k and v must be on one device")
+    if Tq == 0 or not lib().w8a8_attention_quant_supported(H, KV, Tq, Tk, D, int(q_start), int(window)):
+        return k_attn_out(attention(q, k, v, q_start, window, scale), packed=True)
+    packed = torch.empty(packed_act_bytes(Tq, H * D), dtype=torch.int8, device=q.device)
+    sx = torch.empty((Tq,), dtype=torch.float32, device=q.device)
+    qhs, qrs = _strides(q)
+    khs, krs = _strides(k)
+    vhs, vrs = _strides(v)
+    need = lib().w8a8_attention_workspace_bytes(H, KV, Tq, Tk, D, int(q_start), int(window))
+    ws = _split_workspace(q.device, need) if need > 0 else None
+    call("w8a8_attention_quant_bf16", q.data_ptr(), qhs, qrs, k.data_ptr(), khs, krs, v.data_ptr(), vhs, vrs, H, KV,
+         Tq, Tk, D, int(q_start), int(window), float(scale), packed.data_ptr(), sx.data_ptr(),
+         None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), _stream(q))
+    return PackedActivation(packed, Tq, H * D), sx
+
+
 def full_attention(q, k_all, v_all, q_start):
     """q [H, Tq, D] at positions q_start.. ; k/v [KV, q_start + Tq, D] -> [H, Tq, D] (causal, scale 1)."""
     return attention(q, k_all, v_all, q_start, 0, 1.0)

@@ -186,9 +186,8 @@ class Prefill:
         if not p.shares_kv:
             store.write(p.index, start, k, v)
         keys, values = store.visible(p.kv_source, end)
-        o = attention.attention(q, keys, values, start, p.window, 1.0)
-
-        xq, sx = fused.k_attn_out(o, packed=True)
+        # attention with k_attn_out in its epilogue (the two steps where that does not apply)
+        xq, sx = attention.attention_quant(q, keys, values, start, p.window, 1.0)
         acc = gemm(xq, sx, W["o"])
         h, xq, sx = fused.k_post_attn(acc, sx, W["o"].sw, h, p.norm_post_attn, p.norm_pre_ff, eps, packed=True)
         gu = W["gate_up"]

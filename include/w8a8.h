@@ -376,6 +376,25 @@ int w8a8_attention_ws_bf16(const uint16_t *q, int64_t q_head_stride, int64_t q_r
                            int64_t o_row_stride, float *lse, void *workspace, int64_t workspace_bytes,
                            hipStream_t stream);
 
+/* 1 when w8a8_attention_quant_bf16 runs these arguments in one launch (one KV group of at most 16
+ * query heads, a power of two, and a plan that merges split key parts in the attention kernel
+ * itself), else 0. */
+int w8a8_attention_quant_supported(int64_t H, int64_t KV, int64_t Tq, int64_t Tk, int64_t D, int64_t q_start,
+                                   int64_t window);
+
+/* Attention with k_attn_out (pipeline.py:88-92; attention as pipeline.py:140-180) in its epilogue:
+ * instead of o, the per-token int8 rows of the [Tq, H*D] output (row t = [head 0 | head 1 | ...] of
+ * position t) in the packed activation layout (w8a8_packed_act_bytes(Tq, H*D) bytes, 16-byte aligned,
+ * rows Tq.. of the padding written as zeros) and their fp32 scales sx [Tq], the same bits as
+ * w8a8_attention_ws_bf16 followed by w8a8_k_attn_out on its output.  The bf16 output is never
+ * written.  W8A8_ENOTSUP where w8a8_attention_quant_supported is 0; the workspace as
+ * w8a8_attention_ws_bf16's. */
+int w8a8_attention_quant_bf16(const uint16_t *q, int64_t q_head_stride, int64_t q_row_stride, const uint16_t *k,
+                              int64_t k_head_stride, int64_t k_row_stride, const uint16_t *v, int64_t v_head_stride,
+                              int64_t v_row_stride, int64_t H, int64_t KV, int64_t Tq, int64_t Tk, int64_t D,
+                              int64_t q_start, int64_t window, float scale, int8_t *packed, float *sx,
+                              void *workspace, int64_t workspace_bytes, hipStream_t stream);
+
 /* ---- decode attention ------------------------------------------------------------------- */
 
 /* Bytes of the workspace w8a8_attention_decode_bf16 needs: KV * ceil-chunks * (H/KV) * (D + 2) * 4,

@@ -228,6 +228,42 @@ def test_split_plan_past_the_order_table():
     assert np.allclose(lse[:, T - 40:].cpu().numpy(), lse_ref, rtol=1e-5, atol=1e-4)
 
 
+QUANT_CASES = [
+    # H, KV, Tq, Tk, D, q_start, window: attention + k_attn_out in one launch, or the two-step fallback
+    (8, 1, 700, 700, 256, 0, 128),     # sliding, whole prompt (one item per tile), ragged Tq
+    (8, 1, 1300, 1300, 256, 0, 0),     # causal, head_dim 256, long tiles split and merged in the kernel
+    (8, 1, 1300, 1300, 512, 0, 0),     # causal, head_dim 512 (attn_fwd2_kernel), split and merged in the kernel
+    (8, 1, 77, 600, 512, 523, 0),      # a few queries past earlier keys
+    (4, 1, 300, 300, 128, 0, 64),      # head_dim 128, 4 heads
+    (8, 2, 300, 300, 256, 0, 64),      # two KV groups: the two-step form
+    (8, 1, 512, 3658, 256, 3146, 512),  # the reference's last sliding micro-batch: parts merged by a second kernel
+]
+
+
+@pytest.mark.parametrize("H,KV,Tq,Tk,D,q_start,window", QUANT_CASES)
+def test_attention_quant_equals_attention_then_k_attn_out(H, KV, Tq, Tk, D, q_start, window):
+    """attention_quant (k_attn_out, pipeline.py:88-92, in the attention epilogue where it applies):
+    the packed int8 rows (padding included) and scales equal k_attn_out on attention's bf16 output, bit
+    for bit, whichever form runs; the one-launch form runs exactly where the library says it applies."""
+    import ctypes
+    from test_gemm_gpu import unpack_act
+    from w8a8 import fused, lib
+    q, k, v = make(H, KV, Tq, Tk, D, seed=H + Tq + D + window, qscale=0.3)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    fused_form = lib().w8a8_attention_quant_supported(H, KV, Tq, Tk, D, q_start, window)
+    mk = ctypes.c_int(-1)
+    lib().w8a8_attention_plan_items(H, KV, Tq, Tk, D, q_start, window, None, ctypes.byref(mk))
+    assert fused_form == (KV == 1 and mk.value == 0)
+    xq, sx = attn.attention_quant(qd, kd, vd, q_start, window, 1.0)
+    xr, sr = fused.k_attn_out(attn.attention(qd, kd, vd, q_start, window, 1.0), packed=True)
+    assert torch.equal(sx, sr)
+    got = unpack_act(xq.data.cpu().numpy(), Tq, H * D)
+    assert np.array_equal(got[:Tq], unpack_act(xr.data.cpu().numpy(), Tq, H * D)[:Tq])
+    assert not got[Tq:].any(), "padding rows must be zero"
+    xq2, sx2 = attn.attention_quant(qd, kd, vd, q_start, window, 1.0)
+    assert torch.equal(xq2.data, xq.data) and torch.equal(sx2, sx)
+
+
 def test_split_workspace_shared_across_shapes():
     """Split calls of different shapes share the stream's workspace.  A whole-prompt causal call at
     head_dim 512 (T = 3658: ~190 split tiles), then 256 queries at the end of the prompt (16 split
