@@ -199,6 +199,10 @@ static void gemv_launch(const GemvParams& p0, hipStream_t stream) {
       gemv_kernel<1, 4, PACKED, 4><<<unsigned((ntiles + gpb - 1) / gpb), 256, 0, stream>>>(p);
     } else if (split == 8) {
       gemv_kernel<1, 4, PACKED, 8><<<unsigned(ntiles), 512, 0, stream>>>(p);
+    } else if ((p.KB + 15) / 16 > 4 && (p.KB + 15) / 16 <= 6) {
+      // five or six k-blocks per wave (the down projection, K=6144): all of them in one round
+      // trip instead of two (M=1 cold token 837 -> 826 us)
+      gemv_kernel<1, 6, PACKED, 16><<<unsigned(ntiles), 1024, 0, stream>>>(p);
     } else {
       gemv_kernel<1, 4, PACKED, 16><<<unsigned(ntiles), 1024, 0, stream>>>(p);
     }
