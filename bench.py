@@ -627,6 +627,70 @@ def pipeline_prefill_bench(model, ids, hf_logits, reps=3):
     return res
 
 
+def native_decode_bench(model, ids, n):
+    """w8a8.pipeline.Decoder on the same model and prompt: n greedy steps eagerly and n replayed from
+    one HIP graph (one step per replay), each after the whole-prompt prefill; tokens per second from
+    the host clock around the steps (one synchronisation at the end).  Its greedy tokens are checked
+    against HF's own loop on the engine continuing from the same whole-prompt prefill's cache (the
+    first token is the prefill's argmax, then n steps)."""
+    import torch
+    from w8a8.pipeline import Decoder, Prefill
+    T = ids.shape[1]
+    logits, past = Prefill(model)(ids)
+    nxt = logits.argmax().view(1, 1)
+    hf_tokens = [nxt.view(1)]
+    for _ in range(n):
+        o = model(input_ids=nxt, past_key_values=past, use_cache=True, logits_to_keep=1)
+        past, nxt = o.past_key_values, o.logits[0, -1].argmax().view(1, 1)
+        hf_tokens.append(nxt.view(1))
+    hf_tokens = torch.cat(hf_tokens).tolist()
+    del past, o
+    # the same steps fed HF's tokens (teacher-forced): logits against HF's loop step by step
+    dec = Decoder(Prefill(model), max_len=T + n + 8)
+    dec.start(ids)
+    worst, agree = 0.0, 0
+    logits, past = Prefill(model)(ids)
+    nxt = logits.argmax().view(1, 1)
+    for _ in range(n):
+        o = model(input_ids=nxt, past_key_values=past, use_cache=True, logits_to_keep=1)
+        want = o.logits[0, -1].float()
+        dec.tok.copy_(nxt)
+        got = dec.step()
+        worst = max(worst, ((got - want).norm() / want.norm()).item())
+        agree += int(int(got.argmax()) == int(want.argmax()))
+        past, nxt = o.past_key_values, want.argmax().view(1, 1)
+    del dec, past, o
+    res = {"vs_hf_loop": {"max_rel_logits_diff": round(worst, 5), "argmax_agree": f"{agree}/{n}",
+                          "how": "each step fed HF's token; HF's loop on the same engine from the same prefill"}}
+    for name in ("eager", "graph"):
+        dec = Decoder(Prefill(model), max_len=T + n + 8)
+        dec.start(ids)
+        if name == "graph":
+            dec.capture()  # one real step, then the capture
+            steps = n - 1
+            run = dec.replay
+        else:
+            steps = n
+            run = dec.step
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        for _ in range(steps):
+            run()
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t
+        tokens = dec.emitted[:n + 1].tolist()
+        same = next((i for i, (x, y) in enumerate(zip(tokens, hf_tokens)) if x != y), len(tokens))
+        res[name] = {"tok_s": round(steps / dt, 1), "ms_per_token": round(dt / steps * 1e3, 3),
+                     "leading_tokens_equal_hf_loop": f"{same}/{n + 1}"}
+        log(f"bench: native decode {name}: {res[name]}")
+        del dec
+    res["what"] = ("w8a8.pipeline.Decoder after the whole-prompt prefill: per token and layer the int8 GEMVs with "
+                   "bf16 activations, k_qkv, the key / value cache write, the decode attention at a device-held "
+                   "position, the row kernels between; greedy argmax on the device; the graph form replays one "
+                   "captured step per token")
+    return res
+
+
 def e2e_bench(dev, T=ATTN_T, n_decode=32):
     """The reference's run() (gemma_npu.py:278-300) on the GPU: a timed prefill of T tokens, then
     greedy decode through HF's unchanged loop, one model call per token."""
@@ -647,12 +711,14 @@ def e2e_bench(dev, T=ATTN_T, n_decode=32):
         for _ in range(n_decode):
             o = model(input_ids=nxt, past_key_values=past, use_cache=True, logits_to_keep=1)
             past, nxt = o.past_key_values, o.logits[0, -1].argmax().view(1, 1)
-        torch.cuda.synchronize()
+            torch.cuda.synchronize()
         dt = time.perf_counter() - t
+        del past, o
+        native = native_decode_bench(model, ids, n_decode)
         pipe = pipeline_prefill_bench(model, ids, out.logits[0, -1].float())
-    del model, past, out, o
+    del model, out
     return {"prefill_ms": round(statistics.median(ttfts[1:]) * 1e3, 1), "prompt_tokens": T,
-            "pipeline_prefill": pipe,
+            "pipeline_prefill": pipe, "native_decode": native,
             "decode_tok_s": round(n_decode / dt, 1), "decode_ms_per_token": round(dt / n_decode * 1e3, 2),
             "decode_tokens": n_decode, "params": nparams,
             "what": "HF Gemma 4 (transformers' modeling code, unchanged) with E2B's shapes, random-init bf16 weights, "

@@ -1183,7 +1183,28 @@ struct DecodeParams {
   uint32_t k_bytes, v_bytes;
   int H, KV, G, Tk, klo, pos, nchunk;
   float scale, c;
+  // Position in device memory (a decode step replayed from a graph): the query position is
+  // *pos_dev, the keys [klo, pos] with klo from `window`; the grid holds nchunk_grid chunks per KV
+  // head, enough for any position the cache holds.  Null: pos / klo / nchunk / Tk above, and
+  // nchunk_grid = nchunk.
+  const int* pos_dev;
+  int window, nchunk_grid;
 };
+
+// The call's query position, first key, live chunks and key bound: the host's, or with pos_dev the
+// position read from device memory, its chunks clamped to the launched grid (a position past the
+// cache reads zero keys through the buffer bounds and never indexes past the grid's partials).
+struct DecodeGeom {
+  int pos, klo, nchunk, Tk;
+};
+template <int DEC_C>
+__device__ __forceinline__ DecodeGeom decode_geom(const DecodeParams& p) {
+  if (!p.pos_dev) return DecodeGeom{p.pos, p.klo, p.nchunk, p.Tk};
+  const int pos = *p.pos_dev;
+  const int klo = p.window > 0 ? max(0, pos - p.window + 1) : 0;
+  const int nchunk = max(0, min((pos - klo) / DEC_C + 1, p.nchunk_grid));
+  return DecodeGeom{pos, klo, nchunk, pos + 1};
+}
 
 template <int D>
 __global__ __launch_bounds__(256, 2) void attn_decode_split_kernel(DecodeParams p) {
@@ -1204,8 +1225,10 @@ __global__ __launch_bounds__(256, 2) void attn_decode_split_kernel(DecodeParams 
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int qi = lane & 15, qq = lane >> 4;
-  const int g = blockIdx.x / p.nchunk, chunk = blockIdx.x % p.nchunk;
-  const int kc = p.klo + chunk * DEC_C;      // first key of the chunk
+  const DecodeGeom geo = decode_geom<DEC_C>(p);
+  const int g = blockIdx.x / p.nchunk_grid, chunk = blockIdx.x % p.nchunk_grid;
+  if (chunk >= geo.nchunk) return;           // (the whole workgroup, before any barrier)
+  const int kc = geo.klo + chunk * DEC_C;    // first key of the chunk
   const __amdgpu_buffer_rsrc_t rk = make_rsrc(p.k + int64_t(g) * p.khs, p.k_bytes);
   const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.v + int64_t(g) * p.vhs, p.v_bytes);
 
@@ -1253,7 +1276,7 @@ __global__ __launch_bounds__(256, 2) void attn_decode_split_kernel(DecodeParams 
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int key = kc + 16 * wave + 4 * qq + i;
-    sc[i] = attn_mask(s0[i] + s1[i], has_tile & attn_key_visible(key, p.pos, p.Tk, 0x80000000u));
+    sc[i] = attn_mask(s0[i] + s1[i], has_tile & attn_key_visible(key, geo.pos, geo.Tk, 0x80000000u));
     bm = fmaxf(bm, sc[i]);
   }
   bm = lanes4_max(bm);
@@ -1305,7 +1328,7 @@ __global__ __launch_bounds__(256, 2) void attn_decode_split_kernel(DecodeParams 
 
   // partial results: O^T register i of lane (qi, qq) is d = wave D/4 + 16 dt + 4 qq + i, head qi
   if (qi < p.G) {
-    const int64_t base = (int64_t(g) * p.nchunk + chunk) * p.G + qi;
+    const int64_t base = (int64_t(g) * p.nchunk_grid + chunk) * p.G + qi;
     float* po = p.part_o + base * D + wave * (D / 4) + 4 * qq;
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) *reinterpret_cast<v4f*>(po + 16 * dt) = o[dt];
@@ -1330,9 +1353,10 @@ __global__ __launch_bounds__(256) void attn_decode_merge_kernel(DecodeParams p) 
   __shared__ float red[256];
   const int h = blockIdx.x, g = h / p.G, hl = h % p.G;
   const int t = threadIdx.x;
-  const float* ml = p.part_ml + (int64_t(g) * p.nchunk * p.G + hl) * 2;  // chunk c at ml[c * G * 2]
+  const int nchunk = decode_geom<dec_chunk(D)>(p).nchunk;
+  const float* ml = p.part_ml + (int64_t(g) * p.nchunk_grid * p.G + hl) * 2;  // chunk c at ml[c * G * 2]
   float mx = -__builtin_inff();
-  for (int c = t; c < p.nchunk; c += 256) {
+  for (int c = t; c < nchunk; c += 256) {
     const float m = ml[int64_t(c) * p.G * 2];
     wsh[c] = m;
     mx = fmaxf(mx, m);
@@ -1347,7 +1371,7 @@ __global__ __launch_bounds__(256) void attn_decode_merge_kernel(DecodeParams p) 
   __syncthreads();
   const float ms = M == -__builtin_inff() ? 0.0f : M * p.c;
   float lsum = 0.0f;
-  for (int c = t; c < p.nchunk; c += 256) {
+  for (int c = t; c < nchunk; c += 256) {
     const float w = __builtin_amdgcn_exp2f(__builtin_fmaf(wsh[c], p.c, -ms));
     wsh[c] = w;
     lsum = __builtin_fmaf(w, ml[int64_t(c) * p.G * 2 + 1], lsum);
@@ -1364,18 +1388,18 @@ __global__ __launch_bounds__(256) void attn_decode_merge_kernel(DecodeParams p) 
   constexpr int COLS = DEC_MCOLS, PARTS = 256 / COLS;
   const int col = blockIdx.y * COLS + t % COLS, part = t / COLS;
   v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-  const float* po = p.part_o + (int64_t(g) * p.nchunk * p.G + hl) * D + 4 * col;  // chunk c at po[c * G * D]
-  for (int c0 = part; c0 < p.nchunk; c0 += 8 * PARTS) {
+  const float* po = p.part_o + (int64_t(g) * p.nchunk_grid * p.G + hl) * D + 4 * col;  // chunk c at po[c * G * D]
+  for (int c0 = part; c0 < nchunk; c0 += 8 * PARTS) {
     v4f oc[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int c = c0 + u * PARTS;
-      oc[u] = c < p.nchunk ? *reinterpret_cast<const v4f*>(po + int64_t(c) * p.G * D) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+      oc[u] = c < nchunk ? *reinterpret_cast<const v4f*>(po + int64_t(c) * p.G * D) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int c = c0 + u * PARTS;
-      const float w = c < p.nchunk ? wsh[c] : 0.0f;
+      const float w = c < nchunk ? wsh[c] : 0.0f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(w, oc[u][i], acc[i]);
     }
@@ -1828,6 +1852,25 @@ extern "C" int w8a8_attention_quant_bf16(const uint16_t* q, int64_t q_head_strid
                           workspace_bytes, stream, packed, sx);
 }
 
+// The split and merge launches of one decode call: nchunk_grid chunks per KV head, partials in the
+// workspace (nchunk_grid per KV head and query head).
+static void decode_launch(DecodeParams& p, int64_t D, void* workspace, hipStream_t stream) {
+  p.part_o = static_cast<float*>(workspace);
+  p.part_ml = p.part_o + int64_t(p.KV) * p.nchunk_grid * p.G * D;
+  const dim3 grid{unsigned(p.KV * p.nchunk_grid), 1, 1};
+  const dim3 mgrid{unsigned(p.H), unsigned(D / 4 / DEC_MCOLS), 1};
+  if (D == 128) {
+    attn_decode_split_kernel<128><<<grid, dim3{256, 1, 1}, 0, stream>>>(p);
+    attn_decode_merge_kernel<128><<<mgrid, dim3{256, 1, 1}, 0, stream>>>(p);
+  } else if (D == 256) {
+    attn_decode_split_kernel<256><<<grid, dim3{256, 1, 1}, 0, stream>>>(p);
+    attn_decode_merge_kernel<256><<<mgrid, dim3{256, 1, 1}, 0, stream>>>(p);
+  } else {
+    attn_decode_split_kernel<512><<<grid, dim3{256, 1, 1}, 0, stream>>>(p);
+    attn_decode_merge_kernel<512><<<mgrid, dim3{256, 1, 1}, 0, stream>>>(p);
+  }
+}
+
 static void decode_geometry(int64_t D, int64_t q_pos, int64_t window, int& klo, int& nchunk) {
   klo = window > 0 ? int(q_pos - window + 1 > 0 ? q_pos - window + 1 : 0) : 0;
   nchunk = int((q_pos - klo) / dec_chunk(int(D)) + 1);
@@ -1879,26 +1922,76 @@ extern "C" int w8a8_attention_decode_bf16(const uint16_t* q, int64_t q_head_stri
     return fail(W8A8_EALIGN, "attention_decode: q, k, v, o and the workspace must be 16-byte aligned");
   const int64_t kb = ((Tk - 1) * k_row_stride + D) * 2, vb = ((Tk - 1) * v_row_stride + D) * 2;
   if (kb > INT32_MAX || vb > INT32_MAX) return fail(W8A8_ENOTSUP, "attention_decode: one head's K or V above 2 GiB");
-  DecodeParams p;
+  DecodeParams p{};
   p.q = q; p.qhs = q_head_stride; p.k = k; p.khs = k_head_stride; p.krs = k_row_stride;
   p.v = v; p.vhs = v_head_stride; p.vrs = v_row_stride; p.o = o; p.ohs = o_head_stride; p.lse = lse;
   p.k_bytes = uint32_t(kb); p.v_bytes = uint32_t(vb);
   p.H = int(H); p.KV = int(KV); p.G = int(H / KV); p.Tk = int(Tk); p.pos = int(q_pos);
   decode_geometry(D, q_pos, window, p.klo, p.nchunk);
-  p.part_o = static_cast<float*>(workspace);
-  p.part_ml = p.part_o + int64_t(KV) * p.nchunk * p.G * D;
+  p.pos_dev = nullptr;
+  p.window = int(window);
+  p.nchunk_grid = p.nchunk;
   p.scale = scale; p.c = scale * 1.4426950408889634f;
-  const dim3 grid{unsigned(KV * p.nchunk), 1, 1};
-  const dim3 mgrid{unsigned(H), unsigned(D / 4 / DEC_MCOLS), 1};
-  if (D == 128) {
-    attn_decode_split_kernel<128><<<grid, dim3{256, 1, 1}, 0, stream>>>(p);
-    attn_decode_merge_kernel<128><<<mgrid, dim3{256, 1, 1}, 0, stream>>>(p);
-  } else if (D == 256) {
-    attn_decode_split_kernel<256><<<grid, dim3{256, 1, 1}, 0, stream>>>(p);
-    attn_decode_merge_kernel<256><<<mgrid, dim3{256, 1, 1}, 0, stream>>>(p);
-  } else {
-    attn_decode_split_kernel<512><<<grid, dim3{256, 1, 1}, 0, stream>>>(p);
-    attn_decode_merge_kernel<512><<<mgrid, dim3{256, 1, 1}, 0, stream>>>(p);
-  }
+  decode_launch(p, D, workspace, stream);
   return check_launch("attention_decode_bf16");
+}
+
+// Chunks per KV head the device-position launch holds: enough for every position below Tk.
+static int decode_grid_chunks(int64_t D, int64_t Tk, int64_t window) {
+  const int64_t span = window > 0 && window < Tk ? window : Tk;
+  return int((span - 1) / dec_chunk(int(D)) + 1);
+}
+
+extern "C" int64_t w8a8_attention_decode_dev_workspace_bytes(int64_t H, int64_t KV, int64_t Tk, int64_t D,
+                                                             int64_t window) {
+  if (H < 1 || KV < 1 || H % KV != 0 || H / KV > 16 || (D != 128 && D != 256 && D != 512) || Tk < 1 ||
+      Tk > INT32_MAX || window < 0)
+    return -1;
+  return int64_t(KV) * decode_grid_chunks(D, Tk, window) * (H / KV) * (D + 2) * 4;
+}
+
+extern "C" int w8a8_attention_decode_dev_bf16(const uint16_t* q, int64_t q_head_stride, const uint16_t* k,
+                                              int64_t k_head_stride, int64_t k_row_stride, const uint16_t* v,
+                                              int64_t v_head_stride, int64_t v_row_stride, int64_t H, int64_t KV,
+                                              int64_t Tk, int64_t D, const int32_t* q_pos, int64_t window, float scale,
+                                              uint16_t* o, int64_t o_head_stride, void* workspace,
+                                              int64_t workspace_bytes, hipStream_t stream) {
+  if (H < 1 || KV < 1 || H % KV != 0 || H / KV > 16)
+    return fail(W8A8_EINVAL, "attention_decode_dev: H=%lld KV=%lld (H must be a multiple of KV, at most 16 heads per "
+                "KV head)", (long long)H, (long long)KV);
+  if (D != 128 && D != 256 && D != 512)
+    return fail(W8A8_ENOTSUP, "attention_decode_dev: head_dim %lld (supported: 128, 256, 512)", (long long)D);
+  if (Tk < 1 || Tk > INT32_MAX || window < 0 || window > INT32_MAX)
+    return fail(W8A8_EINVAL, "attention_decode_dev: Tk=%lld window=%lld", (long long)Tk, (long long)window);
+  if (decode_grid_chunks(D, Tk, window) > DEC_MAX_CHUNKS)
+    return fail(W8A8_ENOTSUP, "attention_decode_dev: %d key chunks of %d (at most %d)", decode_grid_chunks(D, Tk, window),
+                dec_chunk(int(D)), DEC_MAX_CHUNKS);
+  if (!(scale > 0.0f) || scale == __builtin_inff())
+    return fail(W8A8_EINVAL, "attention_decode_dev: scale must be positive");
+  if (!q || !k || !v || !o || !q_pos || !workspace) return fail(W8A8_EINVAL, "attention_decode_dev: null pointer");
+  const int64_t need = w8a8_attention_decode_dev_workspace_bytes(H, KV, Tk, D, window);
+  if (workspace_bytes < need)
+    return fail(W8A8_EINVAL, "attention_decode_dev: workspace of %lld bytes, %lld needed", (long long)workspace_bytes,
+                (long long)need);
+  if (k_row_stride < D || v_row_stride < D || (H > 1 && (q_head_stride < D || o_head_stride < D)))
+    return fail(W8A8_EINVAL, "attention_decode_dev: strides smaller than head_dim");
+  const int64_t strides[6] = {q_head_stride, k_head_stride, k_row_stride, v_head_stride, v_row_stride, o_head_stride};
+  for (int i = 0; i < 6; ++i)
+    if (strides[i] % 8 != 0) return fail(W8A8_EALIGN, "attention_decode_dev: strides must be multiples of 8 elements");
+  if ((uintptr_t)q % 16 || (uintptr_t)k % 16 || (uintptr_t)v % 16 || (uintptr_t)o % 16 || (uintptr_t)workspace % 16 ||
+      (uintptr_t)q_pos % 4)
+    return fail(W8A8_EALIGN, "attention_decode_dev: q, k, v, o and the workspace 16-byte, q_pos 4-byte aligned");
+  const int64_t kb = ((Tk - 1) * k_row_stride + D) * 2, vb = ((Tk - 1) * v_row_stride + D) * 2;
+  if (kb > INT32_MAX || vb > INT32_MAX) return fail(W8A8_ENOTSUP, "attention_decode_dev: one head's K or V above 2 GiB");
+  DecodeParams p{};
+  p.q = q; p.qhs = q_head_stride; p.k = k; p.khs = k_head_stride; p.krs = k_row_stride;
+  p.v = v; p.vhs = v_head_stride; p.vrs = v_row_stride; p.o = o; p.ohs = o_head_stride; p.lse = nullptr;
+  p.k_bytes = uint32_t(kb); p.v_bytes = uint32_t(vb);
+  p.H = int(H); p.KV = int(KV); p.G = int(H / KV); p.Tk = int(Tk);
+  p.pos_dev = q_pos;
+  p.window = int(window);
+  p.nchunk_grid = decode_grid_chunks(D, Tk, window);
+  p.scale = scale; p.c = scale * 1.4426950408889634f;
+  decode_launch(p, D, workspace, stream);
+  return check_launch("attention_decode_dev_bf16");
 }

@@ -745,6 +745,22 @@ int w8a8_k_gelu(const int32_t* acc, int64_t ldacc, const float* sx, const float*
   return launch_row_chain(p, true, stream, what);
 }
 
+int w8a8_gelu_mul_bf16(const uint16_t* y, int64_t ldy, const uint16_t* mul, int64_t ldm, int64_t M, int64_t N,
+                       uint16_t* out, int64_t ldo, hipStream_t stream) {
+  const char* what = "gelu_mul_bf16";
+  W8A8_TRY(check_rows(what, M, N));
+  W8A8_TRY(check_bf16_rows(what, "y", y, ldy, mul ? N : 2 * N));
+  if (mul) W8A8_TRY(check_bf16_rows(what, "mul", mul, ldm, N));
+  W8A8_TRY(check_bf16_rows(what, "out", out, ldo, N));
+  if (M == 0) return W8A8_OK;
+  RowChain p{};
+  set_input(p, RowInput{y, ldy, nullptr, nullptr, false}, N);
+  p.op = RC_GELU_MUL; p.aux = mul; p.ld_aux = ldm;
+  p.h = out; p.ldh = ldo;
+  p.M = int(M); p.N = int(N);
+  return launch_row_chain(p, false, stream, what);
+}
+
 int w8a8_k_post_ff(const int32_t* acc, int64_t ldacc, const float* sx, const float* sw, const uint16_t* res,
                    int64_t ldr, const uint16_t* w_post_ff, float eps, int64_t M, int64_t N, uint16_t* h, int64_t ldh,
                    int8_t* q, int64_t ldq, int q_packed, float* sq, hipStream_t stream) {

@@ -206,6 +206,52 @@ def decode(q, k, v, q_pos=None, window=0, scale=1.0, out=None, return_lse=False,
     return (out, lse) if return_lse else out
 
 
+def decode_at_workspace_bytes(H, KV, Tk, D, window=0):
+    """Bytes of scratch decode_at() needs for a key cache of Tk rows."""
+    n = lib().w8a8_attention_decode_dev_workspace_bytes(H, KV, Tk, D, int(window))
+    if n < 0:
+        raise ValueError(f"decode_at: invalid shape H={H} KV={KV} Tk={Tk} D={D} window={window}")
+    return n
+
+
+def decode_at(q, k, v, pos, window=0, scale=1.0, out=None, workspace=None):
+    """decode() with the query position read from device memory: pos is an int32 GPU tensor [1]
+    holding q_pos, k / v the key and value cache [KV, Tk, D] of capacity Tk > q_pos.  The launch does
+    not depend on the position, so a decode step captured in a HIP graph replays at each new one.
+    workspace: at least decode_at_workspace_bytes(H, KV, Tk, D, window) bytes (allocate it before a
+    capture); by default a buffer cached per device and stream."""
+    if q.dim() == 3:
+        if q.shape[1] != 1:
+            raise ValueError(f"decode_at: expected one query per head, got shape {tuple(q.shape)}")
+        q = q[:, 0]
+    if not isinstance(q, torch.Tensor) or q.dim() != 2 or q.dtype != torch.bfloat16 or q.device.type != "cuda":
+        raise ValueError("decode_at: q must be a bf16 GPU tensor [H, D]")
+    if q.shape[1] > 1 and q.stride(1) != 1:
+        raise ValueError("decode_at: q's last dimension must be contiguous")
+    _check3(k, "k")
+    _check3(v, "v")
+    if not isinstance(pos, torch.Tensor) or pos.dtype != torch.int32 or pos.numel() != 1 or pos.device != q.device:
+        raise ValueError("decode_at: pos must be an int32 tensor of one element on q's device")
+    H, D = q.shape
+    KV, Tk, Dk = k.shape
+    if tuple(v.shape) != (KV, Tk, Dk) or Dk != D:
+        raise ValueError(f"q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)} do not match")
+    if len({q.device, k.device, v.device}) != 1:
+        raise ValueError("q, k and v must be on one device")
+    if out is None:
+        out = torch.empty((H, D), dtype=torch.bfloat16, device=q.device)
+    elif out.shape != (H, D) or out.dtype != torch.bfloat16 or (D > 1 and out.stride(1) != 1):
+        raise ValueError(f"decode_at: out must be bf16 [{H}, {D}] with a contiguous last dimension")
+    need = decode_at_workspace_bytes(H, KV, Tk, D, window)
+    ws = _workspace(q.device, need) if workspace is None else workspace
+    khs, krs = _strides(k)
+    vhs, vrs = _strides(v)
+    call("w8a8_attention_decode_dev_bf16", q.data_ptr(), q.stride(0) if H > 1 else D, k.data_ptr(), khs, krs,
+         v.data_ptr(), vhs, vrs, H, KV, Tk, D, pos.data_ptr(), int(window), float(scale), out.data_ptr(),
+         out.stride(0) if H > 1 else D, ws.data_ptr(), ws.numel(), _stream(q))
+    return out
+
+
 def split_kv_decode(query, key, value, scale):
     """local_attn.py:44-68: one query per head [1, H, 1, D] against one KV head [1, 1, T, D] ->
     [1, 1, H, D] (the reference's split over up to 16 key chunks and logsumexp merge)."""

@@ -319,6 +319,32 @@ def rms_residual(y, res, w, eps, out=None, quant=False):
     return (out, q, sq) if quant else out
 
 
+def gelu_mul_bf16(y, mul=None, out=None):
+    """bf16(bf16(gelu_tanh(y[:, :N])) * m) as bf16 rows: m = mul [M, N], or y's second half when mul is
+    None (y [M, 2N]).  k_gelu's / k_ple_gate's activation (pipeline.py:102-107, 117-121) without the
+    quant, for the decode step."""
+    _check(y, "y", torch.bfloat16)
+    M = y.shape[0]
+    if mul is None:
+        if y.shape[1] % 2:
+            raise ValueError("gelu_mul_bf16: y must hold [gate | up] halves")
+        N = y.shape[1] // 2
+    else:
+        N = y.shape[1]
+        _check(mul, "mul", torch.bfloat16)
+        if tuple(mul.shape) != (M, N):
+            raise ValueError(f"gelu_mul_bf16: mul {tuple(mul.shape)} does not match y {tuple(y.shape)}")
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=y.device)
+    _check(out, "out", torch.bfloat16)
+    if tuple(out.shape) != (M, N):
+        raise ValueError(f"gelu_mul_bf16: out has shape {tuple(out.shape)}, expected {(M, N)}")
+    _same_device(y, mul, out)
+    call("w8a8_gelu_mul_bf16", y.data_ptr(), _ld(y), None if mul is None else mul.data_ptr(),
+         0 if mul is None else _ld(mul), M, N, out.data_ptr(), _ld(out), _stream(y))
+    return out
+
+
 def linear_workspace_bytes(M, N, K):
     return lib().w8a8_linear_workspace_bytes(M, N, K)
 

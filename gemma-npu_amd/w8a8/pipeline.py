@@ -291,3 +291,200 @@ class CapturedPrefill:
         self.per_layer.copy_(per_layer)
         self.graph.replay()
         return p.last_token_logits(self.rows), self.store.to_cache(p.cfg, copy=True)
+
+
+class Decoder:
+    """Greedy decoding after the prompt, every step on the GPU: the reference's decode loop
+    (gemma_npu.py:278-300, HF's model called once per token) as one fixed sequence of launches.
+
+    Per layer, for the one new token: the decode linears on the int8 GEMV with bf16 activations, the
+    reference's decode copy of each weight (gemma_npu.py:117-121, 155-156); q / k norms and RoPE
+    (k_qkv); the key and value written into the cache at the token's position; the decode attention
+    over the cache (local_attn.py:44-83); and the norms, residuals, GELU-tanh products and
+    per-layer-input steps of pipeline.py:66-127 without the activation quant, since the next linear
+    reads bf16.  The token, its position and the key / value cache [KV, max_len, head_dim] of every
+    layer that owns keys live in device memory, so a step does not depend on host values: capture()
+    records one step in a HIP graph and each replay decodes the next token.  The next token is the
+    argmax of the last logits (greedy), chosen on the device.
+
+        dec = Decoder(Prefill(model), max_len=4096)
+        logits = dec.start(ids)              # the prompt through the prefill; the first new token
+        tokens = dec.generate(32)            # 32 greedy steps, graph-replayed
+    """
+
+    def __init__(self, prefill, max_len):
+        self.pre = prefill
+        self.lm, self.cfg = prefill.lm, prefill.cfg
+        self.max_len = int(max_len)
+        if self.max_len < 2:
+            raise ValueError(f"Decoder: max_len {max_len} leaves no room to decode")
+        dev = self.lm.embed_tokens.weight.device
+        self.device = dev
+        self.tok = torch.zeros((1, 1), dtype=torch.long, device=dev)
+        self.pos = torch.zeros((1,), dtype=torch.int32, device=dev)      # read by the attention kernel
+        self.pos64 = torch.zeros((1,), dtype=torch.long, device=dev)     # for the index operations
+        self.emitted = torch.zeros((self.max_len,), dtype=torch.long, device=dev)
+        self.n_emitted = torch.zeros((1,), dtype=torch.long, device=dev)
+        positions = torch.arange(self.max_len, device=dev)[None]
+        probe = torch.zeros((1, self.max_len, self.cfg.hidden_size), dtype=torch.bfloat16, device=dev)
+        self.rope = {}
+        for kind in dict.fromkeys(self.cfg.layer_types):
+            cos, sin = self.lm.rotary_emb(probe, positions, kind)
+            self.rope[kind] = (cos[0].contiguous(), sin[0].contiguous())
+        del probe
+        self.cache = {}
+        ws = 1 << 16
+        for p in prefill.plans:
+            if not p.shares_kv:
+                shape = (p.kv_heads, self.max_len, p.head_dim)
+                self.cache[p.index] = (torch.zeros(shape, dtype=torch.bfloat16, device=dev),
+                                       torch.zeros(shape, dtype=torch.bfloat16, device=dev))
+            ws = max(ws, attention.decode_at_workspace_bytes(p.heads, p.kv_heads, self.max_len, p.head_dim,
+                                                             p.window))
+        self.workspace = torch.empty(ws, dtype=torch.uint8, device=dev)
+        self.length = None
+        self.graph = None
+
+    @torch.inference_mode()
+    def start(self, ids):
+        """The prompt ids [1, T] through the whole-prompt prefill: fills the key / value cache, sets the
+        first new token (the argmax of the returned last-token logits) at position T."""
+        ids = self.pre.check_ids(ids)
+        T = ids.shape[1]
+        if T >= self.max_len:
+            raise ValueError(f"Decoder: a {T}-token prompt leaves no room in max_len {self.max_len}")
+        h0, per_layer, rope = prompt_inputs(self.lm, ids)
+        rows, store = self.pre.run_layers(h0, per_layer, rope)
+        for layer, (kc, vc) in self.cache.items():
+            k, v = store.kv[layer]
+            kc[:, :T].copy_(k)
+            vc[:, :T].copy_(v)
+        logits = self.pre.last_token_logits(rows)
+        self.pos.fill_(T)
+        self.pos64.fill_(T)
+        self.n_emitted.zero_()
+        self._emit(logits)
+        self.length = T
+        return logits
+
+    def _emit(self, logits):
+        """Greedy choice on the device: the argmax becomes the next input token and is recorded."""
+        nxt = logits.argmax().view(1)
+        self.tok.view(1).copy_(nxt)
+        self.emitted.index_copy_(0, self.n_emitted, nxt)
+        self.n_emitted.add_(1)
+
+    def _logits(self, h):
+        """The model's head on the token's row as HF's decode call computes it (the loop this replaces):
+        final norm, LM head, and the logit softcap in the model's dtype, then fp32.  (The prefill
+        pipeline takes the softcap in fp32, as pipeline.py:334-338 does.)"""
+        logits = self.pre.model.lm_head(self.lm.norm(h[None]))[0, -1]
+        cap = self.cfg.final_logit_softcapping
+        if cap:
+            logits = torch.tanh(logits / cap) * cap
+        return logits.float()
+
+    def _layer(self, p, h, per_layer, scalar):
+        """Decoder layer p on the token's row h [1, hidden] at the device-held position."""
+        eps = self.cfg.rms_norm_eps
+        W = p.weights
+
+        def linear(x, w):
+            return ops.gemv_bf16(x, w.gemv_w, w.sw_bf16)
+
+        x = ops.rms_residual(h, None, p.norm_in, eps)
+        y = linear(x, W["qkv"])
+        cos, sin = (t.index_select(0, self.pos64) for t in self.rope[p.kind])
+        q, k, v = fused.k_qkv(y, None, None, cos, sin, p.norm_q, p.norm_k, eps, p.heads, p.kv_heads, p.head_dim,
+                              p.shares_kv)
+        if not p.shares_kv:
+            kc, vc = self.cache[p.index]
+            kc.index_copy_(1, self.pos64, k)
+            vc.index_copy_(1, self.pos64, v)
+        kc, vc = self.cache[p.kv_source]
+        o = attention.decode_at(q[:, 0], kc, vc, self.pos, p.window, 1.0, workspace=self.workspace)
+        y = linear(o.reshape(1, -1), W["o"])
+        h = ops.rms_residual(y, h, p.norm_post_attn, eps)
+        y = linear(ops.rms_residual(h, None, p.norm_pre_ff, eps), W["gate_up"])
+        y = linear(ops.gelu_mul_bf16(y), W["down"])
+        h = ops.rms_residual(y, h, p.norm_post_ff, eps)
+        y = linear(h, W["ple_gate"])
+        y = linear(ops.gelu_mul_bf16(y, per_layer[:, p.index]), W["ple_proj"])
+        return fused.k_ple_out(y, None, None, h, p.norm_post_ple, scalar[p.index], eps)
+
+    @torch.inference_mode()
+    def step(self):
+        """Decode the current token at the current position: its last-position logits [vocab] fp32;
+        the argmax becomes the next token and the position advances, all on the device."""
+        if self.length is None:
+            raise RuntimeError("Decoder: call start(ids) first")
+        if self.length >= self.max_len:
+            raise RuntimeError(f"Decoder: the cache of {self.max_len} positions is full")
+        logits = self._step()
+        self.length += 1
+        return logits
+
+    def _step(self):
+        emb = self.lm.embed_tokens(self.tok)
+        per_layer = self.lm.project_per_layer_inputs(emb, self.lm.get_per_layer_inputs(self.tok, emb))[0]
+        h = emb[0]
+        scalar = self.pre._scalars()
+        for p in self.pre.plans:
+            h = self._layer(p, h, per_layer, scalar)
+        logits = self._logits(h)
+        self._emit(logits)
+        self.pos.add_(1)
+        self.pos64.add_(1)
+        return logits
+
+    @torch.inference_mode()
+    def capture(self):
+        """One decode step recorded in a HIP graph.  Runs one eager step first on the capture stream
+        (its logits are returned: it is a real step, and it creates every workspace outside the
+        graph), then captures the next step without running it.  replay() then decodes one token per
+        call into the static logits tensor `self.graph_logits`."""
+        if self.length is None:
+            raise RuntimeError("Decoder: call start(ids) first")
+        if self.length + 2 > self.max_len:
+            raise RuntimeError("Decoder: no room left to capture a step")
+        stream = torch.cuda.Stream(self.device)
+        stream.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(stream):
+            first = self.step()
+        torch.cuda.current_stream(self.device).wait_stream(stream)
+        torch.cuda.synchronize(self.device)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            self.graph_logits = self._step()
+        torch.cuda.synchronize(self.device)
+        self.graph = graph
+        return first
+
+    def replay(self):
+        """One graph-replayed decode step: the static logits tensor, the next token chosen."""
+        if self.graph is None:
+            raise RuntimeError("Decoder: capture() first")
+        if self.length >= self.max_len:
+            raise RuntimeError(f"Decoder: the cache of {self.max_len} positions is full")
+        self.graph.replay()
+        self.length += 1
+        return self.graph_logits
+
+    @torch.inference_mode()
+    def generate(self, n, graph=True):
+        """n more greedy tokens (after start): a list of ints, read once at the end."""
+        if self.length is None:
+            raise RuntimeError("Decoder: call start(ids) first")
+        if self.length + n > self.max_len:
+            raise ValueError(f"Decoder: {n} more tokens pass max_len {self.max_len}")
+        first = int(self.n_emitted.item())
+        if graph:
+            if self.graph is None and n >= 2:
+                self.capture()
+                n -= 1
+            for _ in range(n):
+                self.replay()
+        else:
+            for _ in range(n):
+                self.step()
+        return self.emitted[first:int(self.n_emitted.item())].tolist()

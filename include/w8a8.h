@@ -248,6 +248,14 @@ int w8a8_k_ple_out(const int32_t *acc, int64_t ldacc, const float *sx, const flo
                    int64_t ldh, const uint16_t *w_post_ple, const uint16_t *scalar, float eps, int64_t M, int64_t N,
                    uint16_t *out, int64_t ldo, hipStream_t stream);
 
+/* bf16(bf16(gelu_tanh(y[:, :N])) * m) as bf16 rows out [M, N] (ld = ldo), m = mul [M, N] (ld = ldm) or,
+ * with mul NULL, y[:, N:2N] (y then holds 2N columns): k_gelu's and k_ple_gate's activation
+ * (pipeline.py:102-107, 117-121) for the decode step, whose next linear is the bf16-activation
+ * int8 GEMV (gemma_npu.py:117-121, 155-156) rather than a quantised GEMM.  The same kernel and
+ * arithmetic as those two; N % 8 == 0, N <= 12288, 16-byte aligned rows. */
+int w8a8_gelu_mul_bf16(const uint16_t *y, int64_t ldy, const uint16_t *mul, int64_t ldm, int64_t M, int64_t N,
+                       uint16_t *out, int64_t ldo, hipStream_t stream);
+
 /* The same five kernels fed the dequantised bf16 rows y [rows, N] (ld = ldy, 16-byte aligned rows)
  * instead of an int32 result with its scales: y is what the GEMM's dequant epilogue
  * (w8a8_gemm_bf16 epilogue 0) writes, bf16((acc * sx) * sw), the values the int32 entries compute
@@ -416,6 +424,21 @@ int w8a8_attention_decode_bf16(const uint16_t *q, int64_t q_head_stride, const u
                                int64_t H, int64_t KV, int64_t Tk, int64_t D, int64_t q_pos, int64_t window,
                                float scale, uint16_t *o, int64_t o_head_stride, float *lse, void *workspace,
                                int64_t workspace_bytes, hipStream_t stream);
+
+/* The same attention with the query position read from device memory, *q_pos (int32), so that a
+ * decode step captured in a HIP graph replays at each new position (the reference's decode loop,
+ * gemma_npu.py:278-300, with local_attn.py:44-83 per layer).  Tk is the key cache's capacity: the
+ * launch covers every position 0 <= *q_pos < Tk (chunks past the live ones return at once).  A
+ * position outside that range is the caller's error: it yields meaningless values, never an access
+ * outside k, v or the workspace.  Workspace bytes from w8a8_attention_decode_dev_workspace_bytes
+ * (-1 for invalid arguments); no lse output. */
+int64_t w8a8_attention_decode_dev_workspace_bytes(int64_t H, int64_t KV, int64_t Tk, int64_t D, int64_t window);
+int w8a8_attention_decode_dev_bf16(const uint16_t *q, int64_t q_head_stride, const uint16_t *k, int64_t k_head_stride,
+                                   int64_t k_row_stride, const uint16_t *v, int64_t v_head_stride,
+                                   int64_t v_row_stride, int64_t H, int64_t KV, int64_t Tk, int64_t D,
+                                   const int32_t *q_pos, int64_t window, float scale, uint16_t *o,
+                                   int64_t o_head_stride, void *workspace, int64_t workspace_bytes,
+                                   hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,85 @@
+"""w8a8.pipeline.Decoder: greedy decoding after the prompt with every step on the GPU (the reference's
+decode loop, gemma_npu.py:278-300, as one fixed launch sequence per token), on the small Gemma 4
+of hf_tiny.py (sliding and full layers, KV-shared layers, double-wide MLPs, per-layer inputs).
+
+Checks:
+- against HF's own decode loop on the engine (w8a8.hf.to_gpu: the same GEMV weights and decode
+  attention kernel, HF's torch ops between them), continuing from the same prompt: the same greedy
+  tokens for 28 steps, past the sliding window of 16, and the logits within bf16 noise per step;
+- a step replayed from the HIP graph gives the eager step's logits and tokens bit for bit, with
+  eager work between replays;
+- the refusals: no start, a prompt that fills max_len, steps past max_len.
+"""
+import pytest
+import torch
+
+from hf_tiny import build, rel_err
+from test_pipeline_gpu import engine_model
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@torch.inference_mode()
+def test_decoder_matches_hf_decode_loop():
+    from w8a8.pipeline import Decoder, Prefill
+    ours = engine_model(build(seed=31))
+    ids = torch.randint(0, 512, (1, 20), generator=torch.Generator().manual_seed(32))
+    first_logits, past = Prefill(ours)(ids)
+    dec = Decoder(Prefill(ours), max_len=64)
+    logits = dec.start(ids)
+    assert torch.equal(logits, first_logits)
+    nxt = first_logits.argmax().view(1, 1).to(DEV)
+    worst = 0.0
+    for step in range(28):
+        o = ours(input_ids=nxt, past_key_values=past, use_cache=True)
+        want = o.logits[0, -1].float()
+        got = dec.step()
+        e = rel_err(got, want)
+        worst = max(worst, e)
+        assert int(got.argmax()) == int(want.argmax()), f"step {step}: the greedy tokens differ"
+        past = o.past_key_values
+        nxt = want.argmax().view(1, 1)
+    print(f"28 decode steps to position 48: max relative logits difference from HF's loop {worst:.5f}")
+    assert worst < 2e-2
+    assert dec.length == 20 + 28
+    assert dec.emitted[:29].tolist() == [int(first_logits.argmax())] + dec.emitted[1:29].tolist()
+
+
+@torch.inference_mode()
+def test_graph_replay_matches_eager_steps():
+    from w8a8.pipeline import Decoder, Prefill
+    ours = engine_model(build(seed=33))
+    ids = torch.randint(0, 512, (1, 13), generator=torch.Generator().manual_seed(34))
+    eager = Decoder(Prefill(ours), max_len=48)
+    eager.start(ids)
+    want = [eager.step().clone() for _ in range(20)]
+    replayed = Decoder(Prefill(ours), max_len=48)
+    replayed.start(ids)
+    got = [replayed.capture().clone()]
+    for _ in range(19):
+        got.append(replayed.replay().clone())
+        torch.cuda.synchronize()
+        _ = torch.ones(1000, device=DEV).sum().item()  # eager work between replays
+    for i, (g, w) in enumerate(zip(got, want)):
+        assert torch.equal(g, w), f"step {i}: the replayed logits differ from the eager step's"
+    assert torch.equal(replayed.emitted[:21], eager.emitted[:21])
+    toks = replayed.generate(5)
+    assert len(toks) == 5 and replayed.length == 13 + 25
+
+
+def test_decoder_refusals():
+    from w8a8.pipeline import Decoder, Prefill
+    ours = engine_model(build(seed=35))
+    dec = Decoder(Prefill(ours), max_len=16)
+    with pytest.raises(RuntimeError, match="start"):
+        dec.step()
+    with pytest.raises(ValueError, match="max_len"):
+        dec.start(torch.zeros((1, 16), dtype=torch.long))
+    dec.start(torch.zeros((1, 14), dtype=torch.long))
+    dec.step()
+    dec.step()
+    with pytest.raises(RuntimeError, match="full"):
+        dec.step()
+    with pytest.raises(ValueError, match="max_len"):
+        Decoder(Prefill(ours), max_len=1)
