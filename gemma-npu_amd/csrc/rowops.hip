@@ -101,6 +101,7 @@ struct RowChain {
   const uint16_t* scalar;               // one bf16 multiplier applied after the op (null: none)
   uint16_t* h; int64_t ldh;             // bf16 result of op + scale (null: not stored)
   int norm2; const uint16_t* w2;        // quantise bf16(rms(y) * w2) instead of y (w2 null: no weight)
+  uint16_t* h2; int64_t ldh2;           // bf16 rows of what is quantised (the second norm's output); null: not stored
   int8_t* q; int64_t ldq; int KF;       // int8 rows, row-major (KF == 0) or packed (KF = 2 * ceil(N / 64)); null: none
   float* sq;                            // per-row scales of q
   float eps; int M, N;
@@ -182,7 +183,7 @@ __global__ __launch_bounds__(256) void row_chain_kernel(RowChain p) {
       res[c] = (in && p.aux) ? *reinterpret_cast<const v4u*>(p.aux + int64_t(row) * p.ld_aux + k) : v4u{0u, 0u, 0u, 0u};
       w1[c] = (in && p.w1) ? *reinterpret_cast<const v4u*>(p.w1 + k) : one;
     }
-    w2[c] = (in && p.q && p.norm2 && p.w2) ? *reinterpret_cast<const v4u*>(p.w2 + k) : one;
+    w2[c] = (in && (p.q || p.h2) && p.norm2 && p.w2) ? *reinterpret_cast<const v4u*>(p.w2 + k) : one;
   }
 
   if constexpr (OP == RC_GELU_MUL) {
@@ -227,7 +228,7 @@ __global__ __launch_bounds__(256) void row_chain_kernel(RowChain p) {
       if (k < p.N) *reinterpret_cast<v4u*>(p.h + int64_t(row) * p.ldh + k) = pack8(v[c]);
     }
   }
-  if (!p.q) return;
+  if (!p.q && !p.h2) return;
 
   if (p.norm2) {
     float ss = 0.0f;
@@ -249,6 +250,14 @@ __global__ __launch_bounds__(256) void row_chain_kernel(RowChain p) {
       }
     }
   }
+  if (p.h2) {
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int k = 8 * (nt * c + t);
+      if (k < p.N) *reinterpret_cast<v4u*>(p.h2 + int64_t(row) * p.ldh2 + k) = pack8(v[c]);
+    }
+  }
+  if (!p.q) return;
   float amax = 0.0f;
 #pragma unroll
   for (int c = 0; c < CH; ++c)
@@ -743,6 +752,26 @@ int w8a8_k_gelu(const int32_t* acc, int64_t ldacc, const float* sx, const float*
   p.op = RC_GELU_MUL;
   p.M = int(M); p.N = int(I);
   return launch_row_chain(p, true, stream, what);
+}
+
+int w8a8_rms_residual_norm_bf16(const uint16_t* y, int64_t ldy, const uint16_t* res, int64_t ldr, const uint16_t* w1,
+                                const uint16_t* scalar, const uint16_t* w2, float eps, int64_t M, int64_t N, uint16_t* h,
+                                int64_t ldh, uint16_t* x, int64_t ldx, hipStream_t stream) {
+  const char* what = "rms_residual_norm_bf16";
+  W8A8_TRY(check_rows(what, M, N));
+  W8A8_TRY(check_bf16_rows(what, "y", y, ldy, N));
+  W8A8_TRY(check_bf16_rows(what, "res", res, ldr, N));
+  W8A8_TRY(check_bf16_rows(what, "h", h, ldh, N));
+  W8A8_TRY(check_bf16_rows(what, "x", x, ldx, N));
+  if ((w1 && !al16(w1)) || (w2 && !al16(w2))) return fail(W8A8_EALIGN, "%s: norm weights must be 16-byte aligned", what);
+  if (M == 0) return W8A8_OK;
+  RowChain p{};
+  set_input(p, RowInput{y, ldy, nullptr, nullptr, false}, N);
+  p.op = RC_NORM_RES; p.aux = res; p.ld_aux = ldr; p.w1 = w1; p.scalar = scalar;
+  p.h = h; p.ldh = ldh;
+  p.norm2 = 1; p.w2 = w2; p.h2 = x; p.ldh2 = ldx;
+  p.eps = eps; p.M = int(M); p.N = int(N);
+  return launch_row_chain(p, false, stream, what);
 }
 
 int w8a8_gelu_mul_bf16(const uint16_t* y, int64_t ldy, const uint16_t* mul, int64_t ldm, int64_t M, int64_t N,

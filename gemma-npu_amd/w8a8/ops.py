@@ -319,6 +319,30 @@ def rms_residual(y, res, w, eps, out=None, quant=False):
     return (out, q, sq) if quant else out
 
 
+def rms_residual_norm(y, res, w1, w2, eps, scalar=None):
+    """(h, x): h = bf16(bf16(res + bf16(rms(y) * w1)) * scalar) and x = bf16(rms(h) * w2), one launch:
+    k_post_attn's two norms (pipeline.py:95-99), or k_ple_out and the next layer's input norm
+    (pipeline.py:124-127, 66-69), with bf16 outputs (the decode step).  scalar: a bf16 tensor of
+    one element, or None."""
+    _check(y, "y", torch.bfloat16)
+    _check(res, "res", torch.bfloat16)
+    M, N = y.shape
+    if tuple(res.shape) != (M, N):
+        raise ValueError("rms_residual_norm: shapes differ")
+    for t, name in ((w1, "w1"), (w2, "w2")):
+        if t is not None:
+            _check(t, name, torch.bfloat16, 1)
+    if scalar is not None and (scalar.dtype != torch.bfloat16 or scalar.numel() != 1):
+        raise ValueError("rms_residual_norm: scalar must be one bf16 value")
+    h = torch.empty((M, N), dtype=torch.bfloat16, device=y.device)
+    x = torch.empty((M, N), dtype=torch.bfloat16, device=y.device)
+    _same_device(y, res, w1, w2, scalar)
+    call("w8a8_rms_residual_norm_bf16", y.data_ptr(), _ld(y), res.data_ptr(), _ld(res),
+         None if w1 is None else w1.data_ptr(), None if scalar is None else scalar.data_ptr(),
+         None if w2 is None else w2.data_ptr(), float(eps), M, N, h.data_ptr(), N, x.data_ptr(), N, _stream(y))
+    return h, x
+
+
 def gelu_mul_bf16(y, mul=None, out=None):
     """bf16(bf16(gelu_tanh(y[:, :N])) * m) as bf16 rows: m = mul [M, N], or y's second half when mul is
     None (y [M, 2N]).  k_gelu's / k_ple_gate's activation (pipeline.py:102-107, 117-121) without the

@@ -324,6 +324,7 @@ class Decoder:
         self.pos = torch.zeros((1,), dtype=torch.int32, device=dev)      # read by the attention kernel
         self.pos64 = torch.zeros((1,), dtype=torch.long, device=dev)     # for the index operations
         self.emitted = torch.zeros((self.max_len,), dtype=torch.long, device=dev)
+        self.zero_index = torch.zeros((1,), dtype=torch.long, device=dev)
         self.n_emitted = torch.zeros((1,), dtype=torch.long, device=dev)
         positions = torch.arange(self.max_len, device=dev)[None]
         probe = torch.zeros((1, self.max_len, self.cfg.hidden_size), dtype=torch.bfloat16, device=dev)
@@ -368,9 +369,19 @@ class Decoder:
         return logits
 
     def _emit(self, logits):
-        """Greedy choice on the device: the argmax becomes the next input token and is recorded."""
-        nxt = logits.argmax().view(1)
-        self.tok.view(1).copy_(nxt)
+        """Greedy choice on the device: the argmax becomes the next input token and is recorded.
+        The argmax runs in two single-block stages (per row of a [rows, 512] view, then over the
+        rows' maxima; the first index of the maximum, as a flat argmax gives): torch's flat argmax
+        over the whole vocabulary is a multi-block reduction that clears a counter with a memset,
+        which a captured graph must not hold.  Writes are index_copy_ kernels, not copies, for the
+        same reason."""
+        V = logits.shape[0]
+        cols = 512 if V % 512 == 0 else V
+        grid = logits.view(-1, cols)
+        idx = grid.argmax(dim=1)
+        row = grid.amax(dim=1).argmax().view(1)
+        nxt = row * cols + idx.index_select(0, row)
+        self.tok.view(1).index_copy_(0, self.zero_index, nxt)
         self.emitted.index_copy_(0, self.n_emitted, nxt)
         self.n_emitted.add_(1)
 
@@ -384,17 +395,19 @@ class Decoder:
             logits = torch.tanh(logits / cap) * cap
         return logits.float()
 
-    def _layer(self, p, h, per_layer, scalar):
-        """Decoder layer p on the token's row h [1, hidden] at the device-held position."""
+    def _layer(self, p, h, x, per_layer, scalar, rope, norm_next):
+        """Decoder layer p on the token's row h [1, hidden] at the device-held position, x its input
+        norm; rope maps the attention kind to its (cos, sin) rows [1, head_dim] at that position.
+        Returns the layer's output row and, with norm_next (the next layer's input-norm weight), that
+        norm of it from the same launch (else None)."""
         eps = self.cfg.rms_norm_eps
         W = p.weights
 
         def linear(x, w):
             return ops.gemv_bf16(x, w.gemv_w, w.sw_bf16)
 
-        x = ops.rms_residual(h, None, p.norm_in, eps)
         y = linear(x, W["qkv"])
-        cos, sin = (t.index_select(0, self.pos64) for t in self.rope[p.kind])
+        cos, sin = rope[p.kind]
         q, k, v = fused.k_qkv(y, None, None, cos, sin, p.norm_q, p.norm_k, eps, p.heads, p.kv_heads, p.head_dim,
                               p.shares_kv)
         if not p.shares_kv:
@@ -404,13 +417,14 @@ class Decoder:
         kc, vc = self.cache[p.kv_source]
         o = attention.decode_at(q[:, 0], kc, vc, self.pos, p.window, 1.0, workspace=self.workspace)
         y = linear(o.reshape(1, -1), W["o"])
-        h = ops.rms_residual(y, h, p.norm_post_attn, eps)
-        y = linear(ops.rms_residual(h, None, p.norm_pre_ff, eps), W["gate_up"])
-        y = linear(ops.gelu_mul_bf16(y), W["down"])
+        h, x = ops.rms_residual_norm(y, h, p.norm_post_attn, p.norm_pre_ff, eps)
+        y = linear(ops.gelu_mul_bf16(linear(x, W["gate_up"])), W["down"])
         h = ops.rms_residual(y, h, p.norm_post_ff, eps)
         y = linear(h, W["ple_gate"])
         y = linear(ops.gelu_mul_bf16(y, per_layer[:, p.index]), W["ple_proj"])
-        return fused.k_ple_out(y, None, None, h, p.norm_post_ple, scalar[p.index], eps)
+        if norm_next is None:
+            return fused.k_ple_out(y, None, None, h, p.norm_post_ple, scalar[p.index], eps), None
+        return ops.rms_residual_norm(y, h, p.norm_post_ple, norm_next, eps, scalar=scalar[p.index])
 
     @torch.inference_mode()
     def step(self):
@@ -429,8 +443,13 @@ class Decoder:
         per_layer = self.lm.project_per_layer_inputs(emb, self.lm.get_per_layer_inputs(self.tok, emb))[0]
         h = emb[0]
         scalar = self.pre._scalars()
-        for p in self.pre.plans:
-            h = self._layer(p, h, per_layer, scalar)
+        rope = {kind: (c.index_select(0, self.pos64), s.index_select(0, self.pos64))
+                for kind, (c, s) in self.rope.items()}
+        plans = self.pre.plans
+        x = ops.rms_residual(h, None, plans[0].norm_in, self.cfg.rms_norm_eps)
+        for i, p in enumerate(plans):
+            nxt = plans[i + 1].norm_in if i + 1 < len(plans) else None
+            h, x = self._layer(p, h, x, per_layer, scalar, rope, nxt)
         logits = self._logits(h)
         self._emit(logits)
         self.pos.add_(1)

@@ -248,6 +248,15 @@ int w8a8_k_ple_out(const int32_t *acc, int64_t ldacc, const float *sx, const flo
                    int64_t ldh, const uint16_t *w_post_ple, const uint16_t *scalar, float eps, int64_t M, int64_t N,
                    uint16_t *out, int64_t ldo, hipStream_t stream);
 
+/* h = bf16(bf16(res + bf16(rms(y, w1))) * scalar) (scalar one bf16 value in device memory, or NULL: no
+ * product) and x = bf16(rms(h, w2)), both stored as bf16 rows [M, N]: k_post_attn's two norms
+ * (pipeline.py:95-99) and k_ple_out followed by the next layer's input norm (pipeline.py:124-127,
+ * 66-69), with bf16 outputs instead of the quant, for the decode step.  w1 / w2 may be NULL (no
+ * weight).  N % 8 == 0, N <= 12288, 16-byte aligned rows and weights. */
+int w8a8_rms_residual_norm_bf16(const uint16_t *y, int64_t ldy, const uint16_t *res, int64_t ldr, const uint16_t *w1,
+                                const uint16_t *scalar, const uint16_t *w2, float eps, int64_t M, int64_t N,
+                                uint16_t *h, int64_t ldh, uint16_t *x, int64_t ldx, hipStream_t stream);
+
 /* bf16(bf16(gelu_tanh(y[:, :N])) * m) as bf16 rows out [M, N] (ld = ldo), m = mul [M, N] (ld = ldm) or,
  * with mul NULL, y[:, N:2N] (y then holds 2N columns): k_gelu's and k_ple_gate's activation
  * (pipeline.py:102-107, 117-121) for the decode step, whose next linear is the bf16-activation
