@@ -22,6 +22,12 @@ struct GemvParams {
   uint32_t x_bytes, w_bytes;
   int M, N, K, KB;                 // KB = ceil(K / 64)
   int split;                       // waves per group of n-tiles, each taking every split-th k-block
+  // Activation epilogue (ACT template argument): 1, GELU pair: the weight is [gate; up] stacked
+  // (N = 2I, I a multiple of 16) and y [M, I] = bf16(bf16(gelu_tanh(g)) * u) with g, u the bf16
+  // outputs of the gate and up rows; 2, GELU times a multiplier: y = bf16(bf16(gelu_tanh(g)) * mul)
+  // with mul bf16 [M, N] (ld = ldm).
+  const uint16_t* mul; int64_t ldm;
+  int half_tiles;                  // ACT 1: I / 16, the up rows' first tile
 };
 
 // Widen 8 signed bytes (two dwords) to 8 bf16 values, exactly.
@@ -52,8 +58,9 @@ __device__ __forceinline__ v8bf widen8(uint32_t lo, uint32_t hi) {
 // LM head (K=1536, N=262144), 6.2 TB/s against 5.0 TB/s for the row-major weight, where each load
 // takes 64-byte pieces of 16 rows.  Row-major weights keep the default policy (a streamed half
 // line would be fetched twice).
-template <int TPW, int U, bool PACKED, int NWB>
+template <int TPW, int U, bool PACKED, int NWB, int ACT = 0>
 __global__ __launch_bounds__(NWB * 64) void gemv_kernel(GemvParams p) {
+  static_assert(ACT != 1 || TPW == 2, "a GELU pair is one gate and one up tile per wave");
   __shared__ v4f red[NWB][TPW][64];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -61,9 +68,11 @@ __global__ __launch_bounds__(NWB * 64) void gemv_kernel(GemvParams p) {
   const int ks = wave % p.split;
   const int groups_per_block = NWB / p.split;
   const int group = blockIdx.x * groups_per_block + group_in_block;
-  const int tile0 = group * TPW;
+  // ACT 1: group g multiplies gate tile g and up tile g + half_tiles
+  const int tile0 = ACT == 1 ? group : group * TPW;
+  const int tstride = ACT == 1 ? p.half_tiles : 1;
   const int ntiles = (p.N + 15) >> 4;
-  const bool active = tile0 < ntiles;
+  const bool active = ACT == 1 ? tile0 < p.half_tiles : tile0 < ntiles;
 
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.w, p.w_bytes);
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.x, p.x_bytes);
@@ -73,8 +82,8 @@ __global__ __launch_bounds__(NWB * 64) void gemv_kernel(GemvParams p) {
   uint32_t wbase[TPW];
 #pragma unroll
   for (int t = 0; t < TPW; ++t)
-    wbase[t] = PACKED ? uint32_t(tile0 + t) * uint32_t(p.KB) * 1024u + uint32_t(lane) * 16u
-                      : uint32_t((tile0 + t) * 16 + (lane & 15)) * uint32_t(p.ldw) + uint32_t(kc);
+    wbase[t] = PACKED ? uint32_t(tile0 + t * tstride) * uint32_t(p.KB) * 1024u + uint32_t(lane) * 16u
+                      : uint32_t((tile0 + t * tstride) * 16 + (lane & 15)) * uint32_t(p.ldw) + uint32_t(kc);
   constexpr uint32_t W_KB = PACKED ? 1024u : 64u;  // weight bytes between k-blocks
   constexpr int W_POL = PACKED ? 3 : 0;              // sc0 nt for the packed stream
   const uint32_t xbase = (uint32_t(mrow) * uint32_t(p.ldx) + uint32_t(kc)) * 2u;
@@ -130,6 +139,34 @@ __global__ __launch_bounds__(NWB * 64) void gemv_kernel(GemvParams p) {
   // acc[t] lane l: row m = l % 16, columns n0 .. n0+3 with n0 = (tile0 + t)*16 + 4*(l/16).
   const int m = lane & 15;
   if (m >= p.M) return;
+  auto scale_at = [&](int nn) -> float {
+    return p.s_f32 ? reinterpret_cast<const float*>(p.s)[nn] : bf16_to_f32(reinterpret_cast<const uint16_t*>(p.s)[nn]);
+  };
+  if constexpr (ACT != 0) {
+    // the bf16 GEMV outputs, then the activation with the row kernel's roundings
+    const int n0 = tile0 * 16 + 4 * (lane >> 4);
+    const int Nout = ACT == 1 ? p.half_tiles * 16 : p.N;
+    if (n0 >= Nout) return;
+    float o[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int nn = n0 + r;
+      if (nn >= Nout) { o[r] = 0.0f; continue; }
+      const float g = round_bf16(acc[0][r] * scale_at(nn));
+      const float u = ACT == 1 ? round_bf16(acc[1][r] * scale_at(p.half_tiles * 16 + nn))
+                               : bf16_to_f32(p.mul[int64_t(m) * p.ldm + nn]);
+      o[r] = round_bf16(round_bf16(gelu_tanh_f32(g)) * u);
+    }
+    uint16_t* dst = p.y + int64_t(m) * p.ldy + n0;
+    if (n0 + 3 < Nout && ((reinterpret_cast<uintptr_t>(dst) & 7) == 0)) {
+      *reinterpret_cast<v2u*>(dst) = v2u{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (n0 + r < Nout) dst[r] = f32_to_bf16(o[r]);
+    }
+    return;
+  }
 #pragma unroll
   for (int t = 0; t < TPW; ++t) {
     const int n0 = (tile0 + t) * 16 + 4 * (lane >> 4);
@@ -209,6 +246,31 @@ static void gemv_launch(const GemvParams& p0, hipStream_t stream) {
   }
 }
 
+// The few-tile launch with an activation epilogue: ACT 1 over I / 16 gate/up tile pairs (two tiles
+// per wave), ACT 2 over the N / 16 tiles.  The split and the unroll depth are the plain launch's
+// for the whole N (gemv_launch), so every tile's sum is added in the same order and the result is
+// the plain GEMV's, bit for bit, before the activation.
+template <bool PACKED, int ACT>
+static void gemv_launch_act(const GemvParams& p0, hipStream_t stream) {
+  GemvParams p = p0;
+  const int64_t ntiles = (p.N + 15) / 16;
+  const int64_t groups = ACT == 1 ? p.half_tiles : ntiles;
+  int split = 1;
+  while (split < 16 && ntiles * split < 4096 && split * 2 <= p.KB) split *= 2;
+  p.split = split;
+  constexpr int TPW = ACT == 1 ? 2 : 1;
+  if (split <= 4) {
+    const int gpb = 4 / split;
+    gemv_kernel<TPW, 4, PACKED, 4, ACT><<<unsigned((groups + gpb - 1) / gpb), 256, 0, stream>>>(p);
+  } else if (split == 8) {
+    gemv_kernel<TPW, 4, PACKED, 8, ACT><<<unsigned(groups), 512, 0, stream>>>(p);
+  } else if ((p.KB + 15) / 16 > 4 && (p.KB + 15) / 16 <= 6) {
+    gemv_kernel<TPW, 6, PACKED, 16, ACT><<<unsigned(groups), 1024, 0, stream>>>(p);
+  } else {
+    gemv_kernel<TPW, 4, PACKED, 16, ACT><<<unsigned(groups), 1024, 0, stream>>>(p);
+  }
+}
+
 }  // namespace w8a8
 
 using namespace w8a8;
@@ -253,6 +315,37 @@ extern "C" int w8a8_gemv_packed_bf16(const uint16_t* x, int64_t ldx, int64_t M, 
   p.M = int(M); p.N = int(N); p.K = int(K); p.KB = int((K + 63) / 64);
   gemv_launch<true>(p, stream);
   return check_launch("gemv_packed_bf16");
+}
+
+extern "C" int w8a8_gemv_packed_act_bf16(const uint16_t* x, int64_t ldx, int64_t M, const int8_t* packed, int64_t N,
+                                         int64_t K, const void* scales, int scale_is_f32, int act, const uint16_t* mul,
+                                         int64_t ldm, uint16_t* y, int64_t ldy, hipStream_t stream) {
+  if (!x || !packed || !scales || !y || (act == 2 && !mul)) return fail(W8A8_EINVAL, "gemv_packed_act: null pointer");
+  if (act != 1 && act != 2) return fail(W8A8_EINVAL, "gemv_packed_act: act %d (1: GELU pair, 2: GELU times mul)", act);
+  if (M < 1 || M > 16) return fail(W8A8_EINVAL, "gemv_packed_act: M=%lld, the GEMV takes 1..16 rows", (long long)M);
+  if (N < 1 || K < 16) return fail(W8A8_EINVAL, "gemv_packed_act: bad shape N=%lld K=%lld", (long long)N, (long long)K);
+  if (K % 16 != 0) return fail(W8A8_ENOTSUP, "gemv_packed_act: K=%lld must be a multiple of 16", (long long)K);
+  if (act == 1 && N % 32 != 0)
+    return fail(W8A8_ENOTSUP, "gemv_packed_act: a GELU pair needs N = 2I with I a multiple of 16, got N=%lld",
+                (long long)N);
+  const int64_t nout = act == 1 ? N / 2 : N;
+  if ((N + 15) / 16 >= 4096) return fail(W8A8_ENOTSUP, "gemv_packed_act: N=%lld above the few-tile shapes", (long long)N);
+  if (ldx < K || ldy < nout || (act == 2 && ldm < N)) return fail(W8A8_EINVAL, "gemv_packed_act: leading dimension too small");
+  if (ldx % 8 != 0 || (uintptr_t)x % 16 != 0 || (uintptr_t)packed % 16 != 0)
+    return fail(W8A8_EALIGN, "gemv_packed_act: x rows and the packed weight must be 16-byte aligned");
+  const int64_t wb = w8a8_gemv_packed_bytes(N, K);
+  const int64_t xb = ((M - 1) * ldx + K) * 2;
+  if (wb > INT32_MAX || xb > INT32_MAX) return fail(W8A8_ENOTSUP, "gemv_packed_act: operands above 2 GiB");
+  GemvParams p{};
+  p.x = x; p.ldx = ldx; p.w = packed; p.ldw = 0; p.s = scales; p.s_f32 = scale_is_f32 ? 1 : 0;
+  p.y = y; p.ldy = ldy; p.x_bytes = uint32_t(xb); p.w_bytes = uint32_t(wb);
+  p.M = int(M); p.N = int(N); p.K = int(K); p.KB = int((K + 63) / 64);
+  p.mul = mul; p.ldm = ldm; p.half_tiles = int(N / 32);
+  if (act == 1)
+    gemv_launch_act<true, 1>(p, stream);
+  else
+    gemv_launch_act<true, 2>(p, stream);
+  return check_launch("gemv_packed_act_bf16");
 }
 
 extern "C" int w8a8_gemv_bf16(const uint16_t* x, int64_t ldx, int64_t M, const int8_t* w, int64_t ldw, int64_t N,

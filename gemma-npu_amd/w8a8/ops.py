@@ -319,6 +319,42 @@ def rms_residual(y, res, w, eps, out=None, quant=False):
     return (out, q, sq) if quant else out
 
 
+def gemv_act_bf16(x, w, s, act, mul=None, out=None):
+    """gemv_bf16 with its activation in the epilogue (the decode path's MLP and per-layer-input
+    gate): act "gelu_pair" -> y [M, N/2] = bf16(bf16(gelu_tanh(g)) * u) for a [gate; up] stacked
+    GemvWeight; act "gelu_mul" -> y [M, N] = bf16(bf16(gelu_tanh(g)) * mul).  Bit for bit
+    gemv_bf16 followed by gelu_mul_bf16."""
+    _check(x, "x", torch.bfloat16)
+    if not isinstance(w, GemvWeight):
+        raise TypeError("gemv_act_bf16: w must be a packed GemvWeight")
+    if s.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"gemv_act_bf16: scales must be bf16 or fp32, got {s.dtype}")
+    _check(s, "s", s.dtype, 1)
+    code = {"gelu_pair": 1, "gelu_mul": 2}.get(act)
+    if code is None:
+        raise ValueError(f"gemv_act_bf16: act must be 'gelu_pair' or 'gelu_mul', got {act!r}")
+    M, K = x.shape
+    if w.K != K or s.shape[0] != w.N:
+        raise ValueError("gemv_act_bf16: operand shapes do not match")
+    nout = w.N // 2 if code == 1 else w.N
+    if code == 2:
+        if mul is None:
+            raise ValueError("gemv_act_bf16: 'gelu_mul' needs mul")
+        _check(mul, "mul", torch.bfloat16)
+        if tuple(mul.shape) != (M, w.N):
+            raise ValueError(f"gemv_act_bf16: mul {tuple(mul.shape)} does not match ({M}, {w.N})")
+    if out is None:
+        out = torch.empty((M, nout), dtype=torch.bfloat16, device=x.device)
+    _check(out, "out", torch.bfloat16)
+    if tuple(out.shape) != (M, nout):
+        raise ValueError(f"gemv_act_bf16: out has shape {tuple(out.shape)}, expected {(M, nout)}")
+    _same_device(x, w.data, s, mul, out)
+    call("w8a8_gemv_packed_act_bf16", x.data_ptr(), _ld(x), M, w.data.data_ptr(), w.N, K, s.data_ptr(),
+         1 if s.dtype == torch.float32 else 0, code, None if mul is None else mul.data_ptr(),
+         0 if mul is None else _ld(mul), out.data_ptr(), _ld(out), _stream(x))
+    return out
+
+
 def rms_residual_norm(y, res, w1, w2, eps, scalar=None):
     """(h, x): h = bf16(bf16(res + bf16(rms(y) * w1)) * scalar) and x = bf16(rms(h) * w2), one launch:
     k_post_attn's two norms (pipeline.py:95-99), or k_ple_out and the next layer's input norm

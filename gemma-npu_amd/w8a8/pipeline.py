@@ -418,10 +418,11 @@ class Decoder:
         o = attention.decode_at(q[:, 0], kc, vc, self.pos, p.window, 1.0, workspace=self.workspace)
         y = linear(o.reshape(1, -1), W["o"])
         h, x = ops.rms_residual_norm(y, h, p.norm_post_attn, p.norm_pre_ff, eps)
-        y = linear(ops.gelu_mul_bf16(linear(x, W["gate_up"])), W["down"])
+        gu = W["gate_up"]
+        y = linear(ops.gemv_act_bf16(x, gu.gemv_w, gu.sw_bf16, "gelu_pair"), W["down"])
         h = ops.rms_residual(y, h, p.norm_post_ff, eps)
-        y = linear(h, W["ple_gate"])
-        y = linear(ops.gelu_mul_bf16(y, per_layer[:, p.index]), W["ple_proj"])
+        pg = W["ple_gate"]
+        y = linear(ops.gemv_act_bf16(h, pg.gemv_w, pg.sw_bf16, "gelu_mul", mul=per_layer[:, p.index]), W["ple_proj"])
         if norm_next is None:
             return fused.k_ple_out(y, None, None, h, p.norm_post_ple, scalar[p.index], eps), None
         return ops.rms_residual_norm(y, h, p.norm_post_ple, norm_next, eps, scalar=scalar[p.index])

@@ -338,6 +338,18 @@ int w8a8_pack_gemv_weight(const int8_t *w, int64_t ldw, int64_t N, int64_t K, in
 int w8a8_gemv_packed_bf16(const uint16_t *x, int64_t ldx, int64_t M, const int8_t *packed, int64_t N, int64_t K,
                           const void *scales, int scale_is_f32, uint16_t *y, int64_t ldy, hipStream_t stream);
 
+/* w8a8_gemv_packed_bf16 with the activation that follows it on the decode path, in its epilogue:
+ *   act 1 (GELU pair): the packed weight holds [gate; up] stacked (N = 2I, I % 16 == 0); y [M, I] =
+ *     bf16(bf16(gelu_tanh(g)) * u) with g, u the bf16 GEMV outputs of gate row n and up row I + n
+ *     (the MLP's act(gate) * up on the decode rows, pipeline.py:102-107 without the quant);
+ *   act 2 (GELU times a multiplier): y [M, N] = bf16(bf16(gelu_tanh(g)) * mul[m, n]), mul bf16 [M, N]
+ *     (ld = ldm; the per-layer-input gate, pipeline.py:117-121 without the quant).
+ * Bit for bit the GEMV followed by w8a8_gelu_mul_bf16; one launch instead of two.  Shapes with
+ * fewer than 4096 n-tiles of 16 rows (the per-layer decode shapes). */
+int w8a8_gemv_packed_act_bf16(const uint16_t *x, int64_t ldx, int64_t M, const int8_t *packed, int64_t N, int64_t K,
+                              const void *scales, int scale_is_f32, int act, const uint16_t *mul, int64_t ldm,
+                              uint16_t *y, int64_t ldy, hipStream_t stream);
+
 /* ---- prefill attention ------------------------------------------------------------------ */
 
 /* o[h, i, :] = sum_j softmax_j(scale * q[h, i] . k[g, j]) v[g, j] with g = h / (H / KV), over the

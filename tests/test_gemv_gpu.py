@@ -171,3 +171,40 @@ def test_gemv_packed_lm_head_exact_on_integer_activations():
     acc = (xi.to(DEV).double() @ wd.double().t()).float()  # exact integers, |acc| < 2^24
     ref = (acc * s.to(DEV)[None, :]).to(torch.bfloat16)
     assert torch.equal(y, ref)
+
+
+@pytest.mark.parametrize("M, K, I", [(1, 1536, 6144), (4, 1536, 12288), (16, 256, 1536), (1, 64, 16)])
+def test_gemv_gelu_pair_equals_gemv_then_gelu_mul(M, K, I):
+    """The GEMV's GELU-pair epilogue on a [gate; up] stacked weight (the decode MLP) against the
+    GEMV writing [gate | up] followed by the row kernel's gelu_mul: bit for bit, bf16 and fp32
+    scales, including gate / up values around zero and in GELU's saturated range."""
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(M * 1000 + I)
+    x = (torch.randn(M, K, generator=g, device=dev) * 2).to(torch.bfloat16)
+    w = torch.randint(-127, 128, (2 * I, K), generator=g, dtype=torch.int8, device=dev)
+    pw = ops.pack_gemv_weight(w)
+    for s in ((torch.rand(2 * I, generator=g, device=dev) * 0.01).to(torch.bfloat16),
+              torch.rand(2 * I, generator=g, device=dev) * 0.01):
+        want = ops.gelu_mul_bf16(ops.gemv_bf16(x, pw, s))
+        got = ops.gemv_act_bf16(x, pw, s, "gelu_pair")
+        assert got.shape == (M, I)
+        assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("M, K, N", [(1, 1536, 256), (3, 1536, 256), (16, 2048, 1536)])
+def test_gemv_gelu_mul_equals_gemv_then_gelu_mul(M, K, N):
+    """The GEMV's GELU-times-multiplier epilogue (the decode step's per-layer-input gate) against the
+    GEMV followed by gelu_mul with the same multiplier rows, strided as the per-layer slice is."""
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(M * 100 + N)
+    x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+    w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8, device=dev)
+    pw = ops.pack_gemv_weight(w)
+    s = (torch.rand(N, generator=g, device=dev) * 0.01).to(torch.bfloat16)
+    table = torch.randn(M, 5, N, generator=g, device=dev).to(torch.bfloat16)
+    mul = table[:, 2]
+    want = ops.gelu_mul_bf16(ops.gemv_bf16(x, pw, s), mul)
+    got = ops.gemv_act_bf16(x, pw, s, "gelu_mul", mul=mul)
+    assert torch.equal(got, want)
+    with pytest.raises(ValueError, match="needs mul"):
+        ops.gemv_act_bf16(x, pw, s, "gelu_mul")
