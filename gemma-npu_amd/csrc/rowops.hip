@@ -289,6 +289,9 @@ struct QkvParams {
   const uint16_t* qw; const uint16_t* kw;                // q_norm / k_norm weights bf16 [D]
   uint16_t* q; uint16_t* k; uint16_t* v;                 // [H, T, D], [KV, T, D], [KV, T, D]
   float eps; int T, H, KV, slots;                        // slots = H (shared) or H + 2 KV
+  // Non-null: k and v are a key / value cache [KV, kv_rows, D] and token t's rows go to row
+  // *pos_dev + t (a decode step replayed from a graph); rows outside the cache are not written.
+  const int* pos_dev; int kv_rows;
 };
 
 template <int E>
@@ -419,6 +422,12 @@ __global__ __launch_bounds__(256) void qkv_kernel(QkvParams p) {
     dst = is_q ? p.q + (int64_t(slot) * p.T + t) * D : p.k + (int64_t(slot - p.H) * p.T + t) * D;
   } else {
     dst = p.v + (int64_t(slot - p.H - p.KV) * p.T + t) * D;
+  }
+  if (p.pos_dev && slot >= p.H) {
+    const int row = *p.pos_dev + t;
+    if (row < 0 || row >= p.kv_rows) return;  // (the whole wave: one item per wave)
+    const int hk = slot < p.H + p.KV ? slot - p.H : slot - p.H - p.KV;
+    dst = (slot < p.H + p.KV ? p.k : p.v) + (int64_t(hk) * p.kv_rows + row) * D;
   }
   store_bf16<E>(dst + p0, n1);
   store_bf16<E>(dst + p0 + HALF, n2);
@@ -684,7 +693,7 @@ static int k_ple_out(const RowInput& in, const uint16_t* h, int64_t ldh, const u
 
 static int k_qkv(const RowInput& in, const uint16_t* cos_, const uint16_t* sin_, int64_t ldcs, const uint16_t* qw,
                  const uint16_t* kw, float eps, int64_t T, int64_t H, int64_t KV, int64_t D, int shared, uint16_t* q,
-                 uint16_t* k, uint16_t* v, hipStream_t stream) {
+                 uint16_t* k, uint16_t* v, hipStream_t stream, const int* pos_dev = nullptr, int64_t kv_rows = 0) {
   const char* what = "k_qkv";
   if (T < 0 || H <= 0 || KV < 0 || (!shared && KV <= 0))
     return fail(W8A8_EINVAL, "k_qkv: bad shape T=%lld H=%lld KV=%lld", (long long)T, (long long)H, (long long)KV);
@@ -709,6 +718,7 @@ static int k_qkv(const RowInput& in, const uint16_t* cos_, const uint16_t* sin_,
   p.cs = cos_; p.sn = sin_; p.ldcs = ldcs; p.qw = qw; p.kw = shared ? nullptr : kw;
   p.q = q; p.k = k; p.v = v;
   p.eps = eps; p.T = int(T); p.H = int(H); p.KV = shared ? 0 : int(KV); p.slots = int(slots);
+  p.pos_dev = pos_dev; p.kv_rows = int(kv_rows);
   const dim3 grid{static_cast<unsigned>((T * slots + 3) / 4)};
 #define W8A8_QKV(E)                                                                  \
   do {                                                                               \
@@ -826,6 +836,18 @@ int w8a8_k_ple_out_y(const uint16_t* y, int64_t ldy, const uint16_t* h, int64_t 
                      hipStream_t stream) {
   return w8a8::k_ple_out(RowInput{y, ldy, nullptr, nullptr, false}, h, ldh, w_post_ple, scalar, eps, M, N, out, ldo,
                          stream);
+}
+
+int w8a8_k_qkv_cache_y(const uint16_t* y, int64_t ldy, const uint16_t* cos_, const uint16_t* sin_, int64_t ldcs,
+                       const uint16_t* qw, const uint16_t* kw, float eps, int64_t T, int64_t H, int64_t KV, int64_t D,
+                       uint16_t* q, uint16_t* k_cache, uint16_t* v_cache, int64_t kv_rows, const int32_t* pos,
+                       hipStream_t stream) {
+  if (!pos || !k_cache || !v_cache) return fail(W8A8_EINVAL, "k_qkv_cache: null pointer");
+  if ((uintptr_t)pos % 4) return fail(W8A8_EALIGN, "k_qkv_cache: pos must be 4-byte aligned");
+  if (kv_rows < 1 || kv_rows > INT32_MAX || KV * kv_rows * D > INT64_MAX / 2)
+    return fail(W8A8_EINVAL, "k_qkv_cache: kv_rows=%lld", (long long)kv_rows);
+  return w8a8::k_qkv(RowInput{y, ldy, nullptr, nullptr, false}, cos_, sin_, ldcs, qw, kw, eps, T, H, KV, D, 0, q,
+                     k_cache, v_cache, stream, pos, kv_rows);
 }
 
 int w8a8_k_qkv(const int32_t* acc, int64_t ldacc, const float* sx, const float* sw, const uint16_t* cos_,

@@ -58,6 +58,8 @@ SIGNATURES = {
     "w8a8_k_ple_gate_y": (_i32, [_p, _i64, _p, _i64, _i64, _i64, _p, _i64, _i32, _p, _p]),
     "w8a8_k_ple_out_y": (_i32, [_p, _i64, _p, _i64, _p, _p, _f32, _i64, _i64, _p, _i64, _p]),
     "w8a8_gelu_mul_bf16": (_i32, [_p, _i64, _p, _i64, _i64, _i64, _p, _i64, _p]),
+    "w8a8_k_qkv_cache_y": (_i32, [_p, _i64, _p, _p, _i64, _p, _p, _f32, _i64, _i64, _i64, _i64, _p, _p, _p, _i64, _p,
+                                   _p]),
     "w8a8_rms_residual_norm_bf16": (_i32, [_p, _i64, _p, _i64, _p, _p, _p, _f32, _i64, _i64, _p, _i64, _p, _i64, _p]),
     "w8a8_linear_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "w8a8_linear_bf16": (_i32, [_p, _i64, _p, _p, _i64, _i64, _i64, _i32, _i64, _p, _i64, _p, _f32, _p, _i64, _p,

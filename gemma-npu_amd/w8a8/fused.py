@@ -117,6 +117,38 @@ def k_qkv(acc, sx, sw, cos, sin, qw, kw, eps, H, KV, D, shared):
     return q, k, v
 
 
+def k_qkv_cache(y, cos, sin, qw, kw, eps, H, KV, D, k_cache, v_cache, pos):
+    """k_qkv on the decode step's bf16 GEMV rows y [T, (H + 2KV) D] (not a KV-shared layer), writing
+    the keys and values straight into the cache [KV, rows, D] at rows pos[0] + t (pos: an int32 device
+    tensor of one element; rows outside the cache are not written) -> q [H, T, D]."""
+    H, KV, D = int(H), int(KV), int(D)
+    _check(y, "y", torch.bfloat16)
+    T = y.shape[0]
+    if y.shape[1] < (H + 2 * KV) * D:
+        raise ValueError(f"y {tuple(y.shape)} does not cover {(H + 2 * KV) * D} columns")
+    for t, name in ((cos, "cos"), (sin, "sin")):
+        _check(t, name, torch.bfloat16)
+        if t.shape[0] != T or t.shape[1] != D:
+            raise ValueError(f"{name}: expected shape {(T, D)}, got {tuple(t.shape)}")
+    if cos.stride(0) != sin.stride(0):
+        raise ValueError("cos and sin must share a row stride")
+    for t, name in ((k_cache, "k_cache"), (v_cache, "v_cache")):
+        if not isinstance(t, torch.Tensor) or t.dtype != torch.bfloat16 or t.dim() != 3 or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous bf16 tensor [KV, rows, D]")
+        if t.shape[0] != KV or t.shape[2] != D:
+            raise ValueError(f"{name}: expected [{KV}, rows, {D}], got {tuple(t.shape)}")
+    if k_cache.shape != v_cache.shape:
+        raise ValueError("k_cache and v_cache differ in shape")
+    if not isinstance(pos, torch.Tensor) or pos.dtype != torch.int32 or pos.numel() != 1:
+        raise ValueError("pos must be an int32 tensor of one element")
+    q = torch.empty((H, T, D), dtype=torch.bfloat16, device=y.device)
+    _same_device(y, cos, sin, qw, kw, k_cache, v_cache, pos)
+    call("w8a8_k_qkv_cache_y", y.data_ptr(), _ld(y), cos.data_ptr(), sin.data_ptr(), _ld(cos), _vec(qw, "qw", D),
+         _vec(kw, "kw", D), float(eps), T, H, KV, D, q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+         k_cache.shape[1], pos.data_ptr(), _stream(y))
+    return q
+
+
 def k_attn_out(o, packed=False):
     """attention output [H, T, D] -> int8 rows [T, H*D] for o_proj."""
     _check(o, "o", torch.bfloat16, 3)

@@ -408,12 +408,12 @@ class Decoder:
 
         y = linear(x, W["qkv"])
         cos, sin = rope[p.kind]
-        q, k, v = fused.k_qkv(y, None, None, cos, sin, p.norm_q, p.norm_k, eps, p.heads, p.kv_heads, p.head_dim,
-                              p.shares_kv)
-        if not p.shares_kv:
+        if p.shares_kv:
+            q = fused.k_qkv(y, None, None, cos, sin, p.norm_q, None, eps, p.heads, p.kv_heads, p.head_dim, True)[0]
+        else:
             kc, vc = self.cache[p.index]
-            kc.index_copy_(1, self.pos64, k)
-            vc.index_copy_(1, self.pos64, v)
+            q = fused.k_qkv_cache(y, cos, sin, p.norm_q, p.norm_k, eps, p.heads, p.kv_heads, p.head_dim, kc, vc,
+                                  self.pos)
         kc, vc = self.cache[p.kv_source]
         o = attention.decode_at(q[:, 0], kc, vc, self.pos, p.window, 1.0, workspace=self.workspace)
         y = linear(o.reshape(1, -1), W["o"])

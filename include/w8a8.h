@@ -273,6 +273,15 @@ int w8a8_gelu_mul_bf16(const uint16_t *y, int64_t ldy, const uint16_t *mul, int6
 int w8a8_k_qkv_y(const uint16_t *y, int64_t ldy, const uint16_t *cos_, const uint16_t *sin_, int64_t ldcs,
                  const uint16_t *qw, const uint16_t *kw, float eps, int64_t T, int64_t H, int64_t KV, int64_t D,
                  int shared, uint16_t *q, uint16_t *k, uint16_t *v, hipStream_t stream);
+/* k_qkv_y for a decode step that writes its keys and values into the cache: k_cache / v_cache are
+ * [KV, kv_rows, D] bf16 (rows contiguous, heads kv_rows * D apart) and token t's key and value go to
+ * row *pos + t (pos: one int32 in device memory, so a step captured in a HIP graph writes at each new
+ * position); rows at or past kv_rows (or negative) are not written.  q as in k_qkv_y.  Not for
+ * KV-shared layers (they write no keys). */
+int w8a8_k_qkv_cache_y(const uint16_t *y, int64_t ldy, const uint16_t *cos_, const uint16_t *sin_, int64_t ldcs,
+                       const uint16_t *qw, const uint16_t *kw, float eps, int64_t T, int64_t H, int64_t KV, int64_t D,
+                       uint16_t *q, uint16_t *k_cache, uint16_t *v_cache, int64_t kv_rows, const int32_t *pos,
+                       hipStream_t stream);
 int w8a8_k_post_attn_y(const uint16_t *y, int64_t ldy, const uint16_t *res, int64_t ldr, const uint16_t *w_post,
                        const uint16_t *w_pre_ff, float eps, int64_t M, int64_t N, uint16_t *h, int64_t ldh, int8_t *q,
                        int64_t ldq, int q_packed, float *sq, hipStream_t stream);

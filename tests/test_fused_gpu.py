@@ -148,6 +148,34 @@ def test_k_qkv_strided_acc_and_cos():
         assert_bf16_close(f32(npy(got)), f32(ref), what="k_qkv strided", ulp_at=pair_mag(ref))
 
 
+@pytest.mark.parametrize("D, KV, T", [(256, 1, 1), (512, 1, 1), (128, 2, 3)])
+def test_k_qkv_cache_writes_the_cache_rows(D, KV, T):
+    """k_qkv_cache (the decode step's form) against k_qkv on the same bf16 rows: the same q, and the
+    same k / v written into rows pos .. pos+T-1 of the cache at a position held in device memory,
+    every other row untouched; a position outside the cache writes nothing."""
+    H, rows = 4 * KV, 40
+    N = (H + 2 * KV) * D
+    y = (torch.randn(T, N, generator=gen(40 + D)) * 0.5).to(torch.bfloat16).to(DEV)
+    ang = torch.rand(T, D, generator=gen(41)) * 6.0
+    cos, sin = ang.cos().to(torch.bfloat16).to(DEV), ang.sin().to(torch.bfloat16).to(DEV)
+    qw, kw = norm_weight(D, 42).to(DEV), norm_weight(D, 43).to(DEV)
+    q0, k0, v0 = fused.k_qkv(y, None, None, cos, sin, qw, kw, EPS, H, KV, D, False)
+    fill = torch.randn(KV, rows, D, generator=gen(44)).to(torch.bfloat16).to(DEV)
+    for p in (0, 17, rows - T):
+        kc, vc = fill.clone(), fill.clone()
+        pos = torch.tensor([p], dtype=torch.int32, device=DEV)
+        q = fused.k_qkv_cache(y, cos, sin, qw, kw, EPS, H, KV, D, kc, vc, pos)
+        assert torch.equal(q, q0)
+        assert torch.equal(kc[:, p:p + T], k0) and torch.equal(vc[:, p:p + T], v0)
+        keep = torch.ones(rows, dtype=torch.bool)
+        keep[p:p + T] = False
+        assert torch.equal(kc[:, keep.to(DEV)], fill[:, keep.to(DEV)]) and torch.equal(vc[:, keep.to(DEV)], fill[:, keep.to(DEV)])
+    for p in (rows, -T - 1, 1 << 20):
+        kc, vc = fill.clone(), fill.clone()
+        q = fused.k_qkv_cache(y, cos, sin, qw, kw, EPS, H, KV, D, kc, vc, torch.tensor([p], dtype=torch.int32, device=DEV))
+        assert torch.equal(q, q0) and torch.equal(kc, fill) and torch.equal(vc, fill)
+
+
 # ---- k_attn_out ---------------------------------------------------------------------------
 
 @pytest.mark.parametrize("strided", [False, True])
