@@ -95,14 +95,30 @@ class KVStore:
         return kb[:, :end], vb[:, :end]
 
     def to_cache(self, cfg, copy):
-        """A DynamicCache with every owning layer's keys and values (what HF's decode loop reads)."""
+        """A DynamicCache with every owning layer's keys and values (what HF's decode loop reads).
+
+        Each layer is left in the state its first `update` would leave (transformers cache_utils:
+        DynamicLayer.update keeps the keys and values, DynamicSlidingWindowLayer.update counts the T
+        tokens and keeps the last sliding_window - 1 of them) without that update's concatenation
+        onto an empty tensor, which copies every layer's keys and values once more.  The layers hold
+        the store's own tensors, or copies of what they keep when `copy` is set (buffers that a
+        later run overwrites)."""
         from transformers import DynamicCache
+        from transformers.cache_utils import DynamicLayer, DynamicSlidingWindowLayer
         cache = DynamicCache(config=cfg)
         for layer in sorted(self.kv):
             k, v = self.kv[layer]
-            if copy:
-                k, v = k.clone(), v.clone()
-            cache.update(k[None], v[None], layer)
+            k, v = k[None], v[None]
+            lw = cache.layers[layer]
+            if type(lw) not in (DynamicLayer, DynamicSlidingWindowLayer) or lw.is_initialized:
+                cache.update(k.clone() if copy else k, v.clone() if copy else v, layer)
+                continue
+            lw.lazy_initialization(k, v)
+            if lw.is_sliding:
+                lw.cumulative_length += k.shape[-2]
+                if not lw.record_past:
+                    k, v = k[:, :, -lw.sliding_window + 1:], v[:, :, -lw.sliding_window + 1:]
+            lw.keys, lw.values = (k.clone(), v.clone()) if copy else (k, v)
         return cache
 
 
