@@ -28,6 +28,110 @@ struct GemvParams {
   // with mul bf16 [M, N] (ld = ldm).
   const uint16_t* mul; int64_t ldm;
   int half_tiles;                  // ACT 1: I / 16, the up rows' first tile
+  // Row prologue (PRO template argument, M = 1): the activation row is not read from x but made by
+  // every workgroup from the previous step's output, as w8a8_rms_residual_norm_bf16 (norm2 set) or
+  // w8a8_rms_residual_bf16 (norm2 clear) would make it in a launch of its own:
+  //   h = bf16(res + bf16(rms(pro_y) * w1)) [then bf16(h * scalar)],  x = norm2 ? bf16(rms(h) * w2) : h
+  // (no res: h = bf16(rms(pro_y) * w1)).  Workgroup 0 stores h when pro_h is set.
+  const uint16_t* pro_y; const uint16_t* pro_res; const uint16_t* pro_w1; const uint16_t* pro_scalar;
+  const uint16_t* pro_w2; uint16_t* pro_h;
+  float pro_eps; int pro_norm2, pro_ch;  // pro_ch: the row kernel's 8-element chunks per lane for K
+};
+
+// The row prologue on one wave, in the arithmetic and order of the row kernel's one-wave rows
+// (row_chain_kernel with 64 threads, rowops.hip): lane t holds chunks c < CH of 8 elements at
+// k = 8 * (64 c + t); the sums of squares are added chunk by chunk, element by element, then across
+// the wave by wave_sum_dpp.  Its operands are fetched first (RowIn::load), before the kernel issues
+// its weight loads, so the arithmetic (RowIn::make) waits for them alone; the result goes to
+// xs [CH * 512] bf16 (zeros from K on).
+template <int CH>
+struct RowIn {
+  v4u y[CH], res[CH], w1[CH], w2[CH];
+  uint16_t scalar;
+
+  __device__ __forceinline__ void load(const GemvParams& p) {
+    const int t = threadIdx.x & 63;
+    scalar = p.pro_scalar ? *p.pro_scalar : uint16_t(0x3f80);
+    const v4u one = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};  // bf16 1.0 x 8
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int k = 8 * (64 * c + t);
+      const bool in = k < p.K;
+      y[c] = in ? *reinterpret_cast<const v4u*>(p.pro_y + k) : v4u{0u, 0u, 0u, 0u};
+      res[c] = (in && p.pro_res) ? *reinterpret_cast<const v4u*>(p.pro_res + k) : v4u{0u, 0u, 0u, 0u};
+      w1[c] = (in && p.pro_w1) ? *reinterpret_cast<const v4u*>(p.pro_w1 + k) : one;
+      w2[c] = (in && p.pro_norm2 && p.pro_w2) ? *reinterpret_cast<const v4u*>(p.pro_w2 + k) : one;
+    }
+  }
+
+  // The values stay packed as bf16 between steps (every intermediate the row kernel rounds to bf16
+  // is exactly a bf16), which keeps the prologue's registers few while the weights are in flight.
+  __device__ __forceinline__ void make(const GemvParams& p, uint16_t* xs) {
+    const int t = threadIdx.x & 63, N = p.K;
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      float v[8];
+      unpack8(y[c], v);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss += v[i] * v[i];
+    }
+    ss = wave_sum_dpp(ss);
+    const float r = 1.0f / sqrtf(ss / float(N) + p.pro_eps);
+    const float scl = bf16_to_f32(scalar);
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      float v[8], rv[8], wv[8];
+      unpack8(y[c], v);
+      unpack8(res[c], rv);
+      unpack8(w1[c], wv);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float n = v[i] * r;
+        if (p.pro_w1) n = n * wv[i];
+        v[i] = p.pro_res ? round_bf16(rv[i] + round_bf16(n)) : round_bf16(n);
+        if (p.pro_scalar) v[i] = round_bf16(v[i] * scl);
+      }
+      y[c] = pack8(v);  // h
+    }
+    if (p.pro_h && blockIdx.x == 0) {
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const int k = 8 * (64 * c + t);
+        if (k < N) *reinterpret_cast<v4u*>(p.pro_h + k) = y[c];
+      }
+    }
+    if (p.pro_norm2) {
+      float s2 = 0.0f;
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        float v[8];
+        unpack8(y[c], v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s2 += v[i] * v[i];
+      }
+      s2 = wave_sum_dpp(s2);
+      const float r2 = 1.0f / sqrtf(s2 / float(N) + p.pro_eps);
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        float v[8], wv[8];
+        unpack8(y[c], v);
+        unpack8(w2[c], wv);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          float n = v[i] * r2;
+          if (p.pro_w2) n = n * wv[i];
+          v[i] = round_bf16(n);
+        }
+        y[c] = pack8(v);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int k = 8 * (64 * c + t);
+      *reinterpret_cast<v4u*>(xs + k) = k < N ? y[c] : v4u{0u, 0u, 0u, 0u};
+    }
+  }
 };
 
 // Widen 8 signed bytes (two dwords) to 8 bf16 values, exactly.
@@ -58,10 +162,11 @@ __device__ __forceinline__ v8bf widen8(uint32_t lo, uint32_t hi) {
 // LM head (K=1536, N=262144), 6.2 TB/s against 5.0 TB/s for the row-major weight, where each load
 // takes 64-byte pieces of 16 rows.  Row-major weights keep the default policy (a streamed half
 // line would be fetched twice).
-template <int TPW, int U, bool PACKED, int NWB, int ACT = 0>
+template <int TPW, int U, bool PACKED, int NWB, int ACT = 0, int PRO = 0>
 __global__ __launch_bounds__(NWB * 64) void gemv_kernel(GemvParams p) {
   static_assert(ACT != 1 || TPW == 2, "a GELU pair is one gate and one up tile per wave");
   __shared__ v4f red[NWB][TPW][64];
+  __shared__ __attribute__((aligned(16))) uint16_t xs[PRO ? PRO * 512 : 8];  // PRO: the activation row
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int group_in_block = wave / p.split;
@@ -91,16 +196,64 @@ __global__ __launch_bounds__(NWB * 64) void gemv_kernel(GemvParams p) {
   v4f acc[TPW];
 #pragma unroll
   for (int t = 0; t < TPW; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+  // PRO: the activation row is made once per workgroup by its first wave (one row: M = 1) while
+  // every wave's first round of weight fragments is in flight.
+  RowIn<PRO ? PRO : 1> row;
+  v4i wpre[U][TPW];
+  if constexpr (PRO) {
+    if (wave == 0) row.load(p);
+    // Issued without branches (a fragment outside the weight is read past the buffer's end as
+    // zeros), so the prologue's arithmetic can wait for its own operands and leave these in flight.
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int kb = ks + u * p.split;
+      const bool ok = active && kb < p.KB && kb * 64 + kc < p.K;
+#pragma unroll
+      for (int t = 0; t < TPW; ++t)
+        wpre[u][t] = __builtin_bit_cast(
+            v4i, __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? wbase[t] + uint32_t(kb) * W_KB : 0x80000000u, 0, W_POL));
+    }
+    if (wave == 0) row.make(p, xs);
+    __syncthreads();
+  }
   if (active) {
     const int stride = p.split * U;
-    for (int kb0 = ks; kb0 < p.KB; kb0 += stride) {
+    int kb0 = ks;
+    if constexpr (PRO) {
+      // the first round: its weights are in registers, the row in LDS
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int kb = kb0 + u * p.split;
+        v4i xa = {0, 0, 0, 0}, xb = {0, 0, 0, 0};
+        if (kb < p.KB && kb * 64 + kc < p.K && mrow == 0) {
+          const v4i* xv = reinterpret_cast<const v4i*>(xs + kb * 64 + kc);
+          xa = xv[0];
+          xb = xv[1];
+        }
+#pragma unroll
+        for (int t = 0; t < TPW; ++t) {
+          const v8bf wa = widen8(uint32_t(wpre[u][t][0]), uint32_t(wpre[u][t][1]));
+          const v8bf wb = widen8(uint32_t(wpre[u][t][2]), uint32_t(wpre[u][t][3]));
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, __builtin_bit_cast(v8bf, xa), acc[t], 0, 0, 0);
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wb, __builtin_bit_cast(v8bf, xb), acc[t], 0, 0, 0);
+        }
+      }
+      kb0 += stride;
+    }
+    for (; kb0 < p.KB; kb0 += stride) {
       v4i wv[U][TPW], xa[U], xb[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int kb = kb0 + u * p.split;
         if (kb < p.KB && kb * 64 + kc < p.K) {
-          xa[u] = buf_load16(rx, xbase + uint32_t(kb) * 128u);
-          xb[u] = buf_load16(rx, xbase + uint32_t(kb) * 128u + 16u);
+          if constexpr (PRO) {
+            const v4i* xv = reinterpret_cast<const v4i*>(xs + kb * 64 + kc);
+            xa[u] = mrow == 0 ? xv[0] : v4i{0, 0, 0, 0};
+            xb[u] = mrow == 0 ? xv[1] : v4i{0, 0, 0, 0};
+          } else {
+            xa[u] = buf_load16(rx, xbase + uint32_t(kb) * 128u);
+            xb[u] = buf_load16(rx, xbase + uint32_t(kb) * 128u + 16u);
+          }
 #pragma unroll
           for (int t = 0; t < TPW; ++t)
             wv[u][t] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rw, wbase[t] + uint32_t(kb) * W_KB, 0, W_POL));
@@ -249,8 +402,9 @@ static void gemv_launch(const GemvParams& p0, hipStream_t stream) {
 // The few-tile launch with an activation epilogue: ACT 1 over I / 16 gate/up tile pairs (two tiles
 // per wave), ACT 2 over the N / 16 tiles.  The split and the unroll depth are the plain launch's
 // for the whole N (gemv_launch), so every tile's sum is added in the same order and the result is
-// the plain GEMV's, bit for bit, before the activation.
-template <bool PACKED, int ACT>
+// the plain GEMV's, bit for bit, before the activation.  ACT 0 is the plain few-tile launch; PRO
+// (1..3, the prologue row's chunks per lane) adds the row prologue.
+template <bool PACKED, int ACT, int PRO = 0>
 static void gemv_launch_act(const GemvParams& p0, hipStream_t stream) {
   GemvParams p = p0;
   const int64_t ntiles = (p.N + 15) / 16;
@@ -261,13 +415,13 @@ static void gemv_launch_act(const GemvParams& p0, hipStream_t stream) {
   constexpr int TPW = ACT == 1 ? 2 : 1;
   if (split <= 4) {
     const int gpb = 4 / split;
-    gemv_kernel<TPW, 4, PACKED, 4, ACT><<<unsigned((groups + gpb - 1) / gpb), 256, 0, stream>>>(p);
+    gemv_kernel<TPW, 4, PACKED, 4, ACT, PRO><<<unsigned((groups + gpb - 1) / gpb), 256, 0, stream>>>(p);
   } else if (split == 8) {
-    gemv_kernel<TPW, 4, PACKED, 8, ACT><<<unsigned(groups), 512, 0, stream>>>(p);
-  } else if ((p.KB + 15) / 16 > 4 && (p.KB + 15) / 16 <= 6) {
-    gemv_kernel<TPW, 6, PACKED, 16, ACT><<<unsigned(groups), 1024, 0, stream>>>(p);
+    gemv_kernel<TPW, 4, PACKED, 8, ACT, PRO><<<unsigned(groups), 512, 0, stream>>>(p);
+  } else if (!PRO && (p.KB + 15) / 16 > 4 && (p.KB + 15) / 16 <= 6) {  // K > 4096: never with the prologue
+    gemv_kernel<TPW, 6, PACKED, 16, ACT, 0><<<unsigned(groups), 1024, 0, stream>>>(p);
   } else {
-    gemv_kernel<TPW, 4, PACKED, 16, ACT><<<unsigned(groups), 1024, 0, stream>>>(p);
+    gemv_kernel<TPW, 4, PACKED, 16, ACT, PRO><<<unsigned(groups), 1024, 0, stream>>>(p);
   }
 }
 
@@ -346,6 +500,61 @@ extern "C" int w8a8_gemv_packed_act_bf16(const uint16_t* x, int64_t ldx, int64_t
   else
     gemv_launch_act<true, 2>(p, stream);
   return check_launch("gemv_packed_act_bf16");
+}
+
+static bool overlaps(const void* a, int64_t abytes, const void* b, int64_t bbytes) {
+  if (!a || !b) return false;
+  const uintptr_t a0 = reinterpret_cast<uintptr_t>(a), b0 = reinterpret_cast<uintptr_t>(b);
+  return a0 < b0 + uintptr_t(bbytes) && b0 < a0 + uintptr_t(abytes);
+}
+
+extern "C" int w8a8_gemv_packed_norm_bf16(const uint16_t* y, const uint16_t* res, const uint16_t* w1,
+                                          const uint16_t* scalar, int norm2, const uint16_t* w2, float eps, uint16_t* h,
+                                          const int8_t* packed, int64_t N, int64_t K, const void* scales,
+                                          int scale_is_f32, int act, const uint16_t* mul, uint16_t* out,
+                                          hipStream_t stream) {
+  const char* what = "gemv_packed_norm";
+  if (!y || !packed || !scales || !out || (act == 2 && !mul)) return fail(W8A8_EINVAL, "%s: null pointer", what);
+  if (act < 0 || act > 2) return fail(W8A8_EINVAL, "%s: act %d (0: none, 1: GELU pair, 2: GELU times mul)", what, act);
+  if (N < 1 || K < 16) return fail(W8A8_EINVAL, "%s: bad shape N=%lld K=%lld", what, (long long)N, (long long)K);
+  if (K % 16 != 0) return fail(W8A8_ENOTSUP, "%s: K=%lld must be a multiple of 16", what, (long long)K);
+  if (K > 1536) return fail(W8A8_ENOTSUP, "%s: K=%lld above the prologue's row of 1536", what, (long long)K);
+  if ((N + 15) / 16 >= 4096) return fail(W8A8_ENOTSUP, "%s: N=%lld above the few-tile shapes", what, (long long)N);
+  if (act == 1 && N % 32 != 0)
+    return fail(W8A8_ENOTSUP, "%s: a GELU pair needs N = 2I with I a multiple of 16, got N=%lld", what, (long long)N);
+  for (const void* q : {static_cast<const void*>(y), static_cast<const void*>(res), static_cast<const void*>(w1),
+                        static_cast<const void*>(w2), static_cast<const void*>(h), static_cast<const void*>(packed)})
+    if ((reinterpret_cast<uintptr_t>(q) & 15) != 0)
+      return fail(W8A8_EALIGN, "%s: the rows, norm weights and packed weight must be 16-byte aligned", what);
+  const int64_t nout = act == 1 ? N / 2 : N;
+  const int64_t rb = K * 2, ob = nout * 2;
+  // every workgroup reads y and res while workgroup 0 writes h and all of them write out
+  if (overlaps(h, rb, y, rb) || overlaps(h, rb, res, rb) || overlaps(h, rb, out, ob))
+    return fail(W8A8_EINVAL, "%s: h must not overlap y, res or out", what);
+  if (overlaps(out, ob, y, rb) || overlaps(out, ob, res, rb) || (act == 2 && overlaps(out, ob, mul, N * 2)))
+    return fail(W8A8_EINVAL, "%s: out must not overlap y, res or mul", what);
+  const int64_t wb = w8a8_gemv_packed_bytes(N, K);
+  if (wb > INT32_MAX) return fail(W8A8_ENOTSUP, "%s: packed weight above 2 GiB", what);
+  GemvParams p{};
+  p.x = nullptr; p.ldx = K; p.w = packed; p.ldw = 0; p.s = scales; p.s_f32 = scale_is_f32 ? 1 : 0;
+  p.y = out; p.ldy = nout; p.x_bytes = 0; p.w_bytes = uint32_t(wb);
+  p.M = 1; p.N = int(N); p.K = int(K); p.KB = int((K + 63) / 64);
+  p.mul = mul; p.ldm = N; p.half_tiles = int(N / 32);
+  p.pro_y = y; p.pro_res = res; p.pro_w1 = w1; p.pro_scalar = scalar; p.pro_w2 = w2; p.pro_h = h;
+  p.pro_eps = eps; p.pro_norm2 = norm2 ? 1 : 0;
+  // the row kernel's chunks of 8 per lane for a row of K (K <= 1536: one wave, at most three)
+  p.pro_ch = int((K + 511) / 512);
+#define W8A8_NORM_GEMV(CH)                                                   \
+  do {                                                                       \
+    if (act == 0) gemv_launch_act<true, 0, CH>(p, stream);                   \
+    else if (act == 1) gemv_launch_act<true, 1, CH>(p, stream);              \
+    else gemv_launch_act<true, 2, CH>(p, stream);                            \
+  } while (0)
+  if (p.pro_ch == 1) W8A8_NORM_GEMV(1);
+  else if (p.pro_ch == 2) W8A8_NORM_GEMV(2);
+  else W8A8_NORM_GEMV(3);
+#undef W8A8_NORM_GEMV
+  return check_launch("gemv_packed_norm_bf16");
 }
 
 extern "C" int w8a8_gemv_bf16(const uint16_t* x, int64_t ldx, int64_t M, const int8_t* w, int64_t ldw, int64_t N,

@@ -40,29 +40,6 @@ __global__ __launch_bounds__(256) void dequant_kernel(const int32_t* __restrict_
   out[int64_t(m) * ldo + n] = f32_to_bf16(v);
 }
 
-// Wave sum broadcast to every lane: butterflies inside each row of 16 lanes, then row_bcast:15 /
-// row_bcast:31 carry the row sums up to lane 63.  Rows a broadcast step leaves out add 0.
-__device__ __forceinline__ float wave_sum_dpp(float v) {
-  auto dpp = [](float x, int ctrl) {
-    const int xi = __builtin_bit_cast(int, x);
-    switch (ctrl) {
-      case 0xB1: return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, xi, 0xB1, 0xF, 0xF, false));
-      case 0x4E: return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, xi, 0x4E, 0xF, 0xF, false));
-      case 0x141: return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, xi, 0x141, 0xF, 0xF, false));
-      case 0x140: return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, xi, 0x140, 0xF, 0xF, false));
-      case 0x142: return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, xi, 0x142, 0xA, 0xF, false));
-      default: return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, xi, 0x143, 0xC, 0xF, false));
-    }
-  };
-  v += dpp(v, 0xB1);   // quad_perm [1,0,3,2]
-  v += dpp(v, 0x4E);   // quad_perm [2,3,0,1]
-  v += dpp(v, 0x141);  // row_half_mirror: 8 lanes
-  v += dpp(v, 0x140);  // row_mirror: 16 lanes
-  v += dpp(v, 0x142);  // row_bcast:15 into rows 1, 3
-  v += dpp(v, 0x143);  // row_bcast:31 into rows 2, 3
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
-}
-
 // Sum (or maximum) over a block of blockDim.x / 64 <= 4 waves, returned to every thread.  `slot`
 // is 4 floats of LDS used by this reduction only.
 template <bool MAX>
@@ -75,18 +52,6 @@ __device__ __forceinline__ float block_reduce(float v, float* slot) {
   float r = slot[0];
   for (int i = 1; i < nw; ++i) r = MAX ? absmax2(r, slot[i]) : r + slot[i];
   return r;
-}
-
-__device__ __forceinline__ void unpack8(v4u u, float (&v)[8]) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    v[2 * i] = __uint_as_float(u[i] << 16);
-    v[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
-  }
-}
-
-__device__ __forceinline__ v4u pack8(const float (&v)[8]) {
-  return v4u{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
 }
 
 enum RowOp { RC_NONE = 0, RC_GELU_MUL = 1, RC_NORM_RES = 2 };

@@ -71,6 +71,8 @@ SIGNATURES = {
     "w8a8_pack_gemv_weight": (_i32, [_p, _i64, _i64, _i64, _p, _p]),
     "w8a8_gemv_packed_bf16": (_i32, [_p, _i64, _i64, _p, _i64, _i64, _p, _i32, _p, _i64, _p]),
     "w8a8_gemv_packed_act_bf16": (_i32, [_p, _i64, _i64, _p, _i64, _i64, _p, _i32, _i32, _p, _i64, _p, _i64, _p]),
+    "w8a8_gemv_packed_norm_bf16": (_i32, [_p, _p, _p, _p, _i32, _p, _f32, _p, _p, _i64, _i64, _p, _i32, _i32, _p, _p,
+                                          _p]),
     "w8a8_attention_bf16": (_i32, [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                    _i64, _i64, _f32, _p, _i64, _i64, _p, _p]),
     "w8a8_attention_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64, _i64]),

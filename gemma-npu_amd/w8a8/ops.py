@@ -355,6 +355,50 @@ def gemv_act_bf16(x, w, s, act, mul=None, out=None):
     return out
 
 
+def gemv_norm_bf16(y, res, w1, eps, w, s, act=None, w2=None, norm2=True, scalar=None, mul=None, store_h=True):
+    """The decode row's GEMV with its input norm made in the same launch: (out, h) with
+    h = bf16(bf16(res + bf16(rms(y) * w1)) * scalar) (res None: the norm alone), x = bf16(rms(h) * w2)
+    when norm2 (else x = h), and out the GEMV of x (act None), or with act "gelu_pair" / "gelu_mul"
+    as gemv_act_bf16.  h and out are bit for bit rms_residual_norm / rms_residual followed by
+    gemv_bf16 / gemv_act_bf16; h is None unless store_h.  y, res [1, K]; mul [1, N]."""
+    _check(y, "y", torch.bfloat16)
+    if not isinstance(w, GemvWeight):
+        raise TypeError("gemv_norm_bf16: w must be a packed GemvWeight")
+    if s.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"gemv_norm_bf16: scales must be bf16 or fp32, got {s.dtype}")
+    _check(s, "s", s.dtype, 1)
+    code = {None: 0, "gelu_pair": 1, "gelu_mul": 2}.get(act)
+    if code is None:
+        raise ValueError(f"gemv_norm_bf16: act must be None, 'gelu_pair' or 'gelu_mul', got {act!r}")
+    M, K = y.shape
+    if M != 1 or w.K != K or s.shape[0] != w.N:
+        raise ValueError(f"gemv_norm_bf16: one row of {w.K} expected, got {tuple(y.shape)}")
+    if res is not None:
+        _check(res, "res", torch.bfloat16)
+        if tuple(res.shape) != (1, K):
+            raise ValueError("gemv_norm_bf16: res does not match y")
+    for t, name in ((w1, "w1"), (w2, "w2")):
+        if t is not None:
+            _check(t, name, torch.bfloat16, 1)
+    if scalar is not None and (scalar.dtype != torch.bfloat16 or scalar.numel() != 1):
+        raise ValueError("gemv_norm_bf16: scalar must be one bf16 value")
+    if code == 2:
+        if mul is None:
+            raise ValueError("gemv_norm_bf16: 'gelu_mul' needs mul")
+        _check(mul, "mul", torch.bfloat16)
+        if tuple(mul.shape) != (1, w.N):
+            raise ValueError(f"gemv_norm_bf16: mul {tuple(mul.shape)} does not match (1, {w.N})")
+    nout = w.N // 2 if code == 1 else w.N
+    out = torch.empty((1, nout), dtype=torch.bfloat16, device=y.device)
+    h = torch.empty((1, K), dtype=torch.bfloat16, device=y.device) if store_h else None
+    _same_device(y, res, w1, w2, scalar, w.data, s, mul)
+    ptr = lambda t: None if t is None else t.data_ptr()
+    call("w8a8_gemv_packed_norm_bf16", y.data_ptr(), ptr(res), ptr(w1), ptr(scalar), 1 if norm2 else 0, ptr(w2),
+         float(eps), ptr(h), w.data.data_ptr(), w.N, K, s.data_ptr(), 1 if s.dtype == torch.float32 else 0, code,
+         ptr(mul), out.data_ptr(), _stream(y))
+    return out, h
+
+
 def rms_residual_norm(y, res, w1, w2, eps, scalar=None):
     """(h, x): h = bf16(bf16(res + bf16(rms(y) * w1)) * scalar) and x = bf16(rms(h) * w2), one launch:
     k_post_attn's two norms (pipeline.py:95-99), or k_ple_out and the next layer's input norm

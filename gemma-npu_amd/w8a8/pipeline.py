@@ -318,7 +318,9 @@ class Decoder:
     (k_qkv); the key and value written into the cache at the token's position; the decode attention
     over the cache (local_attn.py:44-83); and the norms, residuals, GELU-tanh products and
     per-layer-input steps of pipeline.py:66-127 without the activation quant, since the next linear
-    reads bf16.  The token, its position and the key / value cache [KV, max_len, head_dim] of every
+    reads bf16.  Each residual + norm step is the prologue of the GEMV that reads its result (the
+    norm is made in that launch, bit for bit the row kernel's), so a layer is nine launches: qkv,
+    k_qkv, two of attention, o, gate/up, down, per-layer gate, per-layer projection.  The token, its position and the key / value cache [KV, max_len, head_dim] of every
     layer that owns keys live in device memory, so a step does not depend on host values: capture()
     records one step in a HIP graph and each replay decodes the next token.  The next token is the
     argmax of the last logits (greedy), chosen on the device.
@@ -359,6 +361,14 @@ class Decoder:
             ws = max(ws, attention.decode_at_workspace_bytes(p.heads, p.kv_heads, self.max_len, p.head_dim,
                                                              p.window))
         self.workspace = torch.empty(ws, dtype=torch.uint8, device=dev)
+        # The final norm joins the last layer's per-layer-input norm in one row-kernel launch, with
+        # its weight as the model's module applies it (x * (mean(x^2) + eps)^-0.5 * w, or no weight).
+        norm = self.lm.norm
+        self.final_norm = getattr(norm, "weight", None) if getattr(norm, "with_scale", True) else None
+        if float(getattr(norm, "eps", self.cfg.rms_norm_eps)) != float(self.cfg.rms_norm_eps):
+            raise ValueError("Decoder: the final norm's eps differs from the layers' rms_norm_eps")
+        # the residual stream's norms as the prologue of the linear that reads them (hidden <= 1536)
+        self.fuse_norms = self.cfg.hidden_size <= 1536 and self.cfg.hidden_size % 16 == 0
         self.length = None
         self.graph = None
 
@@ -401,29 +411,47 @@ class Decoder:
         self.emitted.index_copy_(0, self.n_emitted, nxt)
         self.n_emitted.add_(1)
 
-    def _logits(self, h):
-        """The model's head on the token's row as HF's decode call computes it (the loop this replaces):
-        final norm, LM head, and the logit softcap in the model's dtype, then fp32.  (The prefill
+    def _logits(self, x):
+        """The model's head on the token's final-norm row x as HF's decode call computes it (the loop
+        this replaces): LM head, and the logit softcap in the model's dtype, then fp32.  (The prefill
         pipeline takes the softcap in fp32, as pipeline.py:334-338 does.)"""
-        logits = self.pre.model.lm_head(self.lm.norm(h[None]))[0, -1]
+        logits = self.pre.model.lm_head(x[None])[0, -1]
         cap = self.cfg.final_logit_softcapping
         if cap:
             logits = torch.tanh(logits / cap) * cap
         return logits.float()
 
-    def _layer(self, p, h, x, per_layer, scalar, rope, norm_next):
-        """Decoder layer p on the token's row h [1, hidden] at the device-held position, x its input
-        norm; rope maps the attention kind to its (cos, sin) rows [1, head_dim] at that position.
-        Returns the layer's output row and, with norm_next (the next layer's input-norm weight), that
-        norm of it from the same launch (else None)."""
+    def _norm_linear(self, pend, w, act=None, mul=None):
+        """The linear w on the residual stream's norm: pend = (y, res, w1, scalar, w2, store) describes
+        h = bf16(bf16(res + bf16(rms(y) * w1)) * scalar) and x = bf16(rms(h) * w2) (x = h without w2,
+        h = the norm alone without res).  Returns (w's output on x, h or None unless store).  With a
+        hidden size of at most 1536 the norm is the GEMV's own prologue (one launch); otherwise the row
+        kernel runs first."""
+        y, res, w1, scalar, w2, store = pend
         eps = self.cfg.rms_norm_eps
+        if self.fuse_norms:
+            return ops.gemv_norm_bf16(y, res, w1, eps, w.gemv_w, w.sw_bf16, act=act, w2=w2, norm2=w2 is not None,
+                                      scalar=scalar, mul=mul, store_h=store)
+        if w2 is not None:
+            h, x = ops.rms_residual_norm(y, res, w1, w2, eps, scalar=scalar)
+        else:
+            h = x = ops.rms_residual(y, res, w1, eps)
+        out = (ops.gemv_bf16(x, w.gemv_w, w.sw_bf16) if act is None
+               else ops.gemv_act_bf16(x, w.gemv_w, w.sw_bf16, act, mul=mul))
+        return out, (h if store else None)
+
+    def _layer(self, p, h, pend, per_layer, scalar, rope, norm_next):
+        """Decoder layer p on the token's row at the device-held position: h [1, hidden] is the residual
+        stream before the layer's input norm and pend how that norm is made (_norm_linear); rope maps
+        the attention kind to its (cos, sin) rows [1, head_dim] at that position.  Returns the
+        residual stream and the pending norm after the layer: the next layer's input norm with
+        norm_next, else the model's final norm."""
         W = p.weights
-
-        def linear(x, w):
-            return ops.gemv_bf16(x, w.gemv_w, w.sw_bf16)
-
-        y = linear(x, W["qkv"])
+        y, hn = self._norm_linear(pend, W["qkv"])
+        if hn is not None:
+            h = hn
         cos, sin = rope[p.kind]
+        eps = self.cfg.rms_norm_eps
         if p.shares_kv:
             q = fused.k_qkv(y, None, None, cos, sin, p.norm_q, None, eps, p.heads, p.kv_heads, p.head_dim, True)[0]
         else:
@@ -432,16 +460,13 @@ class Decoder:
                                   self.pos)
         kc, vc = self.cache[p.kv_source]
         o = attention.decode_at(q[:, 0], kc, vc, self.pos, p.window, 1.0, workspace=self.workspace)
-        y = linear(o.reshape(1, -1), W["o"])
-        h, x = ops.rms_residual_norm(y, h, p.norm_post_attn, p.norm_pre_ff, eps)
-        gu = W["gate_up"]
-        y = linear(ops.gemv_act_bf16(x, gu.gemv_w, gu.sw_bf16, "gelu_pair"), W["down"])
-        h = ops.rms_residual(y, h, p.norm_post_ff, eps)
-        pg = W["ple_gate"]
-        y = linear(ops.gemv_act_bf16(h, pg.gemv_w, pg.sw_bf16, "gelu_mul", mul=per_layer[:, p.index]), W["ple_proj"])
-        if norm_next is None:
-            return fused.k_ple_out(y, None, None, h, p.norm_post_ple, scalar[p.index], eps), None
-        return ops.rms_residual_norm(y, h, p.norm_post_ple, norm_next, eps, scalar=scalar[p.index])
+        y = ops.gemv_bf16(o.reshape(1, -1), W["o"].gemv_w, W["o"].sw_bf16)
+        g, h = self._norm_linear((y, h, p.norm_post_attn, None, p.norm_pre_ff, True), W["gate_up"], "gelu_pair")
+        y = ops.gemv_bf16(g, W["down"].gemv_w, W["down"].sw_bf16)
+        g, h = self._norm_linear((y, h, p.norm_post_ff, None, None, True), W["ple_gate"], "gelu_mul",
+                                 mul=per_layer[:, p.index])
+        y = ops.gemv_bf16(g, W["ple_proj"].gemv_w, W["ple_proj"].sw_bf16)
+        return h, (y, h, p.norm_post_ple, scalar[p.index], norm_next, True)
 
     @torch.inference_mode()
     def step(self):
@@ -463,11 +488,13 @@ class Decoder:
         rope = {kind: (c.index_select(0, self.pos64), s.index_select(0, self.pos64))
                 for kind, (c, s) in self.rope.items()}
         plans = self.pre.plans
-        x = ops.rms_residual(h, None, plans[0].norm_in, self.cfg.rms_norm_eps)
+        pend = (h, None, plans[0].norm_in, None, None, False)
         for i, p in enumerate(plans):
-            nxt = plans[i + 1].norm_in if i + 1 < len(plans) else None
-            h, x = self._layer(p, h, x, per_layer, scalar, rope, nxt)
-        logits = self._logits(h)
+            nxt = plans[i + 1].norm_in if i + 1 < len(plans) else self.final_norm
+            h, pend = self._layer(p, h, pend, per_layer, scalar, rope, nxt)
+        y, res, w1, sc, w2, _ = pend
+        _, x = ops.rms_residual_norm(y, res, w1, w2, self.cfg.rms_norm_eps, scalar=sc)
+        logits = self._logits(x)
         self._emit(logits)
         self.pos.add_(1)
         self.pos64.add_(1)

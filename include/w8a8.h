@@ -359,6 +359,22 @@ int w8a8_gemv_packed_act_bf16(const uint16_t *x, int64_t ldx, int64_t M, const i
                               const void *scales, int scale_is_f32, int act, const uint16_t *mul, int64_t ldm,
                               uint16_t *y, int64_t ldy, hipStream_t stream);
 
+/* One decode row (M = 1) whose GEMV input is the residual stream's norm, made in the same launch:
+ *   h = bf16(res + bf16(rms(y) * w1)), then h = bf16(h * scalar[0]) when scalar is given
+ *   (no res: h = bf16(rms(y) * w1); no w1: no weight), x = norm2 ? bf16(rms(h) * w2) : h,
+ *   out = the GEMV of x (act 0), or with act 1 / 2 as w8a8_gemv_packed_act_bf16 (mul [N]).
+ * h and x are what w8a8_rms_residual_norm_bf16 (norm2 = 1) or w8a8_rms_residual_bf16 (norm2 = 0)
+ * write, bit for bit, and out is then the GEMV's result on that x: the post-attention / post-MLP /
+ * per-layer-input norms of the decode step (pipeline.py:95-99, 110-114, 124-127 on one row) each
+ * become the prologue of the next linear instead of a launch of their own.  Every workgroup makes
+ * x from y and res; workgroup 0 stores h when h is non-null, so h must not overlap y, res or out,
+ * and out must not overlap y, res or mul.  y, res, h: bf16 [K], K % 16 == 0, K <= 1536; w1, w2
+ * bf16 [K]; 16-byte aligned.  Shapes with fewer than 4096 n-tiles (the per-layer decode shapes). */
+int w8a8_gemv_packed_norm_bf16(const uint16_t *y, const uint16_t *res, const uint16_t *w1, const uint16_t *scalar,
+                               int norm2, const uint16_t *w2, float eps, uint16_t *h, const int8_t *packed, int64_t N,
+                               int64_t K, const void *scales, int scale_is_f32, int act, const uint16_t *mul,
+                               uint16_t *out, hipStream_t stream);
+
 /* ---- prefill attention ------------------------------------------------------------------ */
 
 /* o[h, i, :] = sum_j softmax_j(scale * q[h, i] . k[g, j]) v[g, j] with g = h / (H / KV), over the

@@ -83,3 +83,24 @@ def test_decoder_refusals():
         dec.step()
     with pytest.raises(ValueError, match="max_len"):
         Decoder(Prefill(ours), max_len=1)
+
+
+@torch.inference_mode()
+def test_norm_prologues_match_the_row_kernels():
+    """The residual + norm steps made in the prologue of the GEMV that reads them against the same steps
+    as row-kernel launches of their own (hidden sizes above the prologue's 1536 take that route):
+    the same logits and tokens bit for bit, eager and graph-replayed."""
+    from w8a8.pipeline import Decoder, Prefill
+    ours = engine_model(build(seed=37))
+    ids = torch.randint(0, 512, (1, 11), generator=torch.Generator().manual_seed(38))
+    fused, rows = Decoder(Prefill(ours), max_len=40), Decoder(Prefill(ours), max_len=40)
+    assert fused.fuse_norms
+    rows.fuse_norms = False
+    fused.start(ids)
+    rows.start(ids)
+    for i in range(10):
+        assert torch.equal(fused.step(), rows.step()), f"step {i}"
+    assert torch.equal(fused.capture(), rows.capture())
+    for i in range(5):
+        assert torch.equal(fused.replay(), rows.replay()), f"replay {i}"
+    assert torch.equal(fused.emitted, rows.emitted)

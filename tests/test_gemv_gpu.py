@@ -208,3 +208,73 @@ def test_gemv_gelu_mul_equals_gemv_then_gelu_mul(M, K, N):
     assert torch.equal(got, want)
     with pytest.raises(ValueError, match="needs mul"):
         ops.gemv_act_bf16(x, pw, s, "gelu_mul")
+
+
+@pytest.mark.parametrize("K, N, act", [(1536, 2560, None), (1536, 2 * 6144, "gelu_pair"), (1536, 256, "gelu_mul"),
+                                       (256, 640, None), (1024, 96, "gelu_pair"), (1296, 200, None)])
+def test_gemv_norm_equals_row_kernel_then_gemv(K, N, act):
+    """The decode GEMV with its input norm made in the same launch (the post-attention, post-MLP and
+    per-layer-input norms of the decode step as the next linear's prologue) against the row kernel
+    (rms_residual_norm, or rms_residual without the second norm) followed by the GEMV: h and the
+    GEMV's output bit for bit, with and without the residual, the per-layer scalar and the second
+    norm.  K = 1296 leaves the last k-block partial; K = 256 / 1024 / 1536 take one, two and three
+    8-element chunks per lane."""
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(K * 7 + N)
+    y = (torch.randn(1, K, generator=g, device=dev) * 3).to(torch.bfloat16)
+    res = (torch.randn(1, K, generator=g, device=dev) * 5).to(torch.bfloat16)
+    w1 = (torch.rand(K, generator=g, device=dev) + 0.5).to(torch.bfloat16)
+    w2 = (torch.rand(K, generator=g, device=dev) * 2).to(torch.bfloat16)
+    scalar = torch.tensor([0.75], device=dev).to(torch.bfloat16)
+    w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8, device=dev)
+    pw = ops.pack_gemv_weight(w)
+    s = (torch.rand(N, generator=g, device=dev) * 0.01).to(torch.bfloat16)
+    mul = torch.randn(1, 3, N, generator=g, device=dev).to(torch.bfloat16)[:, 1] if act == "gelu_mul" else None
+    eps = 1e-6
+    for r, sc, norm2 in ((res, None, True), (res, scalar, True), (res, None, False), (None, None, False)):
+        if norm2:
+            h_ref, x_ref = ops.rms_residual_norm(y, r, w1, w2, eps, scalar=sc)
+        else:
+            assert sc is None
+            h_ref = ops.rms_residual(y, r, w1, eps)
+            x_ref = h_ref
+        want = ops.gemv_bf16(x_ref, pw, s) if act is None else ops.gemv_act_bf16(x_ref, pw, s, act, mul=mul)
+        got, h = ops.gemv_norm_bf16(y, r, w1, eps, pw, s, act=act, w2=w2 if norm2 else None, norm2=norm2,
+                                    scalar=sc, mul=mul)
+        assert torch.equal(h, h_ref), (r is None, sc is None, norm2)
+        assert torch.equal(got, want), (r is None, sc is None, norm2)
+    got, h = ops.gemv_norm_bf16(y, res, w1, eps, pw, s, act=act, w2=w2, mul=mul, store_h=False)
+    _, x_ref = ops.rms_residual_norm(y, res, w1, w2, eps)
+    want = ops.gemv_bf16(x_ref, pw, s) if act is None else ops.gemv_act_bf16(x_ref, pw, s, act, mul=mul)
+    assert h is None and torch.equal(got, want)
+
+
+def test_gemv_norm_refusals():
+    """The fused norm + GEMV refuses what its one-wave prologue and concurrent workgroups cannot do:
+    more than one row, K above 1536, h overlapping the rows every workgroup reads, the LM head's
+    many-tile shape."""
+    from w8a8._lib import W8A8Error
+    dev = torch.device("cuda")
+    K = 1536
+    y = torch.randn(1, K, device=dev).to(torch.bfloat16)
+    w1 = torch.ones(K, device=dev).to(torch.bfloat16)
+    pw = ops.pack_gemv_weight(torch.ones((64, K), dtype=torch.int8, device=dev))
+    s = torch.ones(64, device=dev).to(torch.bfloat16)
+    with pytest.raises(ValueError, match="one row"):
+        ops.gemv_norm_bf16(torch.randn(2, K, device=dev).to(torch.bfloat16), None, w1, 1e-6, pw, s)
+    big = ops.pack_gemv_weight(torch.ones((64, 2048), dtype=torch.int8, device=dev))
+    y2 = torch.randn(1, 2048, device=dev).to(torch.bfloat16)
+    with pytest.raises(W8A8Error, match="above the prologue"):
+        ops.gemv_norm_bf16(y2, None, None, 1e-6, big, s)
+    buf = torch.zeros(2 * K, dtype=torch.bfloat16, device=dev)
+    out = torch.empty(64, dtype=torch.bfloat16, device=dev)
+    from w8a8._lib import call
+    with pytest.raises(W8A8Error, match="h must not overlap"):
+        call("w8a8_gemv_packed_norm_bf16", y.data_ptr(), buf.data_ptr(), w1.data_ptr(), None, 0, None, 1e-6,
+             buf.data_ptr() + 64, pw.data.data_ptr(), 64, K, s.data_ptr(), 0, 0, None, out.data_ptr(), None)
+    with pytest.raises(W8A8Error, match="out must not overlap"):
+        call("w8a8_gemv_packed_norm_bf16", y.data_ptr(), None, w1.data_ptr(), None, 0, None, 1e-6,
+             None, pw.data.data_ptr(), 64, K, s.data_ptr(), 0, 0, None, y.data_ptr(), None)
+    head = ops.pack_gemv_weight(torch.ones((65536, K), dtype=torch.int8, device=dev))
+    with pytest.raises(W8A8Error, match="few-tile"):
+        ops.gemv_norm_bf16(y, None, w1, 1e-6, head, torch.ones(65536, device=dev).to(torch.bfloat16))
