@@ -686,8 +686,8 @@ def native_decode_bench(model, ids, n):
         del dec
     res["what"] = ("w8a8.pipeline.Decoder after the whole-prompt prefill: per token and layer the int8 GEMVs with "
                    "bf16 activations, k_qkv, the key / value cache write, the decode attention at a device-held "
-                   "position, the row kernels between; greedy argmax on the device; the graph form replays one "
-                   "captured step per token")
+                   "position, the residual norms made in the prologue of the GEMV that reads them; greedy argmax on "
+                   "the device; the graph form replays one captured step per token")
     return res
 
 
