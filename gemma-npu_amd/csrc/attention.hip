@@ -1189,6 +1189,14 @@ struct DecodeParams {
   // nchunk_grid = nchunk.
   const int* pos_dev;
   int window, nchunk_grid;
+  // k_qkv in the kernel (qkv_y non-null; with pos_dev, G <= 8): q is made from the token's qkv row
+  // [H*D q | KV*D k | KV*D v] (bf16) -- per head RMS norm with qw (null: no weight) and RoPE with the
+  // cos / sin rows [D] -- instead of read from q; with kv_write the workgroup holding the position
+  // also makes the token's key (norm with kw, RoPE) and value (norm without weight) of its KV head,
+  // writes them into k / v at the position (when it is inside the Tk rows) and attends to them there.
+  const uint16_t* qkv_y; const uint16_t* rope_c; const uint16_t* rope_s;
+  const uint16_t* qw; const uint16_t* kw;
+  float qkv_eps; int kv_write; uint32_t qkv_bytes;  // bytes of the qkv row
 };
 
 // The call's query position, first key, live chunks and key bound: the host's, or with pos_dev the
@@ -1206,6 +1214,28 @@ __device__ __forceinline__ DecodeGeom decode_geom(const DecodeParams& p) {
   return DecodeGeom{pos, klo, nchunk, pos + 1};
 }
 
+// E bf16 values as the raw words they are loaded in (unpacked to fp32 when used); zero until loaded.
+template <int E>
+struct Bf16Words {
+  uint32_t w[E == 4 ? 2 : 1] = {};
+  // from byte offset off of the buffer r (past its end: zeros)
+  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    if constexpr (E == 4) {
+      const v2u a = __builtin_bit_cast(v2u, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+      w[0] = a[0];
+      w[1] = a[1];
+    } else if constexpr (E == 2) {
+      w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+    } else {
+      w[0] = __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+    }
+  }
+  __device__ __forceinline__ void unpack(float (&o)[E]) const {
+#pragma unroll
+    for (int e = 0; e < E; ++e) o[e] = __uint_as_float((e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16));
+  }
+};
+
 template <int D>
 __global__ __launch_bounds__(256, 2) void attn_decode_split_kernel(DecodeParams p) {
   constexpr int DEC_C = dec_chunk(D);
@@ -1216,12 +1246,14 @@ __global__ __launch_bounds__(256, 2) void attn_decode_split_kernel(DecodeParams 
   constexpr int NKK = D / 32;
   constexpr int NDT = D / 64;                // 16-wide d tiles per wave
   constexpr int DMA = DEC_C * KCH / 256;     // DMA instructions per thread per operand
-  __shared__ __attribute__((aligned(1024))) char lds[2 * KV_BYTES + 16 * PLD * 2 + 2 * 4 * 16 * 4];
+  constexpr int QBYTES = 8 * D * 2;          // the made q rows of up to 8 heads (k_qkv in the kernel)
+  __shared__ __attribute__((aligned(1024))) char lds[2 * KV_BYTES + 16 * PLD * 2 + 2 * 4 * 16 * 4 + QBYTES];
   char* const kl = lds;
   char* const vl = lds + KV_BYTES;
   uint16_t* const pl = reinterpret_cast<uint16_t*>(lds + 2 * KV_BYTES);
   float* const smax = reinterpret_cast<float*>(lds + 2 * KV_BYTES + 16 * PLD * 2);  // [4 waves][16]
   float* const ssum = smax + 64;
+  uint16_t* const ql = reinterpret_cast<uint16_t*>(lds + 2 * KV_BYTES + 16 * PLD * 2 + 2 * 4 * 16 * 4);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int qi = lane & 15, qq = lane >> 4;
@@ -1231,6 +1263,37 @@ __global__ __launch_bounds__(256, 2) void attn_decode_split_kernel(DecodeParams 
   const int kc = geo.klo + chunk * DEC_C;    // first key of the chunk
   const __amdgpu_buffer_rsrc_t rk = make_rsrc(p.k + int64_t(g) * p.khs, p.k_bytes);
   const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.v + int64_t(g) * p.vhs, p.v_bytes);
+
+  // k_qkv in the kernel: wave w makes q heads w and w + 4 of the group; in the workgroup holding the
+  // position (with kv_write) wave 0 also makes the key and wave 1 the value.  Their operands are
+  // fetched as raw bf16 words before the DMAs are issued and unpacked after, so the DMAs go out first.
+  constexpr int E = D / 128, HALF = D / 2;
+  const bool fused = p.qkv_y != nullptr;
+  const bool make_kv = fused && p.kv_write && chunk == geo.nchunk - 1 && geo.pos >= 0 && geo.pos < p.Tk;
+  const int p0 = lane * E;
+  // operand o, half h: raw[o][h]; o = 0, 1: q heads wave, wave + 4; 2: key / value; 3: q weight;
+  // 4: key weight; 5: cos; 6: sin
+  // Every fetch is issued (an operand this wave does not use reads past its buffer's end as zeros),
+  // so no branch stands between them and the DMAs.
+  Bf16Words<E> raw[7][2];
+  if (fused) {
+    const uint32_t vec = uint32_t(D) * 2u;
+    const __amdgpu_buffer_rsrc_t ry = make_rsrc(p.qkv_y, p.qkv_bytes), rc = make_rsrc(p.rope_c, vec),
+                                 rs = make_rsrc(p.rope_s, vec), rqw = make_rsrc(p.qw, p.qw ? vec : 0u),
+                                 rkw = make_rsrc(p.kw, p.kw ? vec : 0u);
+    auto fetch = [&](int o, __amdgpu_buffer_rsrc_t r, bool on, int row) __attribute__((always_inline)) {
+      const uint32_t off = on ? (uint32_t(row) * uint32_t(D) + uint32_t(p0)) * 2u : 0x80000000u;
+      raw[o][0].load(r, off);
+      raw[o][1].load(r, off + uint32_t(HALF) * 2u);
+    };
+    fetch(5, rc, true, 0);
+    fetch(6, rs, true, 0);
+    fetch(3, rqw, true, 0);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) fetch(j, ry, wave + 4 * j < p.G, g * p.G + wave + 4 * j);
+    fetch(2, ry, make_kv && wave < 2, p.H + (wave == 0 ? 0 : p.KV) + g);
+    fetch(4, rkw, make_kv && wave == 0, 0);
+  }
 
   // K chunk x of row r lands at stored chunk x ^ (r & 15); V chunk x of row r at x ^ 2 (r & 3).
 #pragma unroll
@@ -1243,7 +1306,41 @@ __global__ __launch_bounds__(256, 2) void attn_decode_split_kernel(DecodeParams 
   }
   // Q rows (B operand): lane (qi, qq) holds q[head g*G + qi][32 kk + 8 qq .. + 7], zero past G.
   v8bf qf[NKK];
-  {
+  float xy1[E], xy2[E];
+  if (fused) {
+    // the q heads into LDS; the key / value into the cache (k_qkv_cache's stores)
+    float rc1[E], rc2[E], rs1[E], rs2[E], w1[E], w2[E];
+    raw[5][0].unpack(rc1);
+    raw[5][1].unpack(rc2);
+    raw[6][0].unpack(rs1);
+    raw[6][1].unpack(rs2);
+    raw[3][0].unpack(w1);
+    raw[3][1].unpack(w2);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int hl = wave + 4 * j;
+      if (hl < p.G) {
+        float qy1[E], qy2[E];
+        raw[j][0].unpack(qy1);
+        raw[j][1].unpack(qy2);
+        qkv_head_regs<E>(qy1, qy2, p.qkv_eps, p.qw != nullptr, w1, w2, true, rc1, rc2, rs1, rs2);
+        store_bf16<E>(ql + hl * D + p0, qy1);
+        store_bf16<E>(ql + hl * D + p0 + HALF, qy2);
+      }
+    }
+    if (make_kv && wave < 2) {
+      float xw1[E], xw2[E];
+      raw[2][0].unpack(xy1);
+      raw[2][1].unpack(xy2);
+      raw[4][0].unpack(xw1);
+      raw[4][1].unpack(xw2);
+      qkv_head_regs<E>(xy1, xy2, p.qkv_eps, wave == 0 && p.kw != nullptr, xw1, xw2, wave == 0, rc1, rc2, rs1, rs2);
+      uint16_t* dst = const_cast<uint16_t*>(wave == 0 ? p.k + int64_t(g) * p.khs + int64_t(geo.pos) * p.krs
+                                                      : p.v + int64_t(g) * p.vhs + int64_t(geo.pos) * p.vrs);
+      store_bf16<E>(dst + p0, xy1);
+      store_bf16<E>(dst + p0 + HALF, xy2);
+    }
+  } else {
     const bool has = qi < p.G;
     const uint16_t* qp = p.q + int64_t(g * p.G + (has ? qi : 0)) * p.qhs + 8 * qq;
 #pragma unroll
@@ -1255,6 +1352,30 @@ __global__ __launch_bounds__(256, 2) void attn_decode_split_kernel(DecodeParams 
   }
   attn_wait_vmcnt<0>();
   __syncthreads();
+  if (make_kv) {
+    // the token's row of the chunk (DMA'd from the cache before it was written) replaced by the made
+    // key and value, in the chunk's swizzled layouts
+    if (wave < 2) {
+      const int r = geo.pos - kc;
+      char* row = (wave == 0 ? kl : vl) + r * ROW;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int d = p0 + hh * HALF;
+        const int cs = wave == 0 ? ((d >> 3) ^ (r & 15)) : ((d >> 3) ^ (2 * (r & 3)));
+        store_bf16<E>(reinterpret_cast<uint16_t*>(row + cs * 16 + (d & 7) * 2), hh ? xy2 : xy1);
+      }
+    }
+    __syncthreads();
+  }
+  if (fused) {
+    const bool has = qi < p.G;
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk) {
+      v4i t = v4i{0, 0, 0, 0};
+      if (has) t = *reinterpret_cast<const v4i*>(ql + qi * D + 32 * kk + 8 * qq);
+      qf[kk] = __builtin_bit_cast(v8bf, t);
+    }
+  }
 
   // S^T tile: keys 16 wave + 4 qq + i (i = 0..3) of the chunk, query qi; two accumulators.
   const bool has_tile = 16 * wave < DEC_C;
@@ -1994,4 +2115,55 @@ extern "C" int w8a8_attention_decode_dev_bf16(const uint16_t* q, int64_t q_head_
   p.scale = scale; p.c = scale * 1.4426950408889634f;
   decode_launch(p, D, workspace, stream);
   return check_launch("attention_decode_dev_bf16");
+}
+
+extern "C" int w8a8_attention_decode_qkv_dev_bf16(const uint16_t* y, const uint16_t* cos_, const uint16_t* sin_,
+                                                  const uint16_t* qw, const uint16_t* kw, float eps, uint16_t* k,
+                                                  int64_t k_head_stride, int64_t k_row_stride, uint16_t* v,
+                                                  int64_t v_head_stride, int64_t v_row_stride, int64_t H, int64_t KV,
+                                                  int64_t Tk, int64_t D, int kv_write, const int32_t* q_pos,
+                                                  int64_t window, float scale, uint16_t* o, int64_t o_head_stride,
+                                                  void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  const char* what = "attention_decode_qkv_dev";
+  if (H < 1 || KV < 1 || H % KV != 0 || H / KV > 8)
+    return fail(W8A8_EINVAL, "%s: H=%lld KV=%lld (H must be a multiple of KV, at most 8 heads per KV head)", what,
+                (long long)H, (long long)KV);
+  if (D != 128 && D != 256 && D != 512)
+    return fail(W8A8_ENOTSUP, "%s: head_dim %lld (supported: 128, 256, 512)", what, (long long)D);
+  if (Tk < 1 || Tk > INT32_MAX || window < 0 || window > INT32_MAX)
+    return fail(W8A8_EINVAL, "%s: Tk=%lld window=%lld", what, (long long)Tk, (long long)window);
+  if (decode_grid_chunks(D, Tk, window) > DEC_MAX_CHUNKS)
+    return fail(W8A8_ENOTSUP, "%s: %d key chunks of %d (at most %d)", what, decode_grid_chunks(D, Tk, window),
+                dec_chunk(int(D)), DEC_MAX_CHUNKS);
+  if (!(scale > 0.0f) || scale == __builtin_inff()) return fail(W8A8_EINVAL, "%s: scale must be positive", what);
+  if (!y || !cos_ || !sin_ || !k || !v || !o || !q_pos || !workspace) return fail(W8A8_EINVAL, "%s: null pointer", what);
+  const int64_t need = w8a8_attention_decode_dev_workspace_bytes(H, KV, Tk, D, window);
+  if (workspace_bytes < need)
+    return fail(W8A8_EINVAL, "%s: workspace of %lld bytes, %lld needed", what, (long long)workspace_bytes,
+                (long long)need);
+  if (k_row_stride < D || v_row_stride < D || (H > 1 && o_head_stride < D))
+    return fail(W8A8_EINVAL, "%s: strides smaller than head_dim", what);
+  const int64_t strides[5] = {k_head_stride, k_row_stride, v_head_stride, v_row_stride, o_head_stride};
+  for (int i = 0; i < 5; ++i)
+    if (strides[i] % 8 != 0) return fail(W8A8_EALIGN, "%s: strides must be multiples of 8 elements", what);
+  for (const void* q : {static_cast<const void*>(y), static_cast<const void*>(cos_), static_cast<const void*>(sin_),
+                        static_cast<const void*>(qw), static_cast<const void*>(kw), static_cast<const void*>(k),
+                        static_cast<const void*>(v), static_cast<const void*>(o), static_cast<const void*>(workspace)})
+    if (reinterpret_cast<uintptr_t>(q) % 16) return fail(W8A8_EALIGN, "%s: pointers must be 16-byte aligned", what);
+  if ((uintptr_t)q_pos % 4) return fail(W8A8_EALIGN, "%s: q_pos must be 4-byte aligned", what);
+  const int64_t kb = ((Tk - 1) * k_row_stride + D) * 2, vb = ((Tk - 1) * v_row_stride + D) * 2;
+  if (kb > INT32_MAX || vb > INT32_MAX) return fail(W8A8_ENOTSUP, "%s: one head's K or V above 2 GiB", what);
+  DecodeParams p{};
+  p.q = nullptr; p.qhs = D; p.k = k; p.khs = k_head_stride; p.krs = k_row_stride;
+  p.v = v; p.vhs = v_head_stride; p.vrs = v_row_stride; p.o = o; p.ohs = o_head_stride; p.lse = nullptr;
+  p.k_bytes = uint32_t(kb); p.v_bytes = uint32_t(vb);
+  p.H = int(H); p.KV = int(KV); p.G = int(H / KV); p.Tk = int(Tk);
+  p.pos_dev = q_pos;
+  p.window = int(window);
+  p.nchunk_grid = decode_grid_chunks(D, Tk, window);
+  p.scale = scale; p.c = scale * 1.4426950408889634f;
+  p.qkv_y = y; p.rope_c = cos_; p.rope_s = sin_; p.qw = qw; p.kw = kw; p.qkv_eps = eps; p.kv_write = kv_write ? 1 : 0;
+  p.qkv_bytes = uint32_t((H + (kv_write ? 2 * KV : 0)) * D * 2);
+  decode_launch(p, D, workspace, stream);
+  return check_launch("attention_decode_qkv_dev_bf16");
 }

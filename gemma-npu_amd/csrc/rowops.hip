@@ -281,30 +281,6 @@ __device__ __forceinline__ void load_f32(const float* p, float (&o)[E]) {
     for (int i = 0; i < E; ++i) o[i] = p[i];
   }
 }
-template <int E>
-__device__ __forceinline__ void load_bf16(const uint16_t* p, float (&o)[E]) {
-  if constexpr (E == 4) {
-    const v2u a = *reinterpret_cast<const v2u*>(p);
-    o[0] = __uint_as_float(a[0] << 16); o[1] = __uint_as_float(a[0] & 0xffff0000u);
-    o[2] = __uint_as_float(a[1] << 16); o[3] = __uint_as_float(a[1] & 0xffff0000u);
-  } else if constexpr (E == 2) {
-    const uint32_t a = *reinterpret_cast<const uint32_t*>(p);
-    o[0] = __uint_as_float(a << 16); o[1] = __uint_as_float(a & 0xffff0000u);
-  } else {
-    o[0] = bf16_to_f32(*p);
-  }
-}
-template <int E>
-__device__ __forceinline__ void store_bf16(uint16_t* p, const float (&o)[E]) {
-  if constexpr (E == 4) {
-    *reinterpret_cast<v2u*>(p) = v2u{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
-  } else if constexpr (E == 2) {
-    *reinterpret_cast<uint32_t*>(p) = pack_bf16x2(o[0], o[1]);
-  } else {
-    *p = f32_to_bf16(o[0]);
-  }
-}
-
 // One wave per (token, head slot): slots 0 .. H-1 are the query heads, then KV key heads, then KV
 // value heads, at columns slot * D of the GEMM result (pipeline.py:76-82).  A lane holds E = D/128
 // elements of each half of the head at positions p0 .. p0+E-1 and p0+D/2 .. : the rotation pairs
@@ -338,52 +314,14 @@ __global__ __launch_bounds__(256) void qkv_kernel(QkvParams p) {
       y2[e] = round_bf16((float(a2[e]) * sxm) * s2[e]);
     }
   }
-  float ss = 0.0f;
-#pragma unroll
-  for (int e = 0; e < E; ++e) ss += y1[e] * y1[e] + y2[e] * y2[e];
-  ss = wave_sum_dpp(ss);
-  const float r = 1.0f / sqrtf(ss / float(D) + p.eps);
   const bool is_q = slot < p.H, is_k = !is_q && slot < p.H + p.KV;
   const uint16_t* w = is_q ? p.qw : (is_k ? p.kw : nullptr);
-  float n1[E], n2[E];
-  if (w) {
-    float w1[E], w2[E];
-    load_bf16<E>(w + p0, w1);
-    load_bf16<E>(w + p0 + HALF, w2);
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-      n1[e] = round_bf16((y1[e] * r) * w1[e]);
-      n2[e] = round_bf16((y2[e] * r) * w2[e]);
-    }
-  } else {
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-      n1[e] = round_bf16(y1[e] * r);
-      n2[e] = round_bf16(y2[e] * r);
-    }
-  }
+  qkv_head<E>(y1, y2, p.eps, w, (is_q || is_k) ? p.cs + int64_t(t) * p.ldcs : nullptr,
+              (is_q || is_k) ? p.sn + int64_t(t) * p.ldcs : nullptr, p0);
+  float (&n1)[E] = y1;
+  float (&n2)[E] = y2;
   uint16_t* dst;
   if (is_q || is_k) {
-    // x * cos + cat(-x[D/2:], x[:D/2]) * sin on bf16 tensors: each product and the sum round
-    // (pipeline.py:60-63).
-    float c1[E], c2[E], s1[E], s2[E];
-    const uint16_t* cr = p.cs + int64_t(t) * p.ldcs;
-    const uint16_t* sr = p.sn + int64_t(t) * p.ldcs;
-    load_bf16<E>(cr + p0, c1);
-    load_bf16<E>(cr + p0 + HALF, c2);
-    load_bf16<E>(sr + p0, s1);
-    load_bf16<E>(sr + p0 + HALF, s2);
-    float o1[E], o2[E];
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-      o1[e] = round_bf16(round_bf16(n1[e] * c1[e]) + round_bf16(-n2[e] * s1[e]));
-      o2[e] = round_bf16(round_bf16(n2[e] * c2[e]) + round_bf16(n1[e] * s2[e]));
-    }
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-      n1[e] = o1[e];
-      n2[e] = o2[e];
-    }
     dst = is_q ? p.q + (int64_t(slot) * p.T + t) * D : p.k + (int64_t(slot - p.H) * p.T + t) * D;
   } else {
     dst = p.v + (int64_t(slot - p.H - p.KV) * p.T + t) * D;

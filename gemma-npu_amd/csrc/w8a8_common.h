@@ -115,6 +115,98 @@ __device__ __forceinline__ v4u pack8(const float (&v)[8]) {
   return v4u{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
 }
 
+template <int E>
+__device__ __forceinline__ void load_bf16(const uint16_t* p, float (&o)[E]) {
+  if constexpr (E == 4) {
+    const v2u a = *reinterpret_cast<const v2u*>(p);
+    o[0] = __uint_as_float(a[0] << 16); o[1] = __uint_as_float(a[0] & 0xffff0000u);
+    o[2] = __uint_as_float(a[1] << 16); o[3] = __uint_as_float(a[1] & 0xffff0000u);
+  } else if constexpr (E == 2) {
+    const uint32_t a = *reinterpret_cast<const uint32_t*>(p);
+    o[0] = __uint_as_float(a << 16); o[1] = __uint_as_float(a & 0xffff0000u);
+  } else {
+    o[0] = bf16_to_f32(*p);
+  }
+}
+template <int E>
+__device__ __forceinline__ void store_bf16(uint16_t* p, const float (&o)[E]) {
+  if constexpr (E == 4) {
+    *reinterpret_cast<v2u*>(p) = v2u{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+  } else if constexpr (E == 2) {
+    *reinterpret_cast<uint32_t*>(p) = pack_bf16x2(o[0], o[1]);
+  } else {
+    *p = f32_to_bf16(o[0]);
+  }
+}
+
+// One head of k_qkv (pipeline.py:72-86) on one wave, in place: the lane holds E = D/128 values of
+// each half of the head, at p0 .. p0+E-1 (y1) and p0+D/2 .. (y2).  RMS norm over the head with the
+// weight halves w1 / w2 (has_w false: no weight), each value rounded to bf16; then, with rope, RoPE
+// with the cos / sin halves c1, c2 / s1, s2 on the bf16 values: x * cos + cat(-x[D/2:], x[:D/2]) * sin
+// with every product and the sum rounded (pipeline.py:60-63).  The rotation pairs element d with
+// d + D/2, so it needs no lane exchange.  The operands come in registers, so a caller can fetch them
+// early.
+template <int E>
+__device__ __forceinline__ void qkv_head_regs(float (&y1)[E], float (&y2)[E], float eps, bool has_w,
+                                              const float (&w1)[E], const float (&w2)[E], bool rope,
+                                              const float (&c1)[E], const float (&c2)[E], const float (&s1)[E],
+                                              const float (&s2)[E]) {
+  constexpr int D = 128 * E;
+  float ss = 0.0f;
+#pragma unroll
+  for (int e = 0; e < E; ++e) ss += y1[e] * y1[e] + y2[e] * y2[e];
+  ss = wave_sum_dpp(ss);
+  const float r = 1.0f / sqrtf(ss / float(D) + eps);
+  if (has_w) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      y1[e] = round_bf16((y1[e] * r) * w1[e]);
+      y2[e] = round_bf16((y2[e] * r) * w2[e]);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      y1[e] = round_bf16(y1[e] * r);
+      y2[e] = round_bf16(y2[e] * r);
+    }
+  }
+  if (rope) {
+    float o1[E], o2[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      o1[e] = round_bf16(round_bf16(y1[e] * c1[e]) + round_bf16(-y2[e] * s1[e]));
+      o2[e] = round_bf16(round_bf16(y2[e] * c2[e]) + round_bf16(y1[e] * s2[e]));
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      y1[e] = o1[e];
+      y2[e] = o2[e];
+    }
+  }
+}
+
+// qkv_head_regs with its operands fetched here: the norm weight w (null: none) and, with cr / sr
+// non-null, the RoPE cos / sin rows.
+template <int E>
+__device__ __forceinline__ void qkv_head(float (&y1)[E], float (&y2)[E], float eps, const uint16_t* w,
+                                         const uint16_t* cr, const uint16_t* sr, int p0) {
+  constexpr int HALF = 64 * E;
+  float w1[E], w2[E], c1[E], c2[E], s1[E], s2[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) w1[e] = w2[e] = c1[e] = c2[e] = s1[e] = s2[e] = 0.0f;
+  if (w) {
+    load_bf16<E>(w + p0, w1);
+    load_bf16<E>(w + p0 + HALF, w2);
+  }
+  if (cr) {
+    load_bf16<E>(cr + p0, c1);
+    load_bf16<E>(cr + p0 + HALF, c2);
+    load_bf16<E>(sr + p0, s1);
+    load_bf16<E>(sr + p0 + HALF, s2);
+  }
+  qkv_head_regs<E>(y1, y2, eps, w != nullptr, w1, w2, cr != nullptr, c1, c2, s1, s2);
+}
+
 // ---- per-row int8 quantisation step (pipeline.py:51) -----------------------------------------
 // s = amax.clamp(min=1e-8) / 127 from a row absmax (pipeline.py:51); a NaN absmax stays NaN, as
 // torch's clamp keeps it.

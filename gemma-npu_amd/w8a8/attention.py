@@ -252,6 +252,50 @@ def decode_at(q, k, v, pos, window=0, scale=1.0, out=None, workspace=None):
     return out
 
 
+def decode_qkv_at(y, cos, sin, qw, kw, eps, H, KV, D, k, v, pos, kv_write, window=0, scale=1.0, out=None,
+                  workspace=None):
+    """k_qkv and decode_at in one launch, for the token's qkv row y [1, (H + 2 KV) D] bf16 ([1, H D] when
+    the layer reads another layer's keys): q = RoPE(rms(q head) * qw) per head with the cos / sin rows
+    [1, D] at the position; with kv_write the token's key (rms * kw, RoPE) and value (rms) of each KV
+    head are also written into the cache k / v [KV, Tk, D] at the position read from pos (int32 [1])
+    and attended to there.  Bit for bit fused.k_qkv_cache (or fused.k_qkv for q alone) followed by
+    decode_at.  At most 8 query heads per KV head."""
+    for t, name in ((y, "y"), (cos, "cos"), (sin, "sin")):
+        if not isinstance(t, torch.Tensor) or t.dtype != torch.bfloat16 or t.device.type != "cuda":
+            raise ValueError(f"decode_qkv_at: {name} must be a bf16 GPU tensor")
+        if not t.is_contiguous():
+            raise ValueError(f"decode_qkv_at: {name} must be contiguous")
+    width = (H + (2 * KV if kv_write else 0)) * D
+    if y.numel() != width:
+        raise ValueError(f"decode_qkv_at: y holds {y.numel()} values, expected {width}")
+    if cos.numel() != D or sin.numel() != D:
+        raise ValueError(f"decode_qkv_at: cos / sin must hold one row of {D}")
+    for t, name in ((qw, "qw"), (kw, "kw")):
+        if t is not None and (t.dtype != torch.bfloat16 or t.numel() != D or not t.is_contiguous()):
+            raise ValueError(f"decode_qkv_at: {name} must be a contiguous bf16 [{D}]")
+    _check3(k, "k")
+    _check3(v, "v")
+    if not isinstance(pos, torch.Tensor) or pos.dtype != torch.int32 or pos.numel() != 1 or pos.device != y.device:
+        raise ValueError("decode_qkv_at: pos must be an int32 tensor of one element on y's device")
+    KVk, Tk, Dk = k.shape
+    if KVk != KV or Dk != D or tuple(v.shape) != (KV, Tk, D):
+        raise ValueError(f"decode_qkv_at: k {tuple(k.shape)} / v {tuple(v.shape)} do not match KV={KV} D={D}")
+    if out is None:
+        out = torch.empty((H, D), dtype=torch.bfloat16, device=y.device)
+    elif out.shape != (H, D) or out.dtype != torch.bfloat16 or (D > 1 and out.stride(1) != 1):
+        raise ValueError(f"decode_qkv_at: out must be bf16 [{H}, {D}] with a contiguous last dimension")
+    need = decode_at_workspace_bytes(H, KV, Tk, D, window)
+    ws = _workspace(y.device, need) if workspace is None else workspace
+    khs, krs = _strides(k)
+    vhs, vrs = _strides(v)
+    ptr = lambda t: None if t is None else t.data_ptr()
+    call("w8a8_attention_decode_qkv_dev_bf16", y.data_ptr(), cos.data_ptr(), sin.data_ptr(), ptr(qw), ptr(kw),
+         float(eps), k.data_ptr(), khs, krs, v.data_ptr(), vhs, vrs, H, KV, Tk, D, 1 if kv_write else 0,
+         pos.data_ptr(), int(window), float(scale), out.data_ptr(), out.stride(0) if H > 1 else D, ws.data_ptr(),
+         ws.numel(), _stream(y))
+    return out
+
+
 def split_kv_decode(query, key, value, scale):
     """local_attn.py:44-68: one query per head [1, H, 1, D] against one KV head [1, 1, T, D] ->
     [1, 1, H, D] (the reference's split over up to 16 key chunks and logsumexp merge)."""

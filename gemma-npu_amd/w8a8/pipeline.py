@@ -319,8 +319,9 @@ class Decoder:
     over the cache (local_attn.py:44-83); and the norms, residuals, GELU-tanh products and
     per-layer-input steps of pipeline.py:66-127 without the activation quant, since the next linear
     reads bf16.  Each residual + norm step is the prologue of the GEMV that reads its result (the
-    norm is made in that launch, bit for bit the row kernel's), so a layer is nine launches: qkv,
-    k_qkv, two of attention, o, gate/up, down, per-layer gate, per-layer projection.  The token, its position and the key / value cache [KV, max_len, head_dim] of every
+    norm is made in that launch, bit for bit the row kernel's), and k_qkv runs inside the attention
+    launch, so a layer is eight launches: qkv, two of attention, o, gate/up, down, per-layer gate,
+    per-layer projection.  The token, its position and the key / value cache [KV, max_len, head_dim] of every
     layer that owns keys live in device memory, so a step does not depend on host values: capture()
     records one step in a HIP graph and each replay decodes the next token.  The next token is the
     argmax of the last logits (greedy), chosen on the device.
@@ -452,14 +453,19 @@ class Decoder:
             h = hn
         cos, sin = rope[p.kind]
         eps = self.cfg.rms_norm_eps
-        if p.shares_kv:
-            q = fused.k_qkv(y, None, None, cos, sin, p.norm_q, None, eps, p.heads, p.kv_heads, p.head_dim, True)[0]
-        else:
-            kc, vc = self.cache[p.index]
-            q = fused.k_qkv_cache(y, cos, sin, p.norm_q, p.norm_k, eps, p.heads, p.kv_heads, p.head_dim, kc, vc,
-                                  self.pos)
         kc, vc = self.cache[p.kv_source]
-        o = attention.decode_at(q[:, 0], kc, vc, self.pos, p.window, 1.0, workspace=self.workspace)
+        if p.heads // p.kv_heads <= 8:
+            # k_qkv inside the attention launch (the key and value written at the position there)
+            o = attention.decode_qkv_at(y, cos, sin, p.norm_q, p.norm_k, eps, p.heads, p.kv_heads, p.head_dim, kc,
+                                        vc, self.pos, not p.shares_kv, p.window, 1.0, workspace=self.workspace)
+        else:
+            if p.shares_kv:
+                q = fused.k_qkv(y, None, None, cos, sin, p.norm_q, None, eps, p.heads, p.kv_heads, p.head_dim,
+                                True)[0]
+            else:
+                q = fused.k_qkv_cache(y, cos, sin, p.norm_q, p.norm_k, eps, p.heads, p.kv_heads, p.head_dim, kc, vc,
+                                      self.pos)
+            o = attention.decode_at(q[:, 0], kc, vc, self.pos, p.window, 1.0, workspace=self.workspace)
         y = ops.gemv_bf16(o.reshape(1, -1), W["o"].gemv_w, W["o"].sw_bf16)
         g, h = self._norm_linear((y, h, p.norm_post_attn, None, p.norm_pre_ff, True), W["gate_up"], "gelu_pair")
         y = ops.gemv_bf16(g, W["down"].gemv_w, W["down"].sw_bf16)

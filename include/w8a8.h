@@ -486,6 +486,23 @@ int w8a8_attention_decode_dev_bf16(const uint16_t *q, int64_t q_head_stride, con
                                    int64_t o_head_stride, void *workspace, int64_t workspace_bytes,
                                    hipStream_t stream);
 
+/* w8a8_k_qkv_cache_y (or w8a8_k_qkv_y for q alone) and w8a8_attention_decode_dev_bf16 in one
+ * launch (the decode step's k_qkv and attention, pipeline.py:72-86 and local_attn.py:44-83): y is
+ * the token's qkv row, bf16 [H*D q | KV*D k | KV*D v] (kv_write = 1) or [H*D] (kv_write = 0, a layer
+ * that reads another layer's keys); per q head RMS norm with qw (null: no weight) and RoPE with the
+ * cos / sin rows [D] at the position.  With kv_write the workgroup holding the position also makes
+ * each KV head's key (norm with kw, RoPE) and value (norm without weight), writes them into k / v at
+ * row *q_pos (when it is below Tk) and attends to them there.  Bit for bit the two-launch form.  At
+ * most 8 query heads per KV head; 16-byte aligned pointers; workspace as
+ * w8a8_attention_decode_dev_bf16's. */
+int w8a8_attention_decode_qkv_dev_bf16(const uint16_t *y, const uint16_t *cos_, const uint16_t *sin_,
+                                       const uint16_t *qw, const uint16_t *kw, float eps, uint16_t *k,
+                                       int64_t k_head_stride, int64_t k_row_stride, uint16_t *v,
+                                       int64_t v_head_stride, int64_t v_row_stride, int64_t H, int64_t KV,
+                                       int64_t Tk, int64_t D, int kv_write, const int32_t *q_pos, int64_t window,
+                                       float scale, uint16_t *o, int64_t o_head_stride, void *workspace,
+                                       int64_t workspace_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

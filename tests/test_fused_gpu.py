@@ -372,3 +372,36 @@ def test_layer_chain_stagewise():
     assert_bf16_close(f32(B(out)), f32(ref), what="chain k_ple_out", ulp_at=ulp_at)
     assert (B(out) == ref).mean() > 0.99
     assert np.isfinite(f32(B(out))).all()
+
+
+# ---- k_qkv inside the decode attention ------------------------------------------------------
+
+@pytest.mark.parametrize("D, KV, window", [(256, 1, 512), (512, 1, 0), (256, 2, 0), (128, 1, 64)])
+def test_decode_qkv_at_equals_k_qkv_then_decode_at(D, KV, window):
+    """attention.decode_qkv_at (k_qkv made inside the split-key decode attention) against
+    k_qkv_cache / k_qkv followed by decode_at: the same output and the same cache bit for bit, for a
+    layer that owns its keys (the token's key and value written at the device-held position and
+    attended to there) and one that reads another layer's cache (q only), at positions in the first
+    key chunk, on chunk edges, past the window and at the cache's last row."""
+    from w8a8 import attention
+    H, rows = 8 * KV, 1100
+    y_full = (torch.randn(1, (H + 2 * KV) * D, generator=gen(50 + D)) * 0.7).to(torch.bfloat16).to(DEV)
+    ang = torch.rand(1, D, generator=gen(51)) * 6.0
+    cos, sin = ang.cos().to(torch.bfloat16).to(DEV), ang.sin().to(torch.bfloat16).to(DEV)
+    qw, kw = norm_weight(D, 52).to(DEV), norm_weight(D, 53).to(DEV)
+    fill = (torch.randn(KV, rows, D, generator=gen(54)) * 0.7).to(torch.bfloat16).to(DEV)
+    fill_v = (torch.randn(KV, rows, D, generator=gen(55))).to(torch.bfloat16).to(DEV)
+    for p in (0, 5, 31, 32, 63, 64, 100, 600, rows - 1):
+        pos = torch.tensor([p], dtype=torch.int32, device=DEV)
+        for kv_write in (True, False):
+            y = y_full if kv_write else y_full[:, :H * D].contiguous()
+            kc_ref, vc_ref = fill.clone(), fill_v.clone()
+            if kv_write:
+                q = fused.k_qkv_cache(y, cos, sin, qw, kw, EPS, H, KV, D, kc_ref, vc_ref, pos)
+            else:
+                q = fused.k_qkv(y, None, None, cos, sin, qw, None, EPS, H, KV, D, True)[0]
+            want = attention.decode_at(q[:, 0], kc_ref, vc_ref, pos, window, 0.75)
+            kc, vc = fill.clone(), fill_v.clone()
+            got = attention.decode_qkv_at(y, cos, sin, qw, kw, EPS, H, KV, D, kc, vc, pos, kv_write, window, 0.75)
+            assert torch.equal(got, want), (p, kv_write)
+            assert torch.equal(kc, kc_ref) and torch.equal(vc, vc_ref), (p, kv_write)
