@@ -880,6 +880,9 @@ def main():
     ap.add_argument("--profile-pipeline", action="store_true",
                     help="for kernel traces: --steps whole-prompt prefills of the 3658-token prompt through "
                          "w8a8.pipeline.Prefill on the E2B-shaped HF Gemma 4, then exit")
+    ap.add_argument("--profile-decoder", action="store_true",
+                    help="run w8a8.pipeline.Decoder on the E2B-shaped model after a 3658-token prompt: one captured "
+                         "step, then --steps graph replays (for rocprofv3)")
     ap.add_argument("--profile-decode", action="store_true",
                     help="for kernel traces: decode attention at the end of the 3658-token prompt for each layer "
                          "kind (--steps calls each, eager) and exit")
@@ -965,6 +968,18 @@ def main():
             pre(ids)
         torch.cuda.synchronize()
         log(f"bench: ran {args.steps} whole-prompt pipeline prefills of {ATTN_T} tokens on the E2B-shaped model")
+        return 0
+    if args.profile_decoder:
+        from w8a8.pipeline import Decoder, Prefill
+        model, _ = e2b_model(dev)
+        ids = torch.randint(0, 262144, (1, ATTN_T), generator=torch.Generator().manual_seed(1)).to(dev)
+        dec = Decoder(Prefill(model), max_len=ATTN_T + args.steps + 8)
+        dec.start(ids)
+        dec.capture()
+        for _ in range(args.steps):
+            dec.replay()
+        torch.cuda.synchronize()
+        log(f"bench: decoded {args.steps + 1} tokens after a {ATTN_T}-token prompt, {args.steps} of them graph-replayed")
         return 0
     if args.profile_decode:
         from w8a8 import attention as attn
