@@ -355,26 +355,44 @@ def gemv_layers(dev, reps, cpu=True):
     return out
 
 
-def sweep(M, dev, reps):
-    """All prefill GEMMs of one prompt: 35 layers x 4 groups + the PLE projection, int8 A ->
-    int32 C (the reference's NPU launches, gemma_npu.py:99-115), distinct weights per layer."""
+def sweep(M, dev, reps, epilogues=False):
+    """All prefill GEMMs of one prompt: 35 layers x 4 groups + the PLE projection, distinct weights per
+    layer.  int8 A -> int32 C (the reference's NPU launches, gemma_npu.py:99-115), or with epilogues
+    each group with its epilogue of one E2B-class layer's linears: bf16 out (dequantised with the
+    per-token and per-channel scales), gate/up with the GELU product (N/2 bf16 columns), down with
+    the residual add."""
     import torch
     from w8a8 import ops, workloads
     shapes = workloads.sweep_shapes()
+    epi_of = dict(workloads.LAYER_GROUPS, ple_proj=workloads.PLE_PROJ)
     A = {}
     packed = []
     for name, layer, gi, K, N in shapes:
         if K not in A:
-            A[K] = ops.quant_rows_packed(workloads.activations(M, K, seed=K).to(dev))[0]
+            A[K] = ops.quant_rows_packed(workloads.activations(M, K, seed=K).to(dev))
         g = torch.Generator(device=dev).manual_seed(workloads.layer_seed(layer, gi))
         w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8, device=dev)
-        packed.append((K, N, ops.pack_weight(w, "nk")))
+        epi = epi_of[name][2] if epilogues else "int32"
+        if epilogues:
+            sw = torch.rand(N, generator=g, device=dev) * 0.015 + 0.005
+            packed.append((K, N, epi, ops.pack_weight(w, "nk", N // 2 if epi == "gelu" else 0, sw=sw)))
+        else:
+            packed.append((K, N, epi, ops.pack_weight(w, "nk")))
         del w
-    C = {N: torch.empty((M, N), dtype=torch.int32, device=dev) for _, _, _, _, N in shapes}
+    if epilogues:
+        C = {(N, e): torch.empty((M, N // 2 if e == "gelu" else N), dtype=torch.bfloat16, device=dev)
+             for _, N, e, _ in packed}
+        R = {N: torch.randn((M, N), device=dev).to(torch.bfloat16) for _, N, e, _ in packed if e == "residual"}
+    else:
+        C = {N: torch.empty((M, N), dtype=torch.int32, device=dev) for _, _, _, _, N in shapes}
 
     def run():
-        for K, N, pw in packed:
-            ops.gemm_i32(A[K], pw, C[N])
+        for K, N, epi, pw in packed:
+            if epilogues:
+                ops.gemm_bf16(A[K][0], A[K][1], pw, epilogue=epi, residual=R.get(N) if epi == "residual" else None,
+                              out=C[(N, epi)])
+            else:
+                ops.gemm_i32(A[K][0], pw, C[N])
 
     ms = event_time_ms(run, reps, 2)
     total_ops = sum(workloads.gemm_ops(M, N, K) for _, _, _, K, N in shapes)
@@ -1140,6 +1158,18 @@ def main():
                 entry["speedup_vs_cpu"] = round(cpu_total / ms, 1)
             extra[f"prefill_sweep_m{Ms}"] = entry
             log(f"bench: sweep M={Ms}: {entry}")
+            torch.cuda.empty_cache()
+            ms, tops_ops, wbytes, shp, run = sweep(Ms, dev, reps=5, epilogues=True)
+            tops = tops_ops / (ms * 1e-3) / 1e12
+            clk = clock_during(run, dev, launches=2, window_ms=4.0)
+            extra[f"prefill_sweep_m{Ms}_epilogues"] = {
+                "ms": round(ms, 3), "gemms": len(shp), "tops": round(tops, 1),
+                "frac_mfma": round(tops / PEAK_INT8_TOPS, 4), "clock_ghz": round(clk, 3),
+                "frac_at_clock": round(tops / (256 * 8192 * clk / 1e3), 4),
+                "weights": f"cold: {wbytes / 1e9:.2f} GB of distinct per-layer weights",
+                "what": "the same 141 GEMMs with one E2B-class layer's epilogues: bf16 out (qkv, o, PLE projection "
+                        "dequantised), gate/up with the GELU product, down with the residual add"}
+            log(f"bench: sweep M={Ms} with epilogues: {extra[f'prefill_sweep_m{Ms}_epilogues']}")
             torch.cuda.empty_cache()
         # M=16384 stress: gate_up with fused GELU, down with residual
         for name in ("gate_up", "down"):
