@@ -321,8 +321,8 @@ class Decoder:
     reads bf16.  Each residual + norm step is the prologue of the GEMV that reads its result (the
     norm is made in that launch, bit for bit the row kernel's), and k_qkv runs inside the attention
     launch, so a layer is eight launches: qkv, two of attention, o, gate/up, down, per-layer gate,
-    per-layer projection.  The token, its position and the key / value cache [KV, max_len, head_dim] of every
-    layer that owns keys live in device memory, so a step does not depend on host values: capture()
+    per-layer projection.  The token, its position and the key / value cache [KV, max_len, head_dim]
+    of every layer that owns keys live in device memory, so a step does not depend on host values: capture()
     records one step in a HIP graph and each replay decodes the next token.  The next token is the
     argmax of the last logits (greedy), chosen on the device.
 
