@@ -38,6 +38,8 @@ the bytes.  The embedding, per-layer-input tables, RoPE tables, final norm and l
 softcap are the model's own modules (pipeline.py:318-338); inside them the per-layer model
 projection and the LM head run on the engine after hf.to_gpu.
 """
+import time
+
 import torch
 
 from . import attention, fused, ops
@@ -557,3 +559,50 @@ class Decoder:
             for _ in range(n):
                 self.step()
         return self.emitted[first:int(self.n_emitted.item())].tolist()
+
+
+@torch.inference_mode()
+def run(model, ids, n_decode, prefill=None):
+    """gemma_npu.py:271-296 on the device: prefill (timed) then greedy decode of n_decode tokens;
+    returns (ttft seconds, decode tok/s, tokens, last-token logits fp32), as the reference's run().
+
+    With a Prefill (this module's, on the engine's weights) the prompt runs as the whole-prompt prefill
+    and the decode as Decoder steps: the second token's step runs eagerly while it is captured in a
+    HIP graph (untimed set-up), and the rate is taken over the graph replays of the tokens after it.
+    Without one, HF's own forward and decode loop run on the model (the reference's prefill=None
+    path).  Times include a device synchronisation, so they cover the GPU work."""
+    dev = language_model(model).embed_tokens.weight.device
+    if prefill is None:
+        torch.cuda.synchronize(dev)
+        t = time.perf_counter()
+        out = model(input_ids=ids.to(dev), use_cache=True, logits_to_keep=1)
+        logits, past = out.logits[0, -1].float(), out.past_key_values
+        nxt = logits.argmax().view(1, 1)
+        toks = [int(nxt.item())]
+        ttft = time.perf_counter() - t
+        t = time.perf_counter()
+        for _ in range(n_decode - 1):
+            out = model(input_ids=nxt, past_key_values=past, use_cache=True, logits_to_keep=1)
+            past = out.past_key_values
+            nxt = out.logits[0, -1].argmax().view(1, 1)
+            toks.append(int(nxt.item()))
+        dec = (n_decode - 1) / (time.perf_counter() - t) if n_decode > 1 else 0.0
+        return ttft, dec, toks, logits
+    T = ids.shape[1]
+    decoder = Decoder(prefill, max_len=T + max(n_decode, 2) + 1)
+    torch.cuda.synchronize(dev)
+    t = time.perf_counter()
+    logits = decoder.start(ids)
+    torch.cuda.synchronize(dev)
+    ttft = time.perf_counter() - t
+    dec = 0.0
+    if n_decode > 1:
+        decoder.capture()
+        torch.cuda.synchronize(dev)
+        t = time.perf_counter()
+        for _ in range(n_decode - 2):
+            decoder.replay()
+        torch.cuda.synchronize(dev)
+        if n_decode > 2:
+            dec = (n_decode - 2) / (time.perf_counter() - t)
+    return ttft, dec, decoder.emitted[:n_decode].tolist(), logits

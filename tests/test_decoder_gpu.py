@@ -104,3 +104,23 @@ def test_norm_prologues_match_the_row_kernels():
     for i in range(5):
         assert torch.equal(fused.replay(), rows.replay()), f"replay {i}"
     assert torch.equal(fused.emitted, rows.emitted)
+
+
+@torch.inference_mode()
+def test_run_like_the_reference():
+    """pipeline.run with gemma_npu.py:271-296's signature and results: (ttft, decode tok/s, tokens,
+    last-token logits).  With the engine's Prefill its tokens are a Decoder's (the first the argmax of
+    the prefill logits, the rest greedy steps); without one it is HF's forward and decode loop on the
+    engine, whose first-token logits agree with the pipeline's within the prefill tolerance."""
+    from w8a8.pipeline import Decoder, Prefill, run
+    ours = engine_model(build(seed=39))
+    ids = torch.randint(0, 512, (1, 17), generator=torch.Generator().manual_seed(40))
+    ttft, dec, toks, logits = run(ours, ids, 12, Prefill(ours))
+    assert ttft > 0 and dec > 0 and len(toks) == 12
+    assert toks[0] == int(logits.argmax())
+    ref = Decoder(Prefill(ours), max_len=40)
+    ref.start(ids)
+    assert toks == [toks[0]] + ref.generate(11, graph=False)
+    ttft2, dec2, toks2, logits2 = run(ours, ids, 5)
+    assert ttft2 > 0 and dec2 > 0 and len(toks2) == 5 and toks2[0] == int(logits2.argmax())
+    assert rel_err(logits, logits2) < 0.1
