@@ -399,6 +399,29 @@ def gemv_norm_bf16(y, res, w1, eps, w, s, act=None, w2=None, norm2=True, scalar=
     return out, h
 
 
+def decode_tail(y, cap, pos, pos64, tok, emitted, n_emitted, logits=None, workspace=None):
+    """The decode step's tail in two launches: y bf16 [V] (the LM head's output) softcapped as the
+    model's bf16 ops do it (cap > 0; 0 or None: no softcap) into fp32 logits [V]; the first index of
+    their maximum becomes the next token (tok, int64 [1, 1]) and is written at emitted[n_emitted]
+    (int64 [max]); n_emitted, pos (int32 [1]) and pos64 (int64 [1]) advance by one.  Returns the
+    logits."""
+    _check(y, "y", torch.bfloat16, 1)
+    V = y.shape[0]
+    if logits is None:
+        logits = torch.empty(V, dtype=torch.float32, device=y.device)
+    _check(logits, "logits", torch.float32, 1)
+    for t, name, dt in ((pos, "pos", torch.int32), (pos64, "pos64", torch.int64), (tok, "tok", torch.int64),
+                        (emitted, "emitted", torch.int64), (n_emitted, "n_emitted", torch.int64)):
+        if not isinstance(t, torch.Tensor) or t.dtype != dt or t.device != y.device or not t.is_contiguous():
+            raise ValueError(f"decode_tail: {name} must be a contiguous {dt} tensor on y's device")
+    need = int(lib().w8a8_decode_tail_workspace_bytes(V))
+    ws = workspace if workspace is not None else torch.empty(need, dtype=torch.uint8, device=y.device)
+    call("w8a8_decode_tail", y.data_ptr(), V, float(cap or 0.0), logits.data_ptr(), pos.data_ptr(), pos64.data_ptr(),
+         tok.data_ptr(), emitted.data_ptr(), n_emitted.data_ptr(), emitted.numel(), ws.data_ptr(), ws.numel(),
+         _stream(y))
+    return logits
+
+
 def rms_residual_norm(y, res, w1, w2, eps, scalar=None):
     """(h, x): h = bf16(bf16(res + bf16(rms(y) * w1)) * scalar) and x = bf16(rms(h) * w2), one launch:
     k_post_attn's two norms (pipeline.py:95-99), or k_ple_out and the next layer's input norm

@@ -43,6 +43,7 @@ import time
 import torch
 
 from . import attention, fused, ops
+from ._lib import lib
 from .hf import language_model
 
 ROLES = ("qkv", "o", "gate_up", "down", "ple_gate", "ple_proj")
@@ -370,6 +371,8 @@ class Decoder:
         self.final_norm = getattr(norm, "weight", None) if getattr(norm, "with_scale", True) else None
         if float(getattr(norm, "eps", self.cfg.rms_norm_eps)) != float(self.cfg.rms_norm_eps):
             raise ValueError("Decoder: the final norm's eps differs from the layers' rms_norm_eps")
+        self.tail_ws = torch.empty(int(lib().w8a8_decode_tail_workspace_bytes(self.cfg.vocab_size)),
+                                   dtype=torch.uint8, device=dev)
         # the residual stream's norms as the prologue of the linear that reads them (hidden <= 1536)
         self.fuse_norms = self.cfg.hidden_size <= 1536 and self.cfg.hidden_size % 16 == 0
         self.length = None
@@ -414,15 +417,15 @@ class Decoder:
         self.emitted.index_copy_(0, self.n_emitted, nxt)
         self.n_emitted.add_(1)
 
-    def _logits(self, x):
+    def _head(self, x):
         """The model's head on the token's final-norm row x as HF's decode call computes it (the loop
-        this replaces): LM head, and the logit softcap in the model's dtype, then fp32.  (The prefill
-        pipeline takes the softcap in fp32, as pipeline.py:334-338 does.)"""
-        logits = self.pre.model.lm_head(x[None])[0, -1]
-        cap = self.cfg.final_logit_softcapping
-        if cap:
-            logits = torch.tanh(logits / cap) * cap
-        return logits.float()
+        this replaces), and the step's end: the LM head GEMV, then in two launches the logit softcap
+        in the model's dtype (bf16 ops, then fp32; the prefill pipeline takes it in fp32, as
+        pipeline.py:334-338 does), the greedy argmax into the next token and the emitted list, and
+        the position advanced.  Returns the fp32 logits."""
+        y = self.pre.model.lm_head(x[None])[0, -1]
+        return ops.decode_tail(y, self.cfg.final_logit_softcapping, self.pos, self.pos64, self.tok, self.emitted,
+                               self.n_emitted, workspace=self.tail_ws)
 
     def _norm_linear(self, pend, w, act=None, mul=None):
         """The linear w on the residual stream's norm: pend = (y, res, w1, scalar, w2, store) describes
@@ -502,11 +505,7 @@ class Decoder:
             h, pend = self._layer(p, h, pend, per_layer, scalar, rope, nxt)
         y, res, w1, sc, w2, _ = pend
         _, x = ops.rms_residual_norm(y, res, w1, w2, self.cfg.rms_norm_eps, scalar=sc)
-        logits = self._logits(x)
-        self._emit(logits)
-        self.pos.add_(1)
-        self.pos64.add_(1)
-        return logits
+        return self._head(x)
 
     @torch.inference_mode()
     def capture(self):

@@ -375,6 +375,18 @@ int w8a8_gemv_packed_norm_bf16(const uint16_t *y, const uint16_t *res, const uin
                                int64_t K, const void *scales, int scale_is_f32, int act, const uint16_t *mul,
                                uint16_t *out, hipStream_t stream);
 
+/* The decode step's end (the reference's decode loop, gemma_npu.py:292-295), two launches: y bf16 [V]
+ * (the LM head's output) softcapped as the model's bf16 ops do it when cap > 0 (t = bf16(y * (1/cap)),
+ * u = bf16(tanh(t)), bf16(u * cap); cap 0: none) into fp32 logits [V]; the first index of their
+ * maximum (NaN counting as the largest, as torch.argmax) is written to *tok and to emitted[*n_emitted]
+ * (when below max_emitted); *n_emitted, *pos and *pos64 advance by one.  Everything it reads and
+ * writes is in device memory, so a captured decode step replays it at each new position.  Workspace
+ * bytes from w8a8_decode_tail_workspace_bytes(V). */
+int64_t w8a8_decode_tail_workspace_bytes(int64_t V);
+int w8a8_decode_tail(const uint16_t *y, int64_t V, float cap, float *logits, int32_t *pos, int64_t *pos64,
+                     int64_t *tok, int64_t *emitted, int64_t *n_emitted, int64_t max_emitted, void *workspace,
+                     int64_t workspace_bytes, hipStream_t stream);
+
 /* ---- prefill attention ------------------------------------------------------------------ */
 
 /* o[h, i, :] = sum_j softmax_j(scale * q[h, i] . k[g, j]) v[g, j] with g = h / (H / KV), over the

@@ -124,3 +124,34 @@ def test_run_like_the_reference():
     ttft2, dec2, toks2, logits2 = run(ours, ids, 5)
     assert ttft2 > 0 and dec2 > 0 and len(toks2) == 5 and toks2[0] == int(logits2.argmax())
     assert rel_err(logits, logits2) < 0.1
+
+
+@pytest.mark.parametrize("cap", [30.0, None])
+def test_decode_tail_equals_the_models_softcap_and_argmax(cap):
+    """ops.decode_tail (the decode step's end in two launches) against the ops it replaces: the logit
+    softcap as the model's bf16 ops compute it, bit for bit; the next token = torch.argmax of those
+    logits (the first index of the maximum: a tie planted across candidate workgroups, then a NaN);
+    the emitted list, its count and the position advanced by one.  A ragged vocabulary of 262149."""
+    from w8a8 import ops
+    V = 262144 + 5
+    g = torch.Generator(device=DEV).manual_seed(41)
+    y = (torch.randn(V, generator=g, device=DEV) * 20).to(torch.bfloat16)
+    top = y.float().abs().max().to(torch.bfloat16) * 2
+    y[70000] = top
+    y[3000] = top  # the same maximum at a smaller index, in another workgroup
+    for plant_nan in (False, True):
+        if plant_nan:
+            y[200000] = float("nan")
+        want = (torch.tanh(y / cap) * cap).float() if cap else y.float()
+        pos = torch.tensor([7], dtype=torch.int32, device=DEV)
+        pos64 = torch.tensor([7], dtype=torch.long, device=DEV)
+        tok = torch.zeros((1, 1), dtype=torch.long, device=DEV)
+        emitted = torch.zeros(16, dtype=torch.long, device=DEV)
+        n = torch.tensor([3], dtype=torch.long, device=DEV)
+        got = ops.decode_tail(y, cap, pos, pos64, tok, emitted, n)
+        assert torch.equal(got.isnan(), want.isnan())
+        assert torch.equal(torch.nan_to_num(got), torch.nan_to_num(want))
+        expect = 200000 if plant_nan else 3000
+        assert int(want.argmax()) == expect and int(tok) == expect
+        assert int(emitted[3]) == expect and int(emitted.sum()) == expect
+        assert int(n) == 4 and int(pos) == 8 and int(pos64) == 8
