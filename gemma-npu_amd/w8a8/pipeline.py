@@ -401,12 +401,11 @@ class Decoder:
         return logits
 
     def _emit(self, logits):
-        """Greedy choice on the device: the argmax becomes the next input token and is recorded.
-        The argmax runs in two single-block stages (per row of a [rows, 512] view, then over the
-        rows' maxima; the first index of the maximum, as a flat argmax gives): torch's flat argmax
-        over the whole vocabulary is a multi-block reduction that clears a counter with a memset,
-        which a captured graph must not hold.  Writes are index_copy_ kernels, not copies, for the
-        same reason."""
+        """The first new token after the prefill, chosen on the device: the argmax becomes the next
+        input token and is recorded (the decode steps take theirs in ops.decode_tail).  The argmax
+        runs in two single-block stages (per row of a [rows, 512] view, then over the rows' maxima;
+        the first index of the maximum, as a flat argmax gives) and the writes are index_copy_
+        kernels, so no memset or memcpy is issued."""
         V = logits.shape[0]
         cols = 512 if V % 512 == 0 else V
         grid = logits.view(-1, cols)
