@@ -1170,7 +1170,6 @@ __global__ __launch_bounds__(512) void attn_merge_kernel(AttnParams p) {
 // row-major V rows with ds_read_b64_tr_b16 (result lane i, slot j = lane 4j + i/4's element i%4 of a
 // 16-lane group), its P^T operand from LDS.
 // keys per chunk: 64 (32 at head_dim 512, so that two workgroups fit in a CU's LDS)
-__host__ __device__ constexpr int dec_chunk(int D) { return D >= 512 ? 32 : 64; }
 
 struct DecodeParams {
   const uint16_t* q; int64_t qhs;       // bf16 [H, D]
@@ -1975,20 +1974,22 @@ extern "C" int w8a8_attention_quant_bf16(const uint16_t* q, int64_t q_head_strid
 
 // The split and merge launches of one decode call: nchunk_grid chunks per KV head, partials in the
 // workspace (nchunk_grid per KV head and query head).
-static void decode_launch(DecodeParams& p, int64_t D, void* workspace, hipStream_t stream) {
+// The split kernel, then (merge) the merge kernel.  The chunk partials sit at the start of the
+// workspace: part_o [KV][nchunk_grid][G][D] fp32, then part_ml [KV][nchunk_grid][G][2].
+static void decode_launch(DecodeParams& p, int64_t D, void* workspace, hipStream_t stream, bool merge = true) {
   p.part_o = static_cast<float*>(workspace);
   p.part_ml = p.part_o + int64_t(p.KV) * p.nchunk_grid * p.G * D;
   const dim3 grid{unsigned(p.KV * p.nchunk_grid), 1, 1};
   const dim3 mgrid{unsigned(p.H), unsigned(D / 4 / DEC_MCOLS), 1};
   if (D == 128) {
     attn_decode_split_kernel<128><<<grid, dim3{256, 1, 1}, 0, stream>>>(p);
-    attn_decode_merge_kernel<128><<<mgrid, dim3{256, 1, 1}, 0, stream>>>(p);
+    if (merge) attn_decode_merge_kernel<128><<<mgrid, dim3{256, 1, 1}, 0, stream>>>(p);
   } else if (D == 256) {
     attn_decode_split_kernel<256><<<grid, dim3{256, 1, 1}, 0, stream>>>(p);
-    attn_decode_merge_kernel<256><<<mgrid, dim3{256, 1, 1}, 0, stream>>>(p);
+    if (merge) attn_decode_merge_kernel<256><<<mgrid, dim3{256, 1, 1}, 0, stream>>>(p);
   } else {
     attn_decode_split_kernel<512><<<grid, dim3{256, 1, 1}, 0, stream>>>(p);
-    attn_decode_merge_kernel<512><<<mgrid, dim3{256, 1, 1}, 0, stream>>>(p);
+    if (merge) attn_decode_merge_kernel<512><<<mgrid, dim3{256, 1, 1}, 0, stream>>>(p);
   }
 }
 
@@ -2058,10 +2059,6 @@ extern "C" int w8a8_attention_decode_bf16(const uint16_t* q, int64_t q_head_stri
 }
 
 // Chunks per KV head the device-position launch holds: enough for every position below Tk.
-static int decode_grid_chunks(int64_t D, int64_t Tk, int64_t window) {
-  const int64_t span = window > 0 && window < Tk ? window : Tk;
-  return int((span - 1) / dec_chunk(int(D)) + 1);
-}
 
 extern "C" int64_t w8a8_attention_decode_dev_workspace_bytes(int64_t H, int64_t KV, int64_t Tk, int64_t D,
                                                              int64_t window) {
@@ -2136,7 +2133,10 @@ extern "C" int w8a8_attention_decode_qkv_dev_bf16(const uint16_t* y, const uint1
     return fail(W8A8_ENOTSUP, "%s: %d key chunks of %d (at most %d)", what, decode_grid_chunks(D, Tk, window),
                 dec_chunk(int(D)), DEC_MAX_CHUNKS);
   if (!(scale > 0.0f) || scale == __builtin_inff()) return fail(W8A8_EINVAL, "%s: scale must be positive", what);
-  if (!y || !cos_ || !sin_ || !k || !v || !o || !q_pos || !workspace) return fail(W8A8_EINVAL, "%s: null pointer", what);
+  if (!y || !cos_ || !sin_ || !k || !v || !q_pos || !workspace) return fail(W8A8_EINVAL, "%s: null pointer", what);
+  if (!o && decode_grid_chunks(D, Tk, window) > DEC_MERGE_IN_GEMV_CHUNKS)
+    return fail(W8A8_ENOTSUP, "%s: without o the chunks (%d) are merged by w8a8_gemv_packed_attn_merge_bf16, which "
+                "takes at most %d", what, decode_grid_chunks(D, Tk, window), DEC_MERGE_IN_GEMV_CHUNKS);
   const int64_t need = w8a8_attention_decode_dev_workspace_bytes(H, KV, Tk, D, window);
   if (workspace_bytes < need)
     return fail(W8A8_EINVAL, "%s: workspace of %lld bytes, %lld needed", what, (long long)workspace_bytes,
@@ -2164,6 +2164,6 @@ extern "C" int w8a8_attention_decode_qkv_dev_bf16(const uint16_t* y, const uint1
   p.scale = scale; p.c = scale * 1.4426950408889634f;
   p.qkv_y = y; p.rope_c = cos_; p.rope_s = sin_; p.qw = qw; p.kw = kw; p.qkv_eps = eps; p.kv_write = kv_write ? 1 : 0;
   p.qkv_bytes = uint32_t((H + (kv_write ? 2 * KV : 0)) * D * 2);
-  decode_launch(p, D, workspace, stream);
+  decode_launch(p, D, workspace, stream, o != nullptr);
   return check_launch("attention_decode_qkv_dev_bf16");
 }

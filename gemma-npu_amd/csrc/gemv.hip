@@ -36,7 +36,91 @@ struct GemvParams {
   const uint16_t* pro_y; const uint16_t* pro_res; const uint16_t* pro_w1; const uint16_t* pro_scalar;
   const uint16_t* pro_w2; uint16_t* pro_h;
   float pro_eps; int pro_norm2, pro_ch;  // pro_ch: the row kernel's 8-element chunks per lane for K
+  // Attention-merge prologue (PRO == 4, M = 1): the activation row is one token's decode attention
+  // output [H * D], merged from the split-key kernel's chunk partials (part_o [KV][nchunk_grid][G][D],
+  // part_ml [KV][nchunk_grid][G][2]) as attn_decode_merge_kernel merges them, for at most
+  // DEC_MERGE_IN_GEMV_CHUNKS chunks; the live chunks follow from the position in device memory.
+  const float* m_po; const float* m_ml; const int* m_pos;
+  int m_window, m_nchunk_grid, m_G, m_D, m_chunk; float m_c;
 };
+
+// The merge prologue.  For at most 16 chunks attn_decode_merge_kernel's sums reduce to fixed orders,
+// taken here: per head, its chunk weights w_c = exp2(M_c c - M c) and the weighted l over a 16-leaf
+// tree (t + 8, t + 4, t + 2, t + 1), made once per workgroup by one thread per head into mw
+// [16 heads][17] (w_0 .. w_15, then 1 / l); per element, the chunks in order, each term
+// fma(w_c, o_c, 0), a +0 after them when fewer than 16 are live (the merge kernel's empty parts).
+// Each thread makes elements e, e + 1 of the row (one head, columns d, d + 1); the partials of its
+// first pair are fetched before the weights are made.
+__device__ __forceinline__ void gemv_attn_merge_row(const GemvParams& p, uint16_t* xs, float* mw) {
+  constexpr int NC = DEC_MERGE_IN_GEMV_CHUNKS;
+  const int pos = *p.m_pos;
+  const int klo = p.m_window > 0 ? max(0, pos - p.m_window + 1) : 0;
+  const int nchunk = max(0, min((pos - klo) / p.m_chunk + 1, p.m_nchunk_grid));
+  const int H = p.K / p.m_D;
+  auto head_base = [&](int h) { return int64_t(h / p.m_G) * p.m_nchunk_grid * p.m_G + h % p.m_G; };
+  // this thread's first pair: its partials now
+  int e = 2 * int(threadIdx.x);
+  v2f oc[NC];
+  auto fetch = [&](int e) {
+    const int h = e / p.m_D, d = e % p.m_D;
+    const int64_t hb = head_base(h);
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+      oc[c] = (c < nchunk && e < p.K) ? *reinterpret_cast<const v2f*>(p.m_po + (hb + int64_t(c) * p.m_G) * p.m_D + d)
+                                      : v2f{0.0f, 0.0f};
+  };
+  fetch(e);
+  if (int(threadIdx.x) < H) {
+    const int h = int(threadIdx.x);
+    const int64_t hb = head_base(h);
+    float mc[NC], lc[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const v2f ml = c < nchunk ? *reinterpret_cast<const v2f*>(p.m_ml + (hb + int64_t(c) * p.m_G) * 2)
+                                : v2f{-__builtin_inff(), 0.0f};
+      mc[c] = ml[0];
+      lc[c] = ml[1];
+    }
+    float M = -__builtin_inff();
+#pragma unroll
+    for (int c = 0; c < NC; ++c) M = fmaxf(M, mc[c]);
+    const float ms = M == -__builtin_inff() ? 0.0f : M * p.m_c;
+    float v[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const float w = c < nchunk ? __builtin_amdgcn_exp2f(__builtin_fmaf(mc[c], p.m_c, -ms)) : 0.0f;
+      mw[h * (NC + 1) + c] = w;
+      v[c] = c < nchunk ? __builtin_fmaf(w, lc[c], 0.0f) : 0.0f;
+    }
+#pragma unroll
+    for (int s = 8; s > 0; s >>= 1)
+#pragma unroll
+      for (int t = 0; t < s; ++t) v[t] = v[t] + v[t + s];
+    mw[h * (NC + 1) + NC] = v[0] > 0.0f ? 1.0f / v[0] : 0.0f;
+  }
+  __syncthreads();
+  for (; e < p.K; e += 2 * int(blockDim.x)) {
+    if (e != 2 * int(threadIdx.x)) fetch(e);
+    const float* wh = mw + (e / p.m_D) * (NC + 1);
+    float a0 = 0.0f, a1 = 0.0f;
+    if (nchunk > 0) {
+      a0 = __builtin_fmaf(wh[0], oc[0][0], 0.0f);
+      a1 = __builtin_fmaf(wh[0], oc[0][1], 0.0f);
+    }
+#pragma unroll
+    for (int c = 1; c < NC; ++c)
+      if (c < nchunk) {
+        a0 = a0 + __builtin_fmaf(wh[c], oc[c][0], 0.0f);
+        a1 = a1 + __builtin_fmaf(wh[c], oc[c][1], 0.0f);
+      }
+    if (nchunk < NC) {
+      a0 = a0 + 0.0f;
+      a1 = a1 + 0.0f;
+    }
+    const float inv = wh[NC];
+    *reinterpret_cast<uint32_t*>(xs + e) = pack_bf16x2(a0 * inv, a1 * inv);
+  }
+}
 
 // The row prologue on one wave, in the arithmetic and order of the row kernel's one-wave rows
 // (row_chain_kernel with 64 threads, rowops.hip): lane t holds chunks c < CH of 8 elements at
@@ -166,7 +250,8 @@ template <int TPW, int U, bool PACKED, int NWB, int ACT = 0, int PRO = 0>
 __global__ __launch_bounds__(NWB * 64) void gemv_kernel(GemvParams p) {
   static_assert(ACT != 1 || TPW == 2, "a GELU pair is one gate and one up tile per wave");
   __shared__ v4f red[NWB][TPW][64];
-  __shared__ __attribute__((aligned(16))) uint16_t xs[PRO ? PRO * 512 : 8];  // PRO: the activation row
+  __shared__ __attribute__((aligned(16))) uint16_t xs[PRO == 4 ? 4096 : PRO ? PRO * 512 : 8];  // PRO: the row
+  __shared__ float mw[PRO == 4 ? 16 * (DEC_MERGE_IN_GEMV_CHUNKS + 1) : 1];     // PRO 4: chunk weights
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int group_in_block = wave / p.split;
@@ -198,10 +283,10 @@ __global__ __launch_bounds__(NWB * 64) void gemv_kernel(GemvParams p) {
   for (int t = 0; t < TPW; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
   // PRO: the activation row is made once per workgroup by its first wave (one row: M = 1) while
   // every wave's first round of weight fragments is in flight.
-  RowIn<PRO ? PRO : 1> row;
+  RowIn<(PRO >= 1 && PRO <= 3) ? PRO : 1> row;
   v4i wpre[U][TPW];
   if constexpr (PRO) {
-    if (wave == 0) row.load(p);
+    if (PRO <= 3 && wave == 0) row.load(p);
     // Issued without branches (a fragment outside the weight is read past the buffer's end as
     // zeros), so the prologue's arithmetic can wait for its own operands and leave these in flight.
 #pragma unroll
@@ -213,7 +298,10 @@ __global__ __launch_bounds__(NWB * 64) void gemv_kernel(GemvParams p) {
         wpre[u][t] = __builtin_bit_cast(
             v4i, __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? wbase[t] + uint32_t(kb) * W_KB : 0x80000000u, 0, W_POL));
     }
-    if (wave == 0) row.make(p, xs);
+    if constexpr (PRO == 4)
+      gemv_attn_merge_row(p, xs, mw);
+    else if (wave == 0)
+      row.make(p, xs);
     __syncthreads();
   }
   if (active) {
@@ -555,6 +643,43 @@ extern "C" int w8a8_gemv_packed_norm_bf16(const uint16_t* y, const uint16_t* res
   else W8A8_NORM_GEMV(3);
 #undef W8A8_NORM_GEMV
   return check_launch("gemv_packed_norm_bf16");
+}
+
+extern "C" int w8a8_gemv_packed_attn_merge_bf16(const void* workspace, const int32_t* q_pos, int64_t H, int64_t KV,
+                                                int64_t Tk, int64_t D, int64_t window, float scale,
+                                                const int8_t* packed, int64_t N, const void* scales, int scale_is_f32,
+                                                uint16_t* out, hipStream_t stream) {
+  const char* what = "gemv_packed_attn_merge";
+  if (!workspace || !q_pos || !packed || !scales || !out) return fail(W8A8_EINVAL, "%s: null pointer", what);
+  if (H < 1 || KV < 1 || H % KV != 0 || H / KV > 16)
+    return fail(W8A8_EINVAL, "%s: H=%lld KV=%lld (H a multiple of KV, at most 16 per KV head)", what, (long long)H,
+                (long long)KV);
+  if (D != 128 && D != 256 && D != 512) return fail(W8A8_ENOTSUP, "%s: head_dim %lld", what, (long long)D);
+  if (Tk < 1 || Tk > INT32_MAX || window < 0 || window > INT32_MAX)
+    return fail(W8A8_EINVAL, "%s: Tk=%lld window=%lld", what, (long long)Tk, (long long)window);
+  const int nchunk_grid = decode_grid_chunks(D, Tk, window);
+  if (nchunk_grid > DEC_MERGE_IN_GEMV_CHUNKS)
+    return fail(W8A8_ENOTSUP, "%s: %d key chunks (at most %d)", what, nchunk_grid, DEC_MERGE_IN_GEMV_CHUNKS);
+  const int64_t K = H * D;
+  if (K > 4096) return fail(W8A8_ENOTSUP, "%s: H * D = %lld above 4096", what, (long long)K);
+  if (N < 1 || (N + 15) / 16 >= 4096) return fail(W8A8_ENOTSUP, "%s: N=%lld outside the few-tile shapes", what, (long long)N);
+  if (!(scale > 0.0f) || scale == __builtin_inff()) return fail(W8A8_EINVAL, "%s: scale must be positive", what);
+  if ((uintptr_t)workspace % 16 || (uintptr_t)packed % 16 || (uintptr_t)q_pos % 4)
+    return fail(W8A8_EALIGN, "%s: workspace and packed 16-byte aligned, q_pos 4-byte aligned", what);
+  const int64_t wb = w8a8_gemv_packed_bytes(N, K);
+  if (wb > INT32_MAX) return fail(W8A8_ENOTSUP, "%s: packed weight above 2 GiB", what);
+  GemvParams p{};
+  p.x = nullptr; p.ldx = K; p.w = packed; p.ldw = 0; p.s = scales; p.s_f32 = scale_is_f32 ? 1 : 0;
+  p.y = out; p.ldy = N; p.x_bytes = 0; p.w_bytes = uint32_t(wb);
+  p.M = 1; p.N = int(N); p.K = int(K); p.KB = int((K + 63) / 64);
+  const int G = int(H / KV);
+  p.m_po = static_cast<const float*>(workspace);
+  p.m_ml = p.m_po + int64_t(KV) * nchunk_grid * G * D;
+  p.m_pos = q_pos; p.m_window = int(window); p.m_nchunk_grid = nchunk_grid; p.m_G = G; p.m_D = int(D);
+  p.m_chunk = dec_chunk(int(D));
+  p.m_c = scale * 1.4426950408889634f;  // the attention's exp2 factor, computed as it computes it
+  gemv_launch_act<true, 0, 4>(p, stream);
+  return check_launch("gemv_packed_attn_merge_bf16");
 }
 
 extern "C" int w8a8_gemv_bf16(const uint16_t* x, int64_t ldx, int64_t M, const int8_t* w, int64_t ldw, int64_t N,

@@ -5,6 +5,7 @@
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v2f __attribute__((ext_vector_type(2)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
 typedef unsigned v2u __attribute__((ext_vector_type(2)));
@@ -282,6 +283,17 @@ __device__ __forceinline__ float gelu_tanh_f32(float x) {
   const float inner = kBeta * (x + kKappa * (x * x * x));
   return 0.5f * x * (1.0f + tanh_f32(inner));
 }
+
+// Decode attention chunks: keys per chunk (32 at head_dim 512, so that two workgroups fit in a CU's
+// LDS), and the chunks a launch covers per KV head for a cache of Tk rows (the last `window` of
+// them with a window).  Both the attention and the GEMV that merges its chunks use these.
+__host__ __device__ constexpr int dec_chunk(int D) { return D >= 512 ? 32 : 64; }
+inline int decode_grid_chunks(int64_t D, int64_t Tk, int64_t window) {
+  const int64_t span = window > 0 && window < Tk ? window : Tk;
+  return int((span - 1) / dec_chunk(int(D)) + 1);
+}
+// At most this many chunks are merged inside the o GEMV (w8a8_gemv_packed_attn_merge_bf16).
+constexpr int DEC_MERGE_IN_GEMV_CHUNKS = 16;
 
 // Status codes and the extern "C" declarations every source implements.
 #include "w8a8.h"

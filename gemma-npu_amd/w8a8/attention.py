@@ -206,6 +206,14 @@ def decode(q, k, v, q_pos=None, window=0, scale=1.0, out=None, return_lse=False,
     return (out, lse) if return_lse else out
 
 
+def decode_grid_chunks(D, Tk, window=0):
+    """Key chunks per KV head the decode attention launches for a cache of Tk rows (the last `window`
+    keys with a window): 64 keys a chunk, 32 at head_dim 512."""
+    chunk = 32 if D >= 512 else 64
+    span = window if 0 < window < Tk else Tk
+    return (span - 1) // chunk + 1
+
+
 def decode_at_workspace_bytes(H, KV, Tk, D, window=0):
     """Bytes of scratch decode_at() needs for a key cache of Tk rows."""
     n = lib().w8a8_attention_decode_dev_workspace_bytes(H, KV, Tk, D, int(window))
@@ -253,13 +261,14 @@ def decode_at(q, k, v, pos, window=0, scale=1.0, out=None, workspace=None):
 
 
 def decode_qkv_at(y, cos, sin, qw, kw, eps, H, KV, D, k, v, pos, kv_write, window=0, scale=1.0, out=None,
-                  workspace=None):
+                  workspace=None, merge=True):
     """k_qkv and decode_at in one launch, for the token's qkv row y [1, (H + 2 KV) D] bf16 ([1, H D] when
     the layer reads another layer's keys): q = RoPE(rms(q head) * qw) per head with the cos / sin rows
     [1, D] at the position; with kv_write the token's key (rms * kw, RoPE) and value (rms) of each KV
     head are also written into the cache k / v [KV, Tk, D] at the position read from pos (int32 [1])
     and attended to there.  Bit for bit fused.k_qkv_cache (or fused.k_qkv for q alone) followed by
-    decode_at.  At most 8 query heads per KV head."""
+    decode_at.  At most 8 query heads per KV head.  merge=False leaves the chunk partials in the
+    workspace for ops.gemv_attn_merge_bf16 (the o projection that merges them) and returns None."""
     for t, name in ((y, "y"), (cos, "cos"), (sin, "sin")):
         if not isinstance(t, torch.Tensor) or t.dtype != torch.bfloat16 or t.device.type != "cuda":
             raise ValueError(f"decode_qkv_at: {name} must be a bf16 GPU tensor")
@@ -280,7 +289,11 @@ def decode_qkv_at(y, cos, sin, qw, kw, eps, H, KV, D, k, v, pos, kv_write, windo
     KVk, Tk, Dk = k.shape
     if KVk != KV or Dk != D or tuple(v.shape) != (KV, Tk, D):
         raise ValueError(f"decode_qkv_at: k {tuple(k.shape)} / v {tuple(v.shape)} do not match KV={KV} D={D}")
-    if out is None:
+    if not merge:
+        if workspace is None:
+            raise ValueError("decode_qkv_at: merge=False needs the workspace that holds the partials")
+        out = None
+    elif out is None:
         out = torch.empty((H, D), dtype=torch.bfloat16, device=y.device)
     elif out.shape != (H, D) or out.dtype != torch.bfloat16 or (D > 1 and out.stride(1) != 1):
         raise ValueError(f"decode_qkv_at: out must be bf16 [{H}, {D}] with a contiguous last dimension")
@@ -291,8 +304,8 @@ def decode_qkv_at(y, cos, sin, qw, kw, eps, H, KV, D, k, v, pos, kv_write, windo
     ptr = lambda t: None if t is None else t.data_ptr()
     call("w8a8_attention_decode_qkv_dev_bf16", y.data_ptr(), cos.data_ptr(), sin.data_ptr(), ptr(qw), ptr(kw),
          float(eps), k.data_ptr(), khs, krs, v.data_ptr(), vhs, vrs, H, KV, Tk, D, 1 if kv_write else 0,
-         pos.data_ptr(), int(window), float(scale), out.data_ptr(), out.stride(0) if H > 1 else D, ws.data_ptr(),
-         ws.numel(), _stream(y))
+         pos.data_ptr(), int(window), float(scale), None if out is None else out.data_ptr(),
+         D if out is None or H == 1 else out.stride(0), ws.data_ptr(), ws.numel(), _stream(y))
     return out
 
 

@@ -399,6 +399,28 @@ def gemv_norm_bf16(y, res, w1, eps, w, s, act=None, w2=None, norm2=True, scalar=
     return out, h
 
 
+def gemv_attn_merge_bf16(workspace, pos, H, KV, Tk, D, window, scale, w, s):
+    """The decode step's o projection with the attention's chunk merge as its prologue: the output
+    row [1, N] of the GEMV on the token's attention output [H * D], which every workgroup merges
+    from the chunk partials that attention.decode_qkv_at(..., merge=False) left in `workspace`
+    (the same Tk, window, scale).  Bit for bit the merge kernel followed by gemv_bf16.  At most 16
+    key chunks (a sliding window of 512 keys at head_dim 256 takes 8) and H * D <= 4096."""
+    if not isinstance(w, GemvWeight):
+        raise TypeError("gemv_attn_merge_bf16: w must be a packed GemvWeight")
+    if s.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"gemv_attn_merge_bf16: scales must be bf16 or fp32, got {s.dtype}")
+    if w.K != H * D or s.shape[0] != w.N:
+        raise ValueError(f"gemv_attn_merge_bf16: weight [{w.N}, {w.K}] does not take a row of {H}x{D}")
+    if not isinstance(pos, torch.Tensor) or pos.dtype != torch.int32 or pos.numel() != 1:
+        raise ValueError("gemv_attn_merge_bf16: pos must be an int32 tensor of one element")
+    out = torch.empty((1, w.N), dtype=torch.bfloat16, device=w.data.device)
+    _same_device(workspace, pos, w.data, s, out)
+    call("w8a8_gemv_packed_attn_merge_bf16", workspace.data_ptr(), pos.data_ptr(), H, KV, Tk, D, int(window),
+         float(scale), w.data.data_ptr(), w.N, s.data_ptr(), 1 if s.dtype == torch.float32 else 0, out.data_ptr(),
+         _stream(out))
+    return out
+
+
 def decode_tail(y, cap, pos, pos64, tok, emitted, n_emitted, logits=None, workspace=None):
     """The decode step's tail in two launches: y bf16 [V] (the LM head's output) softcapped as the
     model's bf16 ops do it (cap > 0; 0 or None: no softcap) into fp32 logits [V]; the first index of

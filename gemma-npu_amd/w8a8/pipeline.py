@@ -373,6 +373,10 @@ class Decoder:
             raise ValueError("Decoder: the final norm's eps differs from the layers' rms_norm_eps")
         self.tail_ws = torch.empty(int(lib().w8a8_decode_tail_workspace_bytes(self.cfg.vocab_size)),
                                    dtype=torch.uint8, device=dev)
+        # layers whose few key chunks (a sliding window) the o projection merges in its prologue
+        self.merge_in_o = {p.index for p in prefill.plans
+                           if p.heads // p.kv_heads <= 8 and p.heads * p.head_dim <= 4096
+                           and attention.decode_grid_chunks(p.head_dim, self.max_len, p.window) <= 16}
         # the residual stream's norms as the prologue of the linear that reads them (hidden <= 1536)
         self.fuse_norms = self.cfg.hidden_size <= 1536 and self.cfg.hidden_size % 16 == 0
         self.length = None
@@ -459,10 +463,17 @@ class Decoder:
         eps = self.cfg.rms_norm_eps
         kc, vc = self.cache[p.kv_source]
         if p.heads // p.kv_heads <= 8:
-            # k_qkv inside the attention launch (the key and value written at the position there)
+            # k_qkv inside the attention launch (the key and value written at the position there); a
+            # sliding window's few key chunks are merged in the o projection's prologue
+            merge_in_o = p.index in self.merge_in_o
             o = attention.decode_qkv_at(y, cos, sin, p.norm_q, p.norm_k, eps, p.heads, p.kv_heads, p.head_dim, kc,
-                                        vc, self.pos, not p.shares_kv, p.window, 1.0, workspace=self.workspace)
+                                        vc, self.pos, not p.shares_kv, p.window, 1.0, workspace=self.workspace,
+                                        merge=not merge_in_o)
+            if merge_in_o:
+                y = ops.gemv_attn_merge_bf16(self.workspace, self.pos, p.heads, p.kv_heads, self.max_len, p.head_dim,
+                                             p.window, 1.0, W["o"].gemv_w, W["o"].sw_bf16)
         else:
+            merge_in_o = False
             if p.shares_kv:
                 q = fused.k_qkv(y, None, None, cos, sin, p.norm_q, None, eps, p.heads, p.kv_heads, p.head_dim,
                                 True)[0]
@@ -470,7 +481,8 @@ class Decoder:
                 q = fused.k_qkv_cache(y, cos, sin, p.norm_q, p.norm_k, eps, p.heads, p.kv_heads, p.head_dim, kc, vc,
                                       self.pos)
             o = attention.decode_at(q[:, 0], kc, vc, self.pos, p.window, 1.0, workspace=self.workspace)
-        y = ops.gemv_bf16(o.reshape(1, -1), W["o"].gemv_w, W["o"].sw_bf16)
+        if not merge_in_o:
+            y = ops.gemv_bf16(o.reshape(1, -1), W["o"].gemv_w, W["o"].sw_bf16)
         g, h = self._norm_linear((y, h, p.norm_post_attn, None, p.norm_pre_ff, True), W["gate_up"], "gelu_pair")
         y = ops.gemv_bf16(g, W["down"].gemv_w, W["down"].sw_bf16)
         g, h = self._norm_linear((y, h, p.norm_post_ff, None, None, True), W["ple_gate"], "gelu_mul",

@@ -375,6 +375,17 @@ int w8a8_gemv_packed_norm_bf16(const uint16_t *y, const uint16_t *res, const uin
                                int64_t K, const void *scales, int scale_is_f32, int act, const uint16_t *mul,
                                uint16_t *out, hipStream_t stream);
 
+/* The decode step's o projection (gemma_npu.py:120-121 on the attention output) with the decode
+ * attention's chunk merge (local_attn.py:60-68) as its prologue: out [1, N] = the GEMV of the
+ * token's attention output [H * D], which every workgroup merges from the chunk partials that
+ * w8a8_attention_decode_qkv_dev_bf16 left in `workspace` when called with o = NULL (same H, KV, Tk,
+ * D, window, scale and q_pos).  Bit for bit that attention's merge followed by
+ * w8a8_gemv_packed_bf16; the merge launch is saved.  At most 16 key chunks (a sliding window of 512
+ * keys: 8 at head_dim 256, 16 at 512), H * D <= 4096, the few-tile GEMV shapes. */
+int w8a8_gemv_packed_attn_merge_bf16(const void *workspace, const int32_t *q_pos, int64_t H, int64_t KV, int64_t Tk,
+                                     int64_t D, int64_t window, float scale, const int8_t *packed, int64_t N,
+                                     const void *scales, int scale_is_f32, uint16_t *out, hipStream_t stream);
+
 /* The decode step's end (the reference's decode loop, gemma_npu.py:292-295), two launches: y bf16 [V]
  * (the LM head's output) softcapped as the model's bf16 ops do it when cap > 0 (t = bf16(y * (1/cap)),
  * u = bf16(tanh(t)), bf16(u * cap); cap 0: none) into fp32 logits [V]; the first index of their
@@ -506,7 +517,8 @@ int w8a8_attention_decode_dev_bf16(const uint16_t *q, int64_t q_head_stride, con
  * each KV head's key (norm with kw, RoPE) and value (norm without weight), writes them into k / v at
  * row *q_pos (when it is below Tk) and attends to them there.  Bit for bit the two-launch form.  At
  * most 8 query heads per KV head; 16-byte aligned pointers; workspace as
- * w8a8_attention_decode_dev_bf16's. */
+ * w8a8_attention_decode_dev_bf16's.  o = NULL: the chunks are not merged; their partials stay in
+ * the workspace for w8a8_gemv_packed_attn_merge_bf16 (at most 16 chunks). */
 int w8a8_attention_decode_qkv_dev_bf16(const uint16_t *y, const uint16_t *cos_, const uint16_t *sin_,
                                        const uint16_t *qw, const uint16_t *kw, float eps, uint16_t *k,
                                        int64_t k_head_stride, int64_t k_row_stride, uint16_t *v,

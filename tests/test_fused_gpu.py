@@ -405,3 +405,35 @@ def test_decode_qkv_at_equals_k_qkv_then_decode_at(D, KV, window):
             got = attention.decode_qkv_at(y, cos, sin, qw, kw, EPS, H, KV, D, kc, vc, pos, kv_write, window, 0.75)
             assert torch.equal(got, want), (p, kv_write)
             assert torch.equal(kc, kc_ref) and torch.equal(vc, vc_ref), (p, kv_write)
+
+
+@pytest.mark.parametrize("D, window, H, KV", [(256, 512, 8, 1), (512, 512, 8, 1), (128, 64, 4, 1), (256, 128, 16, 2)])
+def test_o_projection_merging_the_attention_chunks(D, window, H, KV):
+    """ops.gemv_attn_merge_bf16 (the o projection whose prologue merges the decode attention's key
+    chunks) after decode_qkv_at(..., merge=False) against the attention with its merge kernel
+    followed by the GEMV: the same output bit for bit, at positions with one, several and all 16
+    chunks live, on a chunk edge and at the cache's end."""
+    from w8a8 import attention
+    rows, N = 1100, 1536
+    y = (torch.randn(1, (H + 2 * KV) * D, generator=gen(60 + D)) * 0.7).to(torch.bfloat16).to(DEV)
+    ang = torch.rand(1, D, generator=gen(61)) * 6.0
+    cos, sin = ang.cos().to(torch.bfloat16).to(DEV), ang.sin().to(torch.bfloat16).to(DEV)
+    qw, kw = norm_weight(D, 62).to(DEV), norm_weight(D, 63).to(DEV)
+    fill = (torch.randn(KV, rows, D, generator=gen(64)) * 0.7).to(torch.bfloat16).to(DEV)
+    fill_v = torch.randn(KV, rows, D, generator=gen(65)).to(torch.bfloat16).to(DEV)
+    w = torch.randint(-127, 128, (N, H * D), generator=gen(66), dtype=torch.int8).to(DEV)
+    pw = ops.pack_gemv_weight(w)
+    s = (torch.rand(N, generator=gen(67)) * 0.01).to(torch.bfloat16).to(DEV)
+    ws = torch.empty(attention.decode_at_workspace_bytes(H, KV, rows, D, window), dtype=torch.uint8, device=DEV)
+    assert attention.decode_grid_chunks(D, rows, window) <= 16
+    for p in (0, 40, 63, 64, 300, 700, rows - 1):
+        pos = torch.tensor([p], dtype=torch.int32, device=DEV)
+        kc, vc = fill.clone(), fill_v.clone()
+        o = attention.decode_qkv_at(y, cos, sin, qw, kw, EPS, H, KV, D, kc, vc, pos, True, window, 0.5, workspace=ws)
+        want = ops.gemv_bf16(o.reshape(1, -1), pw, s)
+        kc2, vc2 = fill.clone(), fill_v.clone()
+        assert attention.decode_qkv_at(y, cos, sin, qw, kw, EPS, H, KV, D, kc2, vc2, pos, True, window, 0.5,
+                                       workspace=ws, merge=False) is None
+        got = ops.gemv_attn_merge_bf16(ws, pos, H, KV, rows, D, window, 0.5, pw, s)
+        assert torch.equal(got, want), p
+        assert torch.equal(kc2, kc) and torch.equal(vc2, vc), p
