@@ -1196,6 +1196,7 @@ struct DecodeParams {
   const uint16_t* qkv_y; const uint16_t* rope_c; const uint16_t* rope_s;
   const uint16_t* qw; const uint16_t* kw;
   float qkv_eps; int kv_write; uint32_t qkv_bytes;  // bytes of the qkv row
+  int rope_rows;  // rows of the cos / sin tables: row *pos_dev of them (1: that row whatever the position)
 };
 
 // The call's query position, first key, live chunks and key bound: the host's, or with pos_dev the
@@ -1277,16 +1278,18 @@ __global__ __launch_bounds__(256, 2) void attn_decode_split_kernel(DecodeParams 
   Bf16Words<E> raw[7][2];
   if (fused) {
     const uint32_t vec = uint32_t(D) * 2u;
-    const __amdgpu_buffer_rsrc_t ry = make_rsrc(p.qkv_y, p.qkv_bytes), rc = make_rsrc(p.rope_c, vec),
-                                 rs = make_rsrc(p.rope_s, vec), rqw = make_rsrc(p.qw, p.qw ? vec : 0u),
+    const uint32_t tab = uint32_t(p.rope_rows) * vec;  // a position past the tables reads zeros
+    const __amdgpu_buffer_rsrc_t ry = make_rsrc(p.qkv_y, p.qkv_bytes), rc = make_rsrc(p.rope_c, tab),
+                                 rs = make_rsrc(p.rope_s, tab), rqw = make_rsrc(p.qw, p.qw ? vec : 0u),
                                  rkw = make_rsrc(p.kw, p.kw ? vec : 0u);
     auto fetch = [&](int o, __amdgpu_buffer_rsrc_t r, bool on, int row) __attribute__((always_inline)) {
       const uint32_t off = on ? (uint32_t(row) * uint32_t(D) + uint32_t(p0)) * 2u : 0x80000000u;
       raw[o][0].load(r, off);
       raw[o][1].load(r, off + uint32_t(HALF) * 2u);
     };
-    fetch(5, rc, true, 0);
-    fetch(6, rs, true, 0);
+    const int rope_row = p.rope_rows > 1 ? max(geo.pos, 0) : 0;
+    fetch(5, rc, p.rope_rows == 1 || geo.pos < p.rope_rows, rope_row);
+    fetch(6, rs, p.rope_rows == 1 || geo.pos < p.rope_rows, rope_row);
     fetch(3, rqw, true, 0);
 #pragma unroll
     for (int j = 0; j < 2; ++j) fetch(j, ry, wave + 4 * j < p.G, g * p.G + wave + 4 * j);
@@ -2115,7 +2118,8 @@ extern "C" int w8a8_attention_decode_dev_bf16(const uint16_t* q, int64_t q_head_
 }
 
 extern "C" int w8a8_attention_decode_qkv_dev_bf16(const uint16_t* y, const uint16_t* cos_, const uint16_t* sin_,
-                                                  const uint16_t* qw, const uint16_t* kw, float eps, uint16_t* k,
+                                                  int64_t rope_rows, const uint16_t* qw, const uint16_t* kw, float eps,
+                                                  uint16_t* k,
                                                   int64_t k_head_stride, int64_t k_row_stride, uint16_t* v,
                                                   int64_t v_head_stride, int64_t v_row_stride, int64_t H, int64_t KV,
                                                   int64_t Tk, int64_t D, int kv_write, const int32_t* q_pos,
@@ -2134,6 +2138,7 @@ extern "C" int w8a8_attention_decode_qkv_dev_bf16(const uint16_t* y, const uint1
                 dec_chunk(int(D)), DEC_MAX_CHUNKS);
   if (!(scale > 0.0f) || scale == __builtin_inff()) return fail(W8A8_EINVAL, "%s: scale must be positive", what);
   if (!y || !cos_ || !sin_ || !k || !v || !q_pos || !workspace) return fail(W8A8_EINVAL, "%s: null pointer", what);
+  if (rope_rows < 1 || rope_rows * D * 2 > INT32_MAX) return fail(W8A8_EINVAL, "%s: rope_rows=%lld", what, (long long)rope_rows);
   if (!o && decode_grid_chunks(D, Tk, window) > DEC_MERGE_IN_GEMV_CHUNKS)
     return fail(W8A8_ENOTSUP, "%s: without o the chunks (%d) are merged by w8a8_gemv_packed_attn_merge_bf16, which "
                 "takes at most %d", what, decode_grid_chunks(D, Tk, window), DEC_MERGE_IN_GEMV_CHUNKS);
@@ -2164,6 +2169,7 @@ extern "C" int w8a8_attention_decode_qkv_dev_bf16(const uint16_t* y, const uint1
   p.scale = scale; p.c = scale * 1.4426950408889634f;
   p.qkv_y = y; p.rope_c = cos_; p.rope_s = sin_; p.qw = qw; p.kw = kw; p.qkv_eps = eps; p.kv_write = kv_write ? 1 : 0;
   p.qkv_bytes = uint32_t((H + (kv_write ? 2 * KV : 0)) * D * 2);
+  p.rope_rows = int(rope_rows);
   decode_launch(p, D, workspace, stream, o != nullptr);
   return check_launch("attention_decode_qkv_dev_bf16");
 }

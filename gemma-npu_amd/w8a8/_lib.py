@@ -90,7 +90,7 @@ SIGNATURES = {
                                                  _p]),
     "w8a8_decode_tail_workspace_bytes": (_i64, [_i64]),
     "w8a8_decode_tail": (_i32, [_p, _i64, _f32, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _p]),
-    "w8a8_attention_decode_qkv_dev_bf16": (_i32, [_p, _p, _p, _p, _p, _f32, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64,
+    "w8a8_attention_decode_qkv_dev_bf16": (_i32, [_p, _p, _p, _i64, _p, _p, _f32, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64,
                                                    _i64, _i64, _i32, _p, _i64, _f32, _p, _i64, _p, _i64, _p]),
     "w8a8_attention_decode_bf16": (_i32, [_p, _i64, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                           _i64, _f32, _p, _i64, _p, _p, _i64, _p]),

@@ -263,8 +263,8 @@ def decode_at(q, k, v, pos, window=0, scale=1.0, out=None, workspace=None):
 def decode_qkv_at(y, cos, sin, qw, kw, eps, H, KV, D, k, v, pos, kv_write, window=0, scale=1.0, out=None,
                   workspace=None, merge=True):
     """k_qkv and decode_at in one launch, for the token's qkv row y [1, (H + 2 KV) D] bf16 ([1, H D] when
-    the layer reads another layer's keys): q = RoPE(rms(q head) * qw) per head with the cos / sin rows
-    [1, D] at the position; with kv_write the token's key (rms * kw, RoPE) and value (rms) of each KV
+    the layer reads another layer's keys): q = RoPE(rms(q head) * qw) per head with cos / sin [1, D]
+    (the rows at the position) or tables [rows, D] read at the position held in pos; with kv_write the token's key (rms * kw, RoPE) and value (rms) of each KV
     head are also written into the cache k / v [KV, Tk, D] at the position read from pos (int32 [1])
     and attended to there.  Bit for bit fused.k_qkv_cache (or fused.k_qkv for q alone) followed by
     decode_at.  At most 8 query heads per KV head.  merge=False leaves the chunk partials in the
@@ -277,8 +277,8 @@ def decode_qkv_at(y, cos, sin, qw, kw, eps, H, KV, D, k, v, pos, kv_write, windo
     width = (H + (2 * KV if kv_write else 0)) * D
     if y.numel() != width:
         raise ValueError(f"decode_qkv_at: y holds {y.numel()} values, expected {width}")
-    if cos.numel() != D or sin.numel() != D:
-        raise ValueError(f"decode_qkv_at: cos / sin must hold one row of {D}")
+    if cos.dim() != 2 or cos.shape[1] != D or tuple(sin.shape) != tuple(cos.shape):
+        raise ValueError(f"decode_qkv_at: cos / sin must be [rows, {D}]: one row, or a table read at the position")
     for t, name in ((qw, "qw"), (kw, "kw")):
         if t is not None and (t.dtype != torch.bfloat16 or t.numel() != D or not t.is_contiguous()):
             raise ValueError(f"decode_qkv_at: {name} must be a contiguous bf16 [{D}]")
@@ -302,7 +302,7 @@ def decode_qkv_at(y, cos, sin, qw, kw, eps, H, KV, D, k, v, pos, kv_write, windo
     khs, krs = _strides(k)
     vhs, vrs = _strides(v)
     ptr = lambda t: None if t is None else t.data_ptr()
-    call("w8a8_attention_decode_qkv_dev_bf16", y.data_ptr(), cos.data_ptr(), sin.data_ptr(), ptr(qw), ptr(kw),
+    call("w8a8_attention_decode_qkv_dev_bf16", y.data_ptr(), cos.data_ptr(), sin.data_ptr(), cos.shape[0], ptr(qw), ptr(kw),
          float(eps), k.data_ptr(), khs, krs, v.data_ptr(), vhs, vrs, H, KV, Tk, D, 1 if kv_write else 0,
          pos.data_ptr(), int(window), float(scale), None if out is None else out.data_ptr(),
          D if out is None or H == 1 else out.stride(0), ws.data_ptr(), ws.numel(), _stream(y))

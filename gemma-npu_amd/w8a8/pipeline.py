@@ -452,7 +452,7 @@ class Decoder:
     def _layer(self, p, h, pend, per_layer, scalar, rope, norm_next):
         """Decoder layer p on the token's row at the device-held position: h [1, hidden] is the residual
         stream before the layer's input norm and pend how that norm is made (_norm_linear); rope maps
-        the attention kind to its (cos, sin) rows [1, head_dim] at that position.  Returns the
+        the attention kind to its (cos, sin) tables [max_len, head_dim], read at the position.  Returns the
         residual stream and the pending norm after the layer: the next layer's input norm with
         norm_next, else the model's final norm."""
         W = p.weights
@@ -474,6 +474,7 @@ class Decoder:
                                              p.window, 1.0, W["o"].gemv_w, W["o"].sw_bf16)
         else:
             merge_in_o = False
+            cos, sin = cos.index_select(0, self.pos64), sin.index_select(0, self.pos64)
             if p.shares_kv:
                 q = fused.k_qkv(y, None, None, cos, sin, p.norm_q, None, eps, p.heads, p.kv_heads, p.head_dim,
                                 True)[0]
@@ -507,8 +508,7 @@ class Decoder:
         per_layer = self.lm.project_per_layer_inputs(emb, self.lm.get_per_layer_inputs(self.tok, emb))[0]
         h = emb[0]
         scalar = self.pre._scalars()
-        rope = {kind: (c.index_select(0, self.pos64), s.index_select(0, self.pos64))
-                for kind, (c, s) in self.rope.items()}
+        rope = self.rope  # the attention reads the tables' rows at the position itself
         plans = self.pre.plans
         pend = (h, None, plans[0].norm_in, None, None, False)
         for i, p in enumerate(plans):

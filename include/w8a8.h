@@ -513,14 +513,16 @@ int w8a8_attention_decode_dev_bf16(const uint16_t *q, int64_t q_head_stride, con
  * launch (the decode step's k_qkv and attention, pipeline.py:72-86 and local_attn.py:44-83): y is
  * the token's qkv row, bf16 [H*D q | KV*D k | KV*D v] (kv_write = 1) or [H*D] (kv_write = 0, a layer
  * that reads another layer's keys); per q head RMS norm with qw (null: no weight) and RoPE with the
- * cos / sin rows [D] at the position.  With kv_write the workgroup holding the position also makes
+ * cos / sin rows [D] at the position: cos_ / sin_ are tables of rope_rows rows of D (row r for
+ * position r) read at row *q_pos (a position past them reads zeros), or with rope_rows = 1 the one
+ * row to use.  With kv_write the workgroup holding the position also makes
  * each KV head's key (norm with kw, RoPE) and value (norm without weight), writes them into k / v at
  * row *q_pos (when it is below Tk) and attends to them there.  Bit for bit the two-launch form.  At
  * most 8 query heads per KV head; 16-byte aligned pointers; workspace as
  * w8a8_attention_decode_dev_bf16's.  o = NULL: the chunks are not merged; their partials stay in
  * the workspace for w8a8_gemv_packed_attn_merge_bf16 (at most 16 chunks). */
 int w8a8_attention_decode_qkv_dev_bf16(const uint16_t *y, const uint16_t *cos_, const uint16_t *sin_,
-                                       const uint16_t *qw, const uint16_t *kw, float eps, uint16_t *k,
+                                       int64_t rope_rows, const uint16_t *qw, const uint16_t *kw, float eps, uint16_t *k,
                                        int64_t k_head_stride, int64_t k_row_stride, uint16_t *v,
                                        int64_t v_head_stride, int64_t v_row_stride, int64_t H, int64_t KV,
                                        int64_t Tk, int64_t D, int kv_write, const int32_t *q_pos, int64_t window,

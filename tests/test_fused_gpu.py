@@ -391,6 +391,8 @@ def test_decode_qkv_at_equals_k_qkv_then_decode_at(D, KV, window):
     qw, kw = norm_weight(D, 52).to(DEV), norm_weight(D, 53).to(DEV)
     fill = (torch.randn(KV, rows, D, generator=gen(54)) * 0.7).to(torch.bfloat16).to(DEV)
     fill_v = (torch.randn(KV, rows, D, generator=gen(55))).to(torch.bfloat16).to(DEV)
+    tables_c = torch.rand(rows, D, generator=gen(56)).to(torch.bfloat16).to(DEV)
+    tables_s = torch.rand(rows, D, generator=gen(57)).to(torch.bfloat16).to(DEV)
     for p in (0, 5, 31, 32, 63, 64, 100, 600, rows - 1):
         pos = torch.tensor([p], dtype=torch.int32, device=DEV)
         for kv_write in (True, False):
@@ -405,6 +407,13 @@ def test_decode_qkv_at_equals_k_qkv_then_decode_at(D, KV, window):
             got = attention.decode_qkv_at(y, cos, sin, qw, kw, EPS, H, KV, D, kc, vc, pos, kv_write, window, 0.75)
             assert torch.equal(got, want), (p, kv_write)
             assert torch.equal(kc, kc_ref) and torch.equal(vc, vc_ref), (p, kv_write)
+            # the RoPE tables [rows, D] read at the position held in pos
+            ctab, stab = tables_c.clone(), tables_s.clone()
+            ctab[p], stab[p] = cos[0], sin[0]
+            kc, vc = fill.clone(), fill_v.clone()
+            got = attention.decode_qkv_at(y, ctab, stab, qw, kw, EPS, H, KV, D, kc, vc, pos, kv_write, window, 0.75)
+            assert torch.equal(got, want), (p, kv_write, "table")
+            assert torch.equal(kc, kc_ref) and torch.equal(vc, vc_ref), (p, kv_write, "table")
 
 
 @pytest.mark.parametrize("D, window, H, KV", [(256, 512, 8, 1), (512, 512, 8, 1), (128, 64, 4, 1), (256, 128, 16, 2)])
