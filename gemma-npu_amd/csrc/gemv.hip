@@ -448,6 +448,28 @@ __global__ __launch_bounds__(256) void pack_gemv_weight_kernel(const int8_t* __r
   *reinterpret_cast<v4u*>(out + c * 16) = v;
 }
 
+static int gemv_cu_count() {
+  static const int cus = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                                hipSuccess || n <= 0)
+      n = 256;
+    return n;
+  }();
+  return cus;
+}
+
+// Waves of a workgroup sharing one n-tile's K range on the few-tile shapes: doubled up to 16 while
+// the chip holds fewer than ~4096 waves and each wave keeps two k-blocks, but not to 16 (1024-thread
+// workgroups, one per CU) when there are more tiles than CUs: those would run in two rounds, where 8
+// (two workgroups per CU) runs in one (the full-attention qkv, N = 5120: 12.5 -> 7.5 us).
+static int few_tile_split(int64_t ntiles, int KB) {
+  int split = 1;
+  while (split < 16 && ntiles * split < 4096 && split * 2 <= KB) split *= 2;
+  if (split == 16 && ntiles > gemv_cu_count()) split = 8;
+  return split;
+}
+
 template <bool PACKED>
 static void gemv_launch(const GemvParams& p0, hipStream_t stream) {
   GemvParams p = p0;
@@ -469,8 +491,7 @@ static void gemv_launch(const GemvParams& p0, hipStream_t stream) {
     // the chip's 1024 SIMDs, each with at least two k-blocks.  The weights here are 3-19 MB, so
     // what bounds them is how many bytes are in flight: with at most four waves per tile the
     // down projection (96 tiles) ran 384 waves and reached ~1 TB/s.
-    int split = 1;
-    while (split < 16 && ntiles * split < 4096 && split * 2 <= p.KB) split *= 2;
+    const int split = few_tile_split(ntiles, p.KB);
     p.split = split;
     if (split <= 4) {
       const int gpb = 4 / split;
@@ -497,8 +518,7 @@ static void gemv_launch_act(const GemvParams& p0, hipStream_t stream) {
   GemvParams p = p0;
   const int64_t ntiles = (p.N + 15) / 16;
   const int64_t groups = ACT == 1 ? p.half_tiles : ntiles;
-  int split = 1;
-  while (split < 16 && ntiles * split < 4096 && split * 2 <= p.KB) split *= 2;
+  const int split = few_tile_split(ntiles, p.KB);
   p.split = split;
   constexpr int TPW = ACT == 1 ? 2 : 1;
   if (split <= 4) {
