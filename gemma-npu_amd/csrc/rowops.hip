@@ -575,21 +575,32 @@ static int k_ple_gate(const RowInput& in, const uint16_t* ple, int64_t ldp, int6
   return launch_row_chain(p, in.i32, stream, what);
 }
 
+// k_ple_out, and with w_next also the next layer's k_in on the rows it writes (the same launch: the
+// second norm and the quant of the row kernel, on the values stored as out).
 static int k_ple_out(const RowInput& in, const uint16_t* h, int64_t ldh, const uint16_t* w_post_ple,
                      const uint16_t* scalar, float eps, int64_t M, int64_t N, uint16_t* out, int64_t ldo,
-                     hipStream_t stream) {
-  const char* what = "k_ple_out";
+                     hipStream_t stream, const uint16_t* w_next = nullptr, int8_t* q = nullptr, int64_t ldq = 0,
+                     int q_packed = 0, float* sq = nullptr) {
+  const char* what = w_next ? "k_ple_out_k_in" : "k_ple_out";
   W8A8_TRY(check_rows(what, M, N));
   W8A8_TRY(check_input(what, in, N));
   W8A8_TRY(check_bf16_rows(what, "h", h, ldh, N));
   W8A8_TRY(check_bf16_rows(what, "out", out, ldo, N));
   W8A8_TRY(check_vec16(what, "w_post_ple", w_post_ple));
-  if (!scalar) return fail(W8A8_EINVAL, "k_ple_out: scalar is null");
-  if (M == 0) return W8A8_OK;
+  if (!scalar) return fail(W8A8_EINVAL, "%s: scalar is null", what);
   RowChain p{};
+  if (w_next) {
+    W8A8_TRY(check_vec16(what, "w_next", w_next));
+    W8A8_TRY(set_q(what, p, q, ldq, q_packed, sq, N));
+  }
+  if (M == 0) return W8A8_OK;
   set_input(p, in, N);
   p.op = RC_NORM_RES; p.aux = h; p.ld_aux = ldh; p.w1 = w_post_ple; p.scalar = scalar;
   p.h = out; p.ldh = ldo;
+  if (w_next) {
+    p.norm2 = 1;
+    p.w2 = w_next;
+  }
   p.eps = eps; p.M = int(M); p.N = int(N);
   return launch_row_chain(p, in.i32, stream, what);
 }
@@ -732,6 +743,24 @@ int w8a8_k_ple_out(const int32_t* acc, int64_t ldacc, const float* sx, const flo
                    int64_t ldh, const uint16_t* w_post_ple, const uint16_t* scalar, float eps, int64_t M, int64_t N,
                    uint16_t* out, int64_t ldo, hipStream_t stream) {
   return w8a8::k_ple_out(RowInput{acc, ldacc, sx, sw, true}, h, ldh, w_post_ple, scalar, eps, M, N, out, ldo, stream);
+}
+
+int w8a8_k_ple_out_k_in(const int32_t* acc, int64_t ldacc, const float* sx, const float* sw, const uint16_t* h,
+                        int64_t ldh, const uint16_t* w_post_ple, const uint16_t* scalar, const uint16_t* w_in_next,
+                        float eps, int64_t M, int64_t N, uint16_t* out, int64_t ldo, int8_t* q, int64_t ldq,
+                        int q_packed, float* sq, hipStream_t stream) {
+  if (!w_in_next) return fail(W8A8_EINVAL, "k_ple_out_k_in: w_in_next is null");
+  return w8a8::k_ple_out(RowInput{acc, ldacc, sx, sw, true}, h, ldh, w_post_ple, scalar, eps, M, N, out, ldo, stream,
+                         w_in_next, q, ldq, q_packed, sq);
+}
+
+int w8a8_k_ple_out_k_in_y(const uint16_t* y, int64_t ldy, const uint16_t* h, int64_t ldh, const uint16_t* w_post_ple,
+                          const uint16_t* scalar, const uint16_t* w_in_next, float eps, int64_t M, int64_t N,
+                          uint16_t* out, int64_t ldo, int8_t* q, int64_t ldq, int q_packed, float* sq,
+                          hipStream_t stream) {
+  if (!w_in_next) return fail(W8A8_EINVAL, "k_ple_out_k_in: w_in_next is null");
+  return w8a8::k_ple_out(RowInput{y, ldy, nullptr, nullptr, false}, h, ldh, w_post_ple, scalar, eps, M, N, out, ldo,
+                         stream, w_in_next, q, ldq, q_packed, sq);
 }
 
 int w8a8_k_ple_out_y(const uint16_t* y, int64_t ldy, const uint16_t* h, int64_t ldh, const uint16_t* w_post_ple,

@@ -56,6 +56,10 @@ SIGNATURES = {
     "w8a8_k_post_attn_y": (_i32, [_p, _i64, _p, _i64, _p, _p, _f32, _i64, _i64, _p, _i64, _p, _i64, _i32, _p, _p]),
     "w8a8_k_post_ff_y": (_i32, [_p, _i64, _p, _i64, _p, _f32, _i64, _i64, _p, _i64, _p, _i64, _i32, _p, _p]),
     "w8a8_k_ple_gate_y": (_i32, [_p, _i64, _p, _i64, _i64, _i64, _p, _i64, _i32, _p, _p]),
+    "w8a8_k_ple_out_k_in": (_i32, [_p, _i64, _p, _p, _p, _i64, _p, _p, _p, _f32, _i64, _i64, _p, _i64, _p, _i64, _i32,
+                                   _p, _p]),
+    "w8a8_k_ple_out_k_in_y": (_i32, [_p, _i64, _p, _i64, _p, _p, _p, _f32, _i64, _i64, _p, _i64, _p, _i64, _i32, _p,
+                                     _p]),
     "w8a8_k_ple_out_y": (_i32, [_p, _i64, _p, _i64, _p, _p, _f32, _i64, _i64, _p, _i64, _p]),
     "w8a8_gelu_mul_bf16": (_i32, [_p, _i64, _p, _i64, _i64, _i64, _p, _i64, _p]),
     "w8a8_k_qkv_cache_y": (_i32, [_p, _i64, _p, _p, _i64, _p, _p, _f32, _i64, _i64, _i64, _i64, _p, _p, _p, _i64, _p,

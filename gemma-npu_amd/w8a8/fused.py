@@ -230,11 +230,13 @@ def k_ple_gate(acc, sx, sw, ple, packed=False):
     return xq, sq
 
 
-def k_ple_out(acc, sx, sw, h, w_post_ple, scalar, eps):
+def k_ple_out(acc, sx, sw, h, w_post_ple, scalar, eps, norm_next=None, packed=False):
     """PLE projection out -> residual add -> layer scalar: bf16(bf16(h + rms(y)) * scalar).
 
     scalar: a one-element bf16 tensor on the device (the layer scalar), or a Python number,
-    which is rounded to bf16 first."""
+    which is rounded to bf16 first.  With norm_next (the next layer's input-norm weight) the same
+    launch also runs that layer's k_in on the rows it writes: returns (out, xq, sx_next), xq packed
+    or row-major as k_in's."""
     M, N = h.shape
     y = _acc(acc, sx, sw, N, dequantised_ok=True)
     hp, ldh = _rows(h, "h", M, N)
@@ -244,12 +246,20 @@ def k_ple_out(acc, sx, sw, h, w_post_ple, scalar, eps):
         raise ValueError("k_ple_out: scalar must be one bf16 value on the tensors' device")
     scalar = scalar.reshape(1).contiguous()
     out = torch.empty((M, N), dtype=torch.bfloat16, device=h.device)
-    tail = (hp, ldh, _vec(w_post_ple, "w_post_ple", N), scalar.data_ptr(), float(eps), M, N, out.data_ptr(), N,
-            _stream(acc))
-    if y:
-        _same_device(acc, h, w_post_ple)
-        call("w8a8_k_ple_out_y", acc.data_ptr(), _ld(acc), *tail)
+    if norm_next is None:
+        tail = (hp, ldh, _vec(w_post_ple, "w_post_ple", N), scalar.data_ptr(), float(eps), M, N, out.data_ptr(), N,
+                _stream(acc))
+        name = "w8a8_k_ple_out"
     else:
-        _same_device(acc, sx, sw, h, w_post_ple)
-        call("w8a8_k_ple_out", acc.data_ptr(), _ld(acc), sx.data_ptr(), sw.data_ptr(), *tail)
-    return out
+        q, ldq, qp, xq = _q_out(M, N, h.device, packed)
+        sxn = torch.empty((M,), dtype=torch.float32, device=h.device)
+        tail = (hp, ldh, _vec(w_post_ple, "w_post_ple", N), scalar.data_ptr(), _vec(norm_next, "norm_next", N),
+                float(eps), M, N, out.data_ptr(), N, q.data_ptr(), ldq, qp, sxn.data_ptr(), _stream(acc))
+        name = "w8a8_k_ple_out_k_in"
+    if y:
+        _same_device(acc, h, w_post_ple, norm_next)
+        call(name + "_y", acc.data_ptr(), _ld(acc), *tail)
+    else:
+        _same_device(acc, sx, sw, h, w_post_ple, norm_next)
+        call(name, acc.data_ptr(), _ld(acc), sx.data_ptr(), sw.data_ptr(), *tail)
+    return out if norm_next is None else (out, xq, sxn)

@@ -185,8 +185,11 @@ class Prefill:
             self.layer_scalars = [layer.layer_scalar.to(torch.bfloat16) for layer in self.lm.layers]
         return self.layer_scalars
 
-    def _layer(self, p, h, start, end, per_layer, rope, store, scalar):
-        """Rows [start, end) of the prompt through decoder layer p; returns their new hidden rows."""
+    def _layer(self, p, h, start, end, per_layer, rope, store, scalar, xin=None, norm_next=None):
+        """Rows [start, end) of the prompt through decoder layer p; returns their new hidden rows.  xin:
+        the layer's input rows already normed and quantised (k_in), by the previous layer's last
+        launch; with norm_next (the next layer's input-norm weight) that launch also makes the next
+        layer's: returns (rows, xq, sx)."""
         eps = self.cfg.rms_norm_eps
         W = p.weights
 
@@ -198,7 +201,7 @@ class Prefill:
                 return ops.gemm_bf16(xq, sx, w.packed, w.sw)
             return ops.gemm_i32(xq, w.packed)
         cos, sin = (t[start:end] for t in rope[p.kind])
-        xq, sx = fused.k_in(h, p.norm_in, eps, packed=True)
+        xq, sx = fused.k_in(h, p.norm_in, eps, packed=True) if xin is None else xin
         acc = gemm(xq, sx, W["qkv"])
         q, k, v = fused.k_qkv(acc, sx, W["qkv"].sw, cos, sin, p.norm_q, p.norm_k, eps, p.heads, p.kv_heads,
                               p.head_dim, p.shares_kv)
@@ -220,7 +223,8 @@ class Prefill:
         acc = gemm(xq, sx, W["ple_gate"])
         xq, sx = fused.k_ple_gate(acc, sx, W["ple_gate"].sw, per_layer[start:end, p.index], packed=True)
         acc = gemm(xq, sx, W["ple_proj"])
-        return fused.k_ple_out(acc, sx, W["ple_proj"].sw, h, p.norm_post_ple, scalar[p.index], eps)
+        return fused.k_ple_out(acc, sx, W["ple_proj"].sw, h, p.norm_post_ple, scalar[p.index], eps, norm_next,
+                               packed=True)
 
     def run_layers(self, h0, per_layer, rope, scalar=None):
         """Every decoder layer over the prompt: (final hidden rows [T, hidden] before the last norm,
@@ -233,8 +237,13 @@ class Prefill:
         for start in range(0, T, step):  # prompt order: each range sees the keys of those before it
             end = min(start + step, T)
             h = h0[start:end]
-            for p in self.plans:
-                h = self._layer(p, h, start, end, per_layer, rope, store, scalar)
+            xin = None
+            for i, p in enumerate(self.plans):
+                if i + 1 < len(self.plans):
+                    h, *xin = self._layer(p, h, start, end, per_layer, rope, store, scalar, xin,
+                                          self.plans[i + 1].norm_in)
+                else:
+                    h = self._layer(p, h, start, end, per_layer, rope, store, scalar, xin)
             rows.append(h)
         return (rows[0] if len(rows) == 1 else torch.cat(rows)), store
 

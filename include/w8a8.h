@@ -294,6 +294,18 @@ int w8a8_k_ple_out_y(const uint16_t *y, int64_t ldy, const uint16_t *h, int64_t 
                      const uint16_t *scalar, float eps, int64_t M, int64_t N, uint16_t *out, int64_t ldo,
                      hipStream_t stream);
 
+/* w8a8_k_ple_out / _y followed by the next layer's w8a8_k_in on the rows it writes, in one launch:
+ * out as w8a8_k_ple_out writes it, and q / sq = quant(bf16(rms(out) * w_in_next)) as w8a8_k_in
+ * (pipeline.py:124-127 then 66-69; row-major or packed q).  Bit for bit the two launches. */
+int w8a8_k_ple_out_k_in(const int32_t *acc, int64_t ldacc, const float *sx, const float *sw, const uint16_t *h,
+                        int64_t ldh, const uint16_t *w_post_ple, const uint16_t *scalar, const uint16_t *w_in_next,
+                        float eps, int64_t M, int64_t N, uint16_t *out, int64_t ldo, int8_t *q, int64_t ldq,
+                        int q_packed, float *sq, hipStream_t stream);
+int w8a8_k_ple_out_k_in_y(const uint16_t *y, int64_t ldy, const uint16_t *h, int64_t ldh, const uint16_t *w_post_ple,
+                          const uint16_t *scalar, const uint16_t *w_in_next, float eps, int64_t M, int64_t N,
+                          uint16_t *out, int64_t ldo, int8_t *q, int64_t ldq, int q_packed, float *sq,
+                          hipStream_t stream);
+
 /* ---- whole linear: bf16 in -> bf16 out (NPUGemm.matmul, gemma_npu.py:117-152) ------------ */
 
 /* Workspace for w8a8_linear_bf16: the packed int8 rows and the per-row scales, 256-byte aligned

@@ -446,3 +446,28 @@ def test_o_projection_merging_the_attention_chunks(D, window, H, KV):
         got = ops.gemv_attn_merge_bf16(ws, pos, H, KV, rows, D, window, 0.5, pw, s)
         assert torch.equal(got, want), p
         assert torch.equal(kc2, kc) and torch.equal(vc2, vc), p
+
+
+@pytest.mark.parametrize("T", [1, 77, 600])
+@pytest.mark.parametrize("packed", [False, True])
+def test_k_ple_out_with_the_next_k_in(T, packed):
+    """k_ple_out with the next layer's input norm and quant in the same launch (the whole-prompt
+    prefill's layer boundary) against k_ple_out then k_in: the rows and the int8 rows and scales bit
+    for bit, from the int32 GEMM result and from its dequantised bf16 form, row-major and packed."""
+    N = 1536
+    acc, sx, sw = acc_inputs(T, N, seed=95 + T)
+    acc, sx, sw = acc.to(DEV), sx.to(DEV), sw.to(DEV)
+    h = bf16_rows(T, N, 96).to(DEV)
+    w, w_next = norm_weight(N, 97).to(DEV), norm_weight(N, 98).to(DEV)
+    scalar = torch.tensor([0.62], dtype=torch.bfloat16, device=DEV)
+    y = ops.dequant_bf16(acc, sx, sw)
+    for src in ((acc, sx, sw), (y, None, None)):
+        out_ref = fused.k_ple_out(*src, h, w, scalar, EPS)
+        xq_ref, sx_ref = fused.k_in(out_ref, w_next, EPS, packed=packed)
+        out, xq, sxn = fused.k_ple_out(*src, h, w, scalar, EPS, norm_next=w_next, packed=packed)
+        assert torch.equal(out, out_ref)
+        assert torch.equal(sxn, sx_ref)
+        if packed:
+            assert torch.equal(xq.data, xq_ref.data)
+        else:
+            assert torch.equal(xq, xq_ref)
