@@ -158,6 +158,37 @@ def test_gemv_packed_matches_row_major(M, K, N):
         assert_bf16_close(f32(to_bits(y_pk)), f32(ref), what=f"packed gemv M{M} K{K} N{N}", extra=extra)
 
 
+def ragged_gemv_shapes():
+    """Seeded ragged shapes over every row count the GEMV takes and the few-tile, split-K and
+    wide launch forms its picker chooses between."""
+    rng = np.random.default_rng(77)
+    out = []
+    for M in range(1, 17):
+        N = int(rng.integers(1, 4000))
+        K = int(rng.integers(1, 260)) * 16
+        out.append((M, N, K))
+    return out + [(1, 1, 16), (16, 17, 6160), (3, 40000, 48)]
+
+
+@pytest.mark.parametrize("M,N,K", ragged_gemv_shapes())
+def test_gemv_packed_ragged_shapes_vs_oracle(M, N, K):
+    """Packed and row-major GEMV at ragged N and K (K a multiple of 16), both scale types: equal
+    to each other bit for bit and to the oracle within the GEMV tolerance."""
+    x = workloads.activations(M, K, seed=M * 101 + K, outliers=False)
+    g = torch.Generator().manual_seed(N * 3 + K)
+    w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    sf = torch.rand(N, generator=g) * 0.015 + 0.005
+    print(f"gemv ragged M={M} N={N} K={K}", flush=True)
+    pw = ops.pack_gemv_weight(w.to(DEV))
+    for s, kind in ((sf.to(torch.bfloat16), "bf16"), (sf, "f32")):
+        y = ops.gemv_bf16(x.to(DEV), pw, s.to(DEV))
+        assert torch.equal(y, ops.gemv_bf16(x.to(DEV), w.to(DEV), s.to(DEV)))
+        extra = dot_error_bound(x.float().numpy(), w.numpy(), s.float().numpy())
+        ref = orc.gemv(to_bits(x), w.numpy(), to_bits(s) if kind == "bf16" else s.numpy(), kind)
+        assert_bf16_close(f32(to_bits(y)), f32(ref), what=f"ragged gemv M{M} N{N} K{K} {kind} scales",
+                          extra=extra)
+
+
 def test_gemv_packed_lm_head_exact_on_integer_activations():
     """The LM-head shape (K=1536, N=262144) with integer activations: every partial sum is exact,
     so the packed GEMV must equal bf16(int32 product * s)."""
