@@ -352,6 +352,40 @@ def test_decode_matches_oracle(H, KV, Tk, D, q_pos, window):
     assert np.allclose(lse.cpu().numpy(), lse_ref[:, 0], rtol=1e-5, atol=1e-4), "decode logsumexp differs"
 
 
+def ragged_cases(seed, n, decode):
+    """Seeded ragged attention calls: head groupings, head_dims, prompt lengths, query offsets and
+    windows drawn at random (window 0 = full causal)."""
+    rng = np.random.default_rng(seed)
+    groups = [(8, 1), (4, 2), (6, 2), (16, 1), (2, 2), (12, 3)]
+    out = []
+    for _ in range(n):
+        H, KV = groups[int(rng.integers(len(groups)))]
+        D = int(rng.choice([128, 256, 512]))
+        Tk = int(rng.integers(1, 700 if D == 512 else 900))
+        window = int(rng.choice([0, 0, int(rng.integers(1, 600))]))
+        if decode:
+            out.append((H, KV, Tk, D, int(rng.integers(0, Tk)), window))
+        else:
+            q_start = int(rng.integers(0, Tk))
+            out.append((H, KV, Tk - q_start, Tk, D, q_start, window))
+    return out
+
+
+@pytest.mark.parametrize("H,KV,Tq,Tk,D,q_start,window", ragged_cases(404, 10, False))
+def test_attention_ragged_calls_match_oracle(H, KV, Tq, Tk, D, q_start, window):
+    print(f"attention ragged H={H} KV={KV} Tq={Tq} Tk={Tk} D={D} q_start={q_start} W={window}", flush=True)
+    q, k, v = make(H, KV, Tq, Tk, D, seed=Tq * 7 + Tk + D, qscale=0.5)
+    o, lse = attn.attention(q.to(DEV), k.to(DEV), v.to(DEV), q_start, window, return_lse=True)
+    ref, bud, lse_ref = reference(q, k, v, q_start, window)
+    check(o, ref, bud, "ragged attention")
+    assert np.allclose(lse.cpu().numpy(), lse_ref, rtol=1e-5, atol=1e-4), "ragged attention logsumexp differs"
+
+
+@pytest.mark.parametrize("H,KV,Tk,D,q_pos,window", ragged_cases(505, 10, True))
+def test_decode_ragged_calls_match_oracle(H, KV, Tk, D, q_pos, window):
+    test_decode_matches_oracle(H, KV, Tk, D, q_pos, window)
+
+
 def test_decode_mirror_and_determinism():
     """split_kv_decode takes the reference's shapes ([1, H, 1, D] against [1, 1, T, D]) and
     returns [1, 1, H, D]; repeated calls give the same bits."""
