@@ -224,6 +224,37 @@ def test_k_post_ff(T):
     assert np.array_equal(npy(q), q_ref) and np.array_equal(npy(s), s_ref)
 
 
+@pytest.mark.parametrize("N", [8, 200, 1000, 2560, 3840, 5000, 12288])
+def test_row_kernels_at_other_hidden_sizes(N):
+    """k_in, k_post_attn and k_post_ff at hidden sizes other than E2B's 1536 (any multiple of 8 up
+    to 12288: other Gemma sizes and ragged widths), against the oracle with the same bars as the
+    1536-wide tests."""
+    T = 37
+    print(f"row kernels N={N}", flush=True)
+    h = workloads.activations(T, N, seed=N + 1)
+    w = norm_weight(N, N + 2)
+    q, s = fused.k_in(h.to(DEV), w.to(DEV), EPS)
+    q_ref, s_ref = orc.k_in(to_bits(h), to_bits(w), EPS)
+    check_quant(q, s, q_ref, s_ref, f"k_in N={N}", min_exact=0.98)
+    qp, sp = fused.k_in(h.to(DEV), w.to(DEV), EPS, packed=True)
+    assert np.array_equal(unpacked(qp)[0], npy(q)) and np.array_equal(npy(sp), npy(s))
+
+    acc, sx, sw = acc_inputs(T, N, seed=N + 3)
+    res = bf16_rows(T, N, N + 4)
+    w1, w2 = norm_weight(N, N + 5), norm_weight(N, N + 6)
+    hh, q, s = fused.k_post_attn(acc.to(DEV), sx.to(DEV), sw.to(DEV), res.to(DEV), w1.to(DEV), w2.to(DEV), EPS)
+    h_ref, _, _ = orc.k_post_attn(acc.numpy(), sx.numpy(), sw.numpy(), to_bits(res), to_bits(w1), to_bits(w2), EPS)
+    check_h(hh, h_ref, to_bits(res), f"k_post_attn h N={N}")
+    q_ref, s_ref = orc.quant_rows(orc.rms_bf16(npy(hh), to_bits(w2), EPS), "bf16")
+    check_quant(q, s, q_ref, s_ref, f"k_post_attn q N={N}", min_exact=0.98)
+
+    hh, q, s = fused.k_post_ff(acc.to(DEV), sx.to(DEV), sw.to(DEV), res.to(DEV), w1.to(DEV), EPS)
+    h_ref, _, _ = orc.k_post_ff(acc.numpy(), sx.numpy(), sw.numpy(), to_bits(res), to_bits(w1), EPS)
+    check_h(hh, h_ref, to_bits(res), f"k_post_ff h N={N}")
+    q_ref, s_ref = orc.quant_rows(npy(hh), "bf16")
+    assert np.array_equal(npy(q), q_ref) and np.array_equal(npy(s), s_ref)
+
+
 # ---- k_gelu / k_ple_gate ------------------------------------------------------------------
 
 @pytest.mark.parametrize("T,I", [(33, 6144), (5, 256)])
