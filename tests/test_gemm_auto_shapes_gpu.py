@@ -2,7 +2,8 @@
 ragged shapes that cross the picker's rules (M around 1024 and past 8192, K from one k-tile to
 12288, N from one 16-column tile to the double-wide gate/up): int32 bit-exact against an fp64
 product on the GPU (every product and partial sum is an integer below 2^53, so the fp64 result is
-exact), and the dequant epilogue bit-exact against bf16((acc.float() * sx) * sw) (pipeline.py:55-57)."""
+exact), the dequant epilogue bit-exact against bf16((acc.float() * sx) * sw) (pipeline.py:55-57) and
+the residual epilogue against that plus the residual in bf16."""
 import numpy as np
 import pytest
 import torch
@@ -41,3 +42,6 @@ def test_auto_tile_int32_and_dequant_exact(M, N, K):
     y = ops.gemm_bf16(a, sx, pw)
     ref = ((want.int().float() * sx[:, None]) * sw[None, :]).to(torch.bfloat16)
     assert torch.equal(y.view(torch.int16), ref.view(torch.int16)), f"dequant mismatch at M={M} N={N} K={K}"
+    r = torch.randn(M, N, generator=g, device=DEV).to(torch.bfloat16)
+    yr = ops.gemm_bf16(a, sx, pw, epilogue="residual", residual=r)
+    assert torch.equal(yr.view(torch.int16), (ref + r).view(torch.int16)), f"residual mismatch at M={M} N={N} K={K}"
