@@ -125,16 +125,25 @@ class KVStore:
         return cache
 
 
-def prompt_inputs(lm, ids):
+def prompt_inputs(lm, ids, rope_cache=None):
     """The model's own inputs to its decoder layers for ids [1, T]: the token embeddings [T, hidden],
-    the per-layer inputs [T, layers, P] and the RoPE (cos, sin) rows [T, head_dim] per attention kind."""
+    the per-layer inputs [T, layers, P] and the RoPE (cos, sin) rows [T, head_dim] per attention kind.
+    The RoPE rows depend on the prompt length alone (positions 0 .. T-1): with rope_cache (a dict) the
+    rows of the last few lengths are kept there and reused instead of recomputed."""
     emb = lm.embed_tokens(ids)
     per_layer = lm.project_per_layer_inputs(emb, lm.get_per_layer_inputs(ids, emb))[0]
-    positions = torch.arange(ids.shape[1], device=ids.device)[None]
-    rope = {}
-    for kind in dict.fromkeys(lm.config.layer_types):
-        cos, sin = lm.rotary_emb(emb, positions, kind)
-        rope[kind] = (cos[0], sin[0])
+    key = (ids.shape[1], ids.device, emb.dtype)
+    rope = rope_cache.get(key) if rope_cache is not None else None
+    if rope is None:
+        positions = torch.arange(ids.shape[1], device=ids.device)[None]
+        rope = {}
+        for kind in dict.fromkeys(lm.config.layer_types):
+            cos, sin = lm.rotary_emb(emb, positions, kind)
+            rope[kind] = (cos[0], sin[0])
+        if rope_cache is not None:
+            while len(rope_cache) >= 4:
+                rope_cache.pop(next(iter(rope_cache)))
+            rope_cache[key] = rope
     return emb[0], per_layer, rope
 
 
@@ -152,6 +161,7 @@ class Prefill:
             raise ValueError(f"Prefill: row_step {row_step} must be positive")
         self.row_step = None if row_step is None else int(row_step)
         self.fuse_gelu = bool(fuse_gelu)
+        self.rope_cache = {}  # (T, device, dtype) -> the RoPE rows of positions 0 .. T-1 per attention kind
         # The GEMMs that feed k_qkv / k_post_attn / k_post_ff / k_ple_gate / k_ple_out may write their
         # dequantised bf16 result (the dequant epilogue) instead of int32: those kernels dequantise
         # first, so the results are bit-identical with half the bytes written and read.  True / False
@@ -263,7 +273,7 @@ class Prefill:
         """ids [1, T] -> (last-token logits [vocab] fp32, DynamicCache) (pipeline.py:312-339).
 
         With all_hidden, the final-norm hidden states [T, hidden] instead of the logits."""
-        h0, per_layer, rope = prompt_inputs(self.lm, self.check_ids(ids))
+        h0, per_layer, rope = prompt_inputs(self.lm, self.check_ids(ids), self.rope_cache)
         rows, store = self.run_layers(h0, per_layer, rope)
         cache = store.to_cache(self.cfg, copy=False)
         if all_hidden:
@@ -399,7 +409,7 @@ class Decoder:
         T = ids.shape[1]
         if T >= self.max_len:
             raise ValueError(f"Decoder: a {T}-token prompt leaves no room in max_len {self.max_len}")
-        h0, per_layer, rope = prompt_inputs(self.lm, ids)
+        h0, per_layer, rope = prompt_inputs(self.lm, ids, self.pre.rope_cache)
         rows, store = self.pre.run_layers(h0, per_layer, rope)
         for layer, (kc, vc) in self.cache.items():
             k, v = store.kv[layer]
