@@ -132,6 +132,10 @@ def prompt_inputs(lm, ids, rope_cache=None):
     rows of the last few lengths are kept there and reused instead of recomputed."""
     emb = lm.embed_tokens(ids)
     per_layer = lm.project_per_layer_inputs(emb, lm.get_per_layer_inputs(ids, emb))[0]
+    # a dynamic RoPE (its frequencies follow the longest sequence seen) is recomputed every time
+    kinds = getattr(lm.rotary_emb, "rope_type", {})
+    if any("dynamic" in str(t) for t in (kinds.values() if isinstance(kinds, dict) else [kinds])):
+        rope_cache = None
     key = (ids.shape[1], ids.device, emb.dtype)
     rope = rope_cache.get(key) if rope_cache is not None else None
     if rope is None:

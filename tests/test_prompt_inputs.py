@@ -1,6 +1,7 @@
 """prompt_inputs' RoPE rows kept per prompt length (CPU, with a stand-in language model): a second
 prompt of the same length reuses the rows without calling the model's rotary module, another length
-computes its own, at most four lengths are kept, and the rows equal a fresh computation."""
+computes its own, at most four lengths are kept, the rows equal a fresh computation, and a dynamic
+RoPE (frequencies that follow the longest sequence seen) is never kept."""
 import types
 
 import torch
@@ -59,3 +60,19 @@ def test_without_a_cache_nothing_is_kept():
     prompt_inputs(lm, torch.arange(4)[None])
     prompt_inputs(lm, torch.arange(4)[None])
     assert lm.rotary_calls == 4
+
+
+def test_a_dynamic_rope_is_never_kept():
+    cache, dyn = {}, StandIn()
+    rotary = dyn.rotary_emb
+
+    class Rotary:
+        rope_type = {"sliding_attention": "default", "full_attention": "dynamic"}
+
+        def __call__(self, emb, positions, kind):
+            return rotary(emb, positions, kind)
+
+    dyn.rotary_emb = Rotary()
+    prompt_inputs(dyn, torch.arange(4)[None], cache)
+    prompt_inputs(dyn, torch.arange(4)[None], cache)
+    assert dyn.rotary_calls == 4 and not cache
